@@ -1,0 +1,72 @@
+// oracle.h - CPU restatement of the reference's int8 LLaMA decode path.
+//
+// TEST INFRASTRUCTURE ONLY.  This is the checker: tests/, the smoke check and
+// bench.py's cpu_baseline leg may build against it, nothing else.  The GPU
+// library never links, loads or calls it, and has no CPU fallback to it.
+//
+// Every function restates one piece of /root/reference (file:line given at each
+// definition) in plain C11 with the reference's evaluation order, so that when
+// it is compiled like the reference (ISO C11: no floating-point contraction, no
+// reassociation) it reproduces the reference's results bit for bit.  That claim
+// is pinned by tests/test_oracle_golden.py against fixtures written by the
+// compiled reference itself (tests/golden/gen_golden.c).
+//
+// Weight layout is the reference's: a (rows = in, cols = out) matrix is int8
+// row-major with one fp32 scale per column (quant.h:22-27).
+#ifndef QL_ORACLE_H
+#define QL_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+typedef struct { int rows, cols; int8_t *q; float *scale; } OrQT;
+
+typedef struct {
+  float *attn_norm, *ffn_norm, *b_q, *b_k, *b_v;
+  OrQT Wq, Wk, Wv, Wo, Wgate, Wup, Wdown;
+} OrBlock;
+
+typedef struct {
+  int vocab, d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq;
+  float rope_base, eps;
+  OrQT wte;
+  OrBlock *blocks;
+  float *final_norm;
+  OrQT lm_head;
+} OrModel;
+
+// k, v: [n_layers][max_seq][kv_dim] fp32, as llama.c:513-526 (one block per layer).
+typedef struct { int n_layers, max_seq, kv_dim, len; float *k, *v; } OrKV;
+
+void or_set_threads(int n);          // 0 = all online CPUs (TF_THREADS semantics)
+int  or_get_threads(void);
+
+void or_quantize_int8_percol(const float *w, int rows, int cols, int8_t *q, float *scale);
+void or_dequantize_int8_percol(const int8_t *q, const float *scale, int rows, int cols, float *w);
+void or_qacc_columns(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);
+void or_qmatmul(const float *A, int M, const OrQT *W, float *C);
+// qmatmul with its intermediates exposed: qa[M*K], as[M], acc[M*N].
+void or_qmatmul_ex(const float *A, int M, const OrQT *W, float *C,
+                   int8_t *qa_out, float *as_out, int32_t *acc_out);
+void or_rmsnorm(const float *x, int rows, int cols, const float *gamma, float eps, float *y);
+void or_rope_heads_pos(float *x, int rows, int cols, int n_heads, float base, int pos0);
+void or_gqa_forward(const float *Q, const float *K, const float *V, int n, int H, int KVH,
+                    int hd, float *att, float *O);
+void or_attn_decode(const float *q, const float *kc, const float *vc, int kvd, int pos,
+                    int n_heads, int n_kv, int hd, float *sc, float *o);
+int  or_argmax(const float *r, int n);
+
+// Model from the seeded generator (synth.h), quantized as llama.c:490-511 does.
+int  or_model_synth(OrModel *m, const int32_t cfg[8], float rope_base, float eps,
+                    uint64_t seed, int tied);
+// Model whose weights are copied in from caller buffers laid out like the
+// reference (used to take weights back from the GPU for the CPU baseline).
+int  or_model_alloc(OrModel *m, const int32_t cfg[8], float rope_base, float eps);
+void or_model_free(OrModel *m);
+uint64_t or_model_hash(const OrModel *m);
+
+int  or_kv_create(OrKV *kv, const OrModel *m);
+void or_kv_free(OrKV *kv);
+void or_decode_step(const OrModel *m, OrKV *kv, int token, float *logits);
+
+#endif

@@ -1,0 +1,388 @@
+// gen_golden.c - writes the golden fixtures under tests/golden/data/ by calling
+// the REFERENCE's own compiled functions (objects built from /root/reference by
+// oracle/Makefile into oracle/_ref/).  This file contains no reference code: it
+// only calls the reference's public API (quant.h, llama.h, rmsnorm.h, rope.h,
+// gqa.h, sampler.h, tensor.h) on inputs from the seeded generator (oracle/synth.h)
+// and records what comes back.  It builds only where /root/reference exists.
+//
+//   gen_golden <outdir> ops        quantizer, qmatmul, rmsnorm, rope, attention
+//   gen_golden <outdir> gqa8192    decode attention at context 8192 (slow)
+//   gen_golden <outdir> e2e <name> tiny | 1b | 8b greedy token streams
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include "tensor.h"
+#include "quant.h"
+#include "llama.h"
+#include "rmsnorm.h"
+#include "rope.h"
+#include "gqa.h"
+#include "sampler.h"
+#include "synth.h"
+
+static const char *OUT = ".";
+
+static double now_s(void) {
+  struct timespec t; clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+// ---- minimal .npy writer (v1.0, little-endian, C order) --------------------
+static void npy_write(const char *name, const char *descr, const void *data, size_t elem,
+                      int ndim, const long *shape) {
+  char path[1024]; snprintf(path, sizeof path, "%s/%s.npy", OUT, name);
+  char hdr[256], shp[128] = "";
+  size_t n = 1;
+  for (int i = 0; i < ndim; i++) {
+    char t[32]; snprintf(t, sizeof t, "%ld%s", shape[i], (ndim == 1 || i < ndim - 1) ? "," : "");
+    strcat(shp, t); n *= (size_t)shape[i];
+  }
+  int len = snprintf(hdr, sizeof hdr, "{'descr': '%s', 'fortran_order': False, 'shape': (%s), }", descr, shp);
+  int total = 10 + len + 1;
+  int pad = (64 - total % 64) % 64;
+  FILE *f = fopen(path, "wb");
+  if (!f) { fprintf(stderr, "cannot write %s\n", path); exit(1); }
+  unsigned short hl = (unsigned short)(len + pad + 1);
+  fwrite("\x93NUMPY\x01\x00", 1, 8, f);
+  fwrite(&hl, 2, 1, f);
+  fwrite(hdr, 1, (size_t)len, f);
+  for (int i = 0; i < pad; i++) fputc(' ', f);
+  fputc('\n', f);
+  fwrite(data, elem, n, f);
+  fclose(f);
+}
+static void npy_f32(const char *name, const float *d, int ndim, const long *s) { npy_write(name, "<f4", d, 4, ndim, s); }
+static void npy_i8(const char *name, const int8_t *d, int ndim, const long *s) { npy_write(name, "|i1", d, 1, ndim, s); }
+static void npy_i32(const char *name, const int32_t *d, int ndim, const long *s) { npy_write(name, "<i4", d, 4, ndim, s); }
+
+static Tensor mat(int r, int c) { int s[2] = {r, c}; return tensor_create_nograd(s, 2); }
+static Tensor vecf(int n) { int s[1] = {n}; return tensor_create_nograd(s, 1); }
+
+// ---------------------------------------------------------------------------
+// ops fixtures
+// ---------------------------------------------------------------------------
+static void fx_quant(FILE *js) {
+  // (a) crafted 6x4: col 0 all zero (scale 1), col 1 exact half-way ties at
+  // scale 1, col 2 negative extreme, col 3 tiny magnitudes.
+  const int R = 6, C = 4;
+  float w[24] = {
+    0.0f,  127.0f, -3.0f, 1e-30f,
+    0.0f,   0.5f,  1.0f, -2e-30f,
+    0.0f,   1.5f, -127.5f, 3e-30f,
+    0.0f,   2.5f,  64.0f, 0.0f,
+    0.0f,  -0.5f,  0.25f, 5e-31f,
+    0.0f,  -2.5f, -0.25f, -7e-30f};
+  int8_t q[24]; float sc[4];
+  quantize_int8_percol(w, R, C, (signed char*)q, sc);
+  long s2[2] = {R, C}, s1[1] = {C};
+  npy_f32("quant_a_w", w, 2, s2); npy_i8("quant_a_q", q, 2, s2); npy_f32("quant_a_scale", sc, 1, s1);
+  // (b) random 64x48 and (c) 37x5 from the generator
+  const int rb = 64, cb = 48;
+  float *wb = malloc(sizeof(float) * rb * cb); int8_t *qb = malloc(rb * cb); float *sb = malloc(4 * cb);
+  syn_fill(wb, (size_t)rb * cb, 7, SYN_TID_GENERIC + 1, 0.02);
+  quantize_int8_percol(wb, rb, cb, (signed char*)qb, sb);
+  long t2[2] = {rb, cb}, t1[1] = {cb};
+  npy_f32("quant_b_w", wb, 2, t2); npy_i8("quant_b_q", qb, 2, t2); npy_f32("quant_b_scale", sb, 1, t1);
+  float *deq = malloc(sizeof(float) * rb * cb);
+  dequantize_int8_percol((signed char*)qb, sb, rb, cb, deq);
+  npy_f32("quant_b_deq", deq, 2, t2);
+  free(wb); free(qb); free(sb); free(deq);
+  fprintf(js, "  \"quant\": [\"a\", \"b\"],\n");
+}
+
+static void qmm_case(const char *name, int M, int K, int N, uint64_t seed, double asig, int save_inputs,
+                     FILE *js) {
+  QTensor W = qtensor_create(K, N);
+  float *wf = malloc(sizeof(float) * (size_t)K * N);
+  syn_fill(wf, (size_t)K * N, seed, SYN_TID_GENERIC + 10, 0.02);
+  qtensor_quantize(&W, wf);
+  Tensor A = mat(M, K), Cc = mat(M, N);
+  syn_fill(A.data, (size_t)M * K, seed, SYN_TID_GENERIC + 11, asig);
+  qmatmul(&A, &W, &Cc);
+  char nm[128]; long sa[2] = {M, K}, sw[2] = {K, N}, sc[1] = {N}, so[2] = {M, N};
+  if (save_inputs) {
+    snprintf(nm, sizeof nm, "%s_A", name); npy_f32(nm, A.data, 2, sa);
+    snprintf(nm, sizeof nm, "%s_Wq", name); npy_i8(nm, (int8_t*)W.q, 2, sw);
+    snprintf(nm, sizeof nm, "%s_Ws", name); npy_f32(nm, W.scale, 1, sc);
+  }
+  snprintf(nm, sizeof nm, "%s_C", name); npy_f32(nm, Cc.data, 2, so);
+  fprintf(js, "  \"%s\": {\"M\": %d, \"K\": %d, \"N\": %d, \"seed\": %llu, \"asig\": %g},\n",
+          name, M, K, N, (unsigned long long)seed, asig);
+  free(wf); qtensor_free(&W); tensor_free(&A); tensor_free(&Cc);
+}
+
+// Op-level GEMV at the BASELINE shapes: W int8 [M_out, K] (reference layout (K, M_out)),
+// x ~ N(0,1) rows.  Records digests of W and of the output, and the output head.
+static void qmm_op(int si, int Mout, int K, FILE *js) {
+  const uint64_t seed = 1234;
+  QTensor W = qtensor_create(K, Mout);
+  float *wf = malloc(sizeof(float) * (size_t)K * Mout);
+  syn_fill(wf, (size_t)K * Mout, seed, SYN_TID_GEMV_W + (uint64_t)si, 0.02);
+  qtensor_quantize(&W, wf);
+  free(wf);
+  uint64_t hq = syn_hash_i8((int8_t*)W.q, (size_t)K * Mout, 0);
+  uint64_t hs = syn_hash_f32(W.scale, (size_t)Mout, 0);
+  fprintf(js, "  \"gemv_%d\": {\"M\": %d, \"K\": %d, \"w_hash\": \"%016llx\", \"s_hash\": \"%016llx\"",
+          si, Mout, K, (unsigned long long)hq, (unsigned long long)hs);
+  for (int b = 1; b <= 8; b += 7) {
+    Tensor X = mat(b, K), Y = mat(b, Mout);
+    syn_fill(X.data, (size_t)b * K, seed, SYN_TID_GEMV_X + (uint64_t)si, 1.0);
+    double t0 = now_s();
+    qmatmul(&X, &W, &Y);
+    double t1 = now_s();
+    uint64_t hy = syn_hash_f32(Y.data, (size_t)b * Mout, 0);
+    char nm[64]; long s1[1] = {256};
+    snprintf(nm, sizeof nm, "gemv_%d_b%d_head", si, b);
+    npy_f32(nm, Y.data, 1, s1);
+    fprintf(js, ", \"b%d_hash\": \"%016llx\", \"b%d_ref_s\": %.4f", b, (unsigned long long)hy, b, t1 - t0);
+    tensor_free(&X); tensor_free(&Y);
+  }
+  fprintf(js, "},\n");
+  qtensor_free(&W);
+}
+
+static void fx_rmsnorm(FILE *js) {
+  const int cols_list[3] = {288, 2048, 4096};
+  for (int c = 0; c < 3; c++) {
+    const int cols = cols_list[c], rows = 3;
+    Tensor x = mat(rows, cols), y = mat(rows, cols), g = vecf(cols);
+    syn_fill(x.data, (size_t)rows * cols, 11, SYN_TID_GENERIC + 20 + (uint64_t)c, 1.0);
+    syn_fill(g.data, (size_t)cols, 11, SYN_TID_GENERIC + 30 + (uint64_t)c, 0.1);
+    for (int j = 0; j < cols; j++) g.data[j] = 1.0f + g.data[j];
+    x.data[5] = 1e-3f; x.data[6] = -250.0f;                  // spread the dynamic range
+    rmsnorm(&x, &g, &y, 1e-5f);
+    char nm[64]; long s2[2] = {rows, cols}, s1[1] = {cols};
+    snprintf(nm, sizeof nm, "rms_%d_x", cols); npy_f32(nm, x.data, 2, s2);
+    snprintf(nm, sizeof nm, "rms_%d_g", cols); npy_f32(nm, g.data, 1, s1);
+    snprintf(nm, sizeof nm, "rms_%d_y", cols); npy_f32(nm, y.data, 2, s2);
+    tensor_free(&x); tensor_free(&y); tensor_free(&g);
+  }
+  fprintf(js, "  \"rmsnorm\": [288, 2048, 4096],\n");
+}
+
+static void fx_rope(FILE *js) {
+  const int pos_list[7] = {0, 1, 7, 511, 2047, 2559, 8191};
+  for (int p = 0; p < 7; p++) {
+    Tensor x = mat(1, 32 * 128);
+    syn_fill(x.data, 4096, 21, SYN_TID_GENERIC + 40 + (uint64_t)p, 1.0);
+    char nm[64]; long s2[2] = {1, 4096};
+    snprintf(nm, sizeof nm, "rope_p%d_x", pos_list[p]); npy_f32(nm, x.data, 2, s2);
+    rope_heads_pos(&x, 32, 500000.0f, pos_list[p]);
+    snprintf(nm, sizeof nm, "rope_p%d_y", pos_list[p]); npy_f32(nm, x.data, 2, s2);
+    tensor_free(&x);
+  }
+  {  // tiny-config shape, base 10000, three rows starting at position 5
+    Tensor x = mat(3, 6 * 48);
+    syn_fill(x.data, 3 * 288, 21, SYN_TID_GENERIC + 50, 1.0);
+    long s2[2] = {3, 288};
+    npy_f32("rope_tiny_x", x.data, 2, s2);
+    rope_heads_pos(&x, 6, 10000.0f, 5);
+    npy_f32("rope_tiny_y", x.data, 2, s2);
+    tensor_free(&x);
+  }
+  fprintf(js, "  \"rope\": [0, 1, 7, 511, 2047, 2559, 8191],\n");
+}
+
+// Decode attention at context T = last row of gqa_forward over T positions
+// (bit-identical to llama.c:554-576).  q and k rows carry RoPE at their position
+// (theta 500000); the cache is N(0,1).  32 query heads, 8 KV heads, hd 128.
+static void gqa_case(int ci, int T, FILE *js) {
+  const int H = 32, KVH = 8, hd = 128, qd = H * hd, kd = KVH * hd;
+  Tensor Q = mat(T, qd), K = mat(T, kd), V = mat(T, kd), O = mat(T, qd);
+  syn_fill(Q.data, (size_t)T * qd, 31, SYN_TID_GQA_Q + (uint64_t)ci, 1.0);
+  syn_fill(K.data, (size_t)T * kd, 31, SYN_TID_GQA_K + (uint64_t)ci, 1.0);
+  syn_fill(V.data, (size_t)T * kd, 31, SYN_TID_GQA_V + (uint64_t)ci, 1.0);
+  rope_heads_pos(&Q, H, 500000.0f, 0);
+  rope_heads_pos(&K, KVH, 500000.0f, 0);
+  GqaCache c = gqa_cache_create(T, H, KVH, hd);
+  double t0 = now_s();
+  gqa_forward(&Q, &K, &V, &c, &O);
+  double t1 = now_s();
+  char nm[64]; long s1[1] = {qd};
+  snprintf(nm, sizeof nm, "gqa_T%d_o", T); npy_f32(nm, &O.data[(size_t)(T - 1) * qd], 1, s1);
+  snprintf(nm, sizeof nm, "gqa_T%d_q", T); npy_f32(nm, &Q.data[(size_t)(T - 1) * qd], 1, s1);
+  fprintf(js, "  \"gqa_T%d\": {\"case\": %d, \"T\": %d, \"k_hash\": \"%016llx\", \"v_hash\": \"%016llx\", \"ref_s\": %.3f},\n",
+          T, ci, T, (unsigned long long)syn_hash_f32(K.data, (size_t)T * kd, 0),
+          (unsigned long long)syn_hash_f32(V.data, (size_t)T * kd, 0), t1 - t0);
+  gqa_cache_free(&c);
+  tensor_free(&Q); tensor_free(&K); tensor_free(&V); tensor_free(&O);
+}
+
+// ---------------------------------------------------------------------------
+// End-to-end greedy runs through q_llama_decode_step.
+// ---------------------------------------------------------------------------
+typedef struct { const char *name; int32_t cfg[8]; float base; int tied, prompt, gen; } E2E;
+static const E2E CASES[3] = {
+  {"tiny", {32000, 288, 6, 6, 2, 48, 768, 256}, 10000.0f, 0, 128, 128},
+  {"1b", {128256, 2048, 16, 32, 8, 64, 8192, 768}, 500000.0f, 1, 512, 256},
+  {"8b", {128256, 4096, 32, 32, 8, 128, 14336, 2560}, 500000.0f, 0, 2048, 512},
+};
+
+static void synth_q(QTensor *t, float *buf, uint64_t seed, uint64_t tid) {
+  syn_fill(buf, (size_t)t->rows * t->cols, seed, tid, 0.02);
+  qtensor_quantize(t, buf);
+}
+
+static uint64_t qhash(const QTensor *t, uint64_t salt) {
+  return syn_hash_i8((const int8_t*)t->q, (size_t)t->rows * t->cols, salt) * 3 +
+         syn_hash_f32(t->scale, (size_t)t->cols, salt ^ 0x5CA1E5ULL);
+}
+
+static void build_model(QLlamaModel *m, const E2E *e, uint64_t seed) {
+  const int32_t *c = e->cfg;
+  m->vocab = c[0]; m->d_model = c[1]; m->n_layers = c[2]; m->n_heads = c[3]; m->n_kv = c[4];
+  m->head_dim = c[5]; m->d_ff = c[6]; m->max_seq = c[7]; m->rope_base = e->base; m->eps = 1e-5f;
+  const int dm = c[1], qd = c[3] * c[5], kvd = c[4] * c[5], ff = c[6], L = c[2];
+  size_t big = (size_t)c[0] * dm; if ((size_t)dm * ff > big) big = (size_t)dm * ff;
+  float *buf = malloc(big * sizeof(float));
+  m->wte = qtensor_create(c[0], dm);
+  synth_q(&m->wte, buf, seed, 0);
+  m->blocks = malloc(sizeof(QLlamaBlock) * (size_t)L);
+  for (int l = 0; l < L; l++) {
+    QLlamaBlock *b = &m->blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    b->attn_norm = vecf(dm); b->ffn_norm = vecf(dm);
+    for (int j = 0; j < dm; j++) { b->attn_norm.data[j] = 1.0f; b->ffn_norm.data[j] = 1.0f; }
+    b->b_q = vecf(qd); b->b_k = vecf(kvd); b->b_v = vecf(kvd);
+    b->Wq = qtensor_create(dm, qd); synth_q(&b->Wq, buf, seed, t0 + 1);
+    b->Wk = qtensor_create(dm, kvd); synth_q(&b->Wk, buf, seed, t0 + 2);
+    b->Wv = qtensor_create(dm, kvd); synth_q(&b->Wv, buf, seed, t0 + 3);
+    b->Wo = qtensor_create(qd, dm); synth_q(&b->Wo, buf, seed, t0 + 7);
+    b->Wgate = qtensor_create(dm, ff); synth_q(&b->Wgate, buf, seed, t0 + 9);
+    b->Wup = qtensor_create(dm, ff); synth_q(&b->Wup, buf, seed, t0 + 10);
+    b->Wdown = qtensor_create(ff, dm); synth_q(&b->Wdown, buf, seed, t0 + 11);
+  }
+  m->final_norm = vecf(dm);
+  for (int j = 0; j < dm; j++) m->final_norm.data[j] = 1.0f;
+  m->lm_head = qtensor_create(dm, c[0]);
+  if (e->tied) {
+    float *w = malloc((size_t)c[0] * dm * sizeof(float));
+    syn_fill(w, (size_t)c[0] * dm, seed, 0, 0.02);
+    for (int v = 0; v < c[0]; v++)
+      for (int k = 0; k < dm; k++) buf[(size_t)k * c[0] + v] = w[(size_t)v * dm + k];
+    free(w);
+    qtensor_quantize(&m->lm_head, buf);
+  } else {
+    synth_q(&m->lm_head, buf, seed, 2 + 12 * (uint64_t)L);
+  }
+  free(buf);
+}
+
+static uint64_t model_hash(const QLlamaModel *m) {
+  uint64_t h = qhash(&m->wte, 0);
+  for (int l = 0; l < m->n_layers; l++) {
+    const QLlamaBlock *b = &m->blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    h = h * 31 + qhash(&b->Wq, t0 + 1);
+    h = h * 31 + qhash(&b->Wk, t0 + 2);
+    h = h * 31 + qhash(&b->Wv, t0 + 3);
+    h = h * 31 + qhash(&b->Wo, t0 + 7);
+    h = h * 31 + qhash(&b->Wgate, t0 + 9);
+    h = h * 31 + qhash(&b->Wup, t0 + 10);
+    h = h * 31 + qhash(&b->Wdown, t0 + 11);
+  }
+  return h * 31 + qhash(&m->lm_head, 2 + 12 * (uint64_t)m->n_layers);
+}
+
+static void run_e2e(const E2E *e) {
+  const uint64_t seed = 1234;
+  double t0 = now_s();
+  QLlamaModel m;
+  build_model(&m, e, seed);
+  double t1 = now_s();
+  fprintf(stderr, "[%s] model built in %.1f s\n", e->name, t1 - t0);
+  LlamaKV kv = q_llama_kv_create(&m);
+  Tensor logits = mat(1, m.vocab);
+  const int P = e->prompt, G = e->gen, steps = P + G;
+  int *seq = malloc(sizeof(int) * (size_t)m.max_seq);
+  syn_prompt(seq, P, seed, m.vocab);
+  uint64_t *lh = malloc(sizeof(uint64_t) * (size_t)steps);
+  int32_t *amax = malloc(sizeof(int32_t) * (size_t)steps);
+  char nm[128]; long sv[1] = {m.vocab}, sh[1] = {2048};
+  kv.len = 0;
+  double tp0 = now_s();
+  for (int i = 0; i < P; i++) {
+    q_llama_decode_step(&m, &kv, seq[i], &logits);
+    lh[i] = syn_hash_f32(logits.data, (size_t)m.vocab, 0);
+    amax[i] = sample_argmax(&logits, 0);
+    if (i % 64 == 0) fprintf(stderr, "[%s] prompt %d/%d %.1f s\n", e->name, i, P, now_s() - tp0);
+  }
+  double tp1 = now_s();
+  snprintf(nm, sizeof nm, "e2e_%s_logits_prompt_last", e->name);
+  if (m.vocab <= 32000) npy_f32(nm, logits.data, 1, sv); else npy_f32(nm, logits.data, 1, sh);
+  int n = P, s;
+  for (s = 0; s < G && n < m.max_seq; s++) {
+    int nxt = sample_argmax(&logits, 0);
+    seq[n++] = nxt;
+    q_llama_decode_step(&m, &kv, nxt, &logits);
+    lh[P + s] = syn_hash_f32(logits.data, (size_t)m.vocab, 0);
+    amax[P + s] = sample_argmax(&logits, 0);
+    if (s % 32 == 0) fprintf(stderr, "[%s] gen %d/%d %.1f s\n", e->name, s, G, now_s() - tp1);
+  }
+  double tg1 = now_s();
+  snprintf(nm, sizeof nm, "e2e_%s_logits_final", e->name);
+  if (m.vocab <= 32000) npy_f32(nm, logits.data, 1, sv); else npy_f32(nm, logits.data, 1, sh);
+  char path[1024]; snprintf(path, sizeof path, "%s/e2e_%s.json", OUT, e->name);
+  FILE *js = fopen(path, "w");
+  fprintf(js, "{\n  \"name\": \"%s\", \"seed\": %llu, \"cfg\": [%d,%d,%d,%d,%d,%d,%d,%d],\n",
+          e->name, (unsigned long long)seed, e->cfg[0], e->cfg[1], e->cfg[2], e->cfg[3], e->cfg[4],
+          e->cfg[5], e->cfg[6], e->cfg[7]);
+  fprintf(js, "  \"rope_base\": %.1f, \"eps\": 1e-5, \"tied\": %d, \"prompt_len\": %d, \"gen_len\": %d,\n",
+          e->base, e->tied, P, s);
+  fprintf(js, "  \"model_hash\": \"%016llx\",\n", (unsigned long long)model_hash(&m));
+  fprintf(js, "  \"ref_prompt_s\": %.3f, \"ref_gen_s\": %.3f, \"ref_build_s\": %.1f,\n", tp1 - tp0, tg1 - tp1, t1 - t0);
+  fprintf(js, "  \"prompt\": [");
+  for (int i = 0; i < P; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"gen\": [");
+  for (int i = P; i < n; i++) fprintf(js, "%s%d", i > P ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"argmax\": [");
+  for (int i = 0; i < P + s; i++) fprintf(js, "%s%d", i ? "," : "", amax[i]);
+  fprintf(js, "],\n  \"logit_hashes\": [");
+  for (int i = 0; i < P + s; i++) fprintf(js, "%s\"%016llx\"", i ? "," : "", (unsigned long long)lh[i]);
+  fprintf(js, "]\n}\n");
+  fclose(js);
+  fprintf(stderr, "[%s] done: prompt %.1f s, gen %.1f s\n", e->name, tp1 - tp0, tg1 - tp1);
+  free(seq); free(lh); free(amax); tensor_free(&logits); llama_kv_free(&kv); q_llama_model_free(&m);
+}
+
+int main(int argc, char **argv) {
+  if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|e2e <name>\n"); return 2; }
+  OUT = argv[1];
+  if (!strcmp(argv[2], "ops")) {
+    char path[1024]; snprintf(path, sizeof path, "%s/ops.json", OUT);
+    FILE *js = fopen(path, "w");
+    fprintf(js, "{\n");
+    fx_quant(js);
+    qmm_case("qmm_1x64x48", 1, 64, 48, 5, 1.0, 1, js);
+    qmm_case("qmm_3x300x17", 3, 300, 17, 6, 1.0, 1, js);
+    qmm_case("qmm_8x256x96", 8, 256, 96, 8, 0.05, 1, js);
+    qmm_case("qmm_2x1024x1024", 2, 1024, 1024, 9, 1.0, 0, js);   // threaded path (K*N >= 2^19)
+    fx_rmsnorm(js);
+    fx_rope(js);
+    const int Ts[3] = {1, 512, 2048};
+    for (int i = 0; i < 3; i++) gqa_case(i, Ts[i], js);
+    const int shapes[4][2] = {{4096, 4096}, {14336, 4096}, {4096, 14336}, {128256, 4096}};
+    for (int i = 0; i < 4; i++) qmm_op(i, shapes[i][0], shapes[i][1], js);
+    fprintf(js, "  \"done\": true\n}\n");
+    fclose(js);
+    return 0;
+  }
+  if (!strcmp(argv[2], "gqa8192")) {
+    char path[1024]; snprintf(path, sizeof path, "%s/gqa8192.json", OUT);
+    FILE *js = fopen(path, "w");
+    fprintf(js, "{\n");
+    gqa_case(3, 8192, js);
+    fprintf(js, "  \"done\": true\n}\n");
+    fclose(js);
+    return 0;
+  }
+  if (!strcmp(argv[2], "e2e") && argc > 3) {
+    for (int i = 0; i < 3; i++) if (!strcmp(argv[3], CASES[i].name)) { run_e2e(&CASES[i]); return 0; }
+  }
+  fprintf(stderr, "unknown request\n");
+  return 2;
+}

@@ -1,0 +1,247 @@
+"""ctypes bindings to oracle/liboracle*.so, the CPU checker (test infrastructure).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
+module.  The restatement it loads follows the reference file:line cited at each
+function in oracle/oracle.c.
+"""
+import ctypes as C
+import os
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+
+
+class OrQT(C.Structure):
+    _fields_ = [("rows", C.c_int), ("cols", C.c_int),
+                ("q", C.POINTER(C.c_int8)), ("scale", C.POINTER(C.c_float))]
+
+
+class OrBlock(C.Structure):
+    _fields_ = [("attn_norm", C.POINTER(C.c_float)), ("ffn_norm", C.POINTER(C.c_float)),
+                ("b_q", C.POINTER(C.c_float)), ("b_k", C.POINTER(C.c_float)),
+                ("b_v", C.POINTER(C.c_float)),
+                ("Wq", OrQT), ("Wk", OrQT), ("Wv", OrQT), ("Wo", OrQT),
+                ("Wgate", OrQT), ("Wup", OrQT), ("Wdown", OrQT)]
+
+
+class OrModel(C.Structure):
+    _fields_ = [("vocab", C.c_int), ("d_model", C.c_int), ("n_layers", C.c_int),
+                ("n_heads", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("d_ff", C.c_int), ("max_seq", C.c_int),
+                ("rope_base", C.c_float), ("eps", C.c_float),
+                ("wte", OrQT), ("blocks", C.POINTER(OrBlock)),
+                ("final_norm", C.POINTER(C.c_float)), ("lm_head", OrQT)]
+
+
+class OrKV(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("max_seq", C.c_int), ("kv_dim", C.c_int),
+                ("len", C.c_int), ("k", C.POINTER(C.c_float)), ("v", C.POINTER(C.c_float))]
+
+
+def _cpu_has_avx512():
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+        return all(x in flags for x in ("avx512f", "avx512bw", "avx512vl", "avx512dq"))
+    except OSError:
+        return False
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        name = "liboracle_v4.so" if _cpu_has_avx512() else "liboracle.so"
+        path = os.path.join(ORACLE_DIR, name)
+        if not os.path.exists(path):
+            path = os.path.join(ORACLE_DIR, "liboracle.so")
+        L = C.CDLL(path)
+        fp = C.POINTER(C.c_float)
+        i8p = C.POINTER(C.c_int8)
+        L.or_qmatmul_ex.argtypes = [fp, C.c_int, C.POINTER(OrQT), fp, i8p, fp, C.POINTER(C.c_int32)]
+        L.or_quantize_int8_percol.argtypes = [fp, C.c_int, C.c_int, i8p, fp]
+        L.or_dequantize_int8_percol.argtypes = [i8p, fp, C.c_int, C.c_int, fp]
+        L.or_rmsnorm.argtypes = [fp, C.c_int, C.c_int, fp, C.c_float, fp]
+        L.or_rope_heads_pos.argtypes = [fp, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int]
+        L.or_gqa_forward.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, fp, fp]
+        L.or_attn_decode.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, fp, fp]
+        L.or_argmax.argtypes = [fp, C.c_int]
+        L.or_argmax.restype = C.c_int
+        L.or_model_synth.argtypes = [C.POINTER(OrModel), C.POINTER(C.c_int32), C.c_float, C.c_float,
+                                     C.c_uint64, C.c_int]
+        L.or_model_alloc.argtypes = [C.POINTER(OrModel), C.POINTER(C.c_int32), C.c_float, C.c_float]
+        L.or_model_free.argtypes = [C.POINTER(OrModel)]
+        L.or_model_hash.argtypes = [C.POINTER(OrModel)]
+        L.or_model_hash.restype = C.c_uint64
+        L.or_kv_create.argtypes = [C.POINTER(OrKV), C.POINTER(OrModel)]
+        L.or_kv_free.argtypes = [C.POINTER(OrKV)]
+        L.or_decode_step.argtypes = [C.POINTER(OrModel), C.POINTER(OrKV), C.c_int, fp]
+        L.or_set_threads.argtypes = [C.c_int]
+        L.or_get_threads.restype = C.c_int
+        L.syn_key.argtypes = [C.c_uint64, C.c_uint64]
+        L.syn_key.restype = C.c_uint64
+        L.syn_fill.argtypes = [fp, C.c_size_t, C.c_uint64, C.c_uint64, C.c_double]
+        L.syn_prompt.argtypes = [C.POINTER(C.c_int), C.c_int, C.c_uint64, C.c_int]
+        L.syn_hash_f32.argtypes = [fp, C.c_size_t, C.c_uint64]
+        L.syn_hash_f32.restype = C.c_uint64
+        L.syn_hash_i8.argtypes = [i8p, C.c_size_t, C.c_uint64]
+        L.syn_hash_i8.restype = C.c_uint64
+        L.syn_ln.argtypes = [C.c_double]
+        L.syn_ln.restype = C.c_double
+        L.syn_sqrt.argtypes = [C.c_double]
+        L.syn_sqrt.restype = C.c_double
+        L.syn_cos_sin_2pi.argtypes = [C.c_double, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.syn_normal.argtypes = [C.c_uint64, C.c_uint64]
+        L.syn_normal.restype = C.c_double
+        _lib = L
+    return _lib
+
+
+def fptr(a):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def i8ptr(a):
+    assert a.dtype == np.int8 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
+
+
+# ---- thin numpy wrappers --------------------------------------------------
+def synth(n, seed, tid, sigma):
+    out = np.empty(n, np.float32)
+    lib().syn_fill(fptr(out), n, seed, tid, sigma)
+    return out
+
+
+def prompt(n, seed, vocab):
+    ids = (C.c_int * n)()
+    lib().syn_prompt(ids, n, seed, vocab)
+    return list(ids)
+
+
+def hash_f32(a):
+    a = np.ascontiguousarray(a, np.float32)
+    return int(lib().syn_hash_f32(fptr(a), a.size, 0))
+
+
+def hash_i8(a):
+    a = np.ascontiguousarray(a, np.int8)
+    return int(lib().syn_hash_i8(i8ptr(a), a.size, 0))
+
+
+def quantize(w):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(cols, np.float32)
+    lib().or_quantize_int8_percol(fptr(w), rows, cols, i8ptr(q), fptr(s))
+    return q, s
+
+
+def dequantize(q, s):
+    rows, cols = q.shape
+    w = np.empty((rows, cols), np.float32)
+    lib().or_dequantize_int8_percol(i8ptr(np.ascontiguousarray(q)), fptr(np.ascontiguousarray(s)),
+                                    rows, cols, fptr(w))
+    return w
+
+
+def qmatmul(A, q, s, intermediates=False):
+    """C = qmatmul(A, W) with W given as int8 (K, N) + scales (N) (quant.c:60-85)."""
+    A = np.ascontiguousarray(A, np.float32)
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(s, np.float32)
+    M, K = A.shape
+    N = q.shape[1]
+    W = OrQT(K, N, i8ptr(q), fptr(s))
+    Cm = np.empty((M, N), np.float32)
+    if not intermediates:
+        lib().or_qmatmul_ex(fptr(A), M, C.byref(W), fptr(Cm), None, None, None)
+        return Cm
+    qa = np.empty((M, K), np.int8)
+    as_ = np.empty(M, np.float32)
+    acc = np.empty((M, N), np.int32)
+    lib().or_qmatmul_ex(fptr(A), M, C.byref(W), fptr(Cm), i8ptr(qa), fptr(as_),
+                        acc.ctypes.data_as(C.POINTER(C.c_int32)))
+    return Cm, qa, as_, acc
+
+
+def rmsnorm(x, g, eps=1e-5):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    lib().or_rmsnorm(fptr(x), rows, cols, fptr(np.ascontiguousarray(g, np.float32)), eps, fptr(y))
+    return y
+
+
+def rope(x, n_heads, base, pos0):
+    x = np.array(x, np.float32, copy=True, order="C")
+    rows, cols = x.shape
+    lib().or_rope_heads_pos(fptr(x), rows, cols, n_heads, base, pos0)
+    return x
+
+
+def attn_decode(q, kc, vc, pos, n_heads, n_kv, hd):
+    """llama.c:554-576 over cache rows 0..pos; kc/vc are [>=pos+1, n_kv*hd]."""
+    kc = np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc, np.float32)
+    q = np.ascontiguousarray(q, np.float32)
+    sc = np.empty(pos + 1, np.float32)
+    o = np.empty(n_heads * hd, np.float32)
+    lib().or_attn_decode(fptr(q), fptr(kc), fptr(vc), n_kv * hd, pos, n_heads, n_kv, hd,
+                         fptr(sc), fptr(o))
+    return o
+
+
+def gqa_forward(Q, K, V, H, KVH, hd):
+    n = Q.shape[0]
+    O = np.empty((n, H * hd), np.float32)
+    att = np.empty(n, np.float32)
+    lib().or_gqa_forward(fptr(np.ascontiguousarray(Q, np.float32)), fptr(np.ascontiguousarray(K, np.float32)),
+                         fptr(np.ascontiguousarray(V, np.float32)), n, H, KVH, hd, fptr(att), fptr(O))
+    return O
+
+
+class Model:
+    """Oracle model (reference layout, host memory)."""
+
+    def __init__(self, cfg, rope_base, eps=1e-5, seed=1234, tied=False, synth=True):
+        self.m = OrModel()
+        arr = (C.c_int32 * 8)(*cfg)
+        if synth:
+            rc = lib().or_model_synth(C.byref(self.m), arr, rope_base, eps, seed, int(tied))
+        else:
+            rc = lib().or_model_alloc(C.byref(self.m), arr, rope_base, eps)
+        if rc != 0:
+            raise MemoryError("oracle model allocation failed")
+        self.kv = OrKV()
+        if lib().or_kv_create(C.byref(self.kv), C.byref(self.m)) != 0:
+            raise MemoryError("oracle kv allocation failed")
+        self.vocab = cfg[0]
+        self.logits = np.zeros(self.vocab, np.float32)
+
+    def hash(self):
+        return int(lib().or_model_hash(C.byref(self.m)))
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def step(self, token):
+        lib().or_decode_step(C.byref(self.m), C.byref(self.kv), token, fptr(self.logits))
+        return self.logits
+
+    def close(self):
+        if self.m.blocks:
+            lib().or_kv_free(C.byref(self.kv))
+            lib().or_model_free(C.byref(self.m))
+            self.m.blocks = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

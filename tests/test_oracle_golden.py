@@ -1,0 +1,268 @@
+"""Pins the CPU oracle (oracle/oracle.c) to the reference.
+
+Every fixture under tests/golden/data/ was written by the compiled reference
+(tests/golden/gen_golden.c linked against /root/reference's own objects).  The
+oracle must reproduce each one bit for bit; the closed-form and invariant checks
+at the end pin what the fixtures leave open.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import golden, golden_json, have_golden
+
+OPS = golden_json("ops")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bits(got, want):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    assert got.shape == want.shape
+    bad = np.flatnonzero(bits(got).ravel() != bits(want).ravel())
+    assert bad.size == 0, f"{bad.size} mismatches, first at {bad[0]}: {got.ravel()[bad[0]]!r} vs {want.ravel()[bad[0]]!r}"
+
+
+# ---- quant.c:10-33 ----------------------------------------------------------
+@pytest.mark.parametrize("case", ["a", "b"])
+def test_quantize_matches_reference(case):
+    w = golden(f"quant_{case}_w")
+    q, s = O.quantize(w)
+    assert np.array_equal(q, golden(f"quant_{case}_q"))
+    assert_bits(s, golden(f"quant_{case}_scale"))
+
+
+def test_dequantize_matches_reference():
+    w = O.dequantize(golden("quant_b_q"), golden("quant_b_scale"))
+    assert_bits(w, golden("quant_b_deq"))
+
+
+def test_quantize_special_cases():
+    q, s = O.quantize(golden("quant_a_w"))
+    assert s[0] == 1.0 and not q[:, 0].any()               # all-zero column -> scale 1
+    assert list(q[:, 1]) == [127, 0, 2, 2, 0, -2]           # ties round half to even
+    assert np.abs(q).max() <= 127
+
+
+# ---- quant.c:60-85 + matrix.c:354-374 --------------------------------------
+@pytest.mark.parametrize("name", ["qmm_1x64x48", "qmm_3x300x17", "qmm_8x256x96"])
+def test_qmatmul_small_matches_reference(name):
+    A, Wq, Ws = golden(f"{name}_A"), golden(f"{name}_Wq"), golden(f"{name}_Ws")
+    C, qa, as_, acc = O.qmatmul(A, Wq, Ws, intermediates=True)
+    assert_bits(C, golden(f"{name}_C"))
+    # the int32 accumulator is an exact integer product (brute force in int64)
+    assert np.array_equal(acc.astype(np.int64), qa.astype(np.int64) @ Wq.astype(np.int64))
+    # per-row scale is max|a|/127 and quantized values stay in range
+    mx = np.abs(A).max(axis=1).astype(np.float32)
+    assert_bits(as_, np.where(mx > 0, mx / np.float32(127.0), np.float32(1.0)))
+    assert np.abs(qa).max() <= 127
+
+
+def test_qmatmul_threaded_path_matches_reference():
+    meta = OPS["qmm_2x1024x1024"]
+    M, K, N, seed = meta["M"], meta["K"], meta["N"], meta["seed"]
+    wf = O.synth(K * N, seed, 5010, 0.02).reshape(K, N)
+    q, s = O.quantize(wf)
+    A = O.synth(M * K, seed, 5011, 1.0).reshape(M, K)
+    assert_bits(O.qmatmul(A, q, s), golden("qmm_2x1024x1024_C"))
+
+
+def test_qmatmul_activation_quant_is_scale_invariant():
+    rng = np.random.default_rng(0)
+    A = rng.standard_normal((2, 96)).astype(np.float32)
+    q, s = O.quantize((rng.standard_normal((96, 40)) * 0.02).astype(np.float32))
+    _, qa1, as1, acc1 = O.qmatmul(A, q, s, intermediates=True)
+    _, qa2, as2, acc2 = O.qmatmul(A * np.float32(8.0), q, s, intermediates=True)
+    assert np.array_equal(qa1, qa2) and np.array_equal(acc1, acc2)
+    assert_bits(as2, as1 * np.float32(8.0))
+
+
+# ---- op-level GEMV shapes -------------------------------
+def _gemv_case(si):
+    meta = OPS[f"gemv_{si}"]
+    M, K = meta["M"], meta["K"]
+    wf = O.synth(K * M, 1234, 1000 + si, 0.02).reshape(K, M)
+    q, s = O.quantize(wf)
+    del wf
+    assert O.hash_i8(q) == int(meta["w_hash"], 16)
+    assert O.hash_f32(s) == int(meta["s_hash"], 16)
+    for b in (1, 8):
+        x = O.synth(b * K, 1234, 2000 + si, 1.0).reshape(b, K)
+        y = O.qmatmul(x, q, s)
+        assert O.hash_f32(y) == int(meta[f"b{b}_hash"], 16)
+        assert_bits(y.ravel()[:256], golden(f"gemv_{si}_b{b}_head"))
+
+
+@pytest.mark.parametrize("si", [0, 1, 2])
+def test_gemv_shapes_match_reference(si):
+    _gemv_case(si)
+
+
+@pytest.mark.slow
+def test_gemv_lm_head_shape_matches_reference():
+    _gemv_case(3)
+
+
+# ---- rmsnorm.c:7-21 ---------------------------------------------------------
+@pytest.mark.parametrize("cols", [288, 2048, 4096])
+def test_rmsnorm_matches_reference(cols):
+    y = O.rmsnorm(golden(f"rms_{cols}_x"), golden(f"rms_{cols}_g"))
+    assert_bits(y, golden(f"rms_{cols}_y"))
+
+
+def test_rmsnorm_closed_form_on_constant_vector():
+    for cols, c in ((4096, 1.0), (288, 0.5), (2048, 2.0)):
+        x = np.full((1, cols), c, np.float32)
+        y = O.rmsnorm(x, np.ones(cols, np.float32))
+        ms = np.float32(c * c)   # sum of cols copies of c*c is exact here, times 1/cols
+        r = np.float32(1.0) / np.sqrt(ms + np.float32(1e-5))
+        assert_bits(y, np.full((1, cols), np.float32(c) * r, np.float32))
+
+
+# ---- rope.c:48-68 -----------------------------------------------------------
+@pytest.mark.parametrize("pos", OPS["rope"])
+def test_rope_matches_reference(pos):
+    y = O.rope(golden(f"rope_p{pos}_x"), 32, 500000.0, pos)
+    assert_bits(y, golden(f"rope_p{pos}_y"))
+
+
+def test_rope_tiny_rows_match_reference():
+    assert_bits(O.rope(golden("rope_tiny_x"), 6, 10000.0, 5), golden("rope_tiny_y"))
+
+
+def test_rope_invariants():
+    # rotation preserves each pair's norm; <R_m q, R_n k> depends only on m - n
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 128)).astype(np.float32)
+    k = rng.standard_normal((1, 128)).astype(np.float32)
+    y = O.rope(q, 1, 10000.0, 37)
+    n0 = q[0, :64] ** 2 + q[0, 64:] ** 2
+    n1 = y[0, :64] ** 2 + y[0, 64:] ** 2
+    assert np.allclose(n0, n1, rtol=1e-5)
+    d1 = float(O.rope(q, 1, 10000.0, 10)[0] @ O.rope(k, 1, 10000.0, 3)[0])
+    d2 = float(O.rope(q, 1, 10000.0, 27)[0] @ O.rope(k, 1, 10000.0, 20)[0])
+    assert abs(d1 - d2) < 1e-3 * max(1.0, abs(d1))
+    assert_bits(O.rope(q, 1, 10000.0, 0), q)                # position 0 is the identity
+
+
+# ---- llama.c:554-576 == last row of gqa.c:16-50 -----------------------------
+def _gqa_inputs(case, T):
+    H, KVH, hd = 32, 8, 128
+    Q = O.synth(T * H * hd, 31, 3000 + case, 1.0).reshape(T, H * hd)
+    K = O.synth(T * KVH * hd, 31, 3100 + case, 1.0).reshape(T, KVH * hd)
+    V = O.synth(T * KVH * hd, 31, 3200 + case, 1.0).reshape(T, KVH * hd)
+    q = O.rope(Q[T - 1:T], H, 500000.0, T - 1)[0]
+    K = O.rope(K, KVH, 500000.0, 0)
+    return q, K, V
+
+
+@pytest.mark.parametrize("T", [1, 512, 2048])
+def test_decode_attention_matches_reference(T):
+    meta = OPS[f"gqa_T{T}"]
+    q, K, V = _gqa_inputs(meta["case"], T)
+    assert O.hash_f32(K) == int(meta["k_hash"], 16)
+    assert O.hash_f32(V) == int(meta["v_hash"], 16)
+    assert_bits(q, golden(f"gqa_T{T}_q"))
+    o = O.attn_decode(q, K, V, T - 1, 32, 8, 128)
+    assert_bits(o, golden(f"gqa_T{T}_o"))
+
+
+@pytest.mark.slow
+@pytest.mark.skipif(not have_golden("gqa8192.json"), reason="context-8192 fixture not generated")
+def test_decode_attention_8192_matches_reference():
+    meta = golden_json("gqa8192")["gqa_T8192"]
+    q, K, V = _gqa_inputs(meta["case"], 8192)
+    assert O.hash_f32(K) == int(meta["k_hash"], 16)
+    assert_bits(O.attn_decode(q, K, V, 8191, 32, 8, 128), golden("gqa_T8192_o"))
+
+
+def test_decode_attention_closed_forms():
+    rng = np.random.default_rng(2)
+    H, KVH, hd, T = 4, 2, 16, 9
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    K = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    V = rng.standard_normal((T, KVH * hd)).astype(np.float32)
+    # context 1: the single weight is exactly 1, so o = V[0] for every head of a group
+    o1 = O.attn_decode(q, K, V, 0, H, KVH, hd)
+    assert_bits(o1, np.concatenate([V[0, (h // 2) * hd:(h // 2 + 1) * hd] for h in range(H)]))
+    # float64 brute force agrees to rounding; equals the last row of the full-sequence op
+    o = O.attn_decode(q, K, V, T - 1, H, KVH, hd)
+    ref = []
+    for h in range(H):
+        kv = h // 2
+        s = K[:, kv * hd:(kv + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
+        w = np.exp(s - s.max()); w /= w.sum()
+        ref.append(w @ V[:, kv * hd:(kv + 1) * hd].astype(np.float64))
+    assert np.allclose(o, np.concatenate(ref), atol=1e-5)
+    Qf = np.tile(q, (T, 1))
+    assert_bits(O.gqa_forward(Qf, K, V, H, KVH, hd)[T - 1], o)
+
+
+# ---- sampler.c:8-21 ---------------------------------------------------------
+def test_argmax_breaks_ties_to_lowest_index():
+    r = np.array([0.5, 2.0, -1.0, 2.0, 2.0], np.float32)
+    assert O.lib().or_argmax(O.fptr(r), 5) == 1
+
+
+# ---- generator math (synth.c) ----------------------------------------------
+def test_generator_math_is_accurate():
+    L = O.lib()
+    for u in (1.0, 0.5, 0.75, 1e-3, 2.0 ** -53, 0.999999, 0.3):
+        assert abs(L.syn_ln(u) - math.log(u)) <= 4e-16 * max(1.0, abs(math.log(u)))
+    for y in (0.0, 1e-6, 0.25, 2.0, 73.5, 17.0):
+        assert abs(L.syn_sqrt(y) - math.sqrt(y)) <= 4e-16 * max(1.0, math.sqrt(y))
+    import ctypes
+    c, s = ctypes.c_double(), ctypes.c_double()
+    for v in np.linspace(0, 1, 257, endpoint=False):
+        L.syn_cos_sin_2pi(float(v), ctypes.byref(c), ctypes.byref(s))
+        assert abs(c.value - math.cos(2 * math.pi * v)) < 1e-15
+        assert abs(s.value - math.sin(2 * math.pi * v)) < 1e-15
+    z = O.synth(200000, 99, 7, 1.0).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+
+
+# ---- llama.c:528-600 end to end --------------------------------------------
+def _e2e(name):
+    meta = golden_json(f"e2e_{name}")
+    m = O.Model(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    try:
+        assert m.hash() == int(meta["model_hash"], 16)
+        assert O.prompt(meta["prompt_len"], meta["seed"], meta["cfg"][0]) == meta["prompt"]
+        hashes = [int(h, 16) for h in meta["logit_hashes"]]
+        m.reset()
+        for i, t in enumerate(meta["prompt"]):
+            lg = m.step(t)
+            assert O.hash_f32(lg) == hashes[i], f"prompt step {i}"
+        P = len(meta["prompt"])
+        gen = []
+        for s in range(meta["gen_len"]):
+            nxt = int(O.lib().or_argmax(O.fptr(m.logits), m.vocab))
+            gen.append(nxt)
+            lg = m.step(nxt)
+            assert O.hash_f32(lg) == hashes[P + s], f"gen step {s}"
+        assert gen == meta["gen"]
+        head = golden(f"e2e_{name}_logits_final")
+        assert_bits(m.logits[:head.size], head)
+    finally:
+        m.close()
+
+
+def test_e2e_tiny_matches_reference():
+    _e2e("tiny")
+
+
+@pytest.mark.slow
+@pytest.mark.skipif(not have_golden("e2e_1b.json"), reason="1B fixture not generated")
+def test_e2e_1b_matches_reference():
+    _e2e("1b")
+
+
+@pytest.mark.slow
+@pytest.mark.skipif(not have_golden("e2e_8b.json"), reason="8B fixture not generated")
+def test_e2e_8b_matches_reference():
+    _e2e("8b")
