@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Decode / prefill benchmark of the MI355X int8 LLaMA path (one GPU).
+
+Workload (the one the headline metric is quoted on):
+Llama-3-8B-shaped model with seeded synthetic weights (fp32 N(0, 0.02) quantized
+per output channel to int8), a 2048-token uniform-random prompt, then greedy
+decode steps.  A "step" is one decode token through the whole model.  Everything
+the timed region touches is already resident in HBM.
+
+Prints one JSON line (rank 0) with decode tok/s, the dominant kernel's roofline
+(the W8A8 GEMV, timed with HIP events on the library's stream) and the CPU
+oracle timed on this host's cores on the same weights.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+CONFIGS = {
+    # cfg = vocab, d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq; rope base; tied; prefill
+    "8b": ([128256, 4096, 32, 32, 8, 128, 14336, 2560], 500000.0, False, 2048),
+    "1b": ([128256, 2048, 16, 32, 8, 64, 8192, 768], 500000.0, True, 512),
+    "tiny": ([32000, 288, 6, 6, 2, 48, 768, 256], 10000.0, False, 128),
+}
+METRIC = "decode tok/s + % HBM roofline, 8B-shape int8 LLaMA (1 GPU); prefill tok/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def load_qllama():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("qllama", os.path.join(ROOT, "llm-project_amd", "qllama.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def gemv_bytes(cfg):
+    """Algorithmic HBM bytes of each GEMV launch per token: int8 weights + fp32
+    scales + the int8 activation row + fp32 outputs (read too where residual)."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    n_qkv = qd + 2 * kvd
+
+    def g(N, K, extra_per_row):
+        return N * K + 4 * N + K + extra_per_row * N
+
+    return {
+        "gemv_qkv": (L, g(n_qkv, dm, 4 + 4)),      # out + bias
+        "gemv_o": (L, g(dm, qd, 8)),               # residual read + write
+        "gemv_gate_up": (L, g(2 * ff, dm, 4)),
+        "gemv_down": (L, g(dm, ff, 8)),
+        "gemv_head": (1, g(vocab, dm, 4)),
+    }
+
+
+def decode_bytes(cfg, t):
+    """Algorithmic HBM bytes of one decode token attending over t cached rows."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    w = L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab
+    scales = 4 * (L * ((qd + 2 * kvd) + dm + 2 * ff + dm) + vocab)
+    f32 = 4 * (2 * L * dm + L * (qd + 2 * kvd) + dm)
+    kv = 2 * L * kvd * 4 * t + 2 * L * kvd * 4
+    return w + scales + f32 + kv + dm
+
+
+def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
+    """The CPU oracle (a C11 restatement of the reference decode step, threaded
+    like the reference) on this host's cores: same weights, exported from the
+    device; the first pos0 cache rows filled with N(0,1); decode steps timed at
+    positions pos0.. until `seconds` of work."""
+    import oracle_lib as O
+    nthreads = len(os.sched_getaffinity(0))
+    O.lib().or_set_threads(nthreads)
+    om = O.Model(cfg, base, synth=False)
+    L = cfg[2]
+
+    def export(qt, oqt):
+        if Q.lib().q_llama_tensor_export(C.byref(qt), oqt.q, oqt.scale) != 0:
+            raise RuntimeError("tensor export failed")
+
+    export(gm.m.wte, om.m.wte)
+    export(gm.m.lm_head, om.m.lm_head)
+    for l in range(L):
+        gb, ob = gm.m.blocks[l], om.m.blocks[l]
+        for n in ("Wq", "Wk", "Wv", "Wo", "Wgate", "Wup", "Wdown"):
+            export(getattr(gb, n), getattr(ob, n))
+    kvd = cfg[4] * cfg[5]
+    per = cfg[7] * kvd
+    rng = np.random.default_rng(7)
+    for arr_ptr in (om.kv.k, om.kv.v):
+        view = np.ctypeslib.as_array(arr_ptr, shape=(L * per,))
+        for l in range(L):
+            view[l * per:l * per + pos0 * kvd] = rng.standard_normal(pos0 * kvd, dtype=np.float32)
+    om.reset(pos0)
+    om.step(1)                                   # warm-up
+    times = []
+    t_start = time.perf_counter()
+    tok = int(np.argmax(om.logits))
+    while len(times) < 2 or (time.perf_counter() - t_start < seconds and len(times) < 64):
+        t0 = time.perf_counter()
+        lg = om.step(tok)
+        times.append(time.perf_counter() - t0)
+        tok = int(np.argmax(lg))
+    om.close()
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": nthreads, "kind": "port",
+            "sample": f"{len(times)} decode steps at positions {pos0 + 1}..{pos0 + len(times)} of the same "
+                      f"model (weights copied from the GPU, earlier cache rows N(0,1)); median step "
+                      f"{med * 1e3:.1f} ms, oracle/liboracle with {nthreads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="8b", choices=sorted(CONFIGS))
+    ap.add_argument("--prefill", type=int, default=None)
+    ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(1)
+    rank = int(os.environ.get("RANK", "0"))
+
+    Q = load_qllama()
+    cfg, base, tied, prefill = CONFIGS[args.config]
+    P = args.prefill if args.prefill is not None else prefill
+    W, K, NP = args.warmup, args.steps, args.profile_steps
+    if P + W + K + NP > cfg[7]:
+        sys.exit(f"bench.py: prefill {P} + warmup {W} + steps {K} + profile {NP} exceeds max_seq {cfg[7]}")
+
+    t0 = time.perf_counter()
+    gm = Q.Model.synth(cfg, base, seed=1234, tied=tied)
+    t_build = time.perf_counter() - t0
+    import oracle_lib as O
+    prompt = O.prompt(P, 1234, cfg[0])
+
+    # prefill (timed separately)
+    Q.lib().qllama_device_sync()
+    t0 = time.perf_counter()
+    gm.prefill(prompt, want_logits=True)
+    Q.lib().qllama_device_sync()
+    t_prefill = time.perf_counter() - t0
+    tok = int(np.argmax(gm.logits[0]))
+
+    # warm-up decode steps (untimed), then exactly K timed steps
+    out = gm.generate_greedy(tok, W) if W else []
+    tok = out[-1] if out else tok
+    Q.lib().qllama_device_sync()
+    pos_first = gm.pos
+    t0 = time.perf_counter()
+    out = gm.generate_greedy(tok, K)
+    Q.lib().qllama_device_sync()
+    t_decode = time.perf_counter() - t0
+    tok = out[-1]
+    ms_per_step = 1e3 * t_decode / K
+    tok_s = K / t_decode
+    # context of each timed step: pos + 1 cached rows
+    ctx = [pos_first + 1 + i for i in range(K)]
+    step_bytes = statistics.mean(decode_bytes(cfg, t) for t in ctx)
+    step_frac = step_bytes / (t_decode / K) / (HBM_PEAK_GBS * 1e9)
+
+    # per-kernel HIP-event timing of the same decode steps (eager launches)
+    Q.profile(True)
+    gm.generate_greedy(tok, NP)
+    prof = Q.profile_read()
+    Q.profile(False)
+    gb = gemv_bytes(cfg)
+    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
+    gemv_bytes_tok = sum(n * b for (n, b) in gb.values())
+    launches_per_tok = sum(n for (n, _) in gb.values())
+    achieved = gemv_bytes_tok / (gemv_ms * 1e-3) / 1e9 if gemv_ms > 0 else None
+
+    cpu = None
+    if not args.no_cpu_baseline and rank == 0:
+        cpu = cpu_baseline(Q, gm, cfg, base, pos_first, args.cpu_seconds)
+    gm.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights quantized per channel; uniform-random prompt ids)",
+        "config": {
+            "workload": f"{args.config}-shape int8 LLaMA greedy decode after a {P}-token prefill",
+            "cfg": cfg, "rope_base": base, "tied": tied, "prefill_tokens": P,
+            "context_timed": [ctx[0], ctx[-1]],
+        },
+        "decode_hbm_roofline_frac": round(step_frac, 4),
+        "decode_bytes_per_token": int(step_bytes),
+        "prefill_tok_s": round(P / t_prefill, 2) if P else None,
+        "prefill_s": round(t_prefill, 4),
+        "model_build_s": round(t_build, 3),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites)",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": None,
+            "bytes_per_launch": round(gemv_bytes_tok / launches_per_tok),
+            "avg_launch_us": round(1e3 * gemv_ms / launches_per_tok, 3) if gemv_ms else None,
+        },
+        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())},
+        "cpu_baseline": cpu,
+    }
+    if rank == 0:
+        print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

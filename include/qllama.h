@@ -1,0 +1,178 @@
+// qllama.h - C ABI of the MI355X library for the reference's int8 LLaMA decode path.
+//
+// Drop-in for the quantized section of the reference's llama.h (llama.h:114-140),
+// for quant.h (quant.h:15-33) and for qacc_columns (matrix.h:55).  Same names,
+// argument meaning and error behaviour; the difference is where the data lives:
+//
+//   * QTensor.q / QTensor.scale point to DEVICE memory (MI355X HBM).  q is stored
+//     output-channel major: element (row k, col j) of the reference's (rows, cols)
+//     matrix sits at q[j * kpad + k], kpad = rows rounded up to 16 (zero padded),
+//     so each output channel's K inputs are contiguous (layout QT_LAYOUT_NK).  The
+//     token embedding keeps the reference's row-major order (QT_LAYOUT_KN) because
+//     it is read one row per token.  Callers of the reference never read q or
+//     scale (main.c:649-671, selftest.c:1231-1249); they are opaque here.
+//   * Tensor members of QLlamaBlock / QLlamaModel hold device pointers as well.
+//   * LlamaKV.k / .v hold one device pointer per layer; callers only read and
+//     reset LlamaKV.len (main.c:661), which this library honours.
+//   * Tensor arguments of qmatmul and the logits of q_llama_decode_step are host
+//     memory, exactly as in the reference.
+//
+// Errors follow the reference: loaders return nonzero and print "Error: ..." to
+// stderr; void functions print and abort on a device error.  Entry points that
+// are additive (no reference counterpart) return 0 on success.
+#ifndef QLLAMA_H
+#define QLLAMA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// tensor.h:10-16 (host tensors; inside a QLlamaModel the data pointer is device memory)
+typedef struct {
+  float *data;
+  float *grad;
+  int *shape;
+  int ndim;
+  size_t size;
+} Tensor;
+
+#define QT_LAYOUT_NK 0   // device, output-channel major, K contiguous, rows padded to 16
+#define QT_LAYOUT_KN 1   // device, reference row-major (rows, cols)
+
+// quant.h:22-27 plus a layout tag and the padded row length.
+typedef struct {
+  int rows, cols;
+  signed char *q;     // device
+  float *scale;       // device, cols entries
+  int layout;         // QT_LAYOUT_*
+  int kpad;           // padded K for QT_LAYOUT_NK (multiple of 16), else cols
+} QTensor;
+
+// llama.h:19-37 (fp32, host) - input of q_llama_quantize_from.
+typedef struct {
+  int d_model, n_heads, n_kv, head_dim, d_ff;
+  float rope_base, eps;
+  Tensor attn_norm, Wq, Wk, Wv, b_q, b_k, b_v, Wo, ffn_norm, Wgate, Wup, Wdown;
+} LlamaBlock;
+
+// llama.h:58-66 (fp32, host)
+typedef struct {
+  int vocab, d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq;
+  float rope_base, eps;
+  Tensor wte;
+  LlamaBlock *blocks;
+  Tensor final_norm;
+  Tensor lm_head;
+} LlamaModel;
+
+// llama.h:94-99 plus the device-side state.
+typedef struct {
+  int n_layers, max_seq, kv_dim;
+  int len;            // positions cached; callers may reset it to 0 to restart
+  float **k;          // host array of n_layers device pointers, [n_kv][max_seq][head_dim]
+  float **v;
+  void *dev;          // library-private
+} LlamaKV;
+
+// llama.h:117-121
+typedef struct {
+  Tensor attn_norm, ffn_norm;                  // device f32
+  Tensor b_q, b_k, b_v;                        // device f32
+  QTensor Wq, Wk, Wv, Wo, Wgate, Wup, Wdown;   // device int8
+} QLlamaBlock;
+
+// llama.h:123-130 plus the device-side state.
+typedef struct {
+  int vocab, d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq;
+  float rope_base, eps;
+  QTensor wte;
+  QLlamaBlock *blocks;
+  Tensor final_norm;
+  QTensor lm_head;
+  void *dev;          // library-private
+} QLlamaModel;
+
+// ---------------------------------------------------------------------------
+// Drop-in entry points (reference file:line each one replaces)
+// ---------------------------------------------------------------------------
+
+// llama.c:610-657  Load an 'LLMQ' v2 checkpoint straight into device memory.
+int q_llama_model_load(const char *path, QLlamaModel *out);
+// llama.c:483-488
+void q_llama_model_free(QLlamaModel *m);
+// llama.c:490-511  Quantize a host fp32 model (per output channel) on the GPU.
+QLlamaModel q_llama_quantize_from(const LlamaModel *src);
+// llama.c:513-526  Device KV cache of max_seq positions per layer.
+LlamaKV q_llama_kv_create(const QLlamaModel *m);
+// llama.c:290-294
+void llama_kv_free(LlamaKV *kv);
+// llama.c:528-600  One token at position kv->len; logits (1, vocab) in host memory.
+void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *logits);
+
+// quant.c:35-41 / 43-46 / 48-50  (device QTensor, QT_LAYOUT_NK)
+QTensor qtensor_create(int rows, int cols);
+void qtensor_free(QTensor *t);
+void qtensor_quantize(QTensor *t, const float *w);            // w: host (rows, cols) f32
+// quant.c:60-85  C[m,j] = (as[m] * scale[j]) * sum_k qa[m,k] q[k,j]; A, C host.
+void qmatmul(const Tensor *A, const QTensor *W, Tensor *C);
+// quant.c:10-27 / 29-33  (host arrays in, host arrays out; computed on the GPU)
+void quantize_int8_percol(const float *w, int rows, int cols, signed char *q, float *scale);
+void dequantize_int8_percol(const signed char *q, const float *scale, int rows, int cols, float *w);
+// matrix.c:370-374  acc[j] = sum_k qa[k] * qw[k*N + j]  (host arrays, computed on the GPU)
+void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, int32_t *acc);
+
+// ---------------------------------------------------------------------------
+// Additive entry points
+// ---------------------------------------------------------------------------
+
+// Prompt ingestion: n tokens at positions kv->len .. kv->len+n-1.  Same result
+// as n calls of q_llama_decode_step (main.c:662); logits are those of the last
+// token.  logits may be NULL.  Returns 0 on success.
+int q_llama_prefill(const QLlamaModel *m, LlamaKV *kv, const int *ids, int n, Tensor *logits);
+
+// Greedy generation kept on the device: feeds `token` at kv->len, then each
+// argmax (first index of the maximum, sampler.c:8-21) back in, n_steps times;
+// out[i] receives the i-th generated id.  Equals the reference loop
+// main.c:663-668 with temperature 0.  Returns 0 on success.
+int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_steps, int *out);
+
+// Model from the seeded synthetic generator (fp32 N(0, 0.02) weights quantized
+// per output channel, gains 1, biases 0), built on the device.  cfg = {vocab,
+// d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq}.  Returns 0 on success.
+int q_llama_model_synth(QLlamaModel *out, const int32_t cfg[8], float rope_base, float eps,
+                        uint64_t seed, int tied);
+// Order-independent digest of every int8 tensor and scale vector, in the
+// reference's (rows, cols) indexing; equal to the generator's CPU digest.
+uint64_t q_llama_model_hash(const QLlamaModel *m);
+
+// Copy a device QTensor back to host memory in the reference's layout (quant.h:22-27):
+// q (rows, cols) row-major int8 and scale (cols).  Counterpart of the loader's
+// read order (llama.c:603-608).  Returns 0 on success.
+int q_llama_tensor_export(const QTensor *t, signed char *q_host, float *scale_host);
+
+// Device-side helpers for tests and benchmarks.
+int  qllama_device_count(void);
+int  qllama_device_sync(void);
+int  qllama_sync(void);
+void *qllama_stream(void);               // the hipStream_t every launch goes to
+// Average duration (ms) of each kernel class over the decode steps run while
+// profiling was on; returns the number of classes written.
+int  qllama_profile(int enable);
+int  qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max);
+// The device expf (the one attention and SwiGLU use) on the float bit patterns
+// start, start+1, ..., start+count-1, written to host memory.  For parity tests.
+int  qllama_test_expf(uint32_t start, uint32_t count, float *out);
+// Decode attention (llama.c:554-576) of one query row at position T-1 against
+// T cached rows, on the device: q (n_heads*hd), k and v (T, n_kv*hd) in the
+// reference's cache layout, o (n_heads*hd); all host memory.  For op-level parity.
+int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv,
+                       int hd, float *o);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,406 @@
+// k_decode.hip - the per-token kernels of the int8 decode step.
+//
+// Bit-exactness with the reference CPU path rests on three rules kept in every
+// kernel here: integer dot products are exact in any order; every floating
+// point sum the reference forms sequentially (rmsnorm's sum of squares, the
+// attention dot products, the softmax denominator and the weighted sum of V) is
+// formed here in the same sequential order; and no product is fused into an add
+// (the library is compiled with -ffp-contract=off, as ISO C11 compiles the
+// reference).  Maxima are order independent.
+#include <hip/hip_runtime.h>
+
+#include "qdev_math.h"
+#include "qhip.h"
+#include "qhip_internal.h"
+#include "qllama.h"
+
+namespace {
+
+__device__ __forceinline__ float block_max(float m, float *red) {
+  m = qd::wave_max_f32(m);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = m;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = fmaxf(r, red[i]);
+  return r;
+}
+
+// Write row `row` of qa (int8, kpad wide, zero padded) from values v[0..n) held
+// in LDS, given the row's max |v| (quant.c:66-78).
+__device__ __forceinline__ void quantize_row_lds(const float *v, int n, int kpad, float mx, int8_t *qa_row,
+                                                 float *as_out) {
+  const float as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+  const float inv = 1.0f / as;
+  for (int k = threadIdx.x; k < kpad; k += blockDim.x) qa_row[k] = (int8_t)(k < n ? qd::quant_i8(v[k], inv) : 0);
+  if (threadIdx.x == 0) *as_out = as;
+}
+
+// x[j] = (float)wte[token*dm + j] * scale[j]   (llama.c:534-536)
+__global__ void k_embed(const int8_t *wte, const float *s, int dm, const int *d_in, const int *d_state, float *x) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= dm) return;
+  const int tok = d_in[d_state[0]];
+  x[j] = (float)wte[(size_t)tok * dm + j] * s[j];
+}
+
+// One block per row: rmsnorm.c:7-21 then the activation quantization of qmatmul.
+// The sum of squares is accumulated by one lane in index order, as the
+// reference's loop does; the squares themselves are formed in parallel.
+__global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *x, int dm, const float *gamma, float eps,
+                                                         int8_t *qa, int kpad, float *as) {
+  extern __shared__ float lds[];          // dm values, then dm squares
+  __shared__ float red[16];
+  __shared__ float s_r;
+  const int row = blockIdx.x;
+  const float *xr = x + (size_t)row * dm;
+  float *v = lds, *sq = lds + dm;
+  for (int j = threadIdx.x; j < dm; j += blockDim.x) {
+    const float a = xr[j];
+    v[j] = a;
+    sq[j] = a * a;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ms = 0.0f;
+    for (int j = 0; j < dm; j++) ms += sq[j];
+    const float inv_n = 1.0f / (float)dm;
+    ms *= inv_n;
+    s_r = 1.0f / sqrtf(ms + eps);
+  }
+  __syncthreads();
+  const float r = s_r;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < dm; j += blockDim.x) {
+    const float y = v[j] * r * gamma[j];
+    v[j] = y;
+    mx = fmaxf(mx, fabsf(y));
+  }
+  mx = block_max(mx, red);
+  __syncthreads();
+  quantize_row_lds(v, dm, kpad, mx, qa + (size_t)row * kpad, as + row);
+}
+
+// One block per row: quantize v (rows, n) -> qa (rows, kpad), as (rows).
+__global__ __launch_bounds__(1024) void k_quant_rows(const float *vin, int n, int8_t *qa, int kpad, float *as) {
+  extern __shared__ float lds[];
+  __shared__ float red[16];
+  const int row = blockIdx.x;
+  const float *vr = vin + (size_t)row * n;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const float a = vr[j];
+    lds[j] = a;
+    mx = fmaxf(mx, fabsf(a));
+  }
+  mx = block_max(mx, red);
+  __syncthreads();
+  quantize_row_lds(lds, n, kpad, mx, qa + (size_t)row * kpad, as + row);
+}
+
+// h_j = (z * (1 / (1 + expf(-z)))) * u_j over gu = [g | u]  (llama.c:583-587), then quantize h.
+__global__ __launch_bounds__(1024) void k_swiglu_quant(const float *gu, int dff, int8_t *qa, int kpad, float *as) {
+  extern __shared__ float lds[];
+  __shared__ float red[16];
+  const int row = blockIdx.x;
+  const float *g = gu + (size_t)row * 2 * dff, *u = g + dff;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < dff; j += blockDim.x) {
+    const float z = g[j];
+    const float s = 1.0f / (1.0f + qd::expf_glibc(-z));
+    const float h = (z * s) * u[j];
+    lds[j] = h;
+    mx = fmaxf(mx, fabsf(h));
+  }
+  mx = block_max(mx, red);
+  __syncthreads();
+  quantize_row_lds(lds, dff, kpad, mx, qa + (size_t)row * kpad, as + row);
+}
+
+// W8A8 GEMV: one wave per output channel j; lanes stride K in 16-byte chunks and
+// accumulate exact int32 dot products (v_dot4), reduced across the wave.
+// Epilogue: c = (as * ws[j]) * (float)acc  (quant.c:81-82), then + bias or
+// residual (llama.c:546-548, 578, 589).  W is [N][kpad], qa is [rows][kpad].
+constexpr int kMaxRows = 8;
+__global__ __launch_bounds__(256) void k_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W,
+                                              const float *ws, int N, int kpad, float *out, const float *bias,
+                                              int residual) {
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (j >= N) return;
+  const int nchunk = kpad >> 4;
+  const int4 *wrow = reinterpret_cast<const int4 *>(W + (size_t)j * kpad);
+  int acc[kMaxRows];
+#pragma unroll
+  for (int m = 0; m < kMaxRows; m++) acc[m] = 0;
+  for (int c = lane; c < nchunk; c += 64) {
+    const int4 w = wrow[c];
+#pragma unroll
+    for (int m = 0; m < kMaxRows; m++) {
+      if (m < rows) {
+        const int4 a = reinterpret_cast<const int4 *>(qa + (size_t)m * kpad)[c];
+        int t = acc[m];
+        t = __builtin_amdgcn_sdot4(a.x, w.x, t, false);
+        t = __builtin_amdgcn_sdot4(a.y, w.y, t, false);
+        t = __builtin_amdgcn_sdot4(a.z, w.z, t, false);
+        t = __builtin_amdgcn_sdot4(a.w, w.w, t, false);
+        acc[m] = t;
+      }
+    }
+  }
+  const float wsj = ws[j];
+#pragma unroll
+  for (int m = 0; m < kMaxRows; m++) {
+    if (m < rows) {
+      const int a = qd::wave_sum_i32(acc[m]);
+      if (lane == 0) {
+        const float c = (as[m] * wsj) * (float)a;
+        float *o = out + (size_t)m * N + j;
+        if (residual) *o = *o + c;
+        else *o = bias ? c + bias[j] : c;
+      }
+    }
+  }
+}
+
+// rope.c:48-68 with cos/sin from the host tables at position pos; blocks
+// [0, H) rotate query heads into q_out, [H, H+KVH) rotate key heads into the
+// cache, [H+KVH, H+2KVH) copy value heads into the cache.
+__global__ void k_rope_append(const float *qkv, int H, int KVH, int hd, const float *cos_t, const float *sin_t,
+                              const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
+  const int pos = *d_pos;
+  const int half = hd >> 1;
+  const int b = blockIdx.x;
+  const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
+  if (b < H + KVH) {
+    const bool isq = b < H;
+    const float *xh = qkv + (isq ? (size_t)b * hd : (size_t)H * hd + (size_t)(b - H) * hd);
+    float *dst = isq ? q_out + (size_t)b * hd : kc + ((size_t)(b - H) * max_seq + pos) * hd;
+    for (int k = threadIdx.x; k < half; k += blockDim.x) {
+      const float c = ct[k], s = st[k];
+      const float x1 = xh[k], x2 = xh[k + half];
+      dst[k] = x1 * c - x2 * s;
+      dst[k + half] = x2 * c + x1 * s;
+    }
+  } else {
+    const int h = b - H - KVH;
+    const float *vh = qkv + (size_t)(H + KVH) * hd + (size_t)h * hd;
+    float *dst = vc + ((size_t)h * max_seq + pos) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = vh[d];
+  }
+}
+
+// Decode attention, one block per query head (llama.c:554-576): scores with the
+// dot over d in order, max, expf, the sum of exponentials in j order, then each
+// output dimension accumulated over j in order.
+__global__ __launch_bounds__(256) void k_attention(const float *q, const float *kc, const float *vc, const int *d_pos,
+                                                   int H, int KVH, int hd, int max_seq, float scale,
+                                                   float *scores, float *o) {
+  extern __shared__ float qs[];
+  __shared__ float red[4];
+  __shared__ float s_inv;
+  const int h = blockIdx.x;
+  const int kvh = h / (H / KVH);
+  const int T = *d_pos + 1;
+  const float *K = kc + (size_t)kvh * max_seq * hd;
+  const float *V = vc + (size_t)kvh * max_seq * hd;
+  float *sc = scores + (size_t)h * max_seq;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[(size_t)h * hd + d];
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < T; j += blockDim.x) {
+    const float *kj = K + (size_t)j * hd;
+    float dot = 0.0f;
+    for (int d = 0; d < hd; d++) dot += qs[d] * kj[d];
+    const float s = dot * scale;
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_max(mx, red);
+  for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = qd::expf_glibc(sc[j] - mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.0f;
+    for (int j = 0; j < T; j++) sum += sc[j];
+    s_inv = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = s_inv;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < T; j++) {
+      const float w = sc[j] * inv;
+      acc += w * V[(size_t)j * hd + d];
+    }
+    o[(size_t)h * hd + d] = acc;
+  }
+}
+
+// First index of the maximum (sampler.c:8-21), then advance the position.
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out,
+                                                         int max_seq) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const float a = v[j];
+    if (idx == 0x7fffffff || a > best) { best = a; idx = j; }   // a thread's first element, then strict >
+  }
+  // combine: larger value wins, equal values keep the lower index
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) { bv[w] = best; bi[w] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = bv[0];
+    int bi0 = bi[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++)
+      if (bv[i] > b || (bv[i] == b && bi[i] < bi0)) { b = bv[i]; bi0 = bi[i]; }
+    const int pos = d_state[0];
+    if (pos < max_seq) d_out[pos] = bi0;
+    if (pos + 1 >= d_state[1] && pos + 1 <= max_seq) d_in[pos + 1] = bi0;
+    d_state[0] = pos + 1;
+  }
+}
+
+// matrix.c:354-374 on the reference's row-major (K, N) layout: one thread per column.
+__global__ void k_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  int a = 0;
+  for (int k = 0; k < K; k++) a += (int)qa[k] * (int)qw[(size_t)k * N + j];
+  acc[j] = a;
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int qhip_embed(const int8_t *wte, const float *wte_s, int dm, const int *d_in, const int *d_state, float *x) {
+  QH_LAUNCH(QK_EMBED, k_embed, dim3((dm + 255) / 256), dim3(256), 0, wte, wte_s, dm, d_in, d_state, x);
+  return 0;
+}
+
+int qhip_rmsnorm_quant(const float *x, int rows, int dm, const float *gamma, float eps, int8_t *qa, int kpad,
+                       float *as) {
+  if (dm > 16384) return qh::fail_msg("rmsnorm_quant: d_model above 16384");
+  QH_LAUNCH(QK_RMSNORM, k_rmsnorm_quant, dim3(rows), dim3(1024), (size_t)dm * 8, x, dm, gamma, eps, qa, kpad, as);
+  return 0;
+}
+
+int qhip_quant_rows(const float *v, int rows, int n, int8_t *qa, int kpad, float *as) {
+  if (n > 32768) return qh::fail_msg("quant_rows: row above 32768");
+  QH_LAUNCH(QK_QUANT, k_quant_rows, dim3(rows), dim3(1024), (size_t)n * 4, v, n, qa, kpad, as);
+  return 0;
+}
+
+int qhip_swiglu_quant(const float *gu, int rows, int dff, int8_t *qa, int kpad, float *as) {
+  if (dff > 32768) return qh::fail_msg("swiglu_quant: d_ff above 32768");
+  QH_LAUNCH(QK_SWIGLU, k_swiglu_quant, dim3(rows), dim3(1024), (size_t)dff * 4, gu, dff, qa, kpad, as);
+  return 0;
+}
+
+int qhip_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W, const float *ws, int N, int kpad,
+              float *out, const float *bias, int residual, int cls) {
+  if (kpad % 16) return qh::fail_msg("gemv: kpad must be a multiple of 16");
+  for (int m0 = 0; m0 < rows; m0 += kMaxRows) {
+    const int r = rows - m0 < kMaxRows ? rows - m0 : kMaxRows;
+    QH_LAUNCH(cls, k_gemv, dim3((N + 3) / 4), dim3(256), 0, qa + (size_t)m0 * kpad, as + m0,
+              r, W, ws, N, kpad, out + (size_t)m0 * N, bias, residual);
+  }
+  return 0;
+}
+
+int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const float *cos_t, const float *sin_t,
+                     const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
+  QH_LAUNCH(QK_ROPE, k_rope_append, dim3(n_heads + 2 * n_kv), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t, sin_t,
+            d_pos, q_out, kc, vc, max_seq);
+  return 0;
+}
+
+int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads, int n_kv, int hd,
+                   int max_seq, float scale, float *scores, float *o) {
+  QH_LAUNCH(QK_ATTN, k_attention, dim3(n_heads), dim3(256), (size_t)hd * 4, q, kc, vc, d_pos, n_heads, n_kv, hd,
+            max_seq, scale, scores, o);
+  return 0;
+}
+
+int qhip_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out, int max_seq) {
+  QH_LAUNCH(QK_ARGMAX, k_argmax_advance, dim3(1), dim3(1024), 0, v, n, d_in, d_state, d_out, max_seq);
+  return 0;
+}
+
+int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc) {
+  QH_LAUNCH(QK_OTHER, k_qacc_kn, dim3((N + 255) / 256), dim3(256), 0, qa, qw, K, N, acc);
+  return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// test entry points
+// ---------------------------------------------------------------------------
+namespace {
+__global__ void k_expf_range(uint32_t start, uint32_t count, float *out) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
+    out[i] = qd::expf_glibc(__uint_as_float(start + i));
+}
+
+// reference cache rows (T, n_kv*hd) -> [n_kv][T][hd]
+__global__ void k_kv_relayout(const float *src, int T, int n_kv, int hd, float *dst) {
+  const size_t n = (size_t)T * n_kv * hd;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % hd);
+    const int h = (int)((i / hd) % n_kv);
+    const size_t t = i / ((size_t)hd * n_kv);
+    dst[((size_t)h * T + t) * hd + d] = src[i];
+  }
+}
+}  // namespace
+
+extern "C" int qllama_test_expf(uint32_t start, uint32_t count, float *out) {
+  if (qhip_init()) return 1;
+  float *d = (float *)qhip_malloc((size_t)count * 4);
+  if (!d) return 1;
+  hipLaunchKernelGGL(k_expf_range, dim3(8192), dim3(256), 0, qh::stream(), start, count, d);
+  int rc = qh::check_launch("k_expf_range");
+  if (!rc) rc = qhip_d2h(out, d, (size_t)count * 4);
+  qhip_free(d);
+  return rc;
+}
+
+extern "C" int qllama_gqa_decode(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv,
+                                 int hd, float *o) {
+  if (qhip_init()) return 1;
+  if (T <= 0 || n_kv <= 0 || n_heads % n_kv || hd <= 0) return qh::fail_msg("gqa_decode: bad shape");
+  const size_t kvn = (size_t)T * n_kv * hd;
+  float *dq = (float *)qhip_malloc((size_t)n_heads * hd * 4), *dk = (float *)qhip_malloc(kvn * 4);
+  float *dv = (float *)qhip_malloc(kvn * 4), *tmp = (float *)qhip_malloc(kvn * 4);
+  float *dsc = (float *)qhip_malloc((size_t)n_heads * T * 4), *dout = (float *)qhip_malloc((size_t)n_heads * hd * 4);
+  int *dpos = (int *)qhip_malloc(4);
+  const int pos = T - 1;
+  int rc = (!dq || !dk || !dv || !tmp || !dsc || !dout || !dpos) ? 1 : 0;
+  if (!rc) rc = qhip_h2d(dq, q, (size_t)n_heads * hd * 4) || qhip_h2d(dpos, &pos, 4) ||
+                qhip_h2d(tmp, k, kvn * 4);
+  if (!rc) {
+    hipLaunchKernelGGL(k_kv_relayout, dim3(4096), dim3(256), 0, qh::stream(), tmp, T, n_kv, hd, dk);
+    rc = qh::check_launch("k_kv_relayout") || qhip_h2d(tmp, v, kvn * 4);
+  }
+  if (!rc) {
+    hipLaunchKernelGGL(k_kv_relayout, dim3(4096), dim3(256), 0, qh::stream(), tmp, T, n_kv, hd, dv);
+    rc = qh::check_launch("k_kv_relayout");
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (!rc) rc = qhip_attention(dq, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dsc, dout);
+  if (!rc) rc = qhip_d2h(o, dout, (size_t)n_heads * hd * 4);
+  qhip_free(dq); qhip_free(dk); qhip_free(dv); qhip_free(tmp); qhip_free(dsc); qhip_free(dout); qhip_free(dpos);
+  return rc;
+}

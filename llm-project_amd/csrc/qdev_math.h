@@ -1,0 +1,192 @@
+// qdev_math.h - device arithmetic that must agree bit for bit with the host.
+//
+// Compiled with -ffp-contract=off: every product and sum below is rounded where
+// it is written, exactly as ISO C evaluates the same expressions on the host.
+#ifndef QDEV_MATH_H
+#define QDEV_MATH_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qd {
+
+// ---------------------------------------------------------------------------
+// expf with the results of glibc 2.35's x86-64 FMA variant, which is what the
+// reference's `expf` resolves to on its hosts (llama.c:567,585).  Published
+// method (glibc sysdeps/ieee754/flt-32/e_expf.c, from Arm's optimized-routines):
+// x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, 2^(r/32) from a cubic, all
+// in double; the reduction and the polynomial steps are fused multiply-adds.
+// The table holds the double nearest to 2^(i/32), minus i << 47 in its bits, so
+// adding k << 47 applies the exponent.  Verified against the host libm on every
+// float input (tests/test_gpu_numerics.py).
+// ---------------------------------------------------------------------------
+__device__ __constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float expf_glibc(float x) {
+  const uint32_t ux = __float_as_uint(x);
+  const uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {                       // |x| >= 88, inf or nan
+    if (ux == 0xff800000u) return 0.0f;         // -inf
+    if (abstop >= 0x7f8u) return x + x;         // +inf, nan
+    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);   // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;                           // underflow
+  }
+  const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  const double Shift = 0x1.8p+52;
+  const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  const double xd = (double)x;
+  double kd = __builtin_fma(InvLn2N, xd, Shift);
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= Shift;
+  const double r = __builtin_fma(InvLn2N, xd, -kd);
+  const uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+  const double s = __longlong_as_double((long long)t);
+  const double z = __builtin_fma(C0, r, C1);
+  const double r2 = r * r;
+  double y = __builtin_fma(C2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// ---------------------------------------------------------------------------
+// Seeded generator: the device side of the specification in oracle/synth.h
+// (splitmix64 finaliser keyed by (seed, tensor id), Box-Muller with ln, sqrt,
+// cos and sin evaluated by +, -, * only).  Written independently of the CPU
+// checker; equality is proven by the per-tensor digests.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
+__host__ __device__ __forceinline__ uint64_t gen_key(uint64_t seed, uint64_t tid) {
+  return mix64(mix64(seed + 0x9E3779B97F4A7C15ULL) ^ (tid * 0xD1B54A32D192ED03ULL));
+}
+
+__device__ __forceinline__ double gen_ln(double u) {
+  const uint64_t b = (uint64_t)__double_as_longlong(u);
+  int e = (int)((b >> 52) & 0x7ff) - 1023;
+  double m = __longlong_as_double((long long)((b & 0x000FFFFFFFFFFFFFULL) | 0x3FF0000000000000ULL));
+  if (m > 1.4142135623730951) { m = m * 0.5; e = e + 1; }
+  const double d = m + 1.0;
+  double r = 0.5;
+#pragma unroll
+  for (int k = 0; k < 6; k++) r = r * (2.0 - d * r);
+  const double t = (m - 1.0) * r;
+  const double t2 = t * t;
+  double p = 1.0 / 23.0;
+  p = p * t2 + 1.0 / 21.0;
+  p = p * t2 + 1.0 / 19.0;
+  p = p * t2 + 1.0 / 17.0;
+  p = p * t2 + 1.0 / 15.0;
+  p = p * t2 + 1.0 / 13.0;
+  p = p * t2 + 1.0 / 11.0;
+  p = p * t2 + 1.0 / 9.0;
+  p = p * t2 + 1.0 / 7.0;
+  p = p * t2 + 1.0 / 5.0;
+  p = p * t2 + 1.0 / 3.0;
+  p = p * t2 + 1.0;
+  return (double)e * 0.6931471805599453 + (2.0 * t) * p;
+}
+
+__device__ __forceinline__ double gen_sqrt(double y) {
+  if (!(y > 0.0)) return 0.0;
+  double g = __longlong_as_double((long long)(0x5FE6EB50C7B537A9ULL - ((uint64_t)__double_as_longlong(y) >> 1)));
+  const double hy = 0.5 * y;
+#pragma unroll
+  for (int k = 0; k < 6; k++) g = g * (1.5 - (hy * g) * g);
+  return y * g;
+}
+
+__device__ __forceinline__ void gen_cos_sin_2pi(double v, double &c, double &s) {
+  const double v8 = v * 8.0;
+  const int q = (int)v8;
+  double f = v8 - (double)q;
+  const int odd = q & 1;
+  if (odd) f = 1.0 - f;
+  const double a = f * 0.78539816339744830962;
+  const double a2 = a * a;
+  double sp = -1.0 / 355687428096000.0;
+  sp = sp * a2 + 1.0 / 1307674368000.0;
+  sp = sp * a2 - 1.0 / 6227020800.0;
+  sp = sp * a2 + 1.0 / 39916800.0;
+  sp = sp * a2 - 1.0 / 362880.0;
+  sp = sp * a2 + 1.0 / 5040.0;
+  sp = sp * a2 - 1.0 / 120.0;
+  sp = sp * a2 + 1.0 / 6.0;
+  const double sa = a - (a * a2) * sp;
+  double cp = 1.0 / 6402373705728000.0;
+  cp = cp * a2 - 1.0 / 20922789888000.0;
+  cp = cp * a2 + 1.0 / 87178291200.0;
+  cp = cp * a2 - 1.0 / 479001600.0;
+  cp = cp * a2 + 1.0 / 3628800.0;
+  cp = cp * a2 - 1.0 / 40320.0;
+  cp = cp * a2 + 1.0 / 720.0;
+  cp = cp * a2 - 1.0 / 24.0;
+  cp = cp * a2 + 0.5;
+  const double ca = 1.0 - a2 * cp;
+  const double cb = odd ? sa : ca, sb = odd ? ca : sa;
+  switch (q >> 1) {
+    case 0: c = cb; s = sb; break;
+    case 1: c = -sb; s = cb; break;
+    case 2: c = -cb; s = -sb; break;
+    default: c = sb; s = -cb; break;
+  }
+}
+
+__device__ __forceinline__ double gen_normal(uint64_t key, uint64_t i) {
+  const uint64_t p = i >> 1;
+  const uint64_t h1 = mix64(key + (p + 1) * 0x9E3779B97F4A7C15ULL);
+  const uint64_t h2 = mix64(h1 ^ 0x6A09E667F3BCC909ULL);
+  const double u1 = (double)((h1 >> 11) + 1) * 0x1p-53;
+  const double u2 = (double)(h2 >> 11) * 0x1p-53;
+  const double rad = gen_sqrt(-2.0 * gen_ln(u1));
+  double c, s;
+  gen_cos_sin_2pi(u2, c, s);
+  return rad * ((i & 1) ? s : c);
+}
+
+__device__ __forceinline__ float gen_value(uint64_t key, uint64_t i, double sigma) {
+  return (float)(gen_normal(key, i) * sigma);
+}
+
+// int8 quantization of one value with the reference's rounding (quant.c:74-77):
+// lrintf is round-half-even in the default mode, then clamp to +-127.
+__device__ __forceinline__ int quant_i8(float v, float inv) {
+  float r = __builtin_rintf(v * inv);
+  if (r != r) return 0;   // (int)lrintf(NaN): LONG_MIN on x86-64, whose low 32 bits are 0
+  r = r > 127.0f ? 127.0f : r;
+  r = r < -127.0f ? -127.0f : r;
+  return (int)r;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace qd
+
+#endif

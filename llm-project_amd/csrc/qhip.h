@@ -1,0 +1,108 @@
+// qhip.h - the thin extern "C" HIP layer under the C11 decode loop.
+//
+// Every launcher enqueues on the library's single HIP stream and returns 0, or
+// a nonzero code after recording a message for qhip_last_error().  Pointers are
+// device pointers unless a name says "host".  Shapes are plain ints.
+#ifndef QHIP_H
+#define QHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// ---- runtime ----------------------------------------------------------------
+int         qhip_init(void);
+int         qhip_device_count(void);
+const char *qhip_last_error(void);
+void       *qhip_malloc(size_t bytes);                   // NULL on failure
+void        qhip_free(void *p);
+void       *qhip_host_alloc(size_t bytes);               // pinned
+void        qhip_host_free(void *p);
+int         qhip_h2d(void *dst, const void *host_src, size_t n);        // synchronous
+int         qhip_d2h(void *host_dst, const void *src, size_t n);        // synchronous
+int         qhip_h2d_async(void *dst, const void *host_src, size_t n);  // pinned src
+int         qhip_d2h_async(void *host_dst, const void *src, size_t n);
+int         qhip_d2d_async(void *dst, const void *src, size_t n);
+int         qhip_fill_zero(void *p, size_t n);           // kernel, capture-safe
+int         qhip_sync(void);
+void       *qhip_stream(void);
+
+// graphs: capture the launches issued between begin and end on the stream
+int  qhip_capture_begin(void);
+int  qhip_capture_end(void **exec);
+int  qhip_graph_launch(void *exec);
+void qhip_graph_destroy(void *exec);
+
+// per-kernel-class timing with HIP events on the library stream
+int  qhip_profile_enable(int on);
+int  qhip_profile_read(char *names, int names_len, double *ms, long long *count, int max);
+
+// ---- generator / weights ------------------------------------------------------
+// Seeded N(0, sigma) matrix of the reference's (rows, cols) shape, quantized per
+// column and stored output-channel major: q[j*kpad + k], scale[j].  tid_src and
+// transpose_src select the generator tensor and index order (tied heads read the
+// embedding generator at (col, row)).
+int qhip_synth_quant_nk(uint64_t seed, uint64_t tid, int rows, int cols, int kpad, int transpose_src,
+                        double sigma, int8_t *q, float *scale);
+// Same, stored row-major (rows, cols) (embedding).
+int qhip_synth_quant_kn(uint64_t seed, uint64_t tid, int rows, int cols, double sigma,
+                        int8_t *q, float *scale);
+// Seeded f32 values (same generator) into a device buffer.
+int qhip_synth_f32(uint64_t seed, uint64_t tid, size_t n, double sigma, float *out);
+int qhip_fill_f32(float *p, size_t n, float v);
+// Quantize a device f32 (rows, cols) matrix per column (quant.c:10-27) into
+// NK layout or into row-major KN layout.
+int qhip_quantize_percol(const float *w, int rows, int cols, int layout_nk, int kpad,
+                         int8_t *q, float *scale);
+int qhip_dequantize_kn(const int8_t *q, const float *scale, int rows, int cols, float *w);
+// Row-major (rows, cols) int8 -> NK layout.
+int qhip_transpose_kn_to_nk(const int8_t *src, int rows, int cols, int kpad, int8_t *dst);
+// NK layout (q[j*kpad + i]) -> row-major (rows, cols).
+int qhip_nk_to_kn(const int8_t *src, int rows, int cols, int kpad, int8_t *dst);
+int qhip_device_sync(void);
+// Order-independent digests in the reference's (rows, cols) index space.
+int qhip_hash_i8(const int8_t *q, int rows, int cols, int layout_nk, int kpad, uint64_t salt,
+                 uint64_t *out);
+int qhip_hash_f32(const float *x, size_t n, uint64_t salt, uint64_t *out);
+
+// ---- decode kernels ------------------------------------------------------------
+// x[j] = (float)wte[token*dm + j] * s[j]   (llama.c:534-536), token = d_in[d_state[0]]
+int qhip_embed(const int8_t *wte, const float *wte_s, int dm, const int *d_in, const int *d_state,
+               float *x);
+// rows of x (rows, dm): y = rmsnorm(x) (rmsnorm.c:7-21), then per-row int8
+// quantization (quant.c:66-78): qa (rows, kpad), as (rows)
+int qhip_rmsnorm_quant(const float *x, int rows, int dm, const float *gamma, float eps,
+                       int8_t *qa, int kpad, float *as);
+// per-row int8 quantization only
+int qhip_quant_rows(const float *v, int rows, int n, int8_t *qa, int kpad, float *as);
+// h = SiLU(g) * u over gu = [g | u] (llama.c:583-587), then quantize h
+int qhip_swiglu_quant(const float *gu, int rows, int dff, int8_t *qa, int kpad, float *as);
+// out[m, j] = (as[m] * ws[j]) * acc[m, j] (+ bias[j]) or out[m, j] += that (residual);
+// cls names the call site for event timing (QK_* in qhip_internal.h, 12 = other)
+int qhip_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W, const float *ws,
+              int N, int kpad, float *out, const float *bias, int residual, int cls);
+// RoPE from host-built tables (rope.c:48-68) on q and k of qkv = [q | k | v];
+// q -> q_out, k and v appended to the per-layer cache [n_kv][max_seq][hd] at *d_pos.
+int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const float *cos_t,
+                     const float *sin_t, const int *d_pos, float *q_out, float *kc, float *vc,
+                     int max_seq);
+// decode attention over cache rows 0..*d_pos (llama.c:554-576)
+int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos,
+                   int n_heads, int n_kv, int hd, int max_seq, float scale, float *scores,
+                   float *o);
+// first index of the maximum (sampler.c:8-21) of v -> d_out[pos]; when pos + 1 is
+// past the staged inputs (d_state[1]) it also becomes d_in[pos + 1]; then
+// d_state[0] = pos + 1.  pos = d_state[0].
+int qhip_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out, int max_seq);
+
+// reference-layout column accumulate (matrix.c:354-374) for qacc_columns
+int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

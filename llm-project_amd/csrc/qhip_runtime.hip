@@ -1,0 +1,220 @@
+// qhip_runtime.hip - device, memory, stream, graph and event-timing services of the
+// HIP layer.  One stream per process carries every launch, in program order.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "qhip.h"
+#include "qhip_internal.h"
+
+namespace {
+hipStream_t g_stream = nullptr;
+int g_ready = 0;
+thread_local char g_err[512] = "";
+std::mutex g_init_mu;
+
+struct ProfRec { int cls; hipEvent_t a, b; };
+bool g_prof = false;
+std::vector<ProfRec> g_prof_recs;
+std::vector<hipEvent_t> g_event_pool;
+const char *g_class_names[QK_NUM_CLASSES] = {
+    "embed", "rmsnorm_quant", "gemv_qkv", "rope_append", "attention", "quant_rows",
+    "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other"};
+
+hipEvent_t take_event() {
+  if (!g_event_pool.empty()) { hipEvent_t e = g_event_pool.back(); g_event_pool.pop_back(); return e; }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+}  // namespace
+
+namespace qh {
+hipStream_t stream() { return g_stream; }
+
+int fail(const char *what, hipError_t e) {
+  snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
+  return 1;
+}
+
+int fail_msg(const char *msg) {
+  snprintf(g_err, sizeof g_err, "%s", msg);
+  return 1;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : fail(what, e);
+}
+
+void *prof_begin(int cls) {
+  if (!g_prof) return nullptr;
+  hipEvent_t a = take_event(), b = take_event();
+  if (!a || !b) return nullptr;
+  (void)hipEventRecord(a, g_stream);
+  g_prof_recs.push_back({cls, a, b});
+  return (void*)&g_prof_recs.back();
+}
+
+void prof_end(void *tok) {
+  if (!tok) return;
+  (void)hipEventRecord(g_prof_recs.back().b, g_stream);
+}
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+int qhip_init(void) {
+  std::lock_guard<std::mutex> lk(g_init_mu);
+  if (g_ready) return 0;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) return fail_msg("no HIP device visible");
+  if ((e = hipSetDevice(0)) != hipSuccess) return fail("hipSetDevice", e);
+  if ((e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking)) != hipSuccess)
+    return fail("hipStreamCreate", e);
+  g_ready = 1;
+  return 0;
+}
+
+int qhip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+const char *qhip_last_error(void) { return g_err; }
+
+void *qhip_malloc(size_t bytes) {
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+  if (e != hipSuccess) { fail("hipMalloc", e); return nullptr; }
+  return p;
+}
+
+void qhip_free(void *p) { if (p) (void)hipFree(p); }
+
+void *qhip_host_alloc(size_t bytes) {
+  void *p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess) { fail("hipHostMalloc", e); return nullptr; }
+  return p;
+}
+
+void qhip_host_free(void *p) { if (p) (void)hipHostFree(p); }
+
+int qhip_h2d(void *dst, const void *src, size_t n) {
+  if (!n) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? 0 : fail("copy to device", e);
+}
+
+int qhip_d2h(void *dst, const void *src, size_t n) {
+  if (!n) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? 0 : fail("copy to host", e);
+}
+
+int qhip_h2d_async(void *dst, const void *src, size_t n) {
+  if (!n) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream);
+  return e == hipSuccess ? 0 : fail("async copy to device", e);
+}
+
+int qhip_d2h_async(void *dst, const void *src, size_t n) {
+  if (!n) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream);
+  return e == hipSuccess ? 0 : fail("async copy to host", e);
+}
+
+int qhip_d2d_async(void *dst, const void *src, size_t n) {
+  if (!n) return 0;
+  hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, g_stream);
+  return e == hipSuccess ? 0 : fail("device copy", e);
+}
+
+int qhip_sync(void) {
+  if (!g_ready) return 0;
+  hipError_t e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? 0 : fail("stream synchronize", e);
+}
+
+void *qhip_stream(void) { return (void*)g_stream; }
+
+int qhip_device_sync(void) {
+  if (!g_ready) return 0;
+  hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? 0 : fail("device synchronize", e);
+}
+
+int qhip_capture_begin(void) {
+  hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
+  return e == hipSuccess ? 0 : fail("begin capture", e);
+}
+
+int qhip_capture_end(void **exec) {
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  if (e != hipSuccess) return fail("end capture", e);
+  hipGraphExec_t x = nullptr;
+  e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return fail("graph instantiate", e);
+  *exec = (void*)x;
+  return 0;
+}
+
+int qhip_graph_launch(void *exec) {
+  hipError_t e = hipGraphLaunch((hipGraphExec_t)exec, g_stream);
+  return e == hipSuccess ? 0 : fail("graph launch", e);
+}
+
+void qhip_graph_destroy(void *exec) {
+  if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+
+int qhip_profile_enable(int on) {
+  if (qhip_init()) return 1;
+  if (!on && g_prof) qhip_sync();
+  g_prof = on != 0;
+  return 0;
+}
+
+// Aggregates every (start, stop) pair recorded since the last read per class.
+int qhip_profile_read(char *names, int names_len, double *ms, long long *count, int max) {
+  if (qhip_sync()) return -1;
+  double tot[QK_NUM_CLASSES] = {0};
+  long long cnt[QK_NUM_CLASSES] = {0};
+  for (auto &r : g_prof_recs) {
+    float t = 0.0f;
+    if (hipEventElapsedTime(&t, r.a, r.b) == hipSuccess) { tot[r.cls] += t; cnt[r.cls]++; }
+    g_event_pool.push_back(r.a);
+    g_event_pool.push_back(r.b);
+  }
+  g_prof_recs.clear();
+  std::string all;
+  int n = 0;
+  for (int c = 0; c < QK_NUM_CLASSES && n < max; c++) {
+    if (!cnt[c]) continue;
+    ms[n] = tot[c] / (double)cnt[c];
+    count[n] = cnt[c];
+    all += g_class_names[c];
+    all += ",";
+    n++;
+  }
+  if (names && names_len > 0) {
+    strncpy(names, all.c_str(), (size_t)names_len - 1);
+    names[names_len - 1] = '\0';
+  }
+  return n;
+}
+
+}  // extern "C"

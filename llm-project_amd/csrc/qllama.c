@@ -1,0 +1,744 @@
+// qllama.c - C11 host side of the MI355X int8 LLaMA decode path.
+//
+// Keeps the reference's quantized API (llama.h:114-140, quant.h:15-33) and its
+// decode loop structure (llama.c:528-600); every numeric step is a launch into
+// the HIP layer (qhip.h).  The whole per-token sequence reads the token and the
+// position from device memory, so it is captured once into a HIP graph per
+// (model, KV cache) pair and replayed for every token.
+#define _POSIX_C_SOURCE 200809L
+#include "qllama.h"
+#include "qhip.h"
+
+#include <limits.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define LLMQ_MAGIC   0x514D4C4Cu   // llama.c:193
+#define LLMA_VERSION 2u            // llama.c:194
+
+static int pad16(int k) { return (k + 15) & ~15; }
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+static void die(const char *what) {
+  fprintf(stderr, "Error: %s: %s\n", what, qhip_last_error());
+  abort();
+}
+
+// ---------------------------------------------------------------------------
+// Device model state
+// ---------------------------------------------------------------------------
+typedef struct {
+  int vocab, dm, L, H, KVH, hd, dff, max_seq, qd, kvd, nqkv;
+  int kp_dm, kp_qd, kp_ff, kp_max;
+  float eps, rope_base, attn_scale;
+  uint8_t *blob;
+  // per layer (aliases into blob)
+  int8_t **wqkv, **wo, **wgu, **wd;
+  float **sqkv, **bqkv, **so, **sgu, **sd, **g_attn, **g_ffn;
+  int8_t *wte, *head;
+  float *wte_s, *head_s, *g_final;
+  float *rope_cos, *rope_sin;
+  // scratch
+  float *x, *qkv, *q, *o, *gu, *logits, *scores, *as;
+  int8_t *qa;
+  int *d_state;      // [0] pos, [1] fill_end
+  int *d_in;         // max_seq + 1 input tokens by position
+  int *d_out;        // max_seq argmax ids by position
+  int *h_stage;      // pinned staging, max_seq + 2 ints
+} QDev;
+
+typedef struct {
+  float *kbase, *vbase;
+  void *graph;
+  const void *graph_owner;
+} KVDev;
+
+static int config_valid(const int32_t *cfg) {
+  // Same acceptance rule as llama.c:371-386: positive bounded dims, whole GQA
+  // groups, 2-D element counts within int.
+  const long long MAXD = 1000000;
+  for (int i = 0; i < 8; i++)
+    if (cfg[i] <= 0 || cfg[i] > MAXD) return 0;
+  const long long vocab = cfg[0], dm = cfg[1], H = cfg[3], KVH = cfg[4], hd = cfg[5], ff = cfg[6];
+  if (H % KVH != 0) return 0;
+  if (H * hd > MAXD || KVH * hd > MAXD) return 0;
+  if (vocab * dm > INT_MAX || dm * ff > INT_MAX || H * hd * dm > INT_MAX) return 0;
+  return 1;
+}
+
+// Shapes the kernels of this build support (beyond the reference's own checks).
+static int config_supported(const int32_t *cfg) {
+  const int dm = cfg[1], hd = cfg[5], ff = cfg[6];
+  if (hd % 2 != 0 || hd > 512) return 0;
+  if (dm > 32768 || ff > 32768 || cfg[3] * hd > 32768) return 0;
+  return 1;
+}
+
+static Tensor dev_tensor(float *p, int n) {
+  Tensor t;
+  t.data = p; t.grad = NULL; t.ndim = 1; t.size = (size_t)n;
+  t.shape = (int*)malloc(sizeof(int));
+  if (t.shape) t.shape[0] = n;
+  return t;
+}
+
+static QTensor dev_qt(int8_t *q, float *s, int rows, int cols, int layout) {
+  QTensor t;
+  t.rows = rows; t.cols = cols; t.q = (signed char*)q; t.scale = s; t.layout = layout;
+  t.kpad = layout == QT_LAYOUT_NK ? pad16(rows) : cols;
+  return t;
+}
+
+static void qdev_free(QDev *d) {
+  if (!d) return;
+  qhip_free(d->blob);
+  qhip_host_free(d->h_stage);
+  free(d->wqkv); free(d->wo); free(d->wgu); free(d->wd);
+  free(d->sqkv); free(d->bqkv); free(d->so); free(d->sgu); free(d->sd);
+  free(d->g_attn); free(d->g_ffn);
+  free(d);
+}
+
+// Allocate one blob holding every weight and the scratch; fill the QLlamaModel
+// view (config ints, QTensor / Tensor device views).
+static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, float eps) {
+  memset(m, 0, sizeof *m);
+  if (qhip_init() != 0) {
+    fprintf(stderr, "Error: no usable GPU: %s\n", qhip_last_error());
+    return 1;
+  }
+  QDev *d = (QDev*)calloc(1, sizeof(QDev));
+  if (!d) return 1;
+  d->vocab = cfg[0]; d->dm = cfg[1]; d->L = cfg[2]; d->H = cfg[3]; d->KVH = cfg[4];
+  d->hd = cfg[5]; d->dff = cfg[6]; d->max_seq = cfg[7];
+  d->qd = d->H * d->hd; d->kvd = d->KVH * d->hd; d->nqkv = d->qd + 2 * d->kvd;
+  d->kp_dm = pad16(d->dm); d->kp_qd = pad16(d->qd); d->kp_ff = pad16(d->dff);
+  d->kp_max = d->kp_dm;
+  if (d->kp_qd > d->kp_max) d->kp_max = d->kp_qd;
+  if (d->kp_ff > d->kp_max) d->kp_max = d->kp_ff;
+  d->eps = eps; d->rope_base = rope_base;
+  d->attn_scale = 1.0f / sqrtf((float)d->hd);          // llama.c:532
+  const int L = d->L;
+  d->wqkv = calloc(L, sizeof(int8_t*)); d->wo = calloc(L, sizeof(int8_t*));
+  d->wgu = calloc(L, sizeof(int8_t*)); d->wd = calloc(L, sizeof(int8_t*));
+  d->sqkv = calloc(L, sizeof(float*)); d->bqkv = calloc(L, sizeof(float*));
+  d->so = calloc(L, sizeof(float*)); d->sgu = calloc(L, sizeof(float*));
+  d->sd = calloc(L, sizeof(float*)); d->g_attn = calloc(L, sizeof(float*));
+  d->g_ffn = calloc(L, sizeof(float*));
+  if (!d->wqkv || !d->wo || !d->wgu || !d->wd || !d->sqkv || !d->bqkv || !d->so || !d->sgu ||
+      !d->sd || !d->g_attn || !d->g_ffn) { qdev_free(d); return 1; }
+
+  // --- blob layout ---
+  size_t off = 0;
+#define TAKE(n) (off += al256(n), off - al256(n))
+  size_t *o_wqkv = calloc(L, sizeof(size_t)), *o_wo = calloc(L, sizeof(size_t));
+  size_t *o_wgu = calloc(L, sizeof(size_t)), *o_wd = calloc(L, sizeof(size_t));
+  size_t *o_s = calloc((size_t)L * 8, sizeof(size_t));
+  if (!o_wqkv || !o_wo || !o_wgu || !o_wd || !o_s) { qdev_free(d); return 1; }
+  for (int l = 0; l < L; l++) {
+    o_wqkv[l] = TAKE((size_t)d->nqkv * d->kp_dm);
+    o_wo[l] = TAKE((size_t)d->dm * d->kp_qd);
+    o_wgu[l] = TAKE((size_t)2 * d->dff * d->kp_dm);
+    o_wd[l] = TAKE((size_t)d->dm * d->kp_ff);
+    o_s[l * 8 + 0] = TAKE((size_t)d->nqkv * 4);
+    o_s[l * 8 + 1] = TAKE((size_t)d->nqkv * 4);
+    o_s[l * 8 + 2] = TAKE((size_t)d->dm * 4);
+    o_s[l * 8 + 3] = TAKE((size_t)2 * d->dff * 4);
+    o_s[l * 8 + 4] = TAKE((size_t)d->dm * 4);
+    o_s[l * 8 + 5] = TAKE((size_t)d->dm * 4);
+    o_s[l * 8 + 6] = TAKE((size_t)d->dm * 4);
+  }
+  size_t o_wte = TAKE((size_t)d->vocab * d->dm);
+  size_t o_wte_s = TAKE((size_t)d->dm * 4);
+  size_t o_head = TAKE((size_t)d->vocab * d->kp_dm);
+  size_t o_head_s = TAKE((size_t)d->vocab * 4);
+  size_t o_gf = TAKE((size_t)d->dm * 4);
+  const int half = d->hd / 2;
+  size_t o_cos = TAKE((size_t)d->max_seq * half * 4);
+  size_t o_sin = TAKE((size_t)d->max_seq * half * 4);
+  size_t o_x = TAKE((size_t)d->dm * 4);
+  size_t o_qkv = TAKE((size_t)d->nqkv * 4);
+  size_t o_q = TAKE((size_t)d->qd * 4);
+  size_t o_o = TAKE((size_t)d->qd * 4);
+  size_t o_gu = TAKE((size_t)2 * d->dff * 4);
+  size_t o_logits = TAKE((size_t)d->vocab * 4);
+  size_t o_scores = TAKE((size_t)d->H * d->max_seq * 4);
+  size_t o_as = TAKE(64);
+  size_t o_qa = TAKE((size_t)d->kp_max);
+  size_t o_state = TAKE(64);
+  size_t o_in = TAKE((size_t)(d->max_seq + 1) * 4);
+  size_t o_out = TAKE((size_t)(d->max_seq + 1) * 4);
+#undef TAKE
+  d->blob = (uint8_t*)qhip_malloc(off);
+  d->h_stage = (int*)qhip_host_alloc((size_t)(d->max_seq + 2) * sizeof(int));
+  if (!d->blob || !d->h_stage) {
+    fprintf(stderr, "Error: device allocation of %zu bytes failed: %s\n", off, qhip_last_error());
+    free(o_wqkv); free(o_wo); free(o_wgu); free(o_wd); free(o_s);
+    qdev_free(d);
+    return 1;
+  }
+  uint8_t *b = d->blob;
+  for (int l = 0; l < L; l++) {
+    d->wqkv[l] = (int8_t*)(b + o_wqkv[l]); d->wo[l] = (int8_t*)(b + o_wo[l]);
+    d->wgu[l] = (int8_t*)(b + o_wgu[l]); d->wd[l] = (int8_t*)(b + o_wd[l]);
+    d->sqkv[l] = (float*)(b + o_s[l * 8 + 0]); d->bqkv[l] = (float*)(b + o_s[l * 8 + 1]);
+    d->so[l] = (float*)(b + o_s[l * 8 + 2]); d->sgu[l] = (float*)(b + o_s[l * 8 + 3]);
+    d->sd[l] = (float*)(b + o_s[l * 8 + 4]); d->g_attn[l] = (float*)(b + o_s[l * 8 + 5]);
+    d->g_ffn[l] = (float*)(b + o_s[l * 8 + 6]);
+  }
+  free(o_wqkv); free(o_wo); free(o_wgu); free(o_wd); free(o_s);
+  d->wte = (int8_t*)(b + o_wte); d->wte_s = (float*)(b + o_wte_s);
+  d->head = (int8_t*)(b + o_head); d->head_s = (float*)(b + o_head_s);
+  d->g_final = (float*)(b + o_gf);
+  d->rope_cos = (float*)(b + o_cos); d->rope_sin = (float*)(b + o_sin);
+  d->x = (float*)(b + o_x); d->qkv = (float*)(b + o_qkv); d->q = (float*)(b + o_q);
+  d->o = (float*)(b + o_o); d->gu = (float*)(b + o_gu); d->logits = (float*)(b + o_logits);
+  d->scores = (float*)(b + o_scores); d->as = (float*)(b + o_as); d->qa = (int8_t*)(b + o_qa);
+  d->d_state = (int*)(b + o_state); d->d_in = (int*)(b + o_in); d->d_out = (int*)(b + o_out);
+  if (qhip_fill_zero(d->qa, (size_t)d->kp_max) || qhip_fill_zero(d->d_in, (size_t)(d->max_seq + 1) * 4) ||
+      qhip_fill_zero(d->d_state, 64)) {
+    qdev_free(d);
+    return 1;
+  }
+
+  // --- RoPE tables: the expressions of rope.c:58-61, evaluated on the host with
+  // the same libm, so the device reads bit-identical cos/sin values.
+  float *ct = (float*)malloc((size_t)d->max_seq * half * sizeof(float));
+  float *st = (float*)malloc((size_t)d->max_seq * half * sizeof(float));
+  if (!ct || !st) { free(ct); free(st); qdev_free(d); return 1; }
+  for (int pos = 0; pos < d->max_seq; pos++) {
+    for (int k = 0; k < half; k++) {
+      float inv_freq = powf(rope_base, -2.0f * (float)k / (float)d->hd);
+      float ang = (float)pos * inv_freq;
+      float c = cosf(ang), s = sinf(ang);
+      ct[(size_t)pos * half + k] = c;
+      st[(size_t)pos * half + k] = s;
+    }
+  }
+  int rc = qhip_h2d(d->rope_cos, ct, (size_t)d->max_seq * half * 4) |
+           qhip_h2d(d->rope_sin, st, (size_t)d->max_seq * half * 4);
+  free(ct); free(st);
+  if (rc) { qdev_free(d); return 1; }
+
+  // --- API view ---
+  m->vocab = d->vocab; m->d_model = d->dm; m->n_layers = L; m->n_heads = d->H;
+  m->n_kv = d->KVH; m->head_dim = d->hd; m->d_ff = d->dff; m->max_seq = d->max_seq;
+  m->rope_base = rope_base; m->eps = eps;
+  m->wte = dev_qt(d->wte, d->wte_s, d->vocab, d->dm, QT_LAYOUT_KN);
+  m->lm_head = dev_qt(d->head, d->head_s, d->dm, d->vocab, QT_LAYOUT_NK);
+  m->final_norm = dev_tensor(d->g_final, d->dm);
+  m->blocks = (QLlamaBlock*)calloc((size_t)L, sizeof(QLlamaBlock));
+  if (!m->blocks) { qdev_free(d); return 1; }
+  for (int l = 0; l < L; l++) {
+    QLlamaBlock *bl = &m->blocks[l];
+    bl->attn_norm = dev_tensor(d->g_attn[l], d->dm);
+    bl->ffn_norm = dev_tensor(d->g_ffn[l], d->dm);
+    bl->b_q = dev_tensor(d->bqkv[l], d->qd);
+    bl->b_k = dev_tensor(d->bqkv[l] + d->qd, d->kvd);
+    bl->b_v = dev_tensor(d->bqkv[l] + d->qd + d->kvd, d->kvd);
+    bl->Wq = dev_qt(d->wqkv[l], d->sqkv[l], d->dm, d->qd, QT_LAYOUT_NK);
+    bl->Wk = dev_qt(d->wqkv[l] + (size_t)d->qd * d->kp_dm, d->sqkv[l] + d->qd, d->dm, d->kvd, QT_LAYOUT_NK);
+    bl->Wv = dev_qt(d->wqkv[l] + (size_t)(d->qd + d->kvd) * d->kp_dm, d->sqkv[l] + d->qd + d->kvd,
+                    d->dm, d->kvd, QT_LAYOUT_NK);
+    bl->Wo = dev_qt(d->wo[l], d->so[l], d->qd, d->dm, QT_LAYOUT_NK);
+    bl->Wgate = dev_qt(d->wgu[l], d->sgu[l], d->dm, d->dff, QT_LAYOUT_NK);
+    bl->Wup = dev_qt(d->wgu[l] + (size_t)d->dff * d->kp_dm, d->sgu[l] + d->dff, d->dm, d->dff, QT_LAYOUT_NK);
+    bl->Wdown = dev_qt(d->wd[l], d->sd[l], d->dff, d->dm, QT_LAYOUT_NK);
+  }
+  m->dev = d;
+  return 0;
+}
+
+static void free_view(QLlamaModel *m) {
+  if (m->blocks) {
+    for (int l = 0; l < m->n_layers; l++) {
+      QLlamaBlock *b = &m->blocks[l];
+      free(b->attn_norm.shape); free(b->ffn_norm.shape);
+      free(b->b_q.shape); free(b->b_k.shape); free(b->b_v.shape);
+    }
+  }
+  free(m->blocks); m->blocks = NULL;
+  free(m->final_norm.shape); m->final_norm.shape = NULL;
+}
+
+void q_llama_model_free(QLlamaModel *m) {
+  if (!m) return;
+  if (m->dev) qhip_sync();
+  free_view(m);
+  qdev_free((QDev*)m->dev);
+  m->dev = NULL;
+}
+
+// Norm gains 1, biases 0 (the seeded models and any freshly loaded layer start so).
+static int init_vectors(QDev *d) {
+  for (int l = 0; l < d->L; l++) {
+    if (qhip_fill_f32(d->g_attn[l], (size_t)d->dm, 1.0f) || qhip_fill_f32(d->g_ffn[l], (size_t)d->dm, 1.0f) ||
+        qhip_fill_f32(d->bqkv[l], (size_t)d->nqkv, 0.0f)) return 1;
+  }
+  return qhip_fill_f32(d->g_final, (size_t)d->dm, 1.0f);
+}
+
+int q_llama_model_synth(QLlamaModel *out, const int32_t cfg[8], float rope_base, float eps,
+                        uint64_t seed, int tied) {
+  if (!config_valid(cfg) || !config_supported(cfg)) {
+    fprintf(stderr, "Error: invalid/unsupported config\n");
+    return 1;
+  }
+  if (model_alloc(out, cfg, rope_base, eps)) return 1;
+  QDev *d = (QDev*)out->dev;
+  int rc = init_vectors(d);
+  rc |= qhip_synth_quant_kn(seed, 0, d->vocab, d->dm, 0.02, d->wte, d->wte_s);
+  for (int l = 0; l < d->L && !rc; l++) {
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    const int kp = d->kp_dm;
+    rc |= qhip_synth_quant_nk(seed, t0 + 1, d->dm, d->qd, kp, 0, 0.02, d->wqkv[l], d->sqkv[l]);
+    rc |= qhip_synth_quant_nk(seed, t0 + 2, d->dm, d->kvd, kp, 0, 0.02,
+                              d->wqkv[l] + (size_t)d->qd * kp, d->sqkv[l] + d->qd);
+    rc |= qhip_synth_quant_nk(seed, t0 + 3, d->dm, d->kvd, kp, 0, 0.02,
+                              d->wqkv[l] + (size_t)(d->qd + d->kvd) * kp, d->sqkv[l] + d->qd + d->kvd);
+    rc |= qhip_synth_quant_nk(seed, t0 + 7, d->qd, d->dm, d->kp_qd, 0, 0.02, d->wo[l], d->so[l]);
+    rc |= qhip_synth_quant_nk(seed, t0 + 9, d->dm, d->dff, kp, 0, 0.02, d->wgu[l], d->sgu[l]);
+    rc |= qhip_synth_quant_nk(seed, t0 + 10, d->dm, d->dff, kp, 0, 0.02,
+                              d->wgu[l] + (size_t)d->dff * kp, d->sgu[l] + d->dff);
+    rc |= qhip_synth_quant_nk(seed, t0 + 11, d->dff, d->dm, d->kp_ff, 0, 0.02, d->wd[l], d->sd[l]);
+  }
+  if (!rc) {
+    if (tied) rc = qhip_synth_quant_nk(seed, 0, d->dm, d->vocab, d->kp_dm, 1, 0.02, d->head, d->head_s);
+    else rc = qhip_synth_quant_nk(seed, 2 + 12 * (uint64_t)d->L, d->dm, d->vocab, d->kp_dm, 0, 0.02,
+                                  d->head, d->head_s);
+  }
+  if (!rc) rc = qhip_sync();
+  if (rc) {
+    fprintf(stderr, "Error: synthetic model build failed: %s\n", qhip_last_error());
+    q_llama_model_free(out);
+    return 1;
+  }
+  return 0;
+}
+
+// Digest of one tensor: the same combination the generator's CPU side uses.
+static int qt_digest(const QTensor *t, uint64_t salt, uint64_t *h) {
+  uint64_t a = 0, s = 0;
+  if (qhip_hash_i8((const int8_t*)t->q, t->rows, t->cols, t->layout == QT_LAYOUT_NK, t->kpad, salt, &a)) return 1;
+  if (qhip_hash_f32(t->scale, (size_t)t->cols, salt ^ 0x5CA1E5ULL, &s)) return 1;
+  *h = a * 3 + s;
+  return 0;
+}
+
+uint64_t q_llama_model_hash(const QLlamaModel *m) {
+  uint64_t h = 0, t = 0;
+  if (qt_digest(&m->wte, 0, &h)) die("model hash");
+  for (int l = 0; l < m->n_layers; l++) {
+    const QLlamaBlock *b = &m->blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    const QTensor *list[7] = {&b->Wq, &b->Wk, &b->Wv, &b->Wo, &b->Wgate, &b->Wup, &b->Wdown};
+    const int off[7] = {1, 2, 3, 7, 9, 10, 11};
+    for (int i = 0; i < 7; i++) {
+      if (qt_digest(list[i], t0 + (uint64_t)off[i], &t)) die("model hash");
+      h = h * 31 + t;
+    }
+  }
+  if (qt_digest(&m->lm_head, 2 + 12 * (uint64_t)m->n_layers, &t)) die("model hash");
+  return h * 31 + t;
+}
+
+// ---------------------------------------------------------------------------
+// Loading: LLMQ v2 (llama.c:603-657 byte order)
+// ---------------------------------------------------------------------------
+// Read one int8 tensor (cols f32 scales, then rows*cols int8 row-major) into the
+// device, in the requested layout.
+static int read_q(FILE *f, int rows, int cols, int layout_nk, int kpad, int8_t *dq, float *ds,
+                  void *stage, void *dtmp) {
+  float *sc = (float*)stage;
+  if (fread(sc, sizeof(float), (size_t)cols, f) != (size_t)cols) return 1;
+  if (qhip_h2d(ds, sc, (size_t)cols * 4)) return 2;
+  const size_t n = (size_t)rows * cols;
+  int8_t *dst = layout_nk ? (int8_t*)dtmp : dq;
+  // stream the int8 body through the staging buffer
+  const size_t chunk = (size_t)64 << 20;
+  for (size_t o = 0; o < n; o += chunk) {
+    size_t c = n - o < chunk ? n - o : chunk;
+    if (fread(stage, 1, c, f) != c) return 1;
+    if (qhip_h2d(dst + o, stage, c)) return 2;
+  }
+  if (layout_nk && qhip_transpose_kn_to_nk((const int8_t*)dtmp, rows, cols, kpad, dq)) return 2;
+  return 0;
+}
+
+static int read_f(FILE *f, float *dst, int n, void *stage) {
+  if (fread(stage, sizeof(float), (size_t)n, f) != (size_t)n) return 1;
+  return qhip_h2d(dst, stage, (size_t)n * 4) ? 2 : 0;
+}
+
+int q_llama_model_load(const char *path, QLlamaModel *out) {
+  FILE *f = fopen(path, "rb");
+  if (!f) { fprintf(stderr, "Error: cannot open '%s' for reading\n", path); return 1; }
+  uint32_t header[2];
+  int32_t cfg[8];
+  float fcfg[2];
+  if (fread(header, sizeof(uint32_t), 2, f) != 2 || fread(cfg, sizeof(int32_t), 8, f) != 8 ||
+      fread(fcfg, sizeof(float), 2, f) != 2) {
+    fprintf(stderr, "Error: '%s' is truncated (bad header)\n", path);
+    fclose(f); return 1;
+  }
+  if (header[0] != LLMQ_MAGIC || header[1] != LLMA_VERSION) {
+    fprintf(stderr, "Error: '%s' is not a v%u int8 LLMQ checkpoint\n", path, LLMA_VERSION);
+    fclose(f); return 1;
+  }
+  if (!config_valid(cfg)) {
+    fprintf(stderr, "Error: '%s' has an invalid/unsupported config\n", path);
+    fclose(f); return 1;
+  }
+  if (!config_supported(cfg)) {
+    fprintf(stderr, "Error: '%s' has a config this GPU build does not support\n", path);
+    fclose(f); return 1;
+  }
+  if (model_alloc(out, cfg, fcfg[0], fcfg[1])) { fclose(f); return 1; }
+  QDev *d = (QDev*)out->dev;
+  size_t big = (size_t)d->vocab * d->dm;
+  if ((size_t)d->dm * d->dff > big) big = (size_t)d->dm * d->dff;
+  if ((size_t)d->qd * d->dm > big) big = (size_t)d->qd * d->dm;
+  const size_t stage_n = (size_t)64 << 20;
+  void *stage = malloc(stage_n > (size_t)d->vocab * 4 ? stage_n : (size_t)d->vocab * 4);
+  void *dtmp = qhip_malloc(big);
+  int rc = (!stage || !dtmp) ? 2 : 0;
+  const int kp = d->kp_dm;
+  if (!rc) rc = read_q(f, d->vocab, d->dm, 0, d->dm, d->wte, d->wte_s, stage, dtmp);
+  for (int l = 0; l < d->L && !rc; l++) {
+    rc = read_f(f, d->g_attn[l], d->dm, stage);
+    if (!rc) rc = read_q(f, d->dm, d->qd, 1, kp, d->wqkv[l], d->sqkv[l], stage, dtmp);
+    if (!rc) rc = read_q(f, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)d->qd * kp, d->sqkv[l] + d->qd, stage, dtmp);
+    if (!rc) rc = read_q(f, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)(d->qd + d->kvd) * kp,
+                         d->sqkv[l] + d->qd + d->kvd, stage, dtmp);
+    if (!rc) rc = read_f(f, d->bqkv[l], d->qd, stage);
+    if (!rc) rc = read_f(f, d->bqkv[l] + d->qd, d->kvd, stage);
+    if (!rc) rc = read_f(f, d->bqkv[l] + d->qd + d->kvd, d->kvd, stage);
+    if (!rc) rc = read_q(f, d->qd, d->dm, 1, d->kp_qd, d->wo[l], d->so[l], stage, dtmp);
+    if (!rc) rc = read_f(f, d->g_ffn[l], d->dm, stage);
+    if (!rc) rc = read_q(f, d->dm, d->dff, 1, kp, d->wgu[l], d->sgu[l], stage, dtmp);
+    if (!rc) rc = read_q(f, d->dm, d->dff, 1, kp, d->wgu[l] + (size_t)d->dff * kp, d->sgu[l] + d->dff, stage, dtmp);
+    if (!rc) rc = read_q(f, d->dff, d->dm, 1, d->kp_ff, d->wd[l], d->sd[l], stage, dtmp);
+  }
+  if (!rc) rc = read_f(f, d->g_final, d->dm, stage);
+  if (!rc) rc = read_q(f, d->dm, d->vocab, 1, kp, d->head, d->head_s, stage, dtmp);
+  if (!rc && qhip_sync()) rc = 2;
+  fclose(f);
+  free(stage);
+  qhip_free(dtmp);
+  if (rc) {
+    if (rc == 1) fprintf(stderr, "Error: '%s' is truncated (bad weights)\n", path);
+    else fprintf(stderr, "Error: device upload of '%s' failed: %s\n", path, qhip_last_error());
+    q_llama_model_free(out);
+    return 1;
+  }
+  return 0;
+}
+
+// llama.c:490-511 on the device: each 2-D weight is uploaded in f32 and
+// quantized per output column there; norms and biases are copied as f32.
+QLlamaModel q_llama_quantize_from(const LlamaModel *s) {
+  QLlamaModel m;
+  int32_t cfg[8] = {s->vocab, s->d_model, s->n_layers, s->n_heads, s->n_kv, s->head_dim, s->d_ff, s->max_seq};
+  if (!config_valid(cfg) || !config_supported(cfg)) {
+    fprintf(stderr, "Error: q_llama_quantize_from: invalid/unsupported config\n");
+    abort();
+  }
+  if (model_alloc(&m, cfg, s->rope_base, s->eps)) die("q_llama_quantize_from");
+  QDev *d = (QDev*)m.dev;
+  size_t big = (size_t)d->vocab * d->dm;
+  if ((size_t)d->dm * d->dff > big) big = (size_t)d->dm * d->dff;
+  if ((size_t)d->qd * d->dm > big) big = (size_t)d->qd * d->dm;
+  float *dw = (float*)qhip_malloc(big * 4);
+  if (!dw) die("q_llama_quantize_from");
+#define QUANT(src, rows, cols, nk, kpad, q, sc) \
+  do { if (qhip_h2d(dw, (src)->data, (size_t)(rows) * (cols) * 4) || \
+           qhip_quantize_percol(dw, rows, cols, nk, kpad, q, sc)) die("q_llama_quantize_from"); } while (0)
+#define COPYF(dst, src, n) do { if (qhip_h2d(dst, (src)->data, (size_t)(n) * 4)) die("q_llama_quantize_from"); } while (0)
+  const int kp = d->kp_dm;
+  QUANT(&s->wte, d->vocab, d->dm, 0, d->dm, d->wte, d->wte_s);
+  for (int l = 0; l < d->L; l++) {
+    const LlamaBlock *a = &s->blocks[l];
+    COPYF(d->g_attn[l], &a->attn_norm, d->dm);
+    COPYF(d->g_ffn[l], &a->ffn_norm, d->dm);
+    COPYF(d->bqkv[l], &a->b_q, d->qd);
+    COPYF(d->bqkv[l] + d->qd, &a->b_k, d->kvd);
+    COPYF(d->bqkv[l] + d->qd + d->kvd, &a->b_v, d->kvd);
+    QUANT(&a->Wq, d->dm, d->qd, 1, kp, d->wqkv[l], d->sqkv[l]);
+    QUANT(&a->Wk, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)d->qd * kp, d->sqkv[l] + d->qd);
+    QUANT(&a->Wv, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)(d->qd + d->kvd) * kp, d->sqkv[l] + d->qd + d->kvd);
+    QUANT(&a->Wo, d->qd, d->dm, 1, d->kp_qd, d->wo[l], d->so[l]);
+    QUANT(&a->Wgate, d->dm, d->dff, 1, kp, d->wgu[l], d->sgu[l]);
+    QUANT(&a->Wup, d->dm, d->dff, 1, kp, d->wgu[l] + (size_t)d->dff * kp, d->sgu[l] + d->dff);
+    QUANT(&a->Wdown, d->dff, d->dm, 1, d->kp_ff, d->wd[l], d->sd[l]);
+  }
+  COPYF(d->g_final, &s->final_norm, d->dm);
+  QUANT(&s->lm_head, d->dm, d->vocab, 1, kp, d->head, d->head_s);
+#undef QUANT
+#undef COPYF
+  if (qhip_sync()) die("q_llama_quantize_from");
+  qhip_free(dw);
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// KV cache and decode
+// ---------------------------------------------------------------------------
+LlamaKV q_llama_kv_create(const QLlamaModel *m) {
+  LlamaKV kv;
+  memset(&kv, 0, sizeof kv);
+  const QDev *d = (const QDev*)m->dev;
+  kv.n_layers = m->n_layers; kv.max_seq = m->max_seq; kv.kv_dim = m->n_kv * m->head_dim; kv.len = 0;
+  KVDev *kd = (KVDev*)calloc(1, sizeof(KVDev));
+  kv.k = (float**)malloc((size_t)m->n_layers * sizeof(float*));
+  kv.v = (float**)malloc((size_t)m->n_layers * sizeof(float*));
+  const size_t per = (size_t)m->max_seq * kv.kv_dim;
+  if (!d || !kd || !kv.k || !kv.v) { fprintf(stderr, "Error: out of memory (kv)\n"); abort(); }
+  kd->kbase = (float*)qhip_malloc((size_t)m->n_layers * per * 4);
+  kd->vbase = (float*)qhip_malloc((size_t)m->n_layers * per * 4);
+  if (!kd->kbase || !kd->vbase) die("q_llama_kv_create");
+  for (int l = 0; l < m->n_layers; l++) { kv.k[l] = kd->kbase + (size_t)l * per; kv.v[l] = kd->vbase + (size_t)l * per; }
+  kv.dev = kd;
+  return kv;
+}
+
+void llama_kv_free(LlamaKV *kv) {
+  KVDev *kd = (KVDev*)kv->dev;
+  if (kd) {
+    qhip_sync();
+    if (kd->graph) qhip_graph_destroy(kd->graph);
+    qhip_free(kd->kbase); qhip_free(kd->vbase);
+    free(kd);
+  } else if (kv->k && kv->v) {
+    for (int l = 0; l < kv->n_layers; l++) { free(kv->k[l]); free(kv->v[l]); }
+  }
+  free(kv->k); free(kv->v);
+  kv->k = kv->v = NULL;
+  kv->dev = NULL;
+}
+
+// Enqueue one token's work (llama.c:534-594): token at d_in[pos], pos = d_state[0].
+static int enqueue_step(const QDev *d, const KVDev *kd) {
+  const int *dpos = &d->d_state[0];
+  const size_t per = (size_t)d->max_seq * d->kvd;
+  int rc = qhip_embed(d->wte, d->wte_s, d->dm, d->d_in, d->d_state, d->x);
+  for (int l = 0; l < d->L && !rc; l++) {
+    float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
+    rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
+    rc |= qhip_gemv(d->qa, d->as, 1, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], 0, 2);
+    rc |= qhip_rope_append(d->qkv, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, dpos, d->q, kc, vc, d->max_seq);
+    rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o);
+    rc |= qhip_quant_rows(d->o, 1, d->qd, d->qa, d->kp_qd, d->as);
+    rc |= qhip_gemv(d->qa, d->as, 1, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, 1, 6);
+    rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
+    rc |= qhip_gemv(d->qa, d->as, 1, d->wgu[l], d->sgu[l], 2 * d->dff, d->kp_dm, d->gu, NULL, 0, 7);
+    rc |= qhip_swiglu_quant(d->gu, 1, d->dff, d->qa, d->kp_ff, d->as);
+    rc |= qhip_gemv(d->qa, d->as, 1, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, 1, 9);
+  }
+  if (!rc) rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_final, d->eps, d->qa, d->kp_dm, d->as);
+  if (!rc) rc |= qhip_gemv(d->qa, d->as, 1, d->head, d->head_s, d->vocab, d->kp_dm, d->logits, NULL, 0, 10);
+  if (!rc) rc |= qhip_argmax_advance(d->logits, d->vocab, d->d_in, d->d_state, d->d_out, d->max_seq);
+  return rc;
+}
+
+static int profiling = 0;
+
+// Run `n` steps: a graph replay each, or eager launches while profiling.
+static int run_steps(const QDev *d, KVDev *kd, int n) {
+  if (profiling) {
+    for (int i = 0; i < n; i++) if (enqueue_step(d, kd)) return 1;
+    return 0;
+  }
+  if (!kd->graph || kd->graph_owner != (const void*)d) {
+    if (kd->graph) { qhip_graph_destroy(kd->graph); kd->graph = NULL; }
+    if (qhip_capture_begin()) return 1;
+    int rc = enqueue_step(d, kd);
+    void *g = NULL;
+    if (qhip_capture_end(&g) || rc) return 1;
+    kd->graph = g;
+    kd->graph_owner = d;
+  }
+  for (int i = 0; i < n; i++) if (qhip_graph_launch(kd->graph)) return 1;
+  return 0;
+}
+
+// Stage tokens ids[0..n) at positions pos..pos+n-1 and set (pos, fill_end).
+static int stage_inputs(const QDev *d, int pos, const int *ids, int n) {
+  int *h = d->h_stage;
+  h[0] = pos; h[1] = pos + n;
+  if (qhip_h2d_async(d->d_state, h, 2 * sizeof(int))) return 1;
+  memcpy(h + 2, ids, (size_t)n * sizeof(int));
+  return qhip_h2d_async(d->d_in + pos, h + 2, (size_t)n * sizeof(int));
+}
+
+// Host-side guards before any device work: the positions pos .. pos+n-1 must fit
+// the cache (the reference leaves this to its callers, main.c:663,804) and the
+// n_ids staged token ids must be in range (main.c:568 skips bad ids).
+static void check_step(const QLlamaModel *m, const LlamaKV *kv, const int *ids, int n_ids, int n_pos,
+                       const char *who) {
+  if (!m || !m->dev || !kv || !kv->dev) { fprintf(stderr, "Error: %s: model or cache not on the GPU\n", who); abort(); }
+  if (kv->len < 0 || n_pos < 0 || (long long)kv->len + n_pos > m->max_seq) {
+    fprintf(stderr, "Error: %s: position %d + %d exceeds max_seq %d\n", who, kv->len, n_pos, m->max_seq);
+    abort();
+  }
+  for (int i = 0; i < n_ids; i++)
+    if (ids[i] < 0 || ids[i] >= m->vocab) {
+      fprintf(stderr, "Error: %s: token id %d out of range (vocab %d)\n", who, ids[i], m->vocab);
+      abort();
+    }
+}
+
+void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *logits) {
+  check_step(m, kv, &token, 1, 1, "q_llama_decode_step");
+  const QDev *d = (const QDev*)m->dev;
+  KVDev *kd = (KVDev*)kv->dev;
+  if (stage_inputs(d, kv->len, &token, 1) || run_steps(d, kd, 1) ||
+      qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4) || qhip_sync())
+    die("q_llama_decode_step");
+  kv->len += 1;
+}
+
+int q_llama_prefill(const QLlamaModel *m, LlamaKV *kv, const int *ids, int n, Tensor *logits) {
+  if (n <= 0) return 0;
+  check_step(m, kv, ids, n, n, "q_llama_prefill");
+  const QDev *d = (const QDev*)m->dev;
+  KVDev *kd = (KVDev*)kv->dev;
+  if (stage_inputs(d, kv->len, ids, n) || run_steps(d, kd, n)) return 1;
+  if (logits && qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4)) return 1;
+  if (qhip_sync()) return 1;
+  kv->len += n;
+  return 0;
+}
+
+int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_steps, int *out) {
+  if (n_steps <= 0) return 0;
+  check_step(m, kv, &token, 1, n_steps, "q_llama_generate_greedy");
+  const QDev *d = (const QDev*)m->dev;
+  KVDev *kd = (KVDev*)kv->dev;
+  const int pos = kv->len;
+  if (stage_inputs(d, pos, &token, 1) || run_steps(d, kd, n_steps)) return 1;
+  if (out && qhip_d2h_async(d->h_stage, d->d_out + pos, (size_t)n_steps * sizeof(int))) return 1;
+  if (qhip_sync()) return 1;
+  if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
+  kv->len += n_steps;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// quant.h API on device QTensors
+// ---------------------------------------------------------------------------
+QTensor qtensor_create(int rows, int cols) {
+  QTensor t;
+  memset(&t, 0, sizeof t);
+  if (qhip_init()) die("qtensor_create");
+  t.rows = rows; t.cols = cols; t.layout = QT_LAYOUT_NK; t.kpad = pad16(rows);
+  t.q = (signed char*)qhip_malloc((size_t)cols * t.kpad);
+  t.scale = (float*)qhip_malloc((size_t)cols * 4);
+  if (!t.q || !t.scale || qhip_fill_zero(t.q, (size_t)cols * t.kpad)) die("qtensor_create");
+  return t;
+}
+
+void qtensor_free(QTensor *t) {
+  qhip_sync();
+  qhip_free(t->q); qhip_free(t->scale);
+  t->q = NULL; t->scale = NULL;
+}
+
+void qtensor_quantize(QTensor *t, const float *w) {
+  const size_t n = (size_t)t->rows * t->cols;
+  float *dw = (float*)qhip_malloc(n * 4);
+  if (!dw || qhip_h2d(dw, w, n * 4) ||
+      qhip_quantize_percol(dw, t->rows, t->cols, t->layout == QT_LAYOUT_NK, t->kpad, (int8_t*)t->q, t->scale) ||
+      qhip_sync())
+    die("qtensor_quantize");
+  qhip_free(dw);
+}
+
+void qmatmul(const Tensor *A, const QTensor *W, Tensor *C) {
+  const int M = A->shape[0], K = W->rows, N = W->cols;
+  const int kp = pad16(K);
+  if (qhip_init()) die("qmatmul");
+  float *da = (float*)qhip_malloc((size_t)M * K * 4);
+  float *dc = (float*)qhip_malloc((size_t)M * N * 4);
+  int8_t *qa = (int8_t*)qhip_malloc((size_t)M * kp);
+  float *as = (float*)qhip_malloc((size_t)M * 4);
+  int8_t *wnk = (int8_t*)W->q;
+  int8_t *tmp = NULL;
+  if (!da || !dc || !qa || !as) die("qmatmul");
+  if (W->layout != QT_LAYOUT_NK) {     // row-major device tensor: re-lay it once
+    tmp = (int8_t*)qhip_malloc((size_t)N * kp);
+    if (!tmp || qhip_fill_zero(tmp, (size_t)N * kp) ||
+        qhip_transpose_kn_to_nk((const int8_t*)W->q, K, N, kp, tmp)) die("qmatmul");
+    wnk = tmp;
+  }
+  if (qhip_h2d(da, A->data, (size_t)M * K * 4) || qhip_fill_zero(qa, (size_t)M * kp) ||
+      qhip_quant_rows(da, M, K, qa, kp, as) ||
+      qhip_gemv(qa, as, M, wnk, W->scale, N, kp, dc, NULL, 0, 12) ||
+      qhip_d2h_async(C->data, dc, (size_t)M * N * 4) || qhip_sync())
+    die("qmatmul");
+  qhip_free(da); qhip_free(dc); qhip_free(qa); qhip_free(as); qhip_free(tmp);
+}
+
+void quantize_int8_percol(const float *w, int rows, int cols, signed char *q, float *scale) {
+  const size_t n = (size_t)rows * cols;
+  if (qhip_init()) die("quantize_int8_percol");
+  float *dw = (float*)qhip_malloc(n * 4);
+  int8_t *dq = (int8_t*)qhip_malloc(n);
+  float *ds = (float*)qhip_malloc((size_t)cols * 4);
+  if (!dw || !dq || !ds || qhip_h2d(dw, w, n * 4) ||
+      qhip_quantize_percol(dw, rows, cols, 0, cols, dq, ds) ||
+      qhip_d2h_async(q, dq, n) || qhip_d2h_async(scale, ds, (size_t)cols * 4) || qhip_sync())
+    die("quantize_int8_percol");
+  qhip_free(dw); qhip_free(dq); qhip_free(ds);
+}
+
+void dequantize_int8_percol(const signed char *q, const float *scale, int rows, int cols, float *w) {
+  const size_t n = (size_t)rows * cols;
+  if (qhip_init()) die("dequantize_int8_percol");
+  float *dw = (float*)qhip_malloc(n * 4);
+  int8_t *dq = (int8_t*)qhip_malloc(n);
+  float *ds = (float*)qhip_malloc((size_t)cols * 4);
+  if (!dw || !dq || !ds || qhip_h2d(dq, q, n) || qhip_h2d(ds, scale, (size_t)cols * 4) ||
+      qhip_dequantize_kn(dq, ds, rows, cols, dw) || qhip_d2h_async(w, dw, n * 4) || qhip_sync())
+    die("dequantize_int8_percol");
+  qhip_free(dw); qhip_free(dq); qhip_free(ds);
+}
+
+void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, int32_t *acc) {
+  if (qhip_init()) die("qacc_columns");
+  int8_t *da = (int8_t*)qhip_malloc((size_t)K);
+  int8_t *dw = (int8_t*)qhip_malloc((size_t)K * N);
+  int32_t *dacc = (int32_t*)qhip_malloc((size_t)N * 4);
+  if (!da || !dw || !dacc || qhip_h2d(da, qa, (size_t)K) || qhip_h2d(dw, qw, (size_t)K * N) ||
+      qhip_qacc_kn(da, dw, K, N, dacc) || qhip_d2h_async(acc, dacc, (size_t)N * 4) || qhip_sync())
+    die("qacc_columns");
+  qhip_free(da); qhip_free(dw); qhip_free(dacc);
+}
+
+int q_llama_tensor_export(const QTensor *t, signed char *q_host, float *scale_host) {
+  const size_t n = (size_t)t->rows * t->cols;
+  if (qhip_init()) return 1;
+  if (t->layout == QT_LAYOUT_KN) {
+    if (qhip_d2h(q_host, t->q, n)) return 1;
+  } else {
+    int8_t *tmp = (int8_t*)qhip_malloc(n);
+    if (!tmp) return 1;
+    int rc = qhip_nk_to_kn((const int8_t*)t->q, t->rows, t->cols, t->kpad, tmp) || qhip_d2h(q_host, tmp, n);
+    qhip_free(tmp);
+    if (rc) return 1;
+  }
+  return qhip_d2h(scale_host, t->scale, (size_t)t->cols * 4);
+}
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+int qllama_device_count(void) { return qhip_device_count(); }
+int qllama_device_sync(void) { return qhip_device_sync(); }
+int qllama_sync(void) { return qhip_sync(); }
+void *qllama_stream(void) { return qhip_init() ? NULL : qhip_stream(); }
+int qllama_profile(int enable) { profiling = enable ? 1 : 0; return qhip_profile_enable(enable); }
+int qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max) {
+  return qhip_profile_read(names, names_len, ms, count, max);
+}

@@ -1,0 +1,254 @@
+"""Python host mirror of include/qllama.h (ctypes), for tests and the benchmark.
+
+Loads the in-tree libqllama.so built by llm-project_amd/Makefile and raises if
+it is missing: there is no CPU fallback.  Mirrors the reference's quantized API
+(llama.h:114-140, quant.h:15-33) with numpy arrays standing in for host Tensors.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqllama.so")
+
+QT_LAYOUT_NK = 0
+QT_LAYOUT_KN = 1
+
+
+class Tensor(C.Structure):
+    _fields_ = [("data", C.POINTER(C.c_float)), ("grad", C.POINTER(C.c_float)),
+                ("shape", C.POINTER(C.c_int)), ("ndim", C.c_int), ("size", C.c_size_t)]
+
+
+class QTensor(C.Structure):
+    _fields_ = [("rows", C.c_int), ("cols", C.c_int), ("q", C.c_void_p), ("scale", C.c_void_p),
+                ("layout", C.c_int), ("kpad", C.c_int)]
+
+
+class LlamaBlock(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_heads", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("d_ff", C.c_int), ("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n, Tensor) for n in ("attn_norm", "Wq", "Wk", "Wv", "b_q", "b_k", "b_v", "Wo",
+                                      "ffn_norm", "Wgate", "Wup", "Wdown")]
+
+
+class LlamaModel(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "d_model", "n_layers", "n_heads", "n_kv", "head_dim",
+                                       "d_ff", "max_seq")] + \
+               [("rope_base", C.c_float), ("eps", C.c_float), ("wte", Tensor),
+                ("blocks", C.POINTER(LlamaBlock)), ("final_norm", Tensor), ("lm_head", Tensor)]
+
+
+class LlamaKV(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("max_seq", C.c_int), ("kv_dim", C.c_int), ("len", C.c_int),
+                ("k", C.POINTER(C.c_void_p)), ("v", C.POINTER(C.c_void_p)), ("dev", C.c_void_p)]
+
+
+class QLlamaBlock(C.Structure):
+    _fields_ = [("attn_norm", Tensor), ("ffn_norm", Tensor), ("b_q", Tensor), ("b_k", Tensor),
+                ("b_v", Tensor)] + [(n, QTensor) for n in ("Wq", "Wk", "Wv", "Wo", "Wgate", "Wup", "Wdown")]
+
+
+class QLlamaModel(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "d_model", "n_layers", "n_heads", "n_kv", "head_dim",
+                                       "d_ff", "max_seq")] + \
+               [("rope_base", C.c_float), ("eps", C.c_float), ("wte", QTensor),
+                ("blocks", C.POINTER(QLlamaBlock)), ("final_norm", Tensor), ("lm_head", QTensor),
+                ("dev", C.c_void_p)]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libqllama.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C llm-project_amd` "
+                               "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        P = C.POINTER
+        L.q_llama_model_load.argtypes = [C.c_char_p, P(QLlamaModel)]
+        L.q_llama_model_free.argtypes = [P(QLlamaModel)]
+        L.q_llama_quantize_from.argtypes = [P(LlamaModel)]
+        L.q_llama_quantize_from.restype = QLlamaModel
+        L.q_llama_kv_create.argtypes = [P(QLlamaModel)]
+        L.q_llama_kv_create.restype = LlamaKV
+        L.llama_kv_free.argtypes = [P(LlamaKV)]
+        L.q_llama_decode_step.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, P(Tensor)]
+        L.q_llama_prefill.argtypes = [P(QLlamaModel), P(LlamaKV), P(C.c_int), C.c_int, P(Tensor)]
+        L.q_llama_generate_greedy.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, C.c_int, P(C.c_int)]
+        L.q_llama_model_synth.argtypes = [P(QLlamaModel), P(C.c_int32), C.c_float, C.c_float, C.c_uint64, C.c_int]
+        L.q_llama_model_hash.argtypes = [P(QLlamaModel)]
+        L.q_llama_model_hash.restype = C.c_uint64
+        L.qtensor_create.argtypes = [C.c_int, C.c_int]
+        L.qtensor_create.restype = QTensor
+        L.qtensor_free.argtypes = [P(QTensor)]
+        L.qtensor_quantize.argtypes = [P(QTensor), P(C.c_float)]
+        L.qmatmul.argtypes = [P(Tensor), P(QTensor), P(Tensor)]
+        L.quantize_int8_percol.argtypes = [P(C.c_float), C.c_int, C.c_int, P(C.c_int8), P(C.c_float)]
+        L.dequantize_int8_percol.argtypes = [P(C.c_int8), P(C.c_float), C.c_int, C.c_int, P(C.c_float)]
+        L.qacc_columns.argtypes = [P(C.c_int8), P(C.c_int8), C.c_int, C.c_int, P(C.c_int32)]
+        L.q_llama_tensor_export.argtypes = [P(QTensor), P(C.c_int8), P(C.c_float)]
+        L.qllama_device_count.restype = C.c_int
+        L.qllama_device_sync.restype = C.c_int
+        L.qllama_test_expf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
+        L.qllama_gqa_decode.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 4 + [P(C.c_float)]
+        L.qllama_sync.restype = C.c_int
+        L.qllama_stream.restype = C.c_void_p
+        L.qllama_profile.argtypes = [C.c_int]
+        L.qllama_profile_read.argtypes = [C.c_char_p, C.c_int, P(C.c_double), P(C.c_longlong), C.c_int]
+        _lib = L
+    return _lib
+
+
+def _f32(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def host_tensor(a):
+    """A reference Tensor view of a C-contiguous float32 numpy array (kept alive by the caller)."""
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    shape = (C.c_int * a.ndim)(*a.shape)
+    t = Tensor(_f32(a), None, shape, a.ndim, a.size)
+    t._keep = (a, shape)
+    return t
+
+
+class Model:
+    """A QLlamaModel plus one LlamaKV, on the GPU."""
+
+    def __init__(self, m):
+        self.m = m
+        self.kv = lib().q_llama_kv_create(C.byref(self.m))
+        self.vocab = m.vocab
+        self.logits = np.zeros((1, m.vocab), np.float32)
+        self._lt = host_tensor(self.logits)
+
+    @classmethod
+    def synth(cls, cfg, rope_base, eps=1e-5, seed=1234, tied=False):
+        m = QLlamaModel()
+        arr = (C.c_int32 * 8)(*cfg)
+        if lib().q_llama_model_synth(C.byref(m), arr, rope_base, eps, seed, int(tied)) != 0:
+            raise RuntimeError("q_llama_model_synth failed")
+        return cls(m)
+
+    @classmethod
+    def load(cls, path):
+        m = QLlamaModel()
+        if lib().q_llama_model_load(os.fsencode(path), C.byref(m)) != 0:
+            raise RuntimeError(f"q_llama_model_load failed for {path}")
+        return cls(m)
+
+    @property
+    def pos(self):
+        return self.kv.len
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def hash(self):
+        return int(lib().q_llama_model_hash(C.byref(self.m)))
+
+    def step(self, token):
+        lib().q_llama_decode_step(C.byref(self.m), C.byref(self.kv), int(token), C.byref(self._lt))
+        return self.logits[0]
+
+    def prefill(self, ids, want_logits=True):
+        arr = (C.c_int * len(ids))(*ids)
+        rc = lib().q_llama_prefill(C.byref(self.m), C.byref(self.kv), arr, len(ids),
+                                   C.byref(self._lt) if want_logits else None)
+        if rc != 0:
+            raise RuntimeError("q_llama_prefill failed")
+        return self.logits[0]
+
+    def generate_greedy(self, token, n):
+        out = (C.c_int * n)()
+        if lib().q_llama_generate_greedy(C.byref(self.m), C.byref(self.kv), int(token), n, out) != 0:
+            raise RuntimeError("q_llama_generate_greedy failed")
+        return list(out)
+
+    def close(self):
+        if self.m.dev:
+            lib().llama_kv_free(C.byref(self.kv))
+            lib().q_llama_model_free(C.byref(self.m))
+            self.m.dev = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- quant.h API ------------------------------------------------------------
+class QWeight:
+    """A device QTensor (quant.h:22-27) quantized from a host (rows, cols) f32 matrix."""
+
+    def __init__(self, w):
+        w = np.ascontiguousarray(w, np.float32)
+        self.rows, self.cols = w.shape
+        self.t = lib().qtensor_create(self.rows, self.cols)
+        lib().qtensor_quantize(C.byref(self.t), _f32(w))
+
+    def close(self):
+        if self.t.q:
+            lib().qtensor_free(C.byref(self.t))
+            self.t.q = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def qmatmul(A, W):
+    A = np.ascontiguousarray(A, np.float32)
+    Cm = np.zeros((A.shape[0], W.cols), np.float32)
+    ta, tc = host_tensor(A), host_tensor(Cm)
+    lib().qmatmul(C.byref(ta), C.byref(W.t), C.byref(tc))
+    return Cm
+
+
+def quantize_int8_percol(w):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    q = np.zeros((rows, cols), np.int8)
+    s = np.zeros(cols, np.float32)
+    lib().quantize_int8_percol(_f32(w), rows, cols, q.ctypes.data_as(C.POINTER(C.c_int8)), _f32(s))
+    return q, s
+
+
+def dequantize_int8_percol(q, s):
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(s, np.float32)
+    rows, cols = q.shape
+    w = np.zeros((rows, cols), np.float32)
+    lib().dequantize_int8_percol(q.ctypes.data_as(C.POINTER(C.c_int8)), _f32(s), rows, cols, _f32(w))
+    return w
+
+
+def qacc_columns(qa, qw):
+    qa = np.ascontiguousarray(qa, np.int8)
+    qw = np.ascontiguousarray(qw, np.int8)
+    K, N = qw.shape
+    acc = np.zeros(N, np.int32)
+    lib().qacc_columns(qa.ctypes.data_as(C.POINTER(C.c_int8)), qw.ctypes.data_as(C.POINTER(C.c_int8)), K, N,
+                       acc.ctypes.data_as(C.POINTER(C.c_int32)))
+    return acc
+
+
+def profile(enable):
+    lib().qllama_profile(1 if enable else 0)
+
+
+def profile_read():
+    names = C.create_string_buffer(4096)
+    ms = (C.c_double * 32)()
+    cnt = (C.c_longlong * 32)()
+    n = lib().qllama_profile_read(names, 4096, ms, cnt, 32)
+    keys = names.value.decode().split(",")[:max(n, 0)]
+    return {k: (ms[i], cnt[i]) for i, k in enumerate(keys)}

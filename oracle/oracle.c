@@ -473,3 +473,41 @@ void or_decode_step(const OrModel *m, OrKV *kv, int token, float *logits) {
   free(sc); free(x); free(xn); free(q); free(k); free(v); free(o); free(ao);
   free(hn); free(f); free(g); free(u);
 }
+
+// ---------------------------------------------------------------------------
+// Checker for the device expf: counts inputs start..start+count-1 (as float bit
+// patterns) where got[] differs bitwise from this host's libm expf (the function
+// llama.c:567,585 call).  NaN results compare equal to NaN.
+// ---------------------------------------------------------------------------
+typedef struct { uint32_t start; uint32_t lo, hi; const float *got; long long bad; } ExpJob;
+
+static void *expf_worker(void *arg) {
+  ExpJob *j = (ExpJob*)arg;
+  long long bad = 0;
+  for (uint32_t i = j->lo; i < j->hi; i++) {
+    uint32_t b = j->start + i;
+    float x; memcpy(&x, &b, 4);
+    float r = expf(x), g = j->got[i];
+    uint32_t rb, gb; memcpy(&rb, &r, 4); memcpy(&gb, &g, 4);
+    if (rb != gb && !(isnan(r) && isnan(g))) bad++;
+  }
+  j->bad = bad;
+  return NULL;
+}
+
+long long or_expf_mismatches(uint32_t start, uint32_t count, const float *got) {
+  enum { NT = 16 };
+  pthread_t th[NT];
+  ExpJob jobs[NT];
+  uint32_t per = (count + NT - 1) / NT;
+  for (int t = 0; t < NT; t++) {
+    uint32_t lo = (uint32_t)t * per, hi = lo + per;
+    if (lo > count) lo = count;
+    if (hi > count) hi = count;
+    jobs[t] = (ExpJob){start, lo, hi, got, 0};
+    pthread_create(&th[t], NULL, expf_worker, &jobs[t]);
+  }
+  long long bad = 0;
+  for (int t = 0; t < NT; t++) { pthread_join(th[t], NULL); bad += jobs[t].bad; }
+  return bad;
+}

@@ -69,4 +69,7 @@ int  or_kv_create(OrKV *kv, const OrModel *m);
 void or_kv_free(OrKV *kv);
 void or_decode_step(const OrModel *m, OrKV *kv, int token, float *logits);
 
+// Bitwise mismatches of got[i] against the host libm expf at bit pattern start+i.
+long long or_expf_mismatches(uint32_t start, uint32_t count, const float *got);
+
 #endif

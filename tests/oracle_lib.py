@@ -79,6 +79,8 @@ def lib():
         L.or_kv_create.argtypes = [C.POINTER(OrKV), C.POINTER(OrModel)]
         L.or_kv_free.argtypes = [C.POINTER(OrKV)]
         L.or_decode_step.argtypes = [C.POINTER(OrModel), C.POINTER(OrKV), C.c_int, fp]
+        L.or_expf_mismatches.argtypes = [C.c_uint32, C.c_uint32, fp]
+        L.or_expf_mismatches.restype = C.c_longlong
         L.or_set_threads.argtypes = [C.c_int]
         L.or_get_threads.restype = C.c_int
         L.syn_key.argtypes = [C.c_uint64, C.c_uint64]

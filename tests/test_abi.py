@@ -1,0 +1,121 @@
+"""CPU-side checks of the C ABI: the library loads, exports every declared entry
+point, and the loader's host-side validation (llama.c:610-631) rejects bad
+checkpoints before any device work, with the reference's messages."""
+import ctypes as C
+import os
+import re
+import struct
+import subprocess
+
+import pytest
+
+import qlib
+
+ROOT = qlib.ROOT
+HEADER = os.path.join(ROOT, "include", "qllama.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"//.*", "", text)
+    names = re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{}]*\)\s*;", text)
+    return sorted(set(n for n in names if n not in ("sizeof",)))
+
+
+def test_header_declares_the_reference_api():
+    names = declared_functions()
+    for ref in ("q_llama_model_load", "q_llama_model_free", "q_llama_quantize_from", "q_llama_kv_create",
+                "llama_kv_free", "q_llama_decode_step", "qtensor_create", "qtensor_free", "qtensor_quantize",
+                "qmatmul", "quantize_int8_percol", "dequantize_int8_percol", "qacc_columns"):
+        assert ref in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = qlib.load().lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_exports_are_c_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", qlib.load().LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(l.split()[-1] for l in out.splitlines() if l.strip())
+    for n in declared_functions():
+        assert n in exported, f"{n} is not an unmangled C symbol"
+
+
+def test_struct_layouts_match_header():
+    q = qlib.load()
+    # offsets the C side relies on (x86-64 SysV)
+    assert C.sizeof(q.Tensor) == 40
+    assert C.sizeof(q.QTensor) == 32
+    assert q.QLlamaModel.dev.offset == C.sizeof(q.QLlamaModel) - 8
+    assert q.LlamaKV.len.offset == 12
+
+
+def _write(path, header, cfg, fcfg, body=b""):
+    with open(path, "wb") as f:
+        f.write(struct.pack("<2I", *header))
+        f.write(struct.pack("<8i", *cfg))
+        f.write(struct.pack("<2f", *fcfg))
+        f.write(body)
+
+
+def _load_rc(path, capfd):
+    q = qlib.load()
+    m = q.QLlamaModel()
+    rc = q.lib().q_llama_model_load(os.fsencode(str(path)), C.byref(m))
+    err = capfd.readouterr().err
+    return rc, err
+
+
+GOOD_CFG = [32, 8, 1, 4, 2, 2, 16, 64]
+
+
+def test_load_missing_file(tmp_path, capfd):
+    rc, err = _load_rc(tmp_path / "nope.bin", capfd)
+    assert rc != 0 and "cannot open" in err
+
+
+def test_load_truncated_header(tmp_path, capfd):
+    p = tmp_path / "t.bin"
+    p.write_bytes(b"LLMQ\x02\x00")
+    rc, err = _load_rc(p, capfd)
+    assert rc != 0 and "truncated (bad header)" in err
+
+
+@pytest.mark.parametrize("magic,version", [(0x414D4C4C, 2), (0x514D4C4C, 1), (0x12345678, 2)])
+def test_load_rejects_non_llmq(tmp_path, capfd, magic, version):
+    p = tmp_path / "m.bin"
+    _write(p, (magic, version), GOOD_CFG, (10000.0, 1e-5))
+    rc, err = _load_rc(p, capfd)
+    assert rc != 0 and "is not a v2 int8 LLMQ checkpoint" in err
+
+
+@pytest.mark.parametrize("cfg", [
+    [32, 8, 1, 3, 2, 2, 16, 64],        # n_heads % n_kv != 0
+    [32, 0, 1, 4, 2, 2, 16, 64],        # non-positive dim
+    [32, 8, 1, 4, 2, 2, 16, 2000000],   # above the 1e6 bound
+    [1000000, 4096, 1, 4, 2, 2, 16, 64],  # vocab * d_model above INT_MAX
+])
+def test_load_rejects_bad_config(tmp_path, capfd, cfg):
+    p = tmp_path / "c.bin"
+    _write(p, (0x514D4C4C, 2), cfg, (10000.0, 1e-5))
+    rc, err = _load_rc(p, capfd)
+    assert rc != 0 and "invalid/unsupported config" in err
+
+
+def test_synth_rejects_bad_config(capfd):
+    q = qlib.load()
+    m = q.QLlamaModel()
+    arr = (C.c_int32 * 8)(32, 8, 1, 3, 2, 2, 16, 64)
+    assert q.lib().q_llama_model_synth(C.byref(m), arr, 10000.0, 1e-5, 1, 0) != 0
+    assert "invalid" in capfd.readouterr().err
+
+
+@pytest.mark.skipif(qlib.gpu_available(), reason="checks the no-GPU error path")
+def test_load_without_gpu_fails_cleanly(tmp_path, capfd):
+    p = tmp_path / "g.bin"
+    _write(p, (0x514D4C4C, 2), GOOD_CFG, (10000.0, 1e-5))
+    rc, err = _load_rc(p, capfd)
+    assert rc != 0 and "Error:" in err

@@ -173,7 +173,7 @@ def test_decode_attention_matches_reference(T):
 
 
 @pytest.mark.slow
-@pytest.mark.skipif(not have_golden("gqa8192.json"), reason="context-8192 fixture not generated")
+@pytest.mark.skipif(not have_golden("gqa_T8192_o.npy"), reason="context-8192 fixture not generated")
 def test_decode_attention_8192_matches_reference():
     meta = golden_json("gqa8192")["gqa_T8192"]
     q, K, V = _gqa_inputs(meta["case"], 8192)
@@ -263,6 +263,6 @@ def test_e2e_1b_matches_reference():
 
 
 @pytest.mark.slow
-@pytest.mark.skipif(not have_golden("e2e_8b.json"), reason="8B fixture not generated")
+@pytest.mark.skipif(not have_golden("e2e_8b_logits_final.npy"), reason="8B fixture not generated")
 def test_e2e_8b_matches_reference():
     _e2e("8b")
