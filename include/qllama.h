@@ -170,6 +170,11 @@ int  qllama_test_expf(uint32_t start, uint32_t count, float *out);
 // reference's cache layout, o (n_heads*hd); all host memory.  For op-level parity.
 int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv,
                        int hd, float *o);
+// The device's exact evaluation of the sequential float sum ((0 + a_0) + a_1) + ...
+// of n <= 16384 non-negative terms (the form of rmsnorm.c:15 and llama.c:567):
+// *out = the sum, info[0] = number of serially evaluated steps, info[1] = 1 when
+// the block fell back to the plain loop.  For parity tests.
+int  qllama_test_seqsum(const float *a, int n, float *out, int *info);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include "qdev_math.h"
+#include "qdev_seqsum.h"
 #include "qhip.h"
 #include "qhip_internal.h"
 #include "qllama.h"
@@ -46,25 +47,25 @@ __global__ void k_embed(const int8_t *wte, const float *s, int dm, const int *d_
 }
 
 // One block per row: rmsnorm.c:7-21 then the activation quantization of qmatmul.
-// The sum of squares is accumulated by one lane in index order, as the
-// reference's loop does; the squares themselves are formed in parallel.
+// The squares are formed in parallel and their sequential float sum (the
+// reference's loop order) is evaluated exactly by qd::seq_sum_nonneg.
 __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *x, int dm, const float *gamma, float eps,
                                                          int8_t *qa, int kpad, float *as) {
   extern __shared__ float lds[];          // dm values, then dm squares
   __shared__ float red[16];
   __shared__ float s_r;
+  __shared__ qd::SeqSumScratch seq;
   const int row = blockIdx.x;
   const float *xr = x + (size_t)row * dm;
-  float *v = lds, *sq = lds + dm;
+  float *v = lds, *sq = lds + ((dm + 3) & ~3);
   for (int j = threadIdx.x; j < dm; j += blockDim.x) {
     const float a = xr[j];
     v[j] = a;
     sq[j] = a * a;
   }
   __syncthreads();
+  float ms = qd::seq_sum_nonneg<1024>(sq, dm, seq);       // rmsnorm.c:15, exactly
   if (threadIdx.x == 0) {
-    float ms = 0.0f;
-    for (int j = 0; j < dm; j++) ms += sq[j];
     const float inv_n = 1.0f / (float)dm;
     ms *= inv_n;
     s_r = 1.0f / sqrtf(ms + eps);
@@ -191,52 +192,6 @@ __global__ void k_rope_append(const float *qkv, int H, int KVH, int hd, const fl
   }
 }
 
-// Decode attention, one block per query head (llama.c:554-576): scores with the
-// dot over d in order, max, expf, the sum of exponentials in j order, then each
-// output dimension accumulated over j in order.
-__global__ __launch_bounds__(256) void k_attention(const float *q, const float *kc, const float *vc, const int *d_pos,
-                                                   int H, int KVH, int hd, int max_seq, float scale,
-                                                   float *scores, float *o) {
-  extern __shared__ float qs[];
-  __shared__ float red[4];
-  __shared__ float s_inv;
-  const int h = blockIdx.x;
-  const int kvh = h / (H / KVH);
-  const int T = *d_pos + 1;
-  const float *K = kc + (size_t)kvh * max_seq * hd;
-  const float *V = vc + (size_t)kvh * max_seq * hd;
-  float *sc = scores + (size_t)h * max_seq;
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[(size_t)h * hd + d];
-  __syncthreads();
-  float mx = -INFINITY;
-  for (int j = threadIdx.x; j < T; j += blockDim.x) {
-    const float *kj = K + (size_t)j * hd;
-    float dot = 0.0f;
-    for (int d = 0; d < hd; d++) dot += qs[d] * kj[d];
-    const float s = dot * scale;
-    sc[j] = s;
-    mx = fmaxf(mx, s);
-  }
-  mx = block_max(mx, red);
-  for (int j = threadIdx.x; j < T; j += blockDim.x) sc[j] = qd::expf_glibc(sc[j] - mx);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = 0.0f;
-    for (int j = 0; j < T; j++) sum += sc[j];
-    s_inv = 1.0f / sum;
-  }
-  __syncthreads();
-  const float inv = s_inv;
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.0f;
-    for (int j = 0; j < T; j++) {
-      const float w = sc[j] * inv;
-      acc += w * V[(size_t)j * hd + d];
-    }
-    o[(size_t)h * hd + d] = acc;
-  }
-}
-
 // First index of the maximum (sampler.c:8-21), then advance the position.
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out,
                                                          int max_seq) {
@@ -291,8 +246,9 @@ int qhip_embed(const int8_t *wte, const float *wte_s, int dm, const int *d_in, c
 
 int qhip_rmsnorm_quant(const float *x, int rows, int dm, const float *gamma, float eps, int8_t *qa, int kpad,
                        float *as) {
-  if (dm > 16384) return qh::fail_msg("rmsnorm_quant: d_model above 16384");
-  QH_LAUNCH(QK_RMSNORM, k_rmsnorm_quant, dim3(rows), dim3(1024), (size_t)dm * 8, x, dm, gamma, eps, qa, kpad, as);
+  if (dm > qd::kSeqMaxN) return qh::fail_msg("rmsnorm_quant: d_model above 16384");
+  QH_LAUNCH(QK_RMSNORM, k_rmsnorm_quant, dim3(rows), dim3(1024), (size_t)((dm + 3) & ~3) * 8, x, dm, gamma, eps, qa,
+            kpad, as);
   return 0;
 }
 
@@ -323,13 +279,6 @@ int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const floa
                      const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
   QH_LAUNCH(QK_ROPE, k_rope_append, dim3(n_heads + 2 * n_kv), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t, sin_t,
             d_pos, q_out, kc, vc, max_seq);
-  return 0;
-}
-
-int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads, int n_kv, int hd,
-                   int max_seq, float scale, float *scores, float *o) {
-  QH_LAUNCH(QK_ATTN, k_attention, dim3(n_heads), dim3(256), (size_t)hd * 4, q, kc, vc, d_pos, n_heads, n_kv, hd,
-            max_seq, scale, scores, o);
   return 0;
 }
 
@@ -384,7 +333,7 @@ extern "C" int qllama_gqa_decode(const float *q, const float *k, const float *v,
   const size_t kvn = (size_t)T * n_kv * hd;
   float *dq = (float *)qhip_malloc((size_t)n_heads * hd * 4), *dk = (float *)qhip_malloc(kvn * 4);
   float *dv = (float *)qhip_malloc(kvn * 4), *tmp = (float *)qhip_malloc(kvn * 4);
-  float *dsc = (float *)qhip_malloc((size_t)n_heads * T * 4), *dout = (float *)qhip_malloc((size_t)n_heads * hd * 4);
+  float *dsc = (float *)qhip_malloc(qhip_attention_scratch(n_heads, T) * 4), *dout = (float *)qhip_malloc((size_t)n_heads * hd * 4);
   int *dpos = (int *)qhip_malloc(4);
   const int pos = T - 1;
   int rc = (!dq || !dk || !dv || !tmp || !dsc || !dout || !dpos) ? 1 : 0;
@@ -399,8 +348,36 @@ extern "C" int qllama_gqa_decode(const float *q, const float *k, const float *v,
     rc = qh::check_launch("k_kv_relayout");
   }
   const float scale = 1.0f / sqrtf((float)hd);
-  if (!rc) rc = qhip_attention(dq, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dsc, dout);
+  if (!rc) rc = qhip_attention(dq, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dsc, dout, NULL);
   if (!rc) rc = qhip_d2h(o, dout, (size_t)n_heads * hd * 4);
   qhip_free(dq); qhip_free(dk); qhip_free(dv); qhip_free(tmp); qhip_free(dsc); qhip_free(dout); qhip_free(dpos);
+  return rc;
+}
+
+namespace {
+__global__ __launch_bounds__(1024) void k_seqsum_test(const float *a, int n, float *out, int *info) {
+  extern __shared__ float lds[];
+  __shared__ qd::SeqSumScratch S;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = a[i];
+  __syncthreads();
+  const float s = qd::seq_sum_nonneg<1024>(lds, n, S);
+  if (threadIdx.x == 0) { out[0] = s; info[0] = S.nhard; info[1] = S.fail; }
+}
+}  // namespace
+
+extern "C" int qllama_test_seqsum(const float *a, int n, float *out, int *info) {
+  if (qhip_init()) return 1;
+  if (n < 0 || n > qd::kSeqMaxN) return qh::fail_msg("seqsum: n out of range");
+  float *da = (float *)qhip_malloc((size_t)(n + 4) * 4), *dout = (float *)qhip_malloc(16);
+  int *dinfo = (int *)qhip_malloc(16);
+  int rc = (!da || !dout || !dinfo) ? 1 : 0;
+  if (!rc) rc = qhip_h2d(da, a, (size_t)n * 4);
+  if (!rc) {
+    hipLaunchKernelGGL(k_seqsum_test, dim3(1), dim3(1024), (size_t)((n + 3) & ~3) * 4 + 16, qh::stream(), da, n, dout,
+                       dinfo);
+    rc = qh::check_launch("k_seqsum_test");
+  }
+  if (!rc) rc = qhip_d2h(out, dout, 4) || qhip_d2h(info, dinfo, 8);
+  qhip_free(da); qhip_free(dout); qhip_free(dinfo);
   return rc;
 }

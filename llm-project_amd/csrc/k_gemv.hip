@@ -1,0 +1,310 @@
+// k_gemv.hip - the decode W8A8 GEMV (quant.c:60-85 with one activation row).
+//
+// Weights are output-channel major ([N][kpad] int8, K contiguous).  One wave owns
+// R consecutive output channels; its 64 lanes split K in 16-byte chunks, so every
+// load is a coalesced 1 KiB wave access.  The quantized activation row (kpad
+// bytes) is loaded once per wave into registers and reused for all R channels.
+// Products accumulate exactly in int32 (v_dot4_i32_i8; |acc| <= 127^2 * K < 2^31)
+// and are summed across the wave, so the result is independent of the split.
+// The next channel's weights are in flight while the current one is reduced.
+//
+// Epilogues (the reference's order of rounding, quant.c:81-82):
+//   PLAIN  out[j] = (as * ws[j]) * (float)acc (+ bias[j], llama.c:546-548)
+//   RESID  out[j] = out[j] + (as * ws[j]) * (float)acc       (llama.c:578, 589)
+//   SWIGLU rows j and N+j are gate and up; out[j] = (g * (1 / (1 + expf(-g)))) * u
+//          (llama.c:583-587) and each block records max |out| for the quantizer.
+#include <hip/hip_runtime.h>
+
+#include "qdev_math.h"
+#include "qhip.h"
+#include "qhip_internal.h"
+
+namespace {
+
+enum { MODE_PLAIN = 0, MODE_RESID = 1, MODE_SWIGLU = 2, MODE_HEAD = 3 };
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <int KCH>
+__device__ __forceinline__ void load_row(v4i (&w)[KCH], const int8_t *row, int lane) {
+  const v4i *r = reinterpret_cast<const v4i *>(row);
+#pragma unroll
+  for (int i = 0; i < KCH; i++) w[i] = __builtin_nontemporal_load(&r[lane + 64 * i]);
+}
+
+template <int KCH>
+__device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH]) {
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < KCH; i++) {
+    t = __builtin_amdgcn_sdot4(a[i].x, w[i].x, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].y, w[i].y, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].z, w[i].z, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].w, w[i].w, t, false);
+  }
+  return t;
+}
+
+// KCH = kpad / 1024 chunks of 16 bytes per lane (kpad a multiple of 1024).
+template <int MODE, int KCH, int R>
+__global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float *as_p, const int8_t *W,
+                                                  const float *ws, int N, int kpad, float *out, const float *bias,
+                                                  float *bm, int *bi) {
+  __shared__ float red[4];
+  __shared__ int redi[4];
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j0 = (blockIdx.x * 4 + wave) * R;
+  v4i a[KCH];
+  {
+    const v4i *q4 = reinterpret_cast<const v4i *>(qa);
+#pragma unroll
+    for (int i = 0; i < KCH; i++) a[i] = q4[lane + 64 * i];
+  }
+  const float as = *as_p;
+  float hmax = 0.0f;
+  v4i w[KCH], u[KCH];
+  if (j0 < N) {
+    load_row(w, W + (size_t)j0 * kpad, lane);
+    if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j0) * kpad, lane);
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int j = j0 + r;
+    if (j >= N) break;
+    const int accw = dot_row(w, a);
+    int accu = 0;
+    if (MODE == MODE_SWIGLU) accu = dot_row(u, a);
+    if (r + 1 < R && j + 1 < N) {                    // next channel's weights in flight
+      load_row(w, W + (size_t)(j + 1) * kpad, lane);
+      if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j + 1) * kpad, lane);
+    }
+    const int sw = qd::wave_sum_i32(accw);
+    if (MODE == MODE_SWIGLU) {
+      const int su = qd::wave_sum_i32(accu);
+      const float g = (as * ws[j]) * (float)sw;
+      const float up = (as * ws[N + j]) * (float)su;
+      const float s = 1.0f / (1.0f + qd::expf_glibc(-g));
+      const float h = (g * s) * up;
+      hmax = fmaxf(hmax, fabsf(h));
+      if (lane == 0) out[j] = h;
+    } else {
+      const float c = (as * ws[j]) * (float)sw;
+      if (MODE == MODE_HEAD && (besti == 0x7fffffff || c > best)) { best = c; besti = j; }
+      if (lane == 0) {
+        if (MODE == MODE_RESID) out[j] = out[j] + c;
+        else out[j] = bias ? c + bias[j] : c;
+      }
+    }
+  }
+  if (MODE == MODE_SWIGLU) {
+    if (lane == 0) red[wave] = hmax;
+    __syncthreads();
+    if (threadIdx.x == 0) bm[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  }
+  if (MODE == MODE_HEAD) {         // first index of this block's maximum (sampler.c:8-21)
+    if (lane == 0) { red[wave] = best; redi[wave] = besti; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = red[0];
+      int i0 = redi[0];
+      for (int w = 1; w < 4; w++)
+        if (redi[w] != 0x7fffffff && (i0 == 0x7fffffff || red[w] > b || (red[w] == b && redi[w] < i0))) {
+          b = red[w];
+          i0 = redi[w];
+        }
+      bm[blockIdx.x] = b;
+      bi[blockIdx.x] = i0;
+    }
+  }
+}
+
+// Generic K: lanes loop over the 16-byte chunks.
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemv_dec_any(const int8_t *qa, const float *as_p, const int8_t *W,
+                                                      const float *ws, int N, int kpad, float *out,
+                                                      const float *bias, float *bm, int *bi) {
+  __shared__ float red[4];
+  __shared__ int redi[4];
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = blockIdx.x * 4 + wave;
+  const int nchunk = kpad >> 4;
+  float hmax = 0.0f;
+  if (j < N) {
+    const int4 *q4 = reinterpret_cast<const int4 *>(qa);
+    const int4 *wr = reinterpret_cast<const int4 *>(W + (size_t)j * kpad);
+    const int4 *ur = reinterpret_cast<const int4 *>(W + (size_t)(N + j) * kpad);
+    int tw = 0, tu = 0;
+    for (int c = lane; c < nchunk; c += 64) {
+      const int4 av = q4[c], wv = wr[c];
+      tw = __builtin_amdgcn_sdot4(av.x, wv.x, tw, false);
+      tw = __builtin_amdgcn_sdot4(av.y, wv.y, tw, false);
+      tw = __builtin_amdgcn_sdot4(av.z, wv.z, tw, false);
+      tw = __builtin_amdgcn_sdot4(av.w, wv.w, tw, false);
+      if (MODE == MODE_SWIGLU) {
+        const int4 uv = ur[c];
+        tu = __builtin_amdgcn_sdot4(av.x, uv.x, tu, false);
+        tu = __builtin_amdgcn_sdot4(av.y, uv.y, tu, false);
+        tu = __builtin_amdgcn_sdot4(av.z, uv.z, tu, false);
+        tu = __builtin_amdgcn_sdot4(av.w, uv.w, tu, false);
+      }
+    }
+    const float as = *as_p;
+    const int sw = qd::wave_sum_i32(tw);
+    if (MODE == MODE_SWIGLU) {
+      const int su = qd::wave_sum_i32(tu);
+      const float g = (as * ws[j]) * (float)sw;
+      const float up = (as * ws[N + j]) * (float)su;
+      const float s = 1.0f / (1.0f + qd::expf_glibc(-g));
+      const float h = (g * s) * up;
+      hmax = fabsf(h);
+      if (lane == 0) out[j] = h;
+    } else {
+      const float c = (as * ws[j]) * (float)sw;
+      if (MODE == MODE_HEAD) { best = c; besti = j; }
+      if (lane == 0) {
+        if (MODE == MODE_RESID) out[j] = out[j] + c;
+        else out[j] = bias ? c + bias[j] : c;
+      }
+    }
+  }
+  if (MODE == MODE_SWIGLU) {
+    if (lane == 0) red[wave] = hmax;
+    __syncthreads();
+    if (threadIdx.x == 0) bm[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  }
+  if (MODE == MODE_HEAD) {
+    if (lane == 0) { red[wave] = best; redi[wave] = besti; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = red[0];
+      int i0 = redi[0];
+      for (int w = 1; w < 4; w++)
+        if (redi[w] != 0x7fffffff && (i0 == 0x7fffffff || red[w] > b || (red[w] == b && redi[w] < i0))) {
+          b = red[w];
+          i0 = redi[w];
+        }
+      bm[blockIdx.x] = b;
+      bi[blockIdx.x] = i0;
+    }
+  }
+}
+
+// Reduce the per-block (max, first index) candidates of the head GEMV to the
+// greedy token; then record it and advance the position (see qhip.h).
+__global__ __launch_bounds__(1024) void k_argmax_final(const float *bv, const int *bidx, int nb, int *d_in,
+                                                       int *d_state, int *d_out, int max_seq) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+    const float v = bv[i];
+    const int k = bidx[i];
+    if (k != 0x7fffffff && (idx == 0x7fffffff || v > best || (v == best && k < idx))) { best = v; idx = k; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (oi != 0x7fffffff && (idx == 0x7fffffff || ob > best || (ob == best && oi < idx))) { best = ob; idx = oi; }
+  }
+  if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = best; si[threadIdx.x >> 6] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int i0 = si[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+      if (si[w] != 0x7fffffff && (i0 == 0x7fffffff || sv[w] > b || (sv[w] == b && si[w] < i0))) { b = sv[w]; i0 = si[w]; }
+    const int pos = d_state[0];
+    if (pos < max_seq) d_out[pos] = i0;
+    if (pos + 1 >= d_state[1] && pos + 1 <= max_seq) d_in[pos + 1] = i0;
+    d_state[0] = pos + 1;
+  }
+}
+
+// Quantize v (n values, quant.c:66-78) given per-block maxima of |v|; grid
+// ceil(kpad/1024) blocks of 256 threads x 4 values; block 0 writes the scale.
+__global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa,
+                                                      int kpad, float *as_out) {
+  __shared__ float red[4];
+  float mx = 0.0f;
+  for (int i = threadIdx.x; i < nbm; i += 256) mx = fmaxf(mx, bm[i]);
+  mx = qd::wave_max_f32(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+  const float inv = 1.0f / as;
+  const int k0 = blockIdx.x * 1024 + threadIdx.x * 4;
+  if (k0 < kpad) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int k = k0 + r;
+      const int q = k < n ? qd::quant_i8(v[k], inv) : 0;
+      packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * r);
+    }
+    *reinterpret_cast<uint32_t *>(qa + k0) = packed;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
+}
+
+template <int MODE>
+int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws, int N, int kpad, float *out,
+           const float *bias, float *bm, int *bi) {
+  constexpr int R = 2;
+  const dim3 grid((N + 4 * R - 1) / (4 * R));
+  switch (kpad) {
+    case 2048:
+      QH_LAUNCH(cls, (k_gemv_dec<MODE, 2, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+      return 0;
+    case 4096:
+      QH_LAUNCH(cls, (k_gemv_dec<MODE, 4, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+      return 0;
+    case 8192:
+      QH_LAUNCH(cls, (k_gemv_dec<MODE, 8, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+      return 0;
+    case 14336:
+      QH_LAUNCH(cls, (k_gemv_dec<MODE, 14, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+      return 0;
+    default:
+      QH_LAUNCH(cls, k_gemv_dec_any<MODE>, dim3((N + 3) / 4), dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+      return 0;
+  }
+}
+
+}  // namespace
+
+extern "C" int qhip_gemv_blocks(int N, int kpad) {
+  switch (kpad) {
+    case 2048: case 4096: case 8192: case 14336: return (N + 7) / 8;
+    default: return (N + 3) / 4;
+  }
+}
+
+extern "C" int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws,
+                             int N, int kpad, float *out, const float *bias, float *bm, int *bi) {
+  if (kpad % 16) return qh::fail_msg("gemv: kpad must be a multiple of 16");
+  switch (mode) {
+    case MODE_PLAIN: return launch<MODE_PLAIN>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+    case MODE_RESID: return launch<MODE_RESID>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+    case MODE_SWIGLU: return launch<MODE_SWIGLU>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+    case MODE_HEAD: return launch<MODE_HEAD>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+    default: return qh::fail_msg("gemv: bad mode");
+  }
+}
+
+extern "C" int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as) {
+  QH_LAUNCH(QK_QUANT, k_quant_blocks, dim3((kpad + 1023) / 1024), dim3(256), 0, v, n, bm, nbm, qa, kpad, as);
+  return 0;
+}
+
+extern "C" int qhip_argmax_final(const float *bv, const int *bidx, int nb, int *d_in, int *d_state, int *d_out,
+                                 int max_seq) {
+  QH_LAUNCH(QK_ARGMAX, k_argmax_final, dim3(1), dim3(1024), 0, bv, bidx, nb, d_in, d_state, d_out, max_seq);
+  return 0;
+}

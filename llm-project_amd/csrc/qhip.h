@@ -89,10 +89,25 @@ int qhip_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W, cons
 int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const float *cos_t,
                      const float *sin_t, const int *d_pos, float *q_out, float *kc, float *vc,
                      int max_seq);
-// decode attention over cache rows 0..*d_pos (llama.c:554-576)
+// decode attention over cache rows 0..*d_pos (llama.c:554-576); scores must hold
+// qhip_attention_scratch(n_heads, max_seq) floats
+size_t qhip_attention_scratch(int n_heads, int max_seq);
+// obm (optional) receives qhip_attention_nbm(n_heads, hd) maxima of |o| by block.
 int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos,
                    int n_heads, int n_kv, int hd, int max_seq, float scale, float *scores,
-                   float *o);
+                   float *o, float *obm);
+int qhip_attention_nbm(int n_heads, int hd);
+// Decode GEMV with one activation row (k_gemv.hip): mode 0 plain (+bias), 1
+// residual add, 2 SwiGLU over gate rows [0,N) and up rows [N,2N) writing h and
+// per-block max |h| into bm (qhip_gemv_blocks(N, kpad) entries).
+// Mode 3 is plain without bias plus, per block, the first index of its maximum
+// output in bi[] with the value in bm[] (for qhip_argmax_final).
+int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws,
+                  int N, int kpad, float *out, const float *bias, float *bm, int *bi);
+int qhip_argmax_final(const float *bv, const int *bidx, int nb, int *d_in, int *d_state, int *d_out, int max_seq);
+int qhip_gemv_blocks(int N, int kpad);
+// Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
+int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as);
 // first index of the maximum (sampler.c:8-21) of v -> d_out[pos]; when pos + 1 is
 // past the staged inputs (d_state[1]) it also becomes d_in[pos + 1]; then
 // d_state[0] = pos + 1.  pos = d_state[0].

@@ -41,7 +41,8 @@ typedef struct {
   float *wte_s, *head_s, *g_final;
   float *rope_cos, *rope_sin;
   // scratch
-  float *x, *qkv, *q, *o, *gu, *logits, *scores, *as;
+  float *x, *qkv, *q, *o, *gu, *logits, *scores, *as, *obm, *hbm, *amax_v;
+  int *amax_i;
   int8_t *qa;
   int *d_state;      // [0] pos, [1] fill_end
   int *d_in;         // max_seq + 1 input tokens by position
@@ -73,6 +74,7 @@ static int config_supported(const int32_t *cfg) {
   const int dm = cfg[1], hd = cfg[5], ff = cfg[6];
   if (hd % 2 != 0 || hd > 512) return 0;
   if (dm > 32768 || ff > 32768 || cfg[3] * hd > 32768) return 0;
+  if (cfg[7] > 16384) return 0;          // attention keeps a head's softmax weights in LDS
   return 1;
 }
 
@@ -164,8 +166,12 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
   size_t o_o = TAKE((size_t)d->qd * 4);
   size_t o_gu = TAKE((size_t)2 * d->dff * 4);
   size_t o_logits = TAKE((size_t)d->vocab * 4);
-  size_t o_scores = TAKE((size_t)d->H * d->max_seq * 4);
+  size_t o_scores = TAKE(qhip_attention_scratch(d->H, d->max_seq) * 4);
   size_t o_as = TAKE(64);
+  size_t o_obm = TAKE((size_t)qhip_attention_nbm(d->H, d->hd) * 4);
+  size_t o_hbm = TAKE((size_t)qhip_gemv_blocks(d->dff, d->kp_dm) * 4);
+  size_t o_amv = TAKE((size_t)qhip_gemv_blocks(d->vocab, d->kp_dm) * 4);
+  size_t o_ami = TAKE((size_t)qhip_gemv_blocks(d->vocab, d->kp_dm) * 4);
   size_t o_qa = TAKE((size_t)d->kp_max);
   size_t o_state = TAKE(64);
   size_t o_in = TAKE((size_t)(d->max_seq + 1) * 4);
@@ -195,7 +201,9 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
   d->rope_cos = (float*)(b + o_cos); d->rope_sin = (float*)(b + o_sin);
   d->x = (float*)(b + o_x); d->qkv = (float*)(b + o_qkv); d->q = (float*)(b + o_q);
   d->o = (float*)(b + o_o); d->gu = (float*)(b + o_gu); d->logits = (float*)(b + o_logits);
-  d->scores = (float*)(b + o_scores); d->as = (float*)(b + o_as); d->qa = (int8_t*)(b + o_qa);
+  d->scores = (float*)(b + o_scores); d->as = (float*)(b + o_as);
+  d->obm = (float*)(b + o_obm); d->hbm = (float*)(b + o_hbm);
+  d->amax_v = (float*)(b + o_amv); d->amax_i = (int*)(b + o_ami); d->qa = (int8_t*)(b + o_qa);
   d->d_state = (int*)(b + o_state); d->d_in = (int*)(b + o_in); d->d_out = (int*)(b + o_out);
   if (qhip_fill_zero(d->qa, (size_t)d->kp_max) || qhip_fill_zero(d->d_in, (size_t)(d->max_seq + 1) * 4) ||
       qhip_fill_zero(d->d_state, 64)) {
@@ -526,19 +534,21 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
   for (int l = 0; l < d->L && !rc; l++) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
     rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
-    rc |= qhip_gemv(d->qa, d->as, 1, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], 0, 2);
+    rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
     rc |= qhip_rope_append(d->qkv, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, dpos, d->q, kc, vc, d->max_seq);
-    rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o);
-    rc |= qhip_quant_rows(d->o, 1, d->qd, d->qa, d->kp_qd, d->as);
-    rc |= qhip_gemv(d->qa, d->as, 1, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, 1, 6);
+    rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o, d->obm);
+    rc |= qhip_quant_blocks(d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->qa, d->kp_qd, d->as);
+    rc |= qhip_gemv_dec(1, 6, d->qa, d->as, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, NULL, NULL);
     rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
-    rc |= qhip_gemv(d->qa, d->as, 1, d->wgu[l], d->sgu[l], 2 * d->dff, d->kp_dm, d->gu, NULL, 0, 7);
-    rc |= qhip_swiglu_quant(d->gu, 1, d->dff, d->qa, d->kp_ff, d->as);
-    rc |= qhip_gemv(d->qa, d->as, 1, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, 1, 9);
+    rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
+    rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, qhip_gemv_blocks(d->dff, d->kp_dm), d->qa, d->kp_ff, d->as);
+    rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
   }
   if (!rc) rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_final, d->eps, d->qa, d->kp_dm, d->as);
-  if (!rc) rc |= qhip_gemv(d->qa, d->as, 1, d->head, d->head_s, d->vocab, d->kp_dm, d->logits, NULL, 0, 10);
-  if (!rc) rc |= qhip_argmax_advance(d->logits, d->vocab, d->d_in, d->d_state, d->d_out, d->max_seq);
+  if (!rc) rc |= qhip_gemv_dec(3, 10, d->qa, d->as, d->head, d->head_s, d->vocab, d->kp_dm, d->logits, NULL,
+                               d->amax_v, d->amax_i);
+  if (!rc) rc |= qhip_argmax_final(d->amax_v, d->amax_i, qhip_gemv_blocks(d->vocab, d->kp_dm), d->d_in, d->d_state,
+                                   d->d_out, d->max_seq);
   return rc;
 }
 
@@ -546,7 +556,11 @@ static int profiling = 0;
 
 // Run `n` steps: a graph replay each, or eager launches while profiling.
 static int run_steps(const QDev *d, KVDev *kd, int n) {
-  if (profiling) {
+  // QLLAMA_NO_GRAPH=1 launches each kernel directly (same kernels, same order),
+  // for tools that trace kernels but not graph nodes.
+  static int no_graph = -1;
+  if (no_graph < 0) no_graph = getenv("QLLAMA_NO_GRAPH") != NULL;
+  if (profiling || no_graph) {
     for (int i = 0; i < n; i++) if (enqueue_step(d, kd)) return 1;
     return 0;
   }
