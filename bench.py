@@ -32,6 +32,9 @@ CONFIGS = {
 }
 METRIC = "decode tok/s + % HBM roofline, 8B-shape int8 LLaMA (1 GPU); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per GEMV dispatch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+# (scaled by a plain copy of known size), written by llm-project_amd/profsum.py
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "k_gemv_dec_traffic_8b.json")
 
 
 def load_qllama():
@@ -128,6 +131,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (the scale reference "
+                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -174,15 +180,26 @@ def main():
     step_frac = step_bytes / (t_decode / K) / (HBM_PEAK_GBS * 1e9)
 
     # per-kernel HIP-event timing of the same decode steps (eager launches)
-    Q.profile(True)
-    gm.generate_greedy(tok, NP)
-    prof = Q.profile_read()
-    Q.profile(False)
+    prof = {}
+    if NP:
+        Q.profile(True)
+        gm.generate_greedy(tok, NP)
+        prof = Q.profile_read()
+        Q.profile(False)
+    if args.calib_copy_mib:
+        Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
+        if Q.lib().qllama_test_copy(args.calib_copy_mib << 20) != 0:
+            raise RuntimeError("calibration copy failed")
     gb = gemv_bytes(cfg)
     gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
     gemv_bytes_tok = sum(n * b for (n, b) in gb.values())
     launches_per_tok = sum(n for (n, _) in gb.values())
     achieved = gemv_bytes_tok / (gemv_ms * 1e-3) / 1e9 if gemv_ms > 0 else None
+    traffic = None
+    if args.config == "8b" and os.path.exists(TRAFFIC_JSON):
+        per = json.load(open(TRAFFIC_JSON))["bytes_per_dispatch"]
+        if all(k in per for k in gb):
+            traffic = round(sum(n * per[k] for k, (n, _) in gb.items()) / launches_per_tok)
 
     cpu = None
     if not args.no_cpu_baseline and rank == 0:
@@ -219,11 +236,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": round(gemv_bytes_tok / launches_per_tok),
             "avg_launch_us": round(1e3 * gemv_ms / launches_per_tok, 3) if gemv_ms else None,
         },
-        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())},
+        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
         "cpu_baseline": cpu,
     }
     if rank == 0:

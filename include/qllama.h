@@ -175,6 +175,10 @@ int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, in
 // *out = the sum, info[0] = number of serially evaluated steps, info[1] = 1 when
 // the block fell back to the plain loop.  For parity tests.
 int  qllama_test_seqsum(const float *a, int n, float *out, int *info);
+// One plain device-to-device copy of `bytes` (a multiple of 16) between two
+// fresh buffers, on the library's stream: the known-size reference that
+// scales the HBM traffic counters of a profiler run.
+int  qllama_test_copy(size_t bytes);
 
 #ifdef __cplusplus
 }

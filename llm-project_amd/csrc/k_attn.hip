@@ -5,16 +5,21 @@
 //   s_j   = dot_j * scale,  m = max_j s_j,  e_j = expf(s_j - m)
 //   S     = sum_j e_j             (j = 0..T-1, in order)
 //   w_j   = e_j * (1 / S),  o_d = sum_j w_j * V_jd   (j in order, from 0)
-// Every one of those sums is formed here in the same order, by one lane each;
-// the parallelism is across positions (scores), across (head, d) chains, and
-// between the lanes that form the products w_j * V_jd and the lanes that add them.
+// The dot products and the weighted sums of V are formed here in the same order
+// by one lane each; S is evaluated exactly in parallel (qdev_seqsum.h); maxima
+// do not depend on order.  The parallelism is across positions (scores), across
+// (head, d) chains, and between the lanes that form the products w_j * V_jd and
+// the lane that adds them.
 //
 // Kernel 1 (k_attn_scores): grid (H, ceil(max_seq/256)); one thread per (head,
-//   position) computes dot_j and s_j; each block writes its maximum.
-// Kernel 2 (k_attn_pv): grid (H, ceil(hd/64)), 512 threads.  Softmax weights for
-//   the head in LDS, then wave 0 owns 64 output chains o_d while waves 1-7 stream
-//   V tiles of 128 positions, form the products w_j * V_jd into a double-buffered
-//   LDS tile and keep the V values of the next four tiles in flight in registers.
+//   position) computes dot_j and s_j with the whole K row in flight at once;
+//   each block writes its maximum.
+// Kernel 2 (k_attn_pv): grid (H, ceil(hd/64)), 512 threads.  All threads form
+//   the head's softmax weights in LDS (each thread a run of consecutive
+//   positions, in registers).  Then wave 0 owns 64 output chains o_d while waves
+//   1-7 stream V tiles of 128 positions, three tiles ahead, and store the
+//   products w_j * V_jd as [d][j] tiles (double-buffered in LDS), so that the
+//   chain lane reads four consecutive positions with one 16-byte LDS read.
 #include <hip/hip_runtime.h>
 
 #include "qdev_math.h"
@@ -25,11 +30,14 @@
 namespace {
 
 constexpr int kScoreBlock = 256;
-constexpr int kTile = 128;      // positions per PV tile
-constexpr int kChains = 64;     // output dims per PV block (wave 0's lanes)
+constexpr int kTile = 128;                  // positions per PV tile
+constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
+constexpr int kChains = 64;                 // output dims per PV block (wave 0's lanes)
 constexpr int kPvThreads = 512;
 constexpr int kProducers = kPvThreads - 64;
-constexpr int kSlots = (kTile * kChains + kProducers - 1) / kProducers;   // 19
+constexpr int kPWaves = kProducers / 64;    // 7
+constexpr int kGroups = kTile / 4;          // groups of 4 positions per tile
+constexpr int kGSlots = (kGroups + kPWaves - 1) / kPWaves;   // 5 groups per producer lane
 
 // Barrier for LDS hand-offs only: waits for this wave's LDS operations
 // (lgkmcnt(0)) and then for the other waves, but leaves global loads in flight.
@@ -40,6 +48,7 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+template <int NT>
 __device__ __forceinline__ float block_max(float m, float *red) {
   m = qd::wave_max_f32(m);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -47,11 +56,50 @@ __device__ __forceinline__ float block_max(float m, float *red) {
   if (lane == 0) red[w] = m;
   __syncthreads();
   float r = red[0];
-  for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = fmaxf(r, red[i]);
+#pragma unroll
+  for (int i = 1; i < NT / 64; i++) r = fmaxf(r, red[i]);
   return r;
 }
 
-template <bool VEC4>
+// dot_j for one position: q from LDS, the K row from global, HD known at
+// compile time so that every load of the row is issued before the chain starts.
+template <int HD>
+__device__ __forceinline__ float score_dot(const float *qs, const float *kr) {
+  static_assert(HD % 4 == 0, "");
+  float4 kv[HD / 4];
+  const float4 *k4 = reinterpret_cast<const float4 *>(kr);
+#pragma unroll
+  for (int i = 0; i < HD / 4; i++) kv[i] = k4[i];
+  __builtin_amdgcn_sched_barrier(0);       // the whole row is requested before the chain starts
+  const float4 *q4 = reinterpret_cast<const float4 *>(qs);
+  float dot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < HD / 4; i++) {
+    const float4 qv = q4[i];
+    dot += qv.x * kv[i].x;
+    dot += qv.y * kv[i].y;
+    dot += qv.z * kv[i].z;
+    dot += qv.w * kv[i].w;
+  }
+  return dot;
+}
+
+// runtime head_dim: rows loaded 8 floats ahead of the chain
+__device__ __forceinline__ float score_dot_any(const float *qs, const float *kr, int hd) {
+  float dot = 0.0f;
+  int d = 0;
+  for (; d + 8 <= hd; d += 8) {
+    float k[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) k[i] = kr[d + i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) dot += qs[d + i] * k[i];
+  }
+  for (; d < hd; d++) dot += qs[d] * kr[d];
+  return dot;
+}
+
+template <int HD>
 __global__ __launch_bounds__(kScoreBlock) void k_attn_scores(const float *q, const float *kc, const int *d_pos, int H,
                                                               int KVH, int hd, int max_seq, float scale,
                                                               float *scores, float *bmax, int nch) {
@@ -67,58 +115,79 @@ __global__ __launch_bounds__(kScoreBlock) void k_attn_scores(const float *q, con
   float s = -INFINITY;
   if (j < T) {
     const float *kr = kc + ((size_t)kvh * max_seq + j) * hd;
-    float dot = 0.0f;
-    if (VEC4) {
-      const float4 *k4 = reinterpret_cast<const float4 *>(kr);
-      const float4 *q4 = reinterpret_cast<const float4 *>(qs);
-      for (int i = 0; i < (hd >> 2); i++) {
-        const float4 kv = k4[i], qv = q4[i];
-        dot += qv.x * kv.x;
-        dot += qv.y * kv.y;
-        dot += qv.z * kv.z;
-        dot += qv.w * kv.w;
-      }
-    } else {
-      for (int d = 0; d < hd; d++) dot += qs[d] * kr[d];
-    }
+    const float dot = HD ? score_dot<HD ? HD : 4>(qs, kr) : score_dot_any(qs, kr, hd);
     s = dot * scale;
     scores[(size_t)h * max_seq + j] = s;
   }
-  s = block_max(s, red);
+  s = block_max<kScoreBlock>(s, red);
   if (threadIdx.x == 0) bmax[(size_t)h * nch + c] = s;
 }
 
-// Producer slot k of thread pid covers tile row jj = pid / 64 + kRowsPass * k and
-// column dd = pid % 64 (the producers cover kRowsPass rows of 64 per pass).
-constexpr int kRowsPass = kProducers / kChains;
-static_assert(kProducers == kRowsPass * kChains, "producers must fill whole tile rows");
-
-// Products for tile t: P[jj][dd] = w_j * V_j,d0+dd from prefetched V values.
-// Branch-free (a select per slot) so the compiler can keep counting the V loads
-// that are still in flight instead of waiting for all of them.
-__device__ __forceinline__ void pv_produce(float *P, const float *W, const float (&v)[kSlots], int t, int T, int pid) {
-  const int jj0 = pid >> 6, dd = pid & 63;
+// Softmax weights of one head into W[0..T) (llama.c:566-571): thread t forms
+// e_j for j in [t*CM, t*CM + CM) in registers, the block evaluates their
+// sequential sum exactly, then w_j = e_j * (1 / S).
+template <int CM>
+__device__ __forceinline__ void softmax_weights(const float *sh, int T, float m, float *W, qd::SeqScratch &seq) {
+  const int j0 = threadIdx.x * CM;
+  float e[CM];
 #pragma unroll
-  for (int k = 0; k < kSlots; k++) {
-    const int jj = jj0 + kRowsPass * k;
-    if (kRowsPass * k + kRowsPass - 1 < kTile || jj < kTile) {   // compile-time true except the last slot
-      const int j = t * kTile + jj;
-      const float w = W[min(j, T - 1)];
-      const float p = w * v[k];
-      P[min(jj, kTile - 1) * kChains + dd] = (j < T && jj < kTile) ? p : 0.0f;
-    }
-  }
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(sh[j0 + c] - m) : 0.0f;
+  const float sum = qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m); });
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int c = 0; c < CM; c++)
+    if (j0 + c < T) W[j0 + c] = e[c] * inv;
 }
 
-// V values of tile t for this thread's slots; out-of-range slots read an
-// in-bounds element and are zeroed by the producer's select.
-__device__ __forceinline__ void pv_load(float (&v)[kSlots], const float *Vh, int t, int T, int hd, int d0, int pid) {
-  const int jj0 = pid >> 6;
-  const int col = min(d0 + (pid & 63), hd - 1);
+// V values of tile t for this producer lane: slot g covers positions
+// t*kTile + 4*(pw + kPWaves*g) + 0..3 at column d0 + (pid & 63).  The loads go
+// through a buffer resource over this KV head's rows [0, max_seq): the lane's
+// offset of each slot is fixed (vo) and the tile adds one scalar, so a load
+// costs one add of address arithmetic; the whole offset is in the range-checked
+// vector operand, so rows past max_seq (prefetch beyond the last tile) read as
+// 0 without touching memory.  Rows in [T, max_seq) and columns >= hd are
+// zeroed by the producer.
+__device__ __forceinline__ void pv_load(float (&v)[kGSlots][4], __amdgpu_buffer_rsrc_t rs, const int (&vo)[kGSlots],
+                                        int t, int hd) {
+  const int tb = t * kTile * hd * 4;
 #pragma unroll
-  for (int k = 0; k < kSlots; k++) {
-    const int j = min(t * kTile + jj0 + kRowsPass * k, T - 1);
-    v[k] = __builtin_nontemporal_load(&Vh[(size_t)j * hd + col]);
+  for (int g = 0; g < kGSlots; g++)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      v[g][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, vo[g] + tb + i * hd * 4, 0, 0));
+}
+
+// Products of tile t into the [d][j] tile B: B[dd*kTS + jj] = w_j * V_j,d0+dd,
+// +0 for positions >= T or dims >= hd (adding +0 leaves a chain unchanged).
+// Only a partial tile or a partial column block needs the masks; they are
+// applied bitwise, so that no branch delays the LDS reads or splits the quad.
+__device__ __forceinline__ float pv_mask(float p, bool keep) {
+  return __uint_as_float(__float_as_uint(p) & (keep ? 0xffffffffu : 0u));
+}
+
+__device__ __forceinline__ void pv_produce(float *B, const float *W, const float (&v)[kGSlots][4], int t, int T,
+                                           bool cols_full, bool col_ok, int pid) {
+  const int pw = pid >> 6, dd = pid & 63;
+  const bool full = cols_full && (t + 1) * kTile <= T;
+#pragma unroll
+  for (int g = 0; g < kGSlots; g++) {
+    const int grp = pw + kPWaves * g;
+    if (kPWaves * (g + 1) <= kGroups || grp < kGroups) {      // compile-time true except the last slot
+      const int jb = t * kTile + 4 * grp;
+      const float4 w = *reinterpret_cast<const float4 *>(W + jb);
+      float4 p;
+      p.x = w.x * v[g][0];
+      p.y = w.y * v[g][1];
+      p.z = w.z * v[g][2];
+      p.w = w.w * v[g][3];
+      if (!full) {
+        p.x = pv_mask(p.x, col_ok && jb + 0 < T);
+        p.y = pv_mask(p.y, col_ok && jb + 1 < T);
+        p.z = pv_mask(p.z, col_ok && jb + 2 < T);
+        p.w = pv_mask(p.w, col_ok && jb + 3 < T);
+      }
+      *reinterpret_cast<float4 *>(B + dd * kTS + 4 * grp) = p;
+    }
   }
 }
 
@@ -127,49 +196,63 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
                                                         int nch, float *o, float *obm) {
   extern __shared__ float lds[];
   __shared__ float red[kPvThreads / 64];
-  __shared__ float s_inv;
-  __shared__ qd::SeqSumScratch seq;
+  __shared__ qd::SeqScratch seq;
   const int h = blockIdx.x, d0 = blockIdx.y * kChains;
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
-  const int wcap = (max_seq + 3) & ~3;
+  const int wcap = (max_seq + kTile - 1) / kTile * kTile;
   float *W = lds;
-  float *P = lds + wcap;                                 // 2 x kTile x kChains
+  float *P = lds + wcap;                                 // 2 tiles of kChains x kTS
   const int tid = threadIdx.x;
+  const int ntile = (T + kTile - 1) / kTile;
+  const float *Vh = vc + (size_t)kvh * max_seq * hd;
+
+  // the producers' first V tiles are requested before the softmax (three tiles
+  // of loads in flight per lane: 60, within what one wave can have outstanding;
+  // loads past the last tile read in-bounds rows and are never used)
+  const int pid = tid - 64;
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void *)Vh, (short)0, max_seq * hd * 4, 0x00020000);
+  const bool cols_full = d0 + kChains <= hd, col_ok = d0 + (pid & 63) < hd;
+  int vo[kGSlots];
+#pragma unroll
+  for (int g = 0; g < kGSlots; g++) {
+    const int grp = (pid >> 6) + kPWaves * g;
+    vo[g] = grp < kGroups ? (4 * grp * hd + d0 + (pid & 63)) * 4 : 0x40000000;   // unused slot: out of range
+  }
+  float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
+  if (tid >= 64) {
+    pv_load(r0, vrs, vo, 0, hd);
+    pv_load(r1, vrs, vo, 1, hd);
+    pv_load(r2, vrs, vo, 2, hd);
+  }
 
   // softmax weights of head h (llama.c:557-572)
   const int nc = (T + kScoreBlock - 1) / kScoreBlock;
   float m = -INFINITY;
   for (int c = tid; c < nc; c += kPvThreads) m = fmaxf(m, bmax[(size_t)h * nch + c]);
-  m = block_max(m, red);
+  m = block_max<kPvThreads>(m, red);
   const float *sh = scores + (size_t)h * max_seq;
-  for (int j = tid; j < T; j += kPvThreads) W[j] = qd::expf_glibc(sh[j] - m);
-  __syncthreads();
-  {
-    const float sum = qd::seq_sum_nonneg<kPvThreads>(W, T, seq);   // llama.c:567, exactly
-    if (tid == 0) s_inv = 1.0f / sum;
-  }
-  __syncthreads();
-  const float inv = s_inv;
-  for (int j = tid; j < T; j += kPvThreads) W[j] = W[j] * inv;
+  if (T <= kPvThreads * 4) softmax_weights<4>(sh, T, m, W, seq);
+  else if (T <= kPvThreads * 8) softmax_weights<8>(sh, T, m, W, seq);
+  else if (T <= kPvThreads * 16) softmax_weights<16>(sh, T, m, W, seq);
+  else softmax_weights<32>(sh, T, m, W, seq);
   __syncthreads();
 
   // o_d = sum_j w_j * V_jd, j in order (llama.c:570-575)
-  const int ntile = (T + kTile - 1) / kTile;
-  const float *Vh = vc + (size_t)kvh * max_seq * hd;
   if (tid < 64) {
     const int d = d0 + tid;
     float acc = 0.0f;
     for (int t = 0; t < ntile; t++) {
       lds_barrier();
-      const float *Pt = P + (t & 1) * kTile * kChains + tid;
-      const int nj = min(kTile, T - t * kTile);
-      if (nj == kTile) {
-        // straight-line over the whole tile: the reads run ahead of the add chain
+      const float *Pt = P + (t & 1) * kChains * kTS + tid * kTS;
 #pragma unroll
-        for (int jj = 0; jj < kTile; jj++) acc += Pt[jj * kChains];
-      } else {
-        for (int jj = 0; jj < nj; jj++) acc += Pt[jj * kChains];
+      for (int jj = 0; jj < kTile; jj += 4) {
+        const float4 p = *reinterpret_cast<const float4 *>(Pt + jj);
+        acc += p.x;
+        acc += p.y;
+        acc += p.z;
+        acc += p.w;
       }
     }
     if (d < hd) o[(size_t)h * hd + d] = acc;
@@ -178,43 +261,45 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
       if (tid == 0) obm[(size_t)h * gridDim.y + blockIdx.y] = mo;
     }
   } else {
-    // Producers: tile k is formed from register set k % 4 into LDS buffer k % 2;
-    // its V values are requested four tiles ahead of use.
-    const int pid = tid - 64;
-    float r0[kSlots], r1[kSlots], r2[kSlots], r3[kSlots];
-    float *B0 = P, *B1 = P + kTile * kChains;
-    pv_load(r0, Vh, 0, T, hd, d0, pid);
-    if (ntile > 1) pv_load(r1, Vh, 1, T, hd, d0, pid);
-    if (ntile > 2) pv_load(r2, Vh, 2, T, hd, d0, pid);
-    if (ntile > 3) pv_load(r3, Vh, 3, T, hd, d0, pid);
-    pv_produce(B0, W, r0, 0, T, pid);
-    if (ntile > 4) pv_load(r0, Vh, 4, T, hd, d0, pid);
-    for (int t = 0; t < ntile; t += 4) {
+    // tile k is formed from register set k % 3 into LDS buffer k % 2; its V
+    // values are requested three tiles ahead of use
+    float *B0 = P, *B1 = P + kChains * kTS;
+    pv_produce(B0, W, r0, 0, T, cols_full, col_ok, pid);
+    pv_load(r0, vrs, vo, 3, hd);
+    for (int t = 0;; t += 6) {
       lds_barrier();                                   // consumer takes tile t
-      if (t + 1 < ntile) {
-        pv_produce(B1, W, r1, t + 1, T, pid);
-        if (t + 5 < ntile) pv_load(r1, Vh, t + 5, T, hd, d0, pid);
-        lds_barrier();                                 // consumer takes tile t+1
-        if (t + 2 < ntile) {
-          pv_produce(B0, W, r2, t + 2, T, pid);
-          if (t + 6 < ntile) pv_load(r2, Vh, t + 6, T, hd, d0, pid);
-          lds_barrier();                               // tile t+2
-          if (t + 3 < ntile) {
-            pv_produce(B1, W, r3, t + 3, T, pid);
-            if (t + 7 < ntile) pv_load(r3, Vh, t + 7, T, hd, d0, pid);
-            lds_barrier();                             // tile t+3
-            if (t + 4 < ntile) {
-              pv_produce(B0, W, r0, t + 4, T, pid);
-              if (t + 8 < ntile) pv_load(r0, Vh, t + 8, T, hd, d0, pid);
-            }
-          }
-        }
-      }
+      if (t + 1 >= ntile) break;
+      pv_produce(B1, W, r1, t + 1, T, cols_full, col_ok, pid);
+      pv_load(r1, vrs, vo, t + 4, hd);
+      lds_barrier();                                   // tile t+1
+      if (t + 2 >= ntile) break;
+      pv_produce(B0, W, r2, t + 2, T, cols_full, col_ok, pid);
+      pv_load(r2, vrs, vo, t + 5, hd);
+      lds_barrier();                                   // tile t+2
+      if (t + 3 >= ntile) break;
+      pv_produce(B1, W, r0, t + 3, T, cols_full, col_ok, pid);
+      pv_load(r0, vrs, vo, t + 6, hd);
+      lds_barrier();                                   // tile t+3
+      if (t + 4 >= ntile) break;
+      pv_produce(B0, W, r1, t + 4, T, cols_full, col_ok, pid);
+      pv_load(r1, vrs, vo, t + 7, hd);
+      lds_barrier();                                   // tile t+4
+      if (t + 5 >= ntile) break;
+      pv_produce(B1, W, r2, t + 5, T, cols_full, col_ok, pid);
+      pv_load(r2, vrs, vo, t + 8, hd);
+      lds_barrier();                                   // tile t+5
+      if (t + 6 >= ntile) break;
+      pv_produce(B0, W, r0, t + 6, T, cols_full, col_ok, pid);
+      pv_load(r0, vrs, vo, t + 9, hd);
     }
   }
 }
 
 size_t g_pv_attr_bytes = 0;   // dynamic LDS the PV kernel is currently allowed
+
+size_t pv_lds_bytes(int max_seq) {
+  return ((size_t)(max_seq + kTile - 1) / kTile * kTile + 2 * kChains * kTS) * 4;
+}
 
 }  // namespace
 
@@ -222,21 +307,36 @@ extern "C" int qhip_attention(const float *q, const float *kc, const float *vc, 
                               int n_kv, int hd, int max_seq, float scale, float *scores, float *o, float *obm) {
   const int nch = (max_seq + kScoreBlock - 1) / kScoreBlock;
   float *bmax = scores + (size_t)n_heads * max_seq;
-  const size_t pv_lds = ((size_t)((max_seq + 3) & ~3) + 2 * kTile * kChains) * 4;
-  if (pv_lds + sizeof(qd::SeqSumScratch) + 1024 > 160 * 1024)
+  const size_t pv_lds = pv_lds_bytes(max_seq);
+  if (max_seq > kPvThreads * 32 || pv_lds + sizeof(qd::SeqScratch) + 1024 > 160 * 1024)
     return qh::fail_msg("attention: max_seq too large for the LDS-resident weights");
+  if ((long long)max_seq * hd >= (1LL << 27))      // V byte offsets (plus prefetch) stay below 2^30
+    return qh::fail_msg("attention: KV head region too large");
   if (pv_lds > 64 * 1024 && pv_lds > g_pv_attr_bytes) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_pv),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)pv_lds);
     if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_attn_pv)", e);
     g_pv_attr_bytes = pv_lds;
   }
-  if ((hd & 3) == 0) {
-    QH_LAUNCH(QK_ATTN, k_attn_scores<true>, dim3(n_heads, nch), dim3(kScoreBlock), (size_t)hd * 4, q, kc, d_pos,
-              n_heads, n_kv, hd, max_seq, scale, scores, bmax, nch);
-  } else {
-    QH_LAUNCH(QK_ATTN, k_attn_scores<false>, dim3(n_heads, nch), dim3(kScoreBlock), (size_t)hd * 4, q, kc, d_pos,
-              n_heads, n_kv, hd, max_seq, scale, scores, bmax, nch);
+  const dim3 sgrid(n_heads, nch);
+  const size_t qbytes = ((size_t)hd + 4) * 4;
+  switch (hd) {
+    case 128:
+      QH_LAUNCH(QK_ATTN, k_attn_scores<128>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+                max_seq, scale, scores, bmax, nch);
+      break;
+    case 64:
+      QH_LAUNCH(QK_ATTN, k_attn_scores<64>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+                max_seq, scale, scores, bmax, nch);
+      break;
+    case 48:
+      QH_LAUNCH(QK_ATTN, k_attn_scores<48>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+                max_seq, scale, scores, bmax, nch);
+      break;
+    default:
+      QH_LAUNCH(QK_ATTN, k_attn_scores<0>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+                max_seq, scale, scores, bmax, nch);
+      break;
   }
   QH_LAUNCH(QK_ATTN, k_attn_pv, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores, bmax,
             vc, d_pos, n_heads, n_kv, hd, max_seq, nch, o, obm);

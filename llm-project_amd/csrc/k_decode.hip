@@ -47,40 +47,60 @@ __global__ void k_embed(const int8_t *wte, const float *s, int dm, const int *d_
 }
 
 // One block per row: rmsnorm.c:7-21 then the activation quantization of qmatmul.
-// The squares are formed in parallel and their sequential float sum (the
-// reference's loop order) is evaluated exactly by qd::seq_sum_nonneg.
-__global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float *x, int dm, const float *gamma, float eps,
-                                                         int8_t *qa, int kpad, float *as) {
-  extern __shared__ float lds[];          // dm values, then dm squares
-  __shared__ float red[16];
-  __shared__ float s_r;
-  __shared__ qd::SeqSumScratch seq;
+// Thread t holds elements [t*CM, t*CM + CM) (NT*CM >= kpad); the sequential
+// float sum of the squares (the reference's loop order) is evaluated exactly
+// by qd::seq_sum_nonneg.
+template <int NT, int CM>
+__global__ __launch_bounds__(NT) void k_rmsnorm_quant(const float *x, int dm, const float *gamma, float eps,
+                                                       int8_t *qa, int kpad, float *as) {
+  static_assert(CM % 4 == 0, "chunk of whole 16-byte words");
+  __shared__ float red[NT / 64];
+  __shared__ qd::SeqScratch seq;
   const int row = blockIdx.x;
   const float *xr = x + (size_t)row * dm;
-  float *v = lds, *sq = lds + ((dm + 3) & ~3);
-  for (int j = threadIdx.x; j < dm; j += blockDim.x) {
-    const float a = xr[j];
-    v[j] = a;
-    sq[j] = a * a;
+  const int j0 = threadIdx.x * CM;
+  float v[CM], sq[CM];
+  if (j0 + CM <= dm && (dm & 3) == 0) {
+#pragma unroll
+    for (int c = 0; c < CM; c += 4) {
+      const float4 t = *reinterpret_cast<const float4 *>(xr + j0 + c);
+      v[c] = t.x; v[c + 1] = t.y; v[c + 2] = t.z; v[c + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CM; c++) v[c] = j0 + c < dm ? xr[j0 + c] : 0.0f;
   }
-  __syncthreads();
-  float ms = qd::seq_sum_nonneg<1024>(sq, dm, seq);       // rmsnorm.c:15, exactly
-  if (threadIdx.x == 0) {
-    const float inv_n = 1.0f / (float)dm;
-    ms *= inv_n;
-    s_r = 1.0f / sqrtf(ms + eps);
-  }
-  __syncthreads();
-  const float r = s_r;
+#pragma unroll
+  for (int c = 0; c < CM; c++) sq[c] = v[c] * v[c];
+  float ms = qd::seq_sum_nonneg<NT, CM>(sq, dm, seq, [&](int i) { return xr[i] * xr[i]; });   // rmsnorm.c:15
+  const float inv_n = 1.0f / (float)dm;
+  ms *= inv_n;
+  const float r = 1.0f / sqrtf(ms + eps);
   float mx = 0.0f;
-  for (int j = threadIdx.x; j < dm; j += blockDim.x) {
-    const float y = v[j] * r * gamma[j];
-    v[j] = y;
-    mx = fmaxf(mx, fabsf(y));
+#pragma unroll
+  for (int c = 0; c < CM; c++) {
+    v[c] = j0 + c < dm ? v[c] * r * gamma[j0 + c] : 0.0f;
+    mx = fmaxf(mx, fabsf(v[c]));
   }
-  mx = block_max(mx, red);
+  mx = qd::wave_max_f32(mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
-  quantize_row_lds(v, dm, kpad, mx, qa + (size_t)row * kpad, as + row);
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
+  const float a_s = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+  const float inv = 1.0f / a_s;
+  int8_t *qr = qa + (size_t)row * kpad;
+#pragma unroll
+  for (int c = 0; c < CM; c += 4) {
+    if (j0 + c < kpad) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) w |= (uint32_t)(uint8_t)(int8_t)qd::quant_i8(v[c + e], inv) << (8 * e);
+      *reinterpret_cast<uint32_t *>(qr + j0 + c) = w;
+    }
+  }
+  if (threadIdx.x == 0) as[row] = a_s;
 }
 
 // One block per row: quantize v (rows, n) -> qa (rows, kpad), as (rows).
@@ -246,9 +266,17 @@ int qhip_embed(const int8_t *wte, const float *wte_s, int dm, const int *d_in, c
 
 int qhip_rmsnorm_quant(const float *x, int rows, int dm, const float *gamma, float eps, int8_t *qa, int kpad,
                        float *as) {
-  if (dm > qd::kSeqMaxN) return qh::fail_msg("rmsnorm_quant: d_model above 16384");
-  QH_LAUNCH(QK_RMSNORM, k_rmsnorm_quant, dim3(rows), dim3(1024), (size_t)((dm + 3) & ~3) * 8, x, dm, gamma, eps, qa,
-            kpad, as);
+  if (kpad % 4 || kpad < dm) return qh::fail_msg("rmsnorm_quant: bad row padding");
+  if (kpad <= 1024)
+    QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_quant<64, 16>), dim3(rows), dim3(64), 0, x, dm, gamma, eps, qa, kpad, as);
+  else if (kpad <= 4096)
+    QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_quant<256, 16>), dim3(rows), dim3(256), 0, x, dm, gamma, eps, qa, kpad, as);
+  else if (kpad <= 8192)
+    QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_quant<256, 32>), dim3(rows), dim3(256), 0, x, dm, gamma, eps, qa, kpad, as);
+  else if (kpad <= 16384)
+    QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_quant<512, 32>), dim3(rows), dim3(512), 0, x, dm, gamma, eps, qa, kpad, as);
+  else
+    return qh::fail_msg("rmsnorm_quant: d_model above 16384");
   return 0;
 }
 
@@ -356,28 +384,51 @@ extern "C" int qllama_gqa_decode(const float *q, const float *k, const float *v,
 
 namespace {
 __global__ __launch_bounds__(1024) void k_seqsum_test(const float *a, int n, float *out, int *info) {
-  extern __shared__ float lds[];
-  __shared__ qd::SeqSumScratch S;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = a[i];
-  __syncthreads();
-  const float s = qd::seq_sum_nonneg<1024>(lds, n, S);
-  if (threadIdx.x == 0) { out[0] = s; info[0] = S.nhard; info[1] = S.fail; }
+  constexpr int CM = 16;
+  float t[CM];
+  const int i0 = threadIdx.x * CM;
+#pragma unroll
+  for (int c = 0; c < CM; c++) t[c] = i0 + c < n ? a[i0 + c] : 0.0f;
+  __shared__ qd::SeqScratch S;
+  const float s = qd::seq_sum_nonneg<1024, CM>(t, n, S, [&](int i) { return a[i]; }, info);
+  if (threadIdx.x == 0) out[0] = s;
 }
 }  // namespace
 
 extern "C" int qllama_test_seqsum(const float *a, int n, float *out, int *info) {
   if (qhip_init()) return 1;
-  if (n < 0 || n > qd::kSeqMaxN) return qh::fail_msg("seqsum: n out of range");
+  if (n < 0 || n > 16384) return qh::fail_msg("seqsum: n out of range");
   float *da = (float *)qhip_malloc((size_t)(n + 4) * 4), *dout = (float *)qhip_malloc(16);
   int *dinfo = (int *)qhip_malloc(16);
   int rc = (!da || !dout || !dinfo) ? 1 : 0;
   if (!rc) rc = qhip_h2d(da, a, (size_t)n * 4);
   if (!rc) {
-    hipLaunchKernelGGL(k_seqsum_test, dim3(1), dim3(1024), (size_t)((n + 3) & ~3) * 4 + 16, qh::stream(), da, n, dout,
-                       dinfo);
+    hipLaunchKernelGGL(k_seqsum_test, dim3(1), dim3(1024), 0, qh::stream(), da, n, dout, dinfo);
     rc = qh::check_launch("k_seqsum_test");
   }
   if (!rc) rc = qhip_d2h(out, dout, 4) || qhip_d2h(info, dinfo, 8);
   qhip_free(da); qhip_free(dout); qhip_free(dinfo);
+  return rc;
+}
+
+namespace {
+typedef int v4i __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_copy_v4(const v4i *src, v4i *dst, size_t n16) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = __builtin_nontemporal_load(&src[i]);
+}
+}  // namespace
+
+extern "C" int qllama_test_copy(size_t bytes) {
+  if (qhip_init()) return 1;
+  if (bytes == 0 || bytes % 16) return qh::fail_msg("test_copy: size must be a positive multiple of 16");
+  void *a = qhip_malloc(bytes), *b = qhip_malloc(bytes);
+  int rc = (!a || !b) ? 1 : 0;
+  if (!rc) {
+    hipLaunchKernelGGL(k_copy_v4, dim3(4096), dim3(256), 0, qh::stream(), (const v4i *)a, (v4i *)b, bytes / 16);
+    rc = qh::check_launch("k_copy_v4");
+  }
+  if (!rc) rc = qhip_device_sync();
+  qhip_free(a); qhip_free(b);
   return rc;
 }

@@ -9,24 +9,30 @@
 // multiple of u = 2^(e-23), so s + a_i rounds to s + u * rne(a_i / u): the step
 // adds an integer number of u that depends on a_i alone (unless a_i / u ends in
 // exactly .5, where the tie goes to the even neighbour and depends on s).  Sums
-// of integers do not depend on their order.
+// of integers do not depend on their order.  Grids are named by g = max(E, 1),
+// E the biased exponent field, so that 0, the subnormals and [2^-126, 2^-125)
+// share g = 1 and unit 2^-149; the unit of grid g is 2^(g-150).
 //
-// Method (one block, scratch in LDS):
-//   1. P_i = a_0 + ... + a_{i-1} (a float block scan) predicts the binade of
-//      each partial sum s_i.  Steps whose prediction is ambiguous (P_i or P_{i+1}
-//      near a power of two), that change binade, or that are exact ties are hard.
-//   2. Every other (easy) step i contributes k_i = rne(a_i / u_i); a block scan
-//      of the k_i gives the integer total of each run of easy steps between two
-//      hard steps, and that total times the run's u is an exact float.
-//   3. One lane walks the hard steps only: s += run total; s = s + a_hard (a real
-//      float add, so ties and binade changes round exactly as the loop does).
-//   4. Every run is checked afterwards: its exact start must lie in the binade
-//      predicted for it and its exact end must not pass the top of that binade
-//      (reaching it exactly is consistent).  Partial sums are monotone, so then
-//      every step of the run was on that grid.  If any check fails, or there are
-//      more hard steps than the scratch holds, the block falls back to the plain
-//      sequential loop.  The result is the sequential sum in every case; the
-//      prediction margin only decides how often the fast path applies.
+// Method (one block; thread t holds terms [t*CM, t*CM + CM) in registers):
+//   1. P, a float block scan of the chunk totals, predicts every partial sum.
+//      A float sum of non-negative terms is never below the largest term it has
+//      added, so L_i = max(a_0..a_{i-1}) bounds s_i from below for certain.
+//      Step i is easy when max(P_i*(1-rho), L_i) and P_{i+1}*(1+rho) lie on one
+//      grid g and a_i / u_g is not a tie; it then adds k_i = rne(a_i / u_g).
+//      Other steps are hard.  (L keeps the common softmax case, a sum that
+//      sits just above the 1.0 of its largest term, off the binade edge.)  Consecutive easy steps of one thread share their grid
+//      (P is monotone), and a thread-boundary check makes every run of easy
+//      steps between two hard steps share one grid.
+//   2. A block scan of the k_i gives each run's integer total K_m.
+//   3. One lane walks the hard steps: s += K_m * u (exact when the run is on its
+//      grid), then s = s + a_hard, a real float add.  On the way it proves every
+//      run that has steps, K_m = 0 included: the run starts inside its grid's
+//      binade and K_m * u fits below the binade's top.  Partial sums are monotone, so every step of the run was
+//      on that grid; ending exactly at the top is consistent with both grids.
+//   4. If a proof fails, or there are more hard steps than the scratch holds,
+//      thread 0 runs the plain loop.  The result is the sequential sum in every
+//      case; the prediction margin rho only decides how often the fast path
+//      applies.
 #ifndef QDEV_SEQSUM_H
 #define QDEV_SEQSUM_H
 
@@ -35,87 +41,27 @@
 
 namespace qd {
 
-constexpr int kSeqMaxN = 16384;            // longest sum supported
-constexpr int kSeqMaxHard = 480;           // hard steps held in LDS
+constexpr int kSeqMaxHard = 512;           // hard steps held in LDS
 constexpr int kSeqMaxWaves = 16;           // blocks of up to 1024 threads
 
-struct SeqSumScratch {
-  float pscan[kSeqMaxWaves + 1];
-  unsigned kscan[kSeqMaxWaves + 1];
-  int hscan[kSeqMaxWaves + 1];
-  int hidx[kSeqMaxHard];
+struct SeqScratch {
+  float wf[kSeqMaxWaves];
+  float wm[kSeqMaxWaves];
+  unsigned wk[kSeqMaxWaves];
+  int wh[kSeqMaxWaves];
+  int wg[kSeqMaxWaves];
   unsigned hk[kSeqMaxHard];
+  int hx[kSeqMaxHard];
   float ha[kSeqMaxHard];
-  int hafter[kSeqMaxHard];
-  float sa[kSeqMaxHard];
-  float segu[kSeqMaxHard + 1];
-  float sb[kSeqMaxHard + 1];
+  int hg[kSeqMaxHard];
   unsigned ktot;
   int nhard;
-  int fail;
+  int bad;
+  int fell;
   float result;
 };
 
-// Binade of a partial sum predicted as P >= 0: e for P in [2^e, 2^(e+1)), -127
-// for [0, 2^-126) (one grid, 2^-149, covers 0 and the subnormals).  amb = 1
-// when P is within relative margin rho of an edge.
-__device__ __forceinline__ int seq_binade(float P, float rho, int &amb) {
-  const uint32_t b = __float_as_uint(P);
-  const int ex = (int)((b >> 23) & 0xff);
-  if (ex == 0) {
-    amb = P > 0x1p-126f * (1.0f - rho);
-    return -127;
-  }
-  const float m = __uint_as_float((b & 0x007FFFFFu) | 0x3F800000u);   // P / 2^e in [1, 2)
-  amb = (m < 1.0f + rho) || (m > 2.0f - 2.0f * rho);
-  return ex - 127;
-}
-
-// binade of an exact float partial sum s >= 0
-__device__ __forceinline__ int seq_binade_f(float s) {
-  const int ex = (int)((__float_as_uint(s) >> 23) & 0xff);
-  return ex == 0 ? -127 : ex - 127;
-}
-
-__device__ __forceinline__ float seq_unit(int e) {        // grid spacing of binade e (>= 2^-149)
-  return e == -127 ? 0x1p-149f : ldexpf(1.0f, e - 23);
-}
-
-__device__ __forceinline__ float seq_top(int e) {         // 2^(e+1), the binade's upper edge
-  return __uint_as_float((uint32_t)(e + 1 + 127) << 23);
-}
-
-// a scaled to units of the grid of binade e; exact where it is used (a < 2^(e+1))
-__device__ __forceinline__ float seq_scaled(float a, int e) {
-  return e == -127 ? ldexpf(a, 149) : ldexpf(a, 23 - e);
-}
-
-// Step i takes s_i (predicted by P) to s_i + a.  Returns true when the step is
-// easy, with k its exact increment in units of the grid; eafter is the binade
-// predicted for s_{i+1}.  rho is the relative prediction margin.
-__device__ __forceinline__ bool seq_classify(float P, float a, float rho, int &k, int &eafter) {
-  int amb0, amb1;
-  const int e0 = seq_binade(P, rho, amb0);
-  const int e1 = seq_binade(P + a, rho, amb1);
-  eafter = e1;
-  k = 0;
-  if (amb0 || amb1 || e0 != e1) return false;
-  const float t = seq_scaled(a, e0);
-  if (t - floorf(t) == 0.5f) return false;           // exact tie: the parity of s decides
-  k = (int)__builtin_rintf(t);
-  return true;
-}
-
-// Prediction margin for the steps up to index i, relative to the partial sum:
-// 16 standard deviations of the rounding error a sequential sum of i terms
-// accumulates (each below half a unit in the last place), plus the error of the
-// float prefix scan that forms the prediction (a few dozen roundings).
-__device__ __forceinline__ float seq_margin(int i) {
-  return 0x1p-20f * sqrtf((float)(i + 2)) + 0x1p-17f;
-}
-
 // Wave inclusive scan by DPP row shifts and row broadcasts (32-bit lanes).
-
 __device__ __forceinline__ unsigned seq_dpp_u(unsigned x, int sel) {
   int v = (int)x, r = 0;
   switch (sel) {
@@ -135,6 +81,12 @@ __device__ __forceinline__ float seq_wave_scan(float x) {
   return x;
 }
 
+__device__ __forceinline__ float seq_wave_scan_max(float x) {     // x >= 0
+#pragma unroll
+  for (int k = 0; k < 6; k++) x = fmaxf(x, __uint_as_float(seq_dpp_u(__float_as_uint(x), k)));
+  return x;
+}
+
 __device__ __forceinline__ unsigned seq_wave_scan(unsigned x) {
 #pragma unroll
   for (int k = 0; k < 6; k++) x += seq_dpp_u(x, k);
@@ -147,154 +99,182 @@ __device__ __forceinline__ int seq_wave_scan(int x) {
   return x;
 }
 
-// Exclusive block scans of up to two 32-bit quantities at once: wave scans by
-// DPP, then wave 0 scans the wave totals.
-template <int NT, typename A, typename B>
-__device__ __forceinline__ void seq_block_scan2(A va, B vb, A *ta, B *tb, A &ea, B &eb, A &tota, B &totb) {
-  constexpr int NW = NT / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const A xa = seq_wave_scan(va);
-  const B xb = seq_wave_scan(vb);
-  if (lane == 63) { ta[wave] = xa; tb[wave] = xb; }
-  __syncthreads();
-  if (wave == 0) {
-    const A a0 = lane < NW ? ta[lane] : (A)0;
-    const B b0 = lane < NW ? tb[lane] : (B)0;
-    const A wa = seq_wave_scan(a0);
-    const B wb = seq_wave_scan(b0);
-    if (lane < NW) { ta[lane] = wa - a0; tb[lane] = wb - b0; }
-    if (lane == NW - 1) { ta[NW] = wa; tb[NW] = wb; }
-  }
-  __syncthreads();
-  ea = ta[wave] + xa - va;
-  eb = tb[wave] + xb - vb;
-  tota = ta[NW];
-  totb = tb[NW];
-  __syncthreads();
-}
+// grid of a float p >= 0 (see above)
+__device__ __forceinline__ int seq_grid(float p) { return max((int)(__float_as_uint(p) >> 23), 1); }
 
-// The plain loop, for the fallback and as the definition of the result.
-__device__ __forceinline__ float seq_serial(const float *a, int n) {
+// The plain loop over term(0..n), for the fallback and as the definition.
+template <typename Term>
+__device__ float seq_serial(int n, Term term) {
   float s = 0.0f;
-  int i = 0;
-  const float4 *a4 = reinterpret_cast<const float4 *>(a);
-  for (; i + 4 <= n; i += 4) {
-    const float4 v = a4[i >> 2];
-    s += v.x;
-    s += v.y;
-    s += v.z;
-    s += v.w;
-  }
-  for (; i < n; i++) s += a[i];
+  for (int i = 0; i < n; i++) s += term(i);
   return s;
 }
 
-// The sequential float32 sum of a[0..n), a in LDS (16-byte aligned), every a_i
-// finite and >= 0.  All NT threads of the block (NT = blockDim.x, a multiple of
-// 64, at most 1024) must call it; all get the result.  n <= kSeqMaxN.
-template <int NT>
-__device__ float seq_sum_nonneg(const float *a, int n, SeqSumScratch &S) {
+// The sequential float32 sum of n terms, every one finite and >= 0.  Thread t
+// of the NT-thread block (NT = blockDim.x, a multiple of 64, at most 1024) holds
+// terms t*CM .. t*CM+CM-1 in a[], zero past n; n <= NT*CM.  term(i) returns term
+// i again, for the rare fallback.  All threads must call it; all get the result.
+// info (optional, written by thread 0): number of hard steps, 1 if the fallback ran.
+template <int NT, int CM, typename Term>
+__device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term term, int *info = nullptr) {
   static_assert(NT % 64 == 0 && NT / 64 <= kSeqMaxWaves, "block size");
-  const int tid = threadIdx.x;
-  const int per = (n + NT - 1) / NT;
-  const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+  static_assert(CM >= 1 && CM <= 32, "terms per thread");
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // 1. predicted partial sums (float prefix; its own error is inside the margin)
-  float ls = 0.0f;
-  for (int i = i0; i < i1; i++) ls += a[i];
-  float P, ptot;
-  int idummy, idtot;
-  seq_block_scan2<NT, float, int>(ls, 0, S.pscan, S.hscan, P, idummy, ptot, idtot);
-
-  // 2. classify each step; count the hard ones and total the k of the easy ones
-  // (k totals are kept modulo 2^32: only differences within one run are used,
-  // and a run stays inside one binade, so its total is below 2^23)
-  const float Pstart = P;
-  const float rho = seq_margin(i1);                  // covers every step of this thread
-  unsigned ksum = 0;
-  int nh = 0;
-  for (int i = i0; i < i1; i++) {
-    int k, eafter;
-    const float ai = a[i];
-    if (seq_classify(P, ai, rho, k, eafter)) ksum += (unsigned)k;
-    else nh++;
-    P += ai;
-  }
-  unsigned kbase, ktot;
-  int hbase, htot;
-  seq_block_scan2<NT, unsigned, int>(ksum, nh, S.kscan, S.hscan, kbase, hbase, ktot, htot);
-  if (htot > kSeqMaxHard) {
-    if (tid == 0) S.result = seq_serial(a, n);
-    __syncthreads();
-    return S.result;
-  }
-
-  // 3a. hard steps in order (the same classification replayed): index, exclusive
-  // k-prefix, term, and the binade predicted for the run after it
+  // 1. predicted partial sum at the start of this thread's chunk (any order will
+  // do) and the largest term before it
+  float loc, cmx = 0.0f;
   {
-    unsigned kex = kbase;
-    int m = hbase;
-    P = Pstart;
-    for (int i = i0; i < i1; i++) {
-      int k, eafter;
-      const float ai = a[i];
-      if (seq_classify(P, ai, rho, k, eafter)) {
-        kex += (unsigned)k;
-      } else {
-        S.hidx[m] = i;
-        S.hk[m] = kex;
-        S.ha[m] = ai;
-        S.hafter[m] = eafter;
-        m++;
-      }
-      P += ai;
+    float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+      q[c & 3] += a[c];
+      cmx = fmaxf(cmx, a[c]);
     }
+    loc = (q[0] + q[1]) + (q[2] + q[3]);
   }
-  if (tid == 0) { S.nhard = htot; S.ktot = ktot; S.fail = 0; }
+  const float xin = seq_wave_scan(loc);
+  const float min_ = seq_wave_scan_max(cmx);
+  const float mprev = __shfl_up(min_, 1, 64);
+  if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = min_; }
+  if (tid == 0) S.bad = 0;
   __syncthreads();
-  const int H = S.nhard;
-  // 3b. run m precedes hard step m (run H is the tail); its total in exact float
-  for (int m = tid; m <= H; m += NT) {
-    const unsigned k0 = m == 0 ? 0u : S.hk[m - 1];
-    const unsigned k1 = m == H ? S.ktot : S.hk[m];
-    const int e = m == 0 ? -127 : S.hafter[m - 1];
-    S.segu[m] = (float)(k1 - k0) * seq_unit(e);       // difference taken modulo 2^32
+  float P0 = xin - loc, M0 = lane ? mprev : 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW - 1; w++)
+    if (w < wave) { P0 += S.wf[w]; M0 = fmaxf(M0, S.wm[w]); }
+
+  // classify; rho: 16 standard deviations of the rounding error a sequential sum
+  // of i terms accumulates (each below half a unit in the last place), plus the
+  // error of the float scan that forms the prediction
+  const float rho = 0x1p-20f * __builtin_amdgcn_sqrtf((float)((tid + 1) * CM + 2)) + 0x1p-17f;
+  const float lo = 1.0f - rho, hi = 1.0f + rho;
+  float P = P0, L = M0;
+  unsigned ks = 0, hardmask = 0;
+  int nh = 0, gin = -1, gout = 1;
+  int kk[CM];
+#pragma unroll
+  for (int c = 0; c < CM; c++) {
+    const float Pn = P + a[c];
+    const int g0 = seq_grid(fmaxf(P * lo, L));
+    L = fmaxf(L, a[c]);
+    const int g1 = seq_grid(Pn * hi);
+    const float t = fminf(ldexpf(a[c], 150 - g0), 0x1p30f);
+    const bool easy = (g0 == g1) && (__builtin_amdgcn_fractf(t) != 0.5f);
+    kk[c] = easy ? (int)__builtin_rintf(t) : 0;
+    ks += (unsigned)kk[c];
+    nh += easy ? 0 : 1;
+    hardmask |= easy ? 0u : (1u << c);
+    if (c == 0) gin = easy ? g0 : -1;
+    gout = easy ? g0 : seq_grid(fmaxf(Pn * lo, L));   // grid of the run continuing past this step
+    P = Pn;
   }
+
+  // 2. scans of the k totals and hard counts; exchange of boundary grids
+  // (k totals are kept modulo 2^32: only differences within one run are used,
+  // and a run on grid g adds at most 2^23 units)
+  const unsigned kin = seq_wave_scan(ks);
+  const int hin = seq_wave_scan(nh);
+  const int gprev_lane = __shfl_up(gout, 1, 64);
+  if (lane == 63) { S.wk[wave] = kin; S.wh[wave] = hin; S.wg[wave] = gout; }
   __syncthreads();
-  // 3c. the walk over hard steps
-  if (tid == 0) {
-    float s = 0.0f;
-    for (int m = 0; m < H; m++) {
-      s = s + S.segu[m];
-      S.sb[m] = s;
-      s = s + S.ha[m];
-      S.sa[m] = s;
+  unsigned kb = kin - ks, ktot = 0;
+  int hb = hin - nh, htot = 0;
+#pragma unroll
+  for (int w = 0; w < NW; w++) {
+    const unsigned wk = S.wk[w];
+    const int wh = S.wh[w];
+    if (w < wave) { kb += wk; hb += wh; }
+    ktot += wk;
+    htot += wh;
+  }
+  const int gprev = lane ? gprev_lane : (wave ? S.wg[wave - 1] : 1);
+  if (gin >= 0 && gin != gprev) S.bad = 1;
+  if (htot > kSeqMaxHard) {
+    if (tid == 0) {
+      S.result = seq_serial(n, term);
+      if (info) { info[0] = htot; info[1] = 1; }
     }
-    s = s + S.segu[H];
-    S.sb[H] = s;
-    S.result = s;
-  }
-  __syncthreads();
-  // 4. check every non-empty run against its predicted binade
-  for (int m = tid; m <= H; m += NT) {
-    const int first = m == 0 ? 0 : S.hidx[m - 1] + 1;
-    const int end = m == H ? n : S.hidx[m];
-    if (end > first) {
-      const int e = m == 0 ? -127 : S.hafter[m - 1];
-      const float st = m == 0 ? 0.0f : S.sa[m - 1];
-      const float en = S.sb[m];
-      const bool ok = seq_binade_f(st) == e && (seq_binade_f(en) == e || en == seq_top(e));
-      if (!ok) S.fail = 1;
-    }
-  }
-  __syncthreads();
-  if (S.fail) {
-    if (tid == 0) S.result = seq_serial(a, n);
     __syncthreads();
+    const float r = S.result;
+    __syncthreads();
+    return r;
   }
-  const float res = S.result;
+
+  // 3. hard steps in order: k prefix before the step, the term, the grid after it
+  {
+    unsigned kp = kb;
+    int m = hb;
+    P = P0;
+    L = M0;
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+      const float Pn = P + a[c];
+      L = fmaxf(L, a[c]);
+      if ((hardmask >> c) & 1u) {
+        S.hk[m] = kp;
+        S.hx[m] = threadIdx.x * CM + c;
+        S.ha[m] = a[c];
+        S.hg[m] = seq_grid(fmaxf(Pn * lo, L));
+        m++;
+      } else {
+        kp += (unsigned)kk[c];
+      }
+      P = Pn;
+    }
+  }
   __syncthreads();
-  return res;
+
+  // 4. the walk, with the proof of every run.  Wave 0 takes the hard steps 64 at
+  // a time: lane i prepares run m = base + i (the run before hard step m; run
+  // htot is the tail) and its exact total, the serial part adds only run totals
+  // and hard terms (lane i records the partial sum its run starts from), and the
+  // runs are then proven in parallel.
+  if (wave == 0) {
+    float s = 0.0f;
+    bool ok = S.bad == 0;
+    unsigned kprev = 0;
+    int g = 1, xprev = -1;
+    for (int base = 0; base <= htot; base += 64) {
+      const int m = base + lane;
+      const bool has = m < htot;
+      const unsigned kc = has ? S.hk[m] : ktot;
+      const int xc = has ? S.hx[m] : NT * CM;
+      const float ah = has ? S.ha[m] : 0.0f;
+      const int gn = has ? S.hg[m] : 1;
+      unsigned kp = __shfl_up(kc, 1, 64);
+      int xp = __shfl_up(xc, 1, 64), gp = __shfl_up(gn, 1, 64);
+      if (lane == 0) { kp = kprev; xp = xprev; gp = g; }
+      const unsigned K = kc - kp;
+      const bool live = m <= htot && xc > xp + 1;       // run m has steps
+      const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;
+      const int cnt = min(64, htot + 1 - base);
+      float st = 0.0f;
+      for (int i = 0; i < cnt; i++) {
+        const float Ti = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(T), i));
+        const float ai = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ah), i));
+        st = lane == i ? s : st;
+        s = s + Ti;
+        s = s + ai;
+      }
+      const float top = __uint_as_float((unsigned)(gp + 1) << 23);
+      const bool bad = live && !(K <= (1u << 23) && seq_grid(st) == gp && T <= top - st);
+      ok = ok && !__any(bad);
+      kprev = __shfl(kc, 63, 64);
+      xprev = __shfl(xc, 63, 64);
+      g = __shfl(gn, 63, 64);
+    }
+    if (!ok && lane == 0) s = seq_serial(n, term);
+    if (lane == 0) {
+      S.result = s;
+      if (info) { info[0] = htot; info[1] = !ok; }
+    }
+  }
+  __syncthreads();
+  const float r = S.result;
+  __syncthreads();
+  return r;
 }
 
 }  // namespace qd

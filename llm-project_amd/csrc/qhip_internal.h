@@ -3,6 +3,7 @@
 #define QHIP_INTERNAL_H
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 // Kernel classes for event timing (names in qhip_runtime.hip).
 enum {
@@ -15,18 +16,22 @@ hipStream_t stream();
 int fail(const char *what, hipError_t e);
 int fail_msg(const char *msg);
 int check_launch(const char *what);
-void *prof_begin(int cls);
-void prof_end(void *tok);
+// When profiling is on: a (start, stop) event pair for one launch of class cls.
+bool prof_events(int cls, hipEvent_t *start, hipEvent_t *stop);
 }  // namespace qh
 
-// Launch on the library stream, time it when profiling, and turn a launch
-// error into the function's nonzero return.
-#define QH_LAUNCH(cls, kernel, grid, block, shmem, ...)                         \
-  do {                                                                         \
-    void *qh_tok_ = qh::prof_begin(cls);                                       \
-    hipLaunchKernelGGL(kernel, grid, block, shmem, qh::stream(), __VA_ARGS__); \
-    qh::prof_end(qh_tok_);                                                     \
-    if (qh::check_launch(#kernel)) return 1;                                   \
+// Launch on the library stream and turn a launch error into the function's
+// nonzero return.  When profiling, the events are bound to the kernel's own
+// dispatch (hipExtLaunchKernelGGL), so their interval is the kernel's
+// execution alone, without the queue gaps around it.
+#define QH_LAUNCH(cls, kernel, grid, block, shmem, ...)                                             \
+  do {                                                                                             \
+    hipEvent_t qh_a_ = nullptr, qh_b_ = nullptr;                                                   \
+    if (qh::prof_events(cls, &qh_a_, &qh_b_))                                                      \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, qh::stream(), qh_a_, qh_b_, 0, __VA_ARGS__); \
+    else                                                                                           \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, qh::stream(), __VA_ARGS__);                   \
+    if (qh::check_launch(#kernel)) return 1;                                                       \
   } while (0)
 
 #endif

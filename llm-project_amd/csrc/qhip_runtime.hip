@@ -51,18 +51,18 @@ int check_launch(const char *what) {
   return e == hipSuccess ? 0 : fail(what, e);
 }
 
-void *prof_begin(int cls) {
-  if (!g_prof) return nullptr;
+bool prof_events(int cls, hipEvent_t *start, hipEvent_t *stop) {
+  if (!g_prof) return false;
   hipEvent_t a = take_event(), b = take_event();
-  if (!a || !b) return nullptr;
-  (void)hipEventRecord(a, g_stream);
+  if (!a || !b) {
+    if (a) g_event_pool.push_back(a);
+    if (b) g_event_pool.push_back(b);
+    return false;
+  }
   g_prof_recs.push_back({cls, a, b});
-  return (void*)&g_prof_recs.back();
-}
-
-void prof_end(void *tok) {
-  if (!tok) return;
-  (void)hipEventRecord(g_prof_recs.back().b, g_stream);
+  *start = a;
+  *stop = b;
+  return true;
 }
 }  // namespace qh
 

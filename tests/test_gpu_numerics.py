@@ -58,6 +58,12 @@ def cases():
         out.append(("growing", np.arange(n, dtype=np.float32) * np.float32(1.5)))
         out.append(("one_big", np.concatenate([[np.float32(3e8)], np.full(n - 1, 1.0, np.float32)])))
         out.append(("big_last", np.concatenate([np.full(n - 1, 1e-3, np.float32), [np.float32(7e5)]])))
+        # a sum parked on 1.0 whose later terms fall just below / at / above half an ulp
+        half = np.float32(2.0 ** -24)
+        for tail in (np.nextafter(half, np.float32(0)), half, np.nextafter(half, np.float32(1))):
+            out.append(("absorbed", np.concatenate([[np.float32(1.0)], np.full(n - 1, tail, np.float32)])))
+        out.append(("edge_mix", np.concatenate([[np.float32(1.0)],
+                                                (rng.integers(0, 4, n - 1) * half).astype(np.float32)])))
     return out
 
 
