@@ -20,6 +20,11 @@
 // Errors follow the reference: loaders return nonzero and print "Error: ..." to
 // stderr; void functions print and abort on a device error.  Entry points that
 // are additive (no reference counterpart) return 0 on success.
+//
+// Used standalone this header defines every type it needs.  Inside the
+// reference's build it takes the place of quant.h and of the KV / quantized
+// section of llama.h (llama.h:94-140): Tensor then comes from tensor.h and the
+// fp32 LlamaBlock / LlamaModel from llama.h, which must be included first.
 #ifndef QLLAMA_H
 #define QLLAMA_H
 
@@ -30,7 +35,13 @@
 extern "C" {
 #endif
 
+#ifdef QUANT_H
+#error "qllama.h replaces quant.h: its QTensor holds device memory and a layout tag"
+#endif
+#define QUANT_H   // everything quant.h declares is declared here
+
 // tensor.h:10-16 (host tensors; inside a QLlamaModel the data pointer is device memory)
+#ifndef TENSOR_H
 typedef struct {
   float *data;
   float *grad;
@@ -38,6 +49,7 @@ typedef struct {
   int ndim;
   size_t size;
 } Tensor;
+#endif
 
 #define QT_LAYOUT_NK 0   // device, output-channel major, K contiguous, rows padded to 16
 #define QT_LAYOUT_KN 1   // device, reference row-major (rows, cols)
@@ -51,6 +63,7 @@ typedef struct {
   int kpad;           // padded K for QT_LAYOUT_NK (multiple of 16), else cols
 } QTensor;
 
+#ifndef LLAMA_H
 // llama.h:19-37 (fp32, host) - input of q_llama_quantize_from.
 typedef struct {
   int d_model, n_heads, n_kv, head_dim, d_ff;
@@ -67,6 +80,7 @@ typedef struct {
   Tensor final_norm;
   Tensor lm_head;
 } LlamaModel;
+#endif
 
 // llama.h:94-99 plus the device-side state.
 typedef struct {

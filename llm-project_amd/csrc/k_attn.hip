@@ -144,12 +144,12 @@ __device__ __forceinline__ void softmax_weights(const float *sh, int T, float m,
 // through a buffer resource over this KV head's rows [0, max_seq): the lane's
 // offset of each slot is fixed (vo) and the tile adds one scalar, so a load
 // costs one add of address arithmetic; the whole offset is in the range-checked
-// vector operand, so rows past max_seq (prefetch beyond the last tile) read as
-// 0 without touching memory.  Rows in [T, max_seq) and columns >= hd are
-// zeroed by the producer.
+// vector operand, so tiles past the last one (the prefetch runs ahead) and rows
+// past max_seq read as 0 without touching memory.  Rows in [T, max_seq) and
+// columns >= hd are zeroed by the producer.
 __device__ __forceinline__ void pv_load(float (&v)[kGSlots][4], __amdgpu_buffer_rsrc_t rs, const int (&vo)[kGSlots],
-                                        int t, int hd) {
-  const int tb = t * kTile * hd * 4;
+                                        int t, int ntile, int hd) {
+  const int tb = t < ntile ? t * kTile * hd * 4 : 0x40000000;   // tiles past the last: no memory traffic
 #pragma unroll
   for (int g = 0; g < kGSlots; g++)
 #pragma unroll
@@ -222,9 +222,9 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   }
   float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
   if (tid >= 64) {
-    pv_load(r0, vrs, vo, 0, hd);
-    pv_load(r1, vrs, vo, 1, hd);
-    pv_load(r2, vrs, vo, 2, hd);
+    pv_load(r0, vrs, vo, 0, ntile, hd);
+    pv_load(r1, vrs, vo, 1, ntile, hd);
+    pv_load(r2, vrs, vo, 2, ntile, hd);
   }
 
   // softmax weights of head h (llama.c:557-572)
@@ -265,32 +265,32 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
     // values are requested three tiles ahead of use
     float *B0 = P, *B1 = P + kChains * kTS;
     pv_produce(B0, W, r0, 0, T, cols_full, col_ok, pid);
-    pv_load(r0, vrs, vo, 3, hd);
+    pv_load(r0, vrs, vo, 3, ntile, hd);
     for (int t = 0;; t += 6) {
       lds_barrier();                                   // consumer takes tile t
       if (t + 1 >= ntile) break;
       pv_produce(B1, W, r1, t + 1, T, cols_full, col_ok, pid);
-      pv_load(r1, vrs, vo, t + 4, hd);
+      pv_load(r1, vrs, vo, t + 4, ntile, hd);
       lds_barrier();                                   // tile t+1
       if (t + 2 >= ntile) break;
       pv_produce(B0, W, r2, t + 2, T, cols_full, col_ok, pid);
-      pv_load(r2, vrs, vo, t + 5, hd);
+      pv_load(r2, vrs, vo, t + 5, ntile, hd);
       lds_barrier();                                   // tile t+2
       if (t + 3 >= ntile) break;
       pv_produce(B1, W, r0, t + 3, T, cols_full, col_ok, pid);
-      pv_load(r0, vrs, vo, t + 6, hd);
+      pv_load(r0, vrs, vo, t + 6, ntile, hd);
       lds_barrier();                                   // tile t+3
       if (t + 4 >= ntile) break;
       pv_produce(B0, W, r1, t + 4, T, cols_full, col_ok, pid);
-      pv_load(r1, vrs, vo, t + 7, hd);
+      pv_load(r1, vrs, vo, t + 7, ntile, hd);
       lds_barrier();                                   // tile t+4
       if (t + 5 >= ntile) break;
       pv_produce(B1, W, r2, t + 5, T, cols_full, col_ok, pid);
-      pv_load(r2, vrs, vo, t + 8, hd);
+      pv_load(r2, vrs, vo, t + 8, ntile, hd);
       lds_barrier();                                   // tile t+5
       if (t + 6 >= ntile) break;
       pv_produce(B0, W, r0, t + 6, T, cols_full, col_ok, pid);
-      pv_load(r0, vrs, vo, t + 9, hd);
+      pv_load(r0, vrs, vo, t + 9, ntile, hd);
     }
   }
 }

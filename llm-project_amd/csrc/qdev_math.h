@@ -18,7 +18,7 @@ namespace qd {
 // in double; the reduction and the polynomial steps are fused multiply-adds.
 // The table holds the double nearest to 2^(i/32), minus i << 47 in its bits, so
 // adding k << 47 applies the exponent.  Verified against the host libm on every
-// float input (tests/test_gpu_numerics.py).
+// float input (tests/test_gpu_parity.py).
 // ---------------------------------------------------------------------------
 __device__ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,

@@ -73,7 +73,7 @@ static int config_valid(const int32_t *cfg) {
 static int config_supported(const int32_t *cfg) {
   const int dm = cfg[1], hd = cfg[5], ff = cfg[6];
   if (hd % 2 != 0 || hd > 512) return 0;
-  if (dm > 32768 || ff > 32768 || cfg[3] * hd > 32768) return 0;
+  if (dm > 16384 || ff > 32768 || cfg[3] * hd > 32768) return 0;   // rmsnorm holds a row in one block
   if (cfg[7] > 16384) return 0;          // attention keeps a head's softmax weights in LDS
   return 1;
 }

@@ -1,0 +1,54 @@
+#!/bin/bash
+# link_reference.sh SRC DEST - build the reference's own `transformer` binary
+# with its int8 LLaMA path served by libqllama.so (MI355X).
+#
+# Copies the reference checkout SRC to DEST (SRC itself is never modified), then:
+#   llama.h   the LlamaKV typedef (llama.h:94-99) becomes #include "qllama.h",
+#             which brings LlamaKV with its device handle, QTensor, QLlamaModel
+#             and the quantized prototypes; the old quantized section
+#             (llama.h:108-140) and #include "quant.h" (llama.h:17) go away
+#   llama.c   the quantized section (llama.c:447-657) and llama_kv_free
+#             (llama.c:290-294, which the library also serves for fp32 caches)
+#             go away; llama_kv_create zeroes the new device handle
+#   matrix.c  qacc_columns (matrix.c:370-374) goes away (the library exports it)
+#   quant.c   is not compiled (the library exports its functions)
+# and links -lqllama.  The line numbers are those of the reference revision this
+# library was built against; the script checks each anchor before editing.
+set -euo pipefail
+SRC=${1:?usage: link_reference.sh SRC DEST}
+DEST=${2:?usage: link_reference.sh SRC DEST}
+HERE=$(cd "$(dirname "$0")" && pwd)
+INC=$(cd "$HERE/../include" && pwd)
+
+check() {   # file line text: the anchor must be where the edit expects it
+  if ! sed -n "$2p" "$DEST/$1" | grep -qF -- "$3"; then
+    echo "link_reference.sh: $1:$2 is not '$3' (different reference revision?)" >&2
+    exit 1
+  fi
+}
+
+rm -rf "$DEST"
+mkdir -p "$DEST"
+cp -r "$SRC"/. "$DEST"/
+
+check llama.h 17 '#include "quant.h"'
+check llama.h 94 'typedef struct {'
+check llama.h 99 '} LlamaKV;'
+check llama.h 114 'typedef struct {'
+check llama.h 140 'LlamaKV q_llama_kv_create(const QLlamaModel *m);'
+check llama.c 276 'LlamaKV kv;'
+check llama.c 290 'void llama_kv_free(LlamaKV *kv) {'
+check llama.c 447 'static QLlamaBlock q_block_create('
+check matrix.c 370 'void qacc_columns('
+
+# edits from the bottom up so the earlier line numbers stay valid
+sed -i '108,140d; 94,99c #include "qllama.h"' "$DEST/llama.h"
+sed -i '17d' "$DEST/llama.h"
+sed -i '447,657d; 290,294d; 276a\  kv.dev = NULL;' "$DEST/llama.c"
+sed -i '370,374d' "$DEST/matrix.c"
+
+make -C "$DEST" transformer \
+  CFLAGS="-std=c11 -O3 -march=native -Wall -pthread -I$INC" \
+  OBJS="$(make -s -C "$DEST" -p -n 2>/dev/null | sed -n 's/^OBJS *= *//p' | head -1 | sed 's/quant\.o//')" \
+  LDLIBS="-lm -pthread -L$HERE -lqllama -Wl,-rpath,$HERE"
+echo "link_reference.sh: built $DEST/transformer against $HERE/libqllama.so"
