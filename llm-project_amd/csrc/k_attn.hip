@@ -11,9 +11,9 @@
 // (head, d) chains, and between the lanes that form the products w_j * V_jd and
 // the lane that adds them.
 //
-// Kernel 1 (k_attn_scores): grid (H, ceil(max_seq/256)); one thread per (head,
-//   position) computes dot_j and s_j with the whole K row in flight at once;
-//   each block writes its maximum.
+// Kernel 1 (k_attn_scores): grid (H, ceil(max_seq/128)); one thread per (head,
+//   position) computes dot_j and s_j; the block's K rows are copied into LDS
+//   with direct global-to-LDS loads; each block writes its maximum.
 // Kernel 2 (k_attn_pv): grid (H, ceil(hd/64)), 512 threads.  All threads form
 //   the head's softmax weights in LDS (each thread a run of consecutive
 //   positions, in registers).  Then wave 0 owns 64 output chains o_d while waves
@@ -29,7 +29,7 @@
 
 namespace {
 
-constexpr int kScoreBlock = 256;
+constexpr int kScoreBlock = 128;        // positions per scores block
 constexpr int kTile = 128;                  // positions per PV tile
 constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
 constexpr int kChains = 64;                 // output dims per PV block (wave 0's lanes)
@@ -61,29 +61,6 @@ __device__ __forceinline__ float block_max(float m, float *red) {
   return r;
 }
 
-// dot_j for one position: q from LDS, the K row from global, HD known at
-// compile time so that every load of the row is issued before the chain starts.
-template <int HD>
-__device__ __forceinline__ float score_dot(const float *qs, const float *kr) {
-  static_assert(HD % 4 == 0, "");
-  float4 kv[HD / 4];
-  const float4 *k4 = reinterpret_cast<const float4 *>(kr);
-#pragma unroll
-  for (int i = 0; i < HD / 4; i++) kv[i] = k4[i];
-  __builtin_amdgcn_sched_barrier(0);       // the whole row is requested before the chain starts
-  const float4 *q4 = reinterpret_cast<const float4 *>(qs);
-  float dot = 0.0f;
-#pragma unroll
-  for (int i = 0; i < HD / 4; i++) {
-    const float4 qv = q4[i];
-    dot += qv.x * kv[i].x;
-    dot += qv.y * kv[i].y;
-    dot += qv.z * kv[i].z;
-    dot += qv.w * kv[i].w;
-  }
-  return dot;
-}
-
 // runtime head_dim: rows loaded 8 floats ahead of the chain
 __device__ __forceinline__ float score_dot_any(const float *qs, const float *kr, int hd) {
   float dot = 0.0f;
@@ -99,29 +76,119 @@ __device__ __forceinline__ float score_dot_any(const float *qs, const float *kr,
   return dot;
 }
 
+// The block's K rows are copied straight from global memory into LDS
+// (global_load_lds, 16 bytes per lane, no registers), every copy in flight at
+// once; each wave instruction moves two whole 512-byte rows, so the reads are
+// coalesced.  Row r keeps its 16-byte chunk c at slot (c + r mod 8) mod CPR of
+// the row: lane t then reads chunk i of its own row from slot (i + t mod 8) mod
+// CPR, and the eight lanes served per LDS cycle hit eight different bank
+// groups.  A lane's column repeats every four copies, so a copy costs one
+// pointer add.  Blocks that end past T (only the last one) clamp rows to T-1.
+typedef __attribute__((address_space(3))) void *lds_void_ptr;
+
 template <int HD>
-__global__ __launch_bounds__(kScoreBlock) void k_attn_scores(const float *q, const float *kc, const int *d_pos, int H,
-                                                              int KVH, int hd, int max_seq, float scale,
-                                                              float *scores, float *bmax, int nch) {
-  extern __shared__ float qs[];
-  __shared__ float red[kScoreBlock / 64];
-  const int h = blockIdx.x, c = blockIdx.y;
+__device__ __forceinline__ void score_copy_rows(const float *Kh, int j0, int T, float *ks, bool full, int nwaves) {
+  static_assert(HD == 128, "two rows per wave instruction");
+  constexpr int CPR = HD / 4;                                // 16-byte chunks per row (32)
+  constexpr int NCOPY = kScoreBlock * CPR / 64;              // wave instructions for the tile (64)
+  const int per = (NCOPY + nwaves - 1) / nwaves;             // copies per wave
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5, pos = lane & 31;
+  const int k0 = wv * per, k1 = min(NCOPY, k0 + per);
+  if (full) {
+    // copy kk moves rows 2kk and 2kk+1; lane (half, pos) takes chunk
+    // c = (pos - (2kk + half) mod 8) mod CPR of row 2kk + half
+    const char *rb = reinterpret_cast<const char *>(Kh + (size_t)(j0 + half) * HD);
+    for (int kk = k0; kk < k1; kk++) {
+      const int c = (pos - ((2 * kk + half) & 7)) & (CPR - 1);
+      __builtin_amdgcn_global_load_lds((const void *)(rb + (size_t)kk * 2 * HD * 4 + 16 * c),
+                                       (lds_void_ptr)(ks + kk * 64 * 4), 16, 0, 0);
+    }
+  } else {
+    for (int kk = k0; kk < k1; kk++) {
+      const int r = 2 * kk + half;
+      const int c = (pos - (r & 7)) & (CPR - 1);
+      const int j = min(j0 + r, T - 1);
+      __builtin_amdgcn_global_load_lds((const void *)(Kh + (size_t)j * HD + 4 * c), (lds_void_ptr)(ks + kk * 64 * 4),
+                                       16, 0, 0);
+    }
+  }
+}
+
+// dot_j for the lane's own row in LDS: eight 16-byte row reads are issued per
+// batch, then the batch's 32 steps of the sequential chain; q is wave-uniform
+// and comes through the scalar cache.
+template <int HD>
+__device__ __forceinline__ float score_row_dot(const float *qh, const float *ks, int t) {
+  constexpr int CPR = HD / 4;
+  const float4 *row = reinterpret_cast<const float4 *>(ks) + t * CPR;
+  const float4 *q4 = reinterpret_cast<const float4 *>(qh);
+  const int sk = t & 7;
+  float dot = 0.0f;
+#pragma unroll
+  for (int b = 0; b < CPR; b += 8) {
+    float4 kv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) kv[i] = row[(b + i + sk) & (CPR - 1)];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 qv = q4[b + i];
+      dot += qv.x * kv[i].x;
+      dot += qv.y * kv[i].y;
+      dot += qv.z * kv[i].z;
+      dot += qv.w * kv[i].w;
+    }
+  }
+  return dot;
+}
+
+// One block per (KV head, 128 positions) serves the G = H / n_kv query heads of
+// that group: G x 128 threads, thread (g, t) computes head kvh*G + g at position
+// j0 + t, and the K tile is copied into LDS once for all of them.  With n_kv a
+// multiple of 8, consecutive KV heads also fall on different XCDs.
+template <int HD>
+__global__ __launch_bounds__(1024) void k_attn_scores(const float *q, const float *kc, const int *d_pos, int H,
+                                                       int KVH, int hd, int max_seq, float scale, float *scores,
+                                                       float *bmax, int nch) {
+  __shared__ __attribute__((aligned(16))) float qs[HD ? 4 : 8 * 512];
+  __shared__ __attribute__((aligned(16))) float ks[HD ? kScoreBlock * HD : 4];
+  __shared__ float red[16];
+  const int kvh = blockIdx.x, c = blockIdx.y;
+  const int G = H / KVH;
   const int T = *d_pos + 1;
   if (c * kScoreBlock >= T) return;                      // uniform for the block
-  const int kvh = h / (H / KVH);
-  for (int d = threadIdx.x; d < hd; d += kScoreBlock) qs[d] = q[(size_t)h * hd + d];
-  __syncthreads();
-  const int j = c * kScoreBlock + threadIdx.x;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x / kScoreBlock), t = threadIdx.x % kScoreBlock;
+  const int h = kvh * G + g;
+  const int j0 = c * kScoreBlock, j = j0 + t;
+  const float *Kh = kc + (size_t)kvh * max_seq * hd;
+  float dot;
+  if (HD) {
+    score_copy_rows<HD ? HD : 128>(Kh, j0, T, ks, j0 + kScoreBlock <= T, (int)(blockDim.x >> 6));
+    __syncthreads();                                     // the copies (vmcnt)
+    dot = score_row_dot<HD ? HD : 128>(q + (size_t)h * HD, ks, t);
+  } else {
+    for (int d = threadIdx.x; d < G * hd; d += blockDim.x) qs[d] = q[(size_t)kvh * G * hd + d];
+    __syncthreads();
+    dot = j < T ? score_dot_any(qs + g * hd, Kh + (size_t)j * hd, hd) : 0.0f;
+  }
   float s = -INFINITY;
   if (j < T) {
-    const float *kr = kc + ((size_t)kvh * max_seq + j) * hd;
-    const float dot = HD ? score_dot<HD ? HD : 4>(qs, kr) : score_dot_any(qs, kr, hd);
     s = dot * scale;
     scores[(size_t)h * max_seq + j] = s;
   }
-  s = block_max<kScoreBlock>(s, red);
-  if (threadIdx.x == 0) bmax[(size_t)h * nch + c] = s;
+  // per-head block maximum: the head's two waves
+  s = qd::wave_max_f32(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (t == 0) bmax[(size_t)h * nch + c] = fmaxf(red[2 * g], red[2 * g + 1]);
 }
+
+// Head of PV block x: the query heads of one KV head are given block indices
+// congruent modulo n_kv.  Workgroups are dealt to the XCDs round-robin by
+// index, so with n_kv a multiple of 8 a group's blocks share one XCD and its
+// L2, and each KV head's V rows are fetched from HBM once per XCD.
+__device__ __forceinline__ int head_of_block(int x, int H, int KVH) { return (x % KVH) * (H / KVH) + x / KVH; }
 
 // Softmax weights of one head into W[0..T) (llama.c:566-571): thread t forms
 // e_j for j in [t*CM, t*CM + CM) in registers, the block evaluates their
@@ -197,7 +264,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   extern __shared__ float lds[];
   __shared__ float red[kPvThreads / 64];
   __shared__ qd::SeqScratch seq;
-  const int h = blockIdx.x, d0 = blockIdx.y * kChains;
+  const int h = head_of_block(blockIdx.x, H, KVH), d0 = blockIdx.y * kChains;
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
   const int wcap = (max_seq + kTile - 1) / kTile * kTile;
@@ -318,27 +385,22 @@ extern "C" int qhip_attention(const float *q, const float *kc, const float *vc, 
     if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_attn_pv)", e);
     g_pv_attr_bytes = pv_lds;
   }
-  const dim3 sgrid(n_heads, nch);
-  const size_t qbytes = ((size_t)hd + 4) * 4;
+  const int G = n_heads / n_kv;
+  if (G * kScoreBlock > 1024 || G * hd > 512 * 8) return qh::fail_msg("attention: more than 8 query heads per KV head");
+  const dim3 sgrid(n_kv, nch);
+  const dim3 sblock(G * kScoreBlock);
+  if (hd > 512) return qh::fail_msg("attention: head_dim above 512");
   switch (hd) {
     case 128:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<128>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
-                max_seq, scale, scores, bmax, nch);
-      break;
-    case 64:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<64>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
-                max_seq, scale, scores, bmax, nch);
-      break;
-    case 48:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<48>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+      QH_LAUNCH(QK_ATTN, k_attn_scores<128>, sgrid, sblock, 0, q, kc, d_pos, n_heads, n_kv, hd,
                 max_seq, scale, scores, bmax, nch);
       break;
     default:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<0>, sgrid, dim3(kScoreBlock), qbytes, q, kc, d_pos, n_heads, n_kv, hd,
+      QH_LAUNCH(QK_ATTN, k_attn_scores<0>, sgrid, sblock, 0, q, kc, d_pos, n_heads, n_kv, hd,
                 max_seq, scale, scores, bmax, nch);
       break;
   }
-  QH_LAUNCH(QK_ATTN, k_attn_pv, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores, bmax,
+  QH_LAUNCH(QK_ATTN_PV, k_attn_pv, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores, bmax,
             vc, d_pos, n_heads, n_kv, hd, max_seq, nch, o, obm);
   return 0;
 }

@@ -59,16 +59,21 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(const float *x, int dm, co
   const int row = blockIdx.x;
   const float *xr = x + (size_t)row * dm;
   const int j0 = threadIdx.x * CM;
-  float v[CM], sq[CM];
+  float v[CM], sq[CM], gm[CM];
   if (j0 + CM <= dm && (dm & 3) == 0) {
 #pragma unroll
     for (int c = 0; c < CM; c += 4) {
       const float4 t = *reinterpret_cast<const float4 *>(xr + j0 + c);
+      const float4 u = *reinterpret_cast<const float4 *>(gamma + j0 + c);   // in flight during the sum
       v[c] = t.x; v[c + 1] = t.y; v[c + 2] = t.z; v[c + 3] = t.w;
+      gm[c] = u.x; gm[c + 1] = u.y; gm[c + 2] = u.z; gm[c + 3] = u.w;
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < CM; c++) v[c] = j0 + c < dm ? xr[j0 + c] : 0.0f;
+    for (int c = 0; c < CM; c++) {
+      v[c] = j0 + c < dm ? xr[j0 + c] : 0.0f;
+      gm[c] = j0 + c < dm ? gamma[j0 + c] : 0.0f;
+    }
   }
 #pragma unroll
   for (int c = 0; c < CM; c++) sq[c] = v[c] * v[c];
@@ -79,7 +84,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_quant(const float *x, int dm, co
   float mx = 0.0f;
 #pragma unroll
   for (int c = 0; c < CM; c++) {
-    v[c] = j0 + c < dm ? v[c] * r * gamma[j0 + c] : 0.0f;
+    v[c] = j0 + c < dm ? v[c] * r * gm[c] : 0.0f;
     mx = fmaxf(mx, fabsf(v[c]));
   }
   mx = qd::wave_max_f32(mx);

@@ -50,10 +50,7 @@ struct SeqScratch {
   unsigned wk[kSeqMaxWaves];
   int wh[kSeqMaxWaves];
   int wg[kSeqMaxWaves];
-  unsigned hk[kSeqMaxHard];
-  int hx[kSeqMaxHard];
-  float ha[kSeqMaxHard];
-  int hg[kSeqMaxHard];
+  int4 hs[kSeqMaxHard];          // hard step: k prefix before it, index, term bits, grid after it
   unsigned ktot;
   int nhard;
   int bad;
@@ -153,7 +150,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   float P = P0, L = M0;
   unsigned ks = 0, hardmask = 0;
   int nh = 0, gin = -1, gout = 1;
-  int kk[CM];
+  int kk[CM], gh[CM];
 #pragma unroll
   for (int c = 0; c < CM; c++) {
     const float Pn = P + a[c];
@@ -167,7 +164,8 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
     nh += easy ? 0 : 1;
     hardmask |= easy ? 0u : (1u << c);
     if (c == 0) gin = easy ? g0 : -1;
-    gout = easy ? g0 : seq_grid(fmaxf(Pn * lo, L));   // grid of the run continuing past this step
+    gh[c] = seq_grid(fmaxf(Pn * lo, L));               // grid after this step, if it is hard
+    gout = easy ? g0 : gh[c];                          // grid of the run continuing past this step
     P = Pn;
   }
 
@@ -202,26 +200,19 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
     return r;
   }
 
-  // 3. hard steps in order: k prefix before the step, the term, the grid after it
-  {
+  // 3. hard steps in order: k prefix before the step, its index, the term and
+  // the grid after it
+  if (nh) {
     unsigned kp = kb;
     int m = hb;
-    P = P0;
-    L = M0;
 #pragma unroll
     for (int c = 0; c < CM; c++) {
-      const float Pn = P + a[c];
-      L = fmaxf(L, a[c]);
       if ((hardmask >> c) & 1u) {
-        S.hk[m] = kp;
-        S.hx[m] = threadIdx.x * CM + c;
-        S.ha[m] = a[c];
-        S.hg[m] = seq_grid(fmaxf(Pn * lo, L));
+        S.hs[m] = make_int4((int)kp, threadIdx.x * CM + c, __float_as_int(a[c]), gh[c]);
         m++;
       } else {
         kp += (unsigned)kk[c];
       }
-      P = Pn;
     }
   }
   __syncthreads();
@@ -234,21 +225,16 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   if (wave == 0) {
     float s = 0.0f;
     bool ok = S.bad == 0;
-    unsigned kprev = 0;
-    int g = 1, xprev = -1;
     for (int base = 0; base <= htot; base += 64) {
       const int m = base + lane;
-      const bool has = m < htot;
-      const unsigned kc = has ? S.hk[m] : ktot;
-      const int xc = has ? S.hx[m] : NT * CM;
-      const float ah = has ? S.ha[m] : 0.0f;
-      const int gn = has ? S.hg[m] : 1;
-      unsigned kp = __shfl_up(kc, 1, 64);
-      int xp = __shfl_up(xc, 1, 64), gp = __shfl_up(gn, 1, 64);
-      if (lane == 0) { kp = kprev; xp = xprev; gp = g; }
-      const unsigned K = kc - kp;
-      const bool live = m <= htot && xc > xp + 1;       // run m has steps
+      // this lane's hard step (or the tail) and the one before it
+      const int4 cur = m < htot ? S.hs[m] : make_int4((int)ktot, NT * CM, 0, 1);
+      const int4 prv = m > 0 && m <= htot ? S.hs[m - 1] : make_int4(0, -1, 0, 1);
+      const unsigned K = (unsigned)cur.x - (unsigned)prv.x;
+      const int gp = prv.w;
+      const bool live = m <= htot && cur.y > prv.y + 1;   // run m has steps
       const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;
+      const float ah = __int_as_float(cur.z);
       const int cnt = min(64, htot + 1 - base);
       float st = 0.0f;
       for (int i = 0; i < cnt; i++) {
@@ -261,9 +247,6 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
       const float top = __uint_as_float((unsigned)(gp + 1) << 23);
       const bool bad = live && !(K <= (1u << 23) && seq_grid(st) == gp && T <= top - st);
       ok = ok && !__any(bad);
-      kprev = __shfl(kc, 63, 64);
-      xprev = __shfl(xc, 63, 64);
-      g = __shfl(gn, 63, 64);
     }
     if (!ok && lane == 0) s = seq_serial(n, term);
     if (lane == 0) {
