@@ -362,6 +362,181 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prompt ingestion: causal attention of R query rows at positions p0 .. p0+R-1
+// against cache rows 0 .. p0+R-1, each row exactly as its decode step forms it
+// (the same sums in the same order).  Scratch w[h][r][Tp] holds the scores and
+// then, in place, the softmax weights.
+// ---------------------------------------------------------------------------
+constexpr int kPfKeys = 128;          // keys per scores block, one per thread
+constexpr int kPfRows = 16;           // query rows per scores / PV block
+constexpr int kPfTile = 32;           // keys per PV tile
+constexpr int kPfMaxRows = 512;       // rows per attention pass (bounds the scratch)
+
+// Block (KV head, 16 query rows, 128 keys): thread t holds K row j0 + t in
+// registers; the q rows of the group's G heads are in LDS and read as
+// broadcasts; every (head, row) pair is one sequential chain over d, eight at a
+// time per thread.
+template <int HD>
+__global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
+                                                         int KVH, int max_seq, float scale, float *w, int Tp) {
+  extern __shared__ __attribute__((aligned(16))) float qsh[];        // [G * kPfRows][HD]
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows, j0 = blockIdx.z * kPfKeys;
+  const int G = H / KVH;
+  const int rend = min(R, r0 + kPfRows);
+  const int jvis = p0 + rend - 1;                                    // last key any row here sees
+  if (j0 > jvis) return;                                             // uniform for the block
+  const int t = threadIdx.x, j = j0 + t;
+  for (int idx = t; idx < G * kPfRows * HD; idx += kPfKeys) {
+    const int pair = idx / HD, d = idx % HD;
+    const int g = pair / kPfRows, r = min(r0 + pair % kPfRows, R - 1);
+    qsh[idx] = q[(size_t)r * H * HD + (size_t)(kvh * G + g) * HD + d];
+  }
+  float4 kr[HD / 4];
+  {
+    const float4 *k4 = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(j, jvis)) * HD);
+#pragma unroll
+    for (int i = 0; i < HD / 4; i++) kr[i] = k4[i];
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < G * kPfRows; c0 += 8) {
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD / 4; i++) {
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const float4 qv = reinterpret_cast<const float4 *>(qsh + (size_t)(c0 + c) * HD)[i];
+        acc[c] += qv.x * kr[i].x;
+        acc[c] += qv.y * kr[i].y;
+        acc[c] += qv.z * kr[i].z;
+        acc[c] += qv.w * kr[i].w;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      const int pair = c0 + c, g = pair / kPfRows, r = r0 + pair % kPfRows;
+      if (r < R && j <= p0 + r) w[((size_t)(kvh * G + g) * R + r) * Tp + j] = acc[c] * scale;
+    }
+  }
+}
+
+// Softmax weights of one (head, row) (llama.c:557-572): NT threads, thread t
+// forms e_j for j in [t*CM, t*CM + CM), the block evaluates their sequential
+// sum exactly, w_j = e_j * (1 / S) in place.
+template <int NT, int CM>
+__device__ __forceinline__ void pf_softmax_row(float *row, int T, float m, qd::SeqScratch &seq) {
+  const int j0 = threadIdx.x * CM;
+  float e[CM];
+#pragma unroll
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(row[j0 + c] - m) : 0.0f;
+  const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m); });
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int c = 0; c < CM; c++)
+    if (j0 + c < T) row[j0 + c] = e[c] * inv;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int Tp) {
+  __shared__ qd::SeqScratch seq;
+  __shared__ float red[NT / 64];
+  const int r = blockIdx.x, h = blockIdx.y;
+  const int T = p0 + r + 1;
+  float *row = w + ((size_t)h * R + r) * Tp;
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < T; j += NT) m = fmaxf(m, row[j]);
+  m = qd::wave_max_f32(m);
+  if (NT > 64) {
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
+  }
+  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, m, seq);
+  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, m, seq);
+  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, m, seq);
+  else pf_softmax_row<NT, 32>(row, T, m, seq);
+}
+
+// Block (KV head, 16 query rows): thread (g, d) owns the 16 chains o[r][h][d]
+// (h = kvh*G + g), each a sequential sum over its row's visible keys.  V and
+// weight tiles of 32 keys are staged in LDS; weights are broadcast reads.
+template <int HD>
+__global__ __launch_bounds__(1024) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
+                                                int max_seq, int Tp, float *o) {
+  __shared__ __attribute__((aligned(16))) float vs[kPfTile][HD];
+  __shared__ __attribute__((aligned(16))) float wsh[8][kPfRows][kPfTile];
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows;
+  const int G = H / KVH;
+  const int rend = min(R, r0 + kPfRows);
+  const int g = threadIdx.x / HD, d = threadIdx.x % HD;
+  const int h = kvh * G + g;
+  const int kend = p0 + rend;                                        // keys 0 .. kend-1 are used
+  float acc[kPfRows];
+#pragma unroll
+  for (int c = 0; c < kPfRows; c++) acc[c] = 0.0f;
+  for (int k0 = 0; k0 < kend; k0 += kPfTile) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kPfTile * HD; idx += blockDim.x) {
+      const int key = k0 + idx / HD;
+      vs[idx / HD][idx % HD] = key < kend ? vc[((size_t)kvh * max_seq + key) * HD + idx % HD] : 0.0f;
+    }
+    for (int idx = threadIdx.x; idx < G * kPfRows * kPfTile; idx += blockDim.x) {
+      const int gg = idx / (kPfRows * kPfTile), rr = (idx / kPfTile) % kPfRows, kk = idx % kPfTile;
+      const int r = r0 + rr, key = k0 + kk;
+      wsh[gg][rr][kk] = (r < R && key <= p0 + r) ? w[((size_t)(kvh * G + gg) * R + r) * Tp + key] : 0.0f;
+    }
+    __syncthreads();
+    const bool full = k0 + kPfTile <= p0 + r0 + 1;                   // every key here is seen by every row
+    if (full) {
+#pragma unroll 4
+      for (int kk = 0; kk < kPfTile; kk += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = vs[kk + u][d];
+#pragma unroll
+        for (int c = 0; c < kPfRows; c++) {
+          const float4 wv = *reinterpret_cast<const float4 *>(&wsh[g][c][kk]);
+          acc[c] += wv.x * v[0];
+          acc[c] += wv.y * v[1];
+          acc[c] += wv.z * v[2];
+          acc[c] += wv.w * v[3];
+        }
+      }
+    } else {
+      for (int kk = 0; kk < kPfTile; kk++) {
+        const int key = k0 + kk;
+        const float v = vs[kk][d];
+#pragma unroll
+        for (int c = 0; c < kPfRows; c++)
+          if (key <= p0 + r0 + c) acc[c] += wsh[g][c][kk] * v;          // row r0 + c sees keys <= p0 + r0 + c
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kPfRows; c++)
+    if (r0 + c < R) o[(size_t)(r0 + c) * H * HD + (size_t)h * HD + d] = acc[c];
+}
+
+template <int HD>
+int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int H, int KVH, int max_seq,
+                 float scale, float *w, float *o) {
+  const int G = H / KVH, Tp = (max_seq + 3) & ~3;
+  const int Tmax = p0 + R;
+  const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeys - 1) / kPfKeys);
+  QH_LAUNCH(QK_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
+            max_seq, scale, w, Tp);
+  if (Tmax <= 64 * 32) QH_LAUNCH(QK_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
+  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
+  else QH_LAUNCH(QK_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
+  QH_LAUNCH(QK_ATTN_PV, k_pf_pv<HD>, dim3(KVH, (R + kPfRows - 1) / kPfRows), dim3(G * HD), 0, w, vc, R, p0, H, KVH,
+            max_seq, Tp, o);
+  return 0;
+}
+
 size_t g_pv_attr_bytes = 0;   // dynamic LDS the PV kernel is currently allowed
 
 size_t pv_lds_bytes(int max_seq) {
@@ -411,4 +586,32 @@ extern "C" int qhip_attention_nbm(int n_heads, int hd) { return n_heads * ((hd +
 // Size (floats) of the scores scratch qhip_attention needs.
 extern "C" size_t qhip_attention_scratch(int n_heads, int max_seq) {
   return (size_t)n_heads * max_seq + (size_t)n_heads * ((max_seq + kScoreBlock - 1) / kScoreBlock);
+}
+
+// Causal attention of R prompt rows (R may exceed one pass: rows are taken
+// kPfMaxRows at a time, each pass seeing every earlier position).
+extern "C" int qhip_pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads,
+                                 int n_kv, int hd, int max_seq, float scale, float *ws, float *o) {
+  const int G = n_heads / n_kv;
+  if (G < 1 || G > 8 || G * hd > 1024) return qh::fail_msg("pf_attention: unsupported head grouping");
+  if (p0 + R > max_seq || max_seq > 16384) return qh::fail_msg("pf_attention: positions out of range");
+  for (int c0 = 0; c0 < R; c0 += kPfMaxRows) {
+    const int rr = min(kPfMaxRows, R - c0);
+    const float *qc = q + (size_t)c0 * n_heads * hd;
+    float *oc = o + (size_t)c0 * n_heads * hd;
+    int rc;
+    switch (hd) {
+      case 128: rc = pf_attention<128>(qc, kc, vc, rr, p0 + c0, n_heads, n_kv, max_seq, scale, ws, oc); break;
+      case 64: rc = pf_attention<64>(qc, kc, vc, rr, p0 + c0, n_heads, n_kv, max_seq, scale, ws, oc); break;
+      case 48: rc = pf_attention<48>(qc, kc, vc, rr, p0 + c0, n_heads, n_kv, max_seq, scale, ws, oc); break;
+      default: return qh::fail_msg("pf_attention: head_dim not supported");
+    }
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+// Floats of scratch qhip_pf_attention needs.
+extern "C" size_t qhip_pf_attention_scratch(int R, int n_heads, int max_seq) {
+  return (size_t)n_heads * (size_t)(R < kPfMaxRows ? R : kPfMaxRows) * (size_t)((max_seq + 3) & ~3);
 }

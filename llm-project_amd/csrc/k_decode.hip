@@ -217,6 +217,41 @@ __global__ void k_rope_append(const float *qkv, int H, int KVH, int hd, const fl
   }
 }
 
+// Prompt rows: x[r][j] = (float)wte[ids[r]*dm + j] * scale[j]  (llama.c:534-536)
+__global__ void k_pf_embed(const int8_t *wte, const float *s, int dm, const int *ids, float *x) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+  if (j >= dm) return;
+  x[(size_t)r * dm + j] = (float)wte[(size_t)ids[r] * dm + j] * s[j];
+}
+
+// Prompt rows: RoPE at position p0 + r (rope.c:48-68), q -> q_out row r, k and v
+// appended to the cache at p0 + r; the operations of k_rope_append.
+__global__ void k_pf_rope_append(const float *qkv, int H, int KVH, int hd, const float *cos_t, const float *sin_t,
+                                 int p0, float *q_out, float *kc, float *vc, int max_seq) {
+  const int r = blockIdx.y, pos = p0 + r;
+  const int half = hd >> 1;
+  const int b = blockIdx.x;
+  const int nqkv = (H + 2 * KVH) * hd;
+  const float *row = qkv + (size_t)r * nqkv;
+  const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
+  if (b < H + KVH) {
+    const bool isq = b < H;
+    const float *xh = row + (size_t)b * hd;
+    float *dst = isq ? q_out + (size_t)r * H * hd + (size_t)b * hd : kc + ((size_t)(b - H) * max_seq + pos) * hd;
+    for (int k = threadIdx.x; k < half; k += blockDim.x) {
+      const float c = ct[k], s = st[k];
+      const float x1 = xh[k], x2 = xh[k + half];
+      dst[k] = x1 * c - x2 * s;
+      dst[k + half] = x2 * c + x1 * s;
+    }
+  } else {
+    const int h = b - H - KVH;
+    const float *vh = row + (size_t)(H + KVH) * hd + (size_t)h * hd;
+    float *dst = vc + ((size_t)h * max_seq + pos) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = vh[d];
+  }
+}
+
 // First index of the maximum (sampler.c:8-21), then advance the position.
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out,
                                                          int max_seq) {
@@ -312,6 +347,18 @@ int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const floa
                      const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
   QH_LAUNCH(QK_ROPE, k_rope_append, dim3(n_heads + 2 * n_kv), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t, sin_t,
             d_pos, q_out, kc, vc, max_seq);
+  return 0;
+}
+
+int qhip_pf_embed(const int8_t *wte, const float *wte_s, int dm, const int *ids, int R, float *x) {
+  QH_LAUNCH(QK_EMBED, k_pf_embed, dim3((dm + 255) / 256, R), dim3(256), 0, wte, wte_s, dm, ids, x);
+  return 0;
+}
+
+int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, const float *cos_t,
+                        const float *sin_t, int p0, float *q_out, float *kc, float *vc, int max_seq) {
+  QH_LAUNCH(QK_ROPE, k_pf_rope_append, dim3(n_heads + 2 * n_kv, R), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t,
+            sin_t, p0, q_out, kc, vc, max_seq);
   return 0;
 }
 

@@ -113,6 +113,22 @@ int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *q
 // d_state[0] = pos + 1.  pos = d_state[0].
 int qhip_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out, int max_seq);
 
+// Many-row int8 GEMM on MFMA (k_gemm.hip): out[i][j] for i < M, j < N from
+// activation rows A [M][kpad] and weight rows W [N][kpad] (SwiGLU: [2N][kpad]),
+// with the decode GEMV's epilogues (mode 0 plain + bias, 1 residual, 2 SwiGLU).
+int qhip_gemm_i8(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N,
+                 int kpad, float *out, int ldo, const float *bias);
+
+// Prompt ingestion over R rows at positions p0 .. p0+R-1 (k_decode.hip, k_attn.hip).
+int qhip_pf_embed(const int8_t *wte, const float *wte_s, int dm, const int *ids, int R, float *x);
+int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, const float *cos_t,
+                        const float *sin_t, int p0, float *q_out, float *kc, float *vc, int max_seq);
+// Causal attention of the R query rows q [R][n_heads*hd] against cache rows
+// 0 .. p0+R-1; o [R][n_heads*hd].  ws is scratch of qhip_pf_attention_scratch floats.
+int qhip_pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads, int n_kv,
+                      int hd, int max_seq, float scale, float *ws, float *o);
+size_t qhip_pf_attention_scratch(int R, int n_heads, int max_seq);
+
 // reference-layout column accumulate (matrix.c:354-374) for qacc_columns
 int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);
 

@@ -48,6 +48,10 @@ typedef struct {
   int *d_in;         // max_seq + 1 input tokens by position
   int *d_out;        // max_seq argmax ids by position
   int *h_stage;      // pinned staging, max_seq + 2 ints
+  // prompt ingestion (allocated on first use): rows of activations
+  int pf_rows;
+  float *pf_x, *pf_qkv, *pf_q, *pf_o, *pf_h, *pf_as, *pf_attn;
+  int8_t *pf_qa;
 } QDev;
 
 typedef struct {
@@ -93,8 +97,17 @@ static QTensor dev_qt(int8_t *q, float *s, int rows, int cols, int layout) {
   return t;
 }
 
+static void pf_free(QDev *d) {
+  qhip_free(d->pf_x); qhip_free(d->pf_qkv); qhip_free(d->pf_q); qhip_free(d->pf_o);
+  qhip_free(d->pf_h); qhip_free(d->pf_as); qhip_free(d->pf_attn); qhip_free(d->pf_qa);
+  d->pf_x = d->pf_qkv = d->pf_q = d->pf_o = d->pf_h = d->pf_as = d->pf_attn = NULL;
+  d->pf_qa = NULL;
+  d->pf_rows = 0;
+}
+
 static void qdev_free(QDev *d) {
   if (!d) return;
+  pf_free(d);
   qhip_free(d->blob);
   qhip_host_free(d->h_stage);
   free(d->wqkv); free(d->wo); free(d->wgu); free(d->wd);
@@ -613,12 +626,94 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
   kv->len += 1;
 }
 
+// ---------------------------------------------------------------------------
+// Batched prompt ingestion: every row of the prompt through each layer at once
+// (MFMA GEMMs, batched RoPE, causal attention), then the final norm, head and
+// argmax of the last row with the decode kernels.  Each row is computed with
+// the same operations in the same order as its decode step, so the result, the
+// cache and the device position state equal those of n decode steps (only the
+// argmax ids of the earlier prompt rows, which nothing reads, are not written).
+// ---------------------------------------------------------------------------
+#define PF_MIN_ROWS 16      // shorter prompts replay the decode graph
+#define PF_MAX_ROWS 2048    // rows per pass through the layers
+
+static int pf_supported(const QDev *d) {
+  const int G = d->H / d->KVH;
+  return (d->hd == 128 || d->hd == 64 || d->hd == 48) && G <= 8 && G * d->hd <= 1024 && d->dff <= 32768;
+}
+
+static int pf_alloc(QDev *d, int rows) {
+  if (d->pf_rows >= rows) return 0;
+  pf_free(d);
+  const size_t R = (size_t)rows;
+  d->pf_x = (float*)qhip_malloc(R * d->dm * 4);
+  d->pf_qkv = (float*)qhip_malloc(R * d->nqkv * 4);
+  d->pf_q = (float*)qhip_malloc(R * d->qd * 4);
+  d->pf_o = (float*)qhip_malloc(R * d->qd * 4);
+  d->pf_h = (float*)qhip_malloc(R * d->dff * 4);
+  d->pf_as = (float*)qhip_malloc(R * 4);
+  d->pf_attn = (float*)qhip_malloc(qhip_pf_attention_scratch(rows, d->H, d->max_seq) * 4);
+  d->pf_qa = (int8_t*)qhip_malloc(R * d->kp_max);
+  if (!d->pf_x || !d->pf_qkv || !d->pf_q || !d->pf_o || !d->pf_h || !d->pf_as || !d->pf_attn || !d->pf_qa) {
+    pf_free(d);
+    return 1;
+  }
+  d->pf_rows = rows;
+  return qhip_fill_zero(d->pf_qa, R * d->kp_max);
+}
+
+static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
+  const int rows = n < PF_MAX_ROWS ? n : PF_MAX_ROWS;
+  if (pf_alloc(d, rows)) return 1;
+  // the stream is idle here (every entry point ends with a sync): stage the
+  // prompt ids by position and the position state the final argmax advances
+  int st[2] = {pos + n - 1, pos + n};
+  if (qhip_h2d(d->d_in + pos, ids, (size_t)n * sizeof(int)) || qhip_h2d(d->d_state, st, sizeof st)) return 1;
+  const size_t per = (size_t)d->max_seq * d->kvd;
+  int rc = 0;
+  for (int c0 = 0; c0 < n && !rc; c0 += rows) {
+    const int R = n - c0 < rows ? n - c0 : rows, p0 = pos + c0;
+    rc |= qhip_pf_embed(d->wte, d->wte_s, d->dm, d->d_in + p0, R, d->pf_x);
+    for (int l = 0; l < d->L && !rc; l++) {
+      float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
+      rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_attn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
+      rc |= qhip_gemm_i8(0, 2, d->pf_qa, d->pf_as, d->wqkv[l], d->sqkv[l], R, d->nqkv, d->kp_dm, d->pf_qkv, d->nqkv,
+                         d->bqkv[l]);
+      rc |= qhip_pf_rope_append(d->pf_qkv, R, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, p0, d->pf_q, kc, vc,
+                                d->max_seq);
+      rc |= qhip_pf_attention(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_attn,
+                              d->pf_o);
+      rc |= qhip_quant_rows(d->pf_o, R, d->qd, d->pf_qa, d->kp_qd, d->pf_as);
+      rc |= qhip_gemm_i8(1, 6, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm, NULL);
+      rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_ffn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
+      rc |= qhip_gemm_i8(2, 7, d->pf_qa, d->pf_as, d->wgu[l], d->sgu[l], R, d->dff, d->kp_dm, d->pf_h, d->dff, NULL);
+      rc |= qhip_quant_rows(d->pf_h, R, d->dff, d->pf_qa, d->kp_ff, d->pf_as);
+      rc |= qhip_gemm_i8(1, 9, d->pf_qa, d->pf_as, d->wd[l], d->sd[l], R, d->dm, d->kp_ff, d->pf_x, d->dm, NULL);
+    }
+    if (!rc && c0 + R == n) {       // last row: final norm, head, argmax (llama.c:592-593, sampler.c:36-49)
+      const float *xl = d->pf_x + (size_t)(R - 1) * d->dm;
+      rc |= qhip_rmsnorm_quant(xl, 1, d->dm, d->g_final, d->eps, d->qa, d->kp_dm, d->as);
+      rc |= qhip_gemv_dec(3, 10, d->qa, d->as, d->head, d->head_s, d->vocab, d->kp_dm, d->logits, NULL, d->amax_v,
+                          d->amax_i);
+      rc |= qhip_argmax_final(d->amax_v, d->amax_i, qhip_gemv_blocks(d->vocab, d->kp_dm), d->d_in, d->d_state,
+                              d->d_out, d->max_seq);
+    }
+  }
+  return rc;
+}
+
 int q_llama_prefill(const QLlamaModel *m, LlamaKV *kv, const int *ids, int n, Tensor *logits) {
   if (n <= 0) return 0;
   check_step(m, kv, ids, n, n, "q_llama_prefill");
-  const QDev *d = (const QDev*)m->dev;
+  QDev *d = (QDev*)m->dev;
   KVDev *kd = (KVDev*)kv->dev;
-  if (stage_inputs(d, kv->len, ids, n) || run_steps(d, kd, n)) return 1;
+  static int no_batch = -1;     // QLLAMA_PREFILL_STEPS=1: replay decode steps instead (same results)
+  if (no_batch < 0) no_batch = getenv("QLLAMA_PREFILL_STEPS") != NULL;
+  if (n >= PF_MIN_ROWS && pf_supported(d) && !no_batch) {
+    if (pf_run(d, kd, kv->len, ids, n)) return 1;
+  } else {
+    if (stage_inputs(d, kv->len, ids, n) || run_steps(d, kd, n)) return 1;
+  }
   if (logits && qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4)) return 1;
   if (qhip_sync()) return 1;
   kv->len += n;
@@ -688,7 +783,8 @@ void qmatmul(const Tensor *A, const QTensor *W, Tensor *C) {
   }
   if (qhip_h2d(da, A->data, (size_t)M * K * 4) || qhip_fill_zero(qa, (size_t)M * kp) ||
       qhip_quant_rows(da, M, K, qa, kp, as) ||
-      qhip_gemv(qa, as, M, wnk, W->scale, N, kp, dc, NULL, 0, 12) ||
+      (M >= 16 ? qhip_gemm_i8(0, 12, qa, as, wnk, W->scale, M, N, kp, dc, N, NULL)    // many rows: MFMA
+               : qhip_gemv(qa, as, M, wnk, W->scale, N, kp, dc, NULL, 0, 12)) ||
       qhip_d2h_async(C->data, dc, (size_t)M * N * 4) || qhip_sync())
     die("qmatmul");
   qhip_free(da); qhip_free(dc); qhip_free(qa); qhip_free(as); qhip_free(tmp);

@@ -109,6 +109,60 @@ def test_e2e_tiny_prefill_and_device_greedy(Q):
         m.close()
 
 
+def test_prefill_in_pieces_equals_whole_prompt(Q):
+    """Prompt ingestion in pieces (batched pieces of 16 rows and more, shorter
+    ones replayed step by step) continues the cache exactly: the last logits
+    equal the reference's after the whole prompt, bit for bit."""
+    meta = golden_json("e2e_tiny")
+    m = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"])
+    try:
+        p = meta["prompt"]
+        for cut in ((100,), (7, 40), (16, 17, 50, 111)):
+            m.reset(0)
+            prev = 0
+            for c in cut + (len(p),):
+                lg = m.prefill(p[prev:c]).copy()
+                prev = c
+            assert bits_equal(lg, golden("e2e_tiny_logits_prompt_last")), cut
+    finally:
+        m.close()
+
+
+def _big_prefill(Q, name):
+    """The whole prompt through the batched (MFMA) prefill, then device greedy
+    decoding: last prompt logits, the token stream and the final logits equal
+    the reference's."""
+    if not have_golden(f"e2e_{name}.json") or not have_golden(f"e2e_{name}_logits_prompt_last.npy"):
+        pytest.skip(f"{name} fixture not generated")
+    meta = golden_json(f"e2e_{name}")
+    m = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    try:
+        log(f"{name}: batched prefill of {len(meta['prompt'])} tokens")
+        lg = m.prefill(meta["prompt"]).copy()
+        ref = golden(f"e2e_{name}_logits_prompt_last")
+        np.testing.assert_allclose(lg[:ref.size], ref, atol=ATOL, rtol=RTOL)
+        assert bits_equal(lg[:ref.size], ref)
+        first = int(np.argmax(lg))
+        assert first == meta["gen"][0]
+        # feed every generated token, as the reference run did: the device
+        # loop up to gen[-2], then a decode step (which returns logits) for gen[-1]
+        out = m.generate_greedy(first, meta["gen_len"] - 1)
+        assert [first] + out == meta["gen"]
+        final = m.step(out[-1]).copy()
+    finally:
+        m.close()
+    head = golden(f"e2e_{name}_logits_final")
+    assert bits_equal(final[:head.size], head)
+
+
+def test_e2e_1b_batched_prefill_matches_reference(Q):
+    _big_prefill(Q, "1b")
+
+
+def test_e2e_8b_batched_prefill_matches_reference(Q):
+    _big_prefill(Q, "8b")
+
+
 def test_decode_rejects_position_past_max_seq(Q):
     # the reference leaves this to its callers (main.c:663); the library checks
     # it on the host before any device work: run in a child so the abort is seen
@@ -151,6 +205,25 @@ def test_qmatmul_small_matches_reference(Q, name):
         W.close()
     ref = golden(f"{name}_C")
     np.testing.assert_allclose(Cg, ref, atol=ATOL, rtol=RTOL)
+    assert bits_equal(Cg, ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 64, 48), (130, 300, 200), (300, 1000, 517), (1024, 4096, 384)])
+def test_qmatmul_many_rows_matches_oracle(Q, M, K, N):
+    """16 rows and more go through the MFMA GEMM: bit-identical to the C
+    restatement of quant.c:60-85 (int32 accumulation is exact), including
+    partial row/column tiles and K that is not a multiple of the 64-byte step."""
+    rng = np.random.default_rng(M * 7 + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    A[3] = 0.0                                   # an all-zero row: scale 1
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    q, s = O.quantize(w)
+    W = Q.QWeight(w)
+    try:
+        Cg = Q.qmatmul(A, W)
+    finally:
+        W.close()
+    ref = O.qmatmul(A, q, s)
     assert bits_equal(Cg, ref)
 
 
