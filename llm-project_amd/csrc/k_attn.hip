@@ -373,13 +373,19 @@ constexpr int kPfRows = 16;           // query rows per scores / PV block
 constexpr int kPfTile = 32;           // keys per PV tile
 constexpr int kPfMaxRows = 512;       // rows per attention pass (bounds the scratch)
 
-// Block (KV head, 16 query rows, 128 keys): thread t holds K row j0 + t in
-// registers; the q rows of the group's G heads are in LDS and read as
-// broadcasts; every (head, row) pair is one sequential chain over d, eight at a
-// time per thread.
+// Block (KV head, 16 query rows, 128 keys): thread t owns key j0 + t and every
+// (head, row) pair of the block as a sequential chain over d.  The pairs go 8 at
+// a time; the K row streams through registers 16 dims at a time while the 8
+// chains advance together (their independent adds hide each other's latency);
+// q comes from LDS as broadcast reads.  A compiler barrier per chunk keeps the
+// loads of later chunks from being hoisted (they would need hundreds of VGPRs).
+constexpr int kPfChains = 8;
+
 template <int HD>
 __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
                                                          int KVH, int max_seq, float scale, float *w, int Tp) {
+  static_assert(HD % 16 == 0, "K rows stream in 16-dim chunks");
+  constexpr int NQ = HD / 4;
   extern __shared__ __attribute__((aligned(16))) float qsh[];        // [G * kPfRows][HD]
   const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows, j0 = blockIdx.z * kPfKeys;
   const int G = H / KVH;
@@ -387,35 +393,40 @@ __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const flo
   const int jvis = p0 + rend - 1;                                    // last key any row here sees
   if (j0 > jvis) return;                                             // uniform for the block
   const int t = threadIdx.x, j = j0 + t;
-  for (int idx = t; idx < G * kPfRows * HD; idx += kPfKeys) {
+  const int npair = G * kPfRows;                                     // a multiple of 16
+  for (int idx = t; idx < npair * HD; idx += kPfKeys) {
     const int pair = idx / HD, d = idx % HD;
     const int g = pair / kPfRows, r = min(r0 + pair % kPfRows, R - 1);
     qsh[idx] = q[(size_t)r * H * HD + (size_t)(kvh * G + g) * HD + d];
   }
-  float4 kr[HD / 4];
-  {
-    const float4 *k4 = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(j, jvis)) * HD);
-#pragma unroll
-    for (int i = 0; i < HD / 4; i++) kr[i] = k4[i];
-  }
   __syncthreads();
-  for (int c0 = 0; c0 < G * kPfRows; c0 += 8) {
-    float acc[8];
+  const float4 *krow = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(j, jvis)) * HD);
+#pragma unroll 1
+  for (int c0 = 0; c0 < npair; c0 += kPfChains) {
+    float acc[kPfChains];
 #pragma unroll
-    for (int c = 0; c < 8; c++) acc[c] = 0.0f;
+    for (int c = 0; c < kPfChains; c++) acc[c] = 0.0f;
+    const float4 *qb = reinterpret_cast<const float4 *>(qsh + (size_t)c0 * HD);
+#pragma unroll 1
+    for (int dc = 0; dc < NQ; dc += 4) {
+      float4 kr[4];
 #pragma unroll
-    for (int i = 0; i < HD / 4; i++) {
+      for (int i = 0; i < 4; i++) kr[i] = krow[dc + i];
 #pragma unroll
-      for (int c = 0; c < 8; c++) {
-        const float4 qv = reinterpret_cast<const float4 *>(qsh + (size_t)(c0 + c) * HD)[i];
-        acc[c] += qv.x * kr[i].x;
-        acc[c] += qv.y * kr[i].y;
-        acc[c] += qv.z * kr[i].z;
-        acc[c] += qv.w * kr[i].w;
+      for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int c = 0; c < kPfChains; c++) {
+          const float4 qv = qb[c * NQ + dc + i];
+          acc[c] += qv.x * kr[i].x;
+          acc[c] += qv.y * kr[i].y;
+          acc[c] += qv.z * kr[i].z;
+          acc[c] += qv.w * kr[i].w;
+        }
       }
+      asm volatile("" ::: "memory");
     }
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
+    for (int c = 0; c < kPfChains; c++) {
       const int pair = c0 + c, g = pair / kPfRows, r = r0 + pair % kPfRows;
       if (r < R && j <= p0 + r) w[((size_t)(kvh * G + g) * R + r) * Tp + j] = acc[c] * scale;
     }
