@@ -32,6 +32,7 @@ CONFIGS = {
 }
 METRIC = "decode tok/s + % HBM roofline, 8B-shape int8 LLaMA (1 GPU); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+INT8_MFMA_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 # HBM bytes per GEMV dispatch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs
 # (scaled by a plain copy of known size), written by llm-project_amd/profsum.py
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "k_gemv_dec_traffic_8b.json")
@@ -62,6 +63,13 @@ def gemv_bytes(cfg):
         "gemv_down": (L, g(dm, ff, 8)),
         "gemv_head": (1, g(vocab, dm, 4)),
     }
+
+
+def prefill_gemm_ops(cfg, P):
+    """int8 multiply-adds x 2 of the prompt GEMMs (QKV, O, gate|up, down per layer)."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    return 2 * P * L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm)
 
 
 def decode_bytes(cfg, t):
@@ -154,7 +162,10 @@ def main():
     import oracle_lib as O
     prompt = O.prompt(P, 1234, cfg[0])
 
-    # prefill (timed separately)
+    # prefill (timed separately, after one untimed ingestion that allocates its buffers)
+    if P:
+        gm.prefill(prompt, want_logits=False)
+        gm.reset(0)
     Q.lib().qllama_device_sync()
     t0 = time.perf_counter()
     gm.prefill(prompt, want_logits=True)
@@ -201,6 +212,23 @@ def main():
         if all(k in per for k in gb):
             traffic = round(sum(n * per[k] for k, (n, _) in gb.items()) / launches_per_tok)
 
+    # prefill GEMMs on MFMA: a second, profiled ingestion of the same prompt
+    pf_roof = None
+    if P >= 16 and NP:
+        gm.reset(0)
+        Q.profile(True)
+        gm.prefill(prompt, want_logits=False)
+        pprof = Q.profile_read()
+        Q.profile(False)
+        if "pf_gemm" in pprof:
+            g_ms = pprof["pf_gemm"][0] * pprof["pf_gemm"][1]
+            a_ms = pprof["pf_attn"][0] * pprof["pf_attn"][1] if "pf_attn" in pprof else None
+            tops = prefill_gemm_ops(cfg, P) / (g_ms * 1e-3) / 1e12
+            pf_roof = {"bound": "mfma", "kernel": "k_gemm_i8 (int8 MFMA GEMM, all call sites)",
+                       "achieved": round(tops, 1), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                       "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "gemm_ms": round(g_ms, 3),
+                       "attention_ms": round(a_ms, 3) if a_ms is not None else None}
+
     cpu = None
     if not args.no_cpu_baseline and rank == 0:
         cpu = cpu_baseline(Q, gm, cfg, base, pos_first, args.cpu_seconds)
@@ -227,6 +255,7 @@ def main():
         "decode_hbm_roofline_frac": round(step_frac, 4),
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
+        "prefill_roofline": pf_roof,
         "prefill_s": round(t_prefill, 4),
         "model_build_s": round(t_build, 3),
         "roofline": {

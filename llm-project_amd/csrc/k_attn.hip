@@ -538,12 +538,12 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
   const int G = H / KVH, Tp = (max_seq + 3) & ~3;
   const int Tmax = p0 + R;
   const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeys - 1) / kPfKeys);
-  QH_LAUNCH(QK_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
+  QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
             max_seq, scale, w, Tp);
-  if (Tmax <= 64 * 32) QH_LAUNCH(QK_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
-  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
-  else QH_LAUNCH(QK_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
-  QH_LAUNCH(QK_ATTN_PV, k_pf_pv<HD>, dim3(KVH, (R + kPfRows - 1) / kPfRows), dim3(G * HD), 0, w, vc, R, p0, H, KVH,
+  if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
+  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
+  else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
+  QH_LAUNCH(QK_PF_ATTN, k_pf_pv<HD>, dim3(KVH, (R + kPfRows - 1) / kPfRows), dim3(G * HD), 0, w, vc, R, p0, H, KVH,
             max_seq, Tp, o);
   return 0;
 }

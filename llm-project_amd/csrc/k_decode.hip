@@ -351,13 +351,13 @@ int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const floa
 }
 
 int qhip_pf_embed(const int8_t *wte, const float *wte_s, int dm, const int *ids, int R, float *x) {
-  QH_LAUNCH(QK_EMBED, k_pf_embed, dim3((dm + 255) / 256, R), dim3(256), 0, wte, wte_s, dm, ids, x);
+  QH_LAUNCH(QK_PF_OTHER, k_pf_embed, dim3((dm + 255) / 256, R), dim3(256), 0, wte, wte_s, dm, ids, x);
   return 0;
 }
 
 int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, const float *cos_t,
                         const float *sin_t, int p0, float *q_out, float *kc, float *vc, int max_seq) {
-  QH_LAUNCH(QK_ROPE, k_pf_rope_append, dim3(n_heads + 2 * n_kv, R), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t,
+  QH_LAUNCH(QK_PF_OTHER, k_pf_rope_append, dim3(n_heads + 2 * n_kv, R), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t,
             sin_t, p0, q_out, kc, vc, max_seq);
   return 0;
 }

@@ -46,28 +46,73 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
 }
 
 // KCH = kpad / 1024 chunks of 16 bytes per lane (kpad a multiple of 1024).
-template <int MODE, int KCH, int R>
+// PRO = 1: the activation arrives unquantized (v, n values, with per-block
+// maxima of |v| in vbm); every block quantizes it itself (quant.c:66-78, the
+// operations of k_quant_blocks) into LDS while its first weights are in flight.
+template <int MODE, int KCH, int R, int PRO>
 __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float *as_p, const int8_t *W,
                                                   const float *ws, int N, int kpad, float *out, const float *bias,
-                                                  float *bm, int *bi) {
+                                                  float *bm, int *bi, const float *v, int n, const float *vbm,
+                                                  int nvbm) {
   __shared__ float red[4];
   __shared__ int redi[4];
+  __shared__ __attribute__((aligned(16))) int8_t qsh[PRO ? KCH * 1024 : 16];
   float best = -INFINITY;
   int besti = 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j0 = (blockIdx.x * 4 + wave) * R;
+  float hmax = 0.0f;
+  v4i w[KCH], u[KCH];
+  if (j0 < N) {                                      // weights first: in flight during the prologue
+    load_row(w, W + (size_t)j0 * kpad, lane);
+    if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j0) * kpad, lane);
+  }
   v4i a[KCH];
-  {
+  float as;
+  if (PRO) {
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
+    mx = qd::wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+    const float inv = 1.0f / as;
+    for (int c = threadIdx.x; c < KCH * 64; c += 256) {        // 16 values per chunk
+      const int k0 = 16 * c;
+      float x[16];
+      if (k0 + 16 <= n) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+          const float4 t = *reinterpret_cast<const float4 *>(v + k0 + e);
+          x[e] = t.x; x[e + 1] = t.y; x[e + 2] = t.z; x[e + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) x[e] = k0 + e < n ? v[k0 + e] : 0.0f;
+      }
+      v4i pk;
+#pragma unroll
+      for (int wd = 0; wd < 4; wd++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int k = k0 + 4 * wd + e;
+          const int q = k < n ? qd::quant_i8(x[4 * wd + e], inv) : 0;
+          word |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
+        }
+        pk[wd] = (int)word;
+      }
+      *reinterpret_cast<v4i *>(qsh + k0) = pk;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+  } else {
     const v4i *q4 = reinterpret_cast<const v4i *>(qa);
 #pragma unroll
     for (int i = 0; i < KCH; i++) a[i] = q4[lane + 64 * i];
-  }
-  const float as = *as_p;
-  float hmax = 0.0f;
-  v4i w[KCH], u[KCH];
-  if (j0 < N) {
-    load_row(w, W + (size_t)j0 * kpad, lane);
-    if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j0) * kpad, lane);
+    as = *as_p;
   }
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -228,9 +273,14 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float *bv, const in
 
 // Quantize v (n values, quant.c:66-78) given per-block maxima of |v|; grid
 // ceil(kpad/1024) blocks of 256 threads x 4 values; block 0 writes the scale.
+// The values are requested together with the maxima (one memory round trip).
 __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa,
                                                       int kpad, float *as_out) {
   __shared__ float red[4];
+  const int k0 = blockIdx.x * 1024 + threadIdx.x * 4;
+  float x[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) x[r] = k0 + r < n ? v[k0 + r] : 0.0f;
   float mx = 0.0f;
   for (int i = threadIdx.x; i < nbm; i += 256) mx = fmaxf(mx, bm[i]);
   mx = qd::wave_max_f32(mx);
@@ -239,13 +289,11 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
   const float inv = 1.0f / as;
-  const int k0 = blockIdx.x * 1024 + threadIdx.x * 4;
   if (k0 < kpad) {
     uint32_t packed = 0;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int k = k0 + r;
-      const int q = k < n ? qd::quant_i8(v[k], inv) : 0;
+      const int q = k0 + r < n ? qd::quant_i8(x[r], inv) : 0;
       packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * r);
     }
     *reinterpret_cast<uint32_t *>(qa + k0) = packed;
@@ -253,28 +301,25 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
 }
 
-template <int MODE>
+template <int MODE, int PRO>
 int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws, int N, int kpad, float *out,
-           const float *bias, float *bm, int *bi) {
+           const float *bias, float *bm, int *bi, const float *v, int n, const float *vbm, int nvbm) {
   constexpr int R = 2;
   const dim3 grid((N + 4 * R - 1) / (4 * R));
+#define QG(KCH)                                                                                             \
+  QH_LAUNCH(cls, (k_gemv_dec<MODE, KCH, R, PRO>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi, \
+            v, n, vbm, nvbm)
   switch (kpad) {
-    case 2048:
-      QH_LAUNCH(cls, (k_gemv_dec<MODE, 2, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-      return 0;
-    case 4096:
-      QH_LAUNCH(cls, (k_gemv_dec<MODE, 4, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-      return 0;
-    case 8192:
-      QH_LAUNCH(cls, (k_gemv_dec<MODE, 8, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-      return 0;
-    case 14336:
-      QH_LAUNCH(cls, (k_gemv_dec<MODE, 14, R>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-      return 0;
+    case 2048: QG(2); return 0;
+    case 4096: QG(4); return 0;
+    case 8192: QG(8); return 0;
+    case 14336: QG(14); return 0;
     default:
+      if (PRO) return qh::fail_msg("gemv: fused quantization needs kpad 2048/4096/8192/14336");
       QH_LAUNCH(cls, k_gemv_dec_any<MODE>, dim3((N + 3) / 4), dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
       return 0;
   }
+#undef QG
 }
 
 }  // namespace
@@ -290,13 +335,24 @@ extern "C" int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *a
                              int N, int kpad, float *out, const float *bias, float *bm, int *bi) {
   if (kpad % 16) return qh::fail_msg("gemv: kpad must be a multiple of 16");
   switch (mode) {
-    case MODE_PLAIN: return launch<MODE_PLAIN>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-    case MODE_RESID: return launch<MODE_RESID>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-    case MODE_SWIGLU: return launch<MODE_SWIGLU>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-    case MODE_HEAD: return launch<MODE_HEAD>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi);
+    case MODE_PLAIN: return launch<MODE_PLAIN, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
+    case MODE_RESID: return launch<MODE_RESID, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
+    case MODE_SWIGLU: return launch<MODE_SWIGLU, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
+    case MODE_HEAD: return launch<MODE_HEAD, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
     default: return qh::fail_msg("gemv: bad mode");
   }
 }
+
+// Residual GEMV whose activation v (n values) is quantized inside the kernel from
+// the per-block maxima vbm of its producer (replaces qhip_quant_blocks + mode 1).
+extern "C" int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vbm, int nvbm, const int8_t *W,
+                                 const float *ws, int N, int kpad, float *out) {
+  if (kpad % 16 || n > kpad) return qh::fail_msg("gemv_resid_q: bad shape");
+  return launch<MODE_RESID, 1>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, NULL, NULL, v, n, vbm, nvbm);
+}
+
+// Shapes qhip_gemv_resid_q supports.
+extern "C" int qhip_gemv_fused_ok(int kpad) { return kpad == 2048 || kpad == 4096 || kpad == 8192 || kpad == 14336; }
 
 extern "C" int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as) {
   QH_LAUNCH(QK_QUANT, k_quant_blocks, dim3((kpad + 1023) / 1024), dim3(256), 0, v, n, bm, nbm, qa, kpad, as);

@@ -105,6 +105,12 @@ int qhip_attention_nbm(int n_heads, int hd);
 int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws,
                   int N, int kpad, float *out, const float *bias, float *bm, int *bi);
 int qhip_argmax_final(const float *bv, const int *bidx, int nb, int *d_in, int *d_state, int *d_out, int max_seq);
+// Residual GEMV (mode 1) quantizing its activation v (n values) in each block
+// from the producer's per-block maxima vbm (nvbm of them); kpad in
+// {2048, 4096, 8192, 14336} (qhip_gemv_fused_ok).
+int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vbm, int nvbm, const int8_t *W, const float *ws,
+                      int N, int kpad, float *out);
+int qhip_gemv_fused_ok(int kpad);
 int qhip_gemv_blocks(int N, int kpad);
 // Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
 int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as);

@@ -23,7 +23,7 @@ std::vector<ProfRec> g_prof_recs;
 std::vector<hipEvent_t> g_event_pool;
 const char *g_class_names[QK_NUM_CLASSES] = {
     "embed", "rmsnorm_quant", "gemv_qkv", "rope_append", "attn_scores", "quant_rows",
-    "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other", "attn_pv"};
+    "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other", "attn_pv", "pf_gemm", "pf_attn", "pf_other"};
 
 hipEvent_t take_event() {
   if (!g_event_pool.empty()) { hipEvent_t e = g_event_pool.back(); g_event_pool.pop_back(); return e; }

@@ -550,10 +550,16 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
     rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
     rc |= qhip_rope_append(d->qkv, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, dpos, d->q, kc, vc, d->max_seq);
     rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o, d->obm);
-    rc |= qhip_quant_blocks(d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->qa, d->kp_qd, d->as);
-    rc |= qhip_gemv_dec(1, 6, d->qa, d->as, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, NULL, NULL);
+    if (qhip_gemv_fused_ok(d->kp_qd)) {        // o quantized inside the Wo GEMV
+      rc |= qhip_gemv_resid_q(6, d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->wo[l], d->so[l], d->dm,
+                              d->kp_qd, d->x);
+    } else {
+      rc |= qhip_quant_blocks(d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->qa, d->kp_qd, d->as);
+      rc |= qhip_gemv_dec(1, 6, d->qa, d->as, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, NULL, NULL);
+    }
     rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
     rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
+    // (h is quantized by its own kernel: every down block quantizing d_ff values costs more than it saves)
     rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, qhip_gemv_blocks(d->dff, d->kp_dm), d->qa, d->kp_ff, d->as);
     rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
   }
@@ -635,6 +641,7 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
 // argmax ids of the earlier prompt rows, which nothing reads, are not written).
 // ---------------------------------------------------------------------------
 #define PF_MIN_ROWS 16      // shorter prompts replay the decode graph
+#define PF_CLS_GEMM 14      // profiling class of the prefill GEMMs (QK_PF_GEMM)
 #define PF_MAX_ROWS 2048    // rows per pass through the layers
 
 static int pf_supported(const QDev *d) {
@@ -677,18 +684,18 @@ static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
     for (int l = 0; l < d->L && !rc; l++) {
       float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
       rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_attn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
-      rc |= qhip_gemm_i8(0, 2, d->pf_qa, d->pf_as, d->wqkv[l], d->sqkv[l], R, d->nqkv, d->kp_dm, d->pf_qkv, d->nqkv,
+      rc |= qhip_gemm_i8(0, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wqkv[l], d->sqkv[l], R, d->nqkv, d->kp_dm, d->pf_qkv, d->nqkv,
                          d->bqkv[l]);
       rc |= qhip_pf_rope_append(d->pf_qkv, R, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, p0, d->pf_q, kc, vc,
                                 d->max_seq);
       rc |= qhip_pf_attention(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_attn,
                               d->pf_o);
       rc |= qhip_quant_rows(d->pf_o, R, d->qd, d->pf_qa, d->kp_qd, d->pf_as);
-      rc |= qhip_gemm_i8(1, 6, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm, NULL);
+      rc |= qhip_gemm_i8(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm, NULL);
       rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_ffn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
-      rc |= qhip_gemm_i8(2, 7, d->pf_qa, d->pf_as, d->wgu[l], d->sgu[l], R, d->dff, d->kp_dm, d->pf_h, d->dff, NULL);
+      rc |= qhip_gemm_i8(2, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wgu[l], d->sgu[l], R, d->dff, d->kp_dm, d->pf_h, d->dff, NULL);
       rc |= qhip_quant_rows(d->pf_h, R, d->dff, d->pf_qa, d->kp_ff, d->pf_as);
-      rc |= qhip_gemm_i8(1, 9, d->pf_qa, d->pf_as, d->wd[l], d->sd[l], R, d->dm, d->kp_ff, d->pf_x, d->dm, NULL);
+      rc |= qhip_gemm_i8(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wd[l], d->sd[l], R, d->dm, d->kp_ff, d->pf_x, d->dm, NULL);
     }
     if (!rc && c0 + R == n) {       // last row: final norm, head, argmax (llama.c:592-593, sampler.c:36-49)
       const float *xl = d->pf_x + (size_t)(R - 1) * d->dm;
