@@ -48,7 +48,8 @@ def load_qllama():
 
 def gemv_bytes(cfg):
     """Algorithmic HBM bytes of each GEMV launch per token: int8 weights + fp32
-    scales + the int8 activation row + fp32 outputs (read too where residual)."""
+    scales + the activation row (int8; fp32 for Wo, which quantizes it itself)
+    + fp32 outputs (read too where residual)."""
     vocab, dm, L, H, KVH, hd, ff, _ = cfg
     qd, kvd = H * hd, KVH * hd
     n_qkv = qd + 2 * kvd
@@ -58,7 +59,7 @@ def gemv_bytes(cfg):
 
     return {
         "gemv_qkv": (L, g(n_qkv, dm, 4 + 4)),      # out + bias
-        "gemv_o": (L, g(dm, qd, 8)),               # residual read + write
+        "gemv_o": (L, g(dm, qd, 8) + 3 * qd),      # fp32 activation; residual read + write
         "gemv_gate_up": (L, g(2 * ff, dm, 4)),
         "gemv_down": (L, g(dm, ff, 8)),
         "gemv_head": (1, g(vocab, dm, 4)),
