@@ -29,6 +29,8 @@
 
 namespace {
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 constexpr int kScoreBlock = 128;        // positions per scores block
 constexpr int kTile = 128;                  // positions per PV tile
 constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
@@ -190,30 +192,16 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, const floa
 // L2, and each KV head's V rows are fetched from HBM once per XCD.
 __device__ __forceinline__ int head_of_block(int x, int H, int KVH) { return (x % KVH) * (H / KVH) + x / KVH; }
 
-// Softmax weights of one head into W[0..T) (llama.c:566-571): thread t forms
-// e_j for j in [t*CM, t*CM + CM) in registers, the block evaluates their
-// sequential sum exactly, then w_j = e_j * (1 / S).
-template <int CM>
-__device__ __forceinline__ void softmax_weights(const float *sh, int T, float m, float *W, qd::SeqScratch &seq) {
-  const int j0 = threadIdx.x * CM;
-  float e[CM];
-#pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(sh[j0 + c] - m) : 0.0f;
-  const float sum = qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m); });
-  const float inv = 1.0f / sum;
-#pragma unroll
-  for (int c = 0; c < CM; c++)
-    if (j0 + c < T) W[j0 + c] = e[c] * inv;
-}
-
 // V values of tile t for this producer lane: slot g covers positions
 // t*kTile + 4*(pw + kPWaves*g) + 0..3 at column d0 + (pid & 63).  The loads go
 // through a buffer resource over this KV head's rows [0, max_seq): the lane's
 // offset of each slot is fixed (vo) and the tile adds one scalar, so a load
 // costs one add of address arithmetic; the whole offset is in the range-checked
-// vector operand, so tiles past the last one (the prefetch runs ahead) and rows
-// past max_seq read as 0 without touching memory.  Rows in [T, max_seq) and
-// columns >= hd are zeroed by the producer.
+// vector operand, so tiles past the last one (the prefetch runs ahead), rows
+// past max_seq and the slots of wave 0 (which has none, but issues the same
+// loads so that every wave's memory counter runs alike) read as 0 without
+// touching memory.  Rows in [T, max_seq) and columns >= hd are zeroed by the
+// producer.
 __device__ __forceinline__ void pv_load(float (&v)[kGSlots][4], __amdgpu_buffer_rsrc_t rs, const int (&vo)[kGSlots],
                                         int t, int ntile, int hd) {
   const int tb = t < ntile ? t * kTile * hd * 4 : 0x40000000;   // tiles past the last: no memory traffic
@@ -228,6 +216,7 @@ __device__ __forceinline__ void pv_load(float (&v)[kGSlots][4], __amdgpu_buffer_
 // +0 for positions >= T or dims >= hd (adding +0 leaves a chain unchanged).
 // Only a partial tile or a partial column block needs the masks; they are
 // applied bitwise, so that no branch delays the LDS reads or splits the quad.
+// The weights of all slots are read before any product is stored.
 __device__ __forceinline__ float pv_mask(float p, bool keep) {
   return __uint_as_float(__float_as_uint(p) & (keep ? 0xffffffffu : 0u));
 }
@@ -236,17 +225,23 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
                                            bool cols_full, bool col_ok, int pid) {
   const int pw = pid >> 6, dd = pid & 63;
   const bool full = cols_full && (t + 1) * kTile <= T;
+  float4 w[kGSlots];
 #pragma unroll
   for (int g = 0; g < kGSlots; g++) {
     const int grp = pw + kPWaves * g;
-    if (kPWaves * (g + 1) <= kGroups || grp < kGroups) {      // compile-time true except the last slot
+    if (kPWaves * (g + 1) <= kGroups || grp < kGroups)         // compile-time true except the last slot
+      w[g] = *reinterpret_cast<const float4 *>(W + t * kTile + 4 * grp);
+  }
+#pragma unroll
+  for (int g = 0; g < kGSlots; g++) {
+    const int grp = pw + kPWaves * g;
+    if (kPWaves * (g + 1) <= kGroups || grp < kGroups) {
       const int jb = t * kTile + 4 * grp;
-      const float4 w = *reinterpret_cast<const float4 *>(W + jb);
       float4 p;
-      p.x = w.x * v[g][0];
-      p.y = w.y * v[g][1];
-      p.z = w.z * v[g][2];
-      p.w = w.w * v[g][3];
+      p.x = w[g].x * v[g][0];
+      p.y = w[g].y * v[g][1];
+      p.z = w[g].z * v[g][2];
+      p.w = w[g].w * v[g][3];
       if (!full) {
         p.x = pv_mask(p.x, col_ok && jb + 0 < T);
         p.y = pv_mask(p.y, col_ok && jb + 1 < T);
@@ -258,26 +253,40 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
   }
 }
 
-__global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, const float *bmax, const float *vc,
-                                                        const int *d_pos, int H, int KVH, int hd, int max_seq,
-                                                        int nch, float *o, float *obm) {
-  extern __shared__ float lds[];
-  __shared__ float red[kPvThreads / 64];
-  __shared__ qd::SeqScratch seq;
-  const int h = head_of_block(blockIdx.x, H, KVH), d0 = blockIdx.y * kChains;
-  const int T = *d_pos + 1;
-  const int kvh = h / (H / KVH);
+// One PV block with CM softmax terms per thread (512 * CM >= T).
+//  1. Requests the head's block maxima, this thread's CM scores, and the
+//     producers' first three V tiles, in that order, so that each wait leaves
+//     the later requests in flight.
+//  2. Softmax weights (llama.c:557-572): m = max of the block maxima,
+//     e_j = expf(s_j - m) in registers, their sequential sum S exactly
+//     (qdev_seqsum.h), then w_j = e_j * (1 / S) into LDS.
+//  3. o_d = sum_j w_j * V_jd, j in order (llama.c:570-575): wave 0 owns the
+//     chains; waves 1-7 form the product tiles.
+template <int CM>
+__device__ __forceinline__ void pv_block(const float *scores, const float *bmax, const float *vc, int T, int h,
+                                         int kvh, int hd, int max_seq, int nch, float *o, float *obm, float *lds,
+                                         float *red, qd::SeqScratch &seq) {
+  const int d0 = blockIdx.y * kChains, tid = threadIdx.x;
   const int wcap = (max_seq + kTile - 1) / kTile * kTile;
   float *W = lds;
   float *P = lds + wcap;                                 // 2 tiles of kChains x kTS
-  const int tid = threadIdx.x;
   const int ntile = (T + kTile - 1) / kTile;
-  const float *Vh = vc + (size_t)kvh * max_seq * hd;
+  const float *sh = scores + (size_t)h * max_seq;
 
-  // the producers' first V tiles are requested before the softmax (three tiles
-  // of loads in flight per lane: 60, within what one wave can have outstanding;
-  // loads past the last tile read in-bounds rows and are never used)
+  // 1. requests (block maxima: at most 128 <= 512 per head)
+  const int nc = (T + kScoreBlock - 1) / kScoreBlock;
+  float m = tid < nc ? bmax[(size_t)h * nch + tid] : -INFINITY;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void *)sh, (short)0, max_seq * 4, 0x00020000);
+  const int j0 = tid * CM;
+  float e[CM];
+#pragma unroll
+  for (int c = 0; c < CM; c += 4) {       // positions past max_seq read as 0; past T they are masked below
+    const v4i q = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(srs, (j0 + c) * 4, 0, 0));
+    e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
+    e[c + 2] = __int_as_float(q.z); e[c + 3] = __int_as_float(q.w);
+  }
   const int pid = tid - 64;
+  const float *Vh = vc + (size_t)kvh * max_seq * hd;
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)Vh, (short)0, max_seq * hd * 4, 0x00020000);
   const bool cols_full = d0 + kChains <= hd, col_ok = d0 + (pid & 63) < hd;
@@ -285,41 +294,53 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 #pragma unroll
   for (int g = 0; g < kGSlots; g++) {
     const int grp = (pid >> 6) + kPWaves * g;
-    vo[g] = grp < kGroups ? (4 * grp * hd + d0 + (pid & 63)) * 4 : 0x40000000;   // unused slot: out of range
+    vo[g] = tid >= 64 && grp < kGroups ? (4 * grp * hd + d0 + (pid & 63)) * 4 : 0x40000000;   // else: no traffic
   }
   float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
-  if (tid >= 64) {
-    pv_load(r0, vrs, vo, 0, ntile, hd);
-    pv_load(r1, vrs, vo, 1, ntile, hd);
-    pv_load(r2, vrs, vo, 2, ntile, hd);
-  }
+  pv_load(r0, vrs, vo, 0, ntile, hd);
+  pv_load(r1, vrs, vo, 1, ntile, hd);
+  pv_load(r2, vrs, vo, 2, ntile, hd);
 
-  // softmax weights of head h (llama.c:557-572)
-  const int nc = (T + kScoreBlock - 1) / kScoreBlock;
-  float m = -INFINITY;
-  for (int c = tid; c < nc; c += kPvThreads) m = fmaxf(m, bmax[(size_t)h * nch + c]);
+  // 2. softmax weights
   m = block_max<kPvThreads>(m, red);
-  const float *sh = scores + (size_t)h * max_seq;
-  if (T <= kPvThreads * 4) softmax_weights<4>(sh, T, m, W, seq);
-  else if (T <= kPvThreads * 8) softmax_weights<8>(sh, T, m, W, seq);
-  else if (T <= kPvThreads * 16) softmax_weights<16>(sh, T, m, W, seq);
-  else softmax_weights<32>(sh, T, m, W, seq);
+#pragma unroll
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m) : 0.0f;
+  const float sum = qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m); });
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int c = 0; c < CM; c += 4)
+    if (j0 + c < wcap)
+      *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
   __syncthreads();
 
-  // o_d = sum_j w_j * V_jd, j in order (llama.c:570-575)
+  // 3. the chains
   if (tid < 64) {
     const int d = d0 + tid;
     float acc = 0.0f;
     for (int t = 0; t < ntile; t++) {
       lds_barrier();
-      const float *Pt = P + (t & 1) * kChains * kTS + tid * kTS;
+      // tile t: four groups of eight 16-byte reads, the next group in flight
+      // while the current one is added
+      const float4 *Pt = reinterpret_cast<const float4 *>(P + (t & 1) * kChains * kTS + tid * kTS);
+      constexpr int GR = 8, NG = kTile / 4 / GR;
+      float4 buf[2][GR];
 #pragma unroll
-      for (int jj = 0; jj < kTile; jj += 4) {
-        const float4 p = *reinterpret_cast<const float4 *>(Pt + jj);
-        acc += p.x;
-        acc += p.y;
-        acc += p.z;
-        acc += p.w;
+      for (int i = 0; i < GR; i++) buf[0][i] = Pt[i];
+#pragma unroll
+      for (int g = 0; g < NG; g++) {
+        if (g + 1 < NG) {
+#pragma unroll
+          for (int i = 0; i < GR; i++) buf[(g + 1) & 1][i] = Pt[(g + 1) * GR + i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < GR; i++) {
+          acc += buf[g & 1][i].x;
+          acc += buf[g & 1][i].y;
+          acc += buf[g & 1][i].z;
+          acc += buf[g & 1][i].w;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (d < hd) o[(size_t)h * hd + d] = acc;
@@ -360,6 +381,21 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
       pv_load(r0, vrs, vo, t + 9, ntile, hd);
     }
   }
+}
+
+__global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, const float *bmax, const float *vc,
+                                                        const int *d_pos, int H, int KVH, int hd, int max_seq,
+                                                        int nch, float *o, float *obm) {
+  extern __shared__ float lds[];
+  __shared__ float red[kPvThreads / 64];
+  __shared__ qd::SeqScratch seq;
+  const int h = head_of_block(blockIdx.x, H, KVH);
+  const int T = *d_pos + 1;
+  const int kvh = h / (H / KVH);
+  if (T <= kPvThreads * 4) pv_block<4>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
+  else if (T <= kPvThreads * 8) pv_block<8>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
+  else if (T <= kPvThreads * 16) pv_block<16>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
+  else pv_block<32>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
 }
 
 // ---------------------------------------------------------------------------

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include "qdev_math.h"
+#include "qdev_norm.h"
 #include "qdev_seqsum.h"
 #include "qhip.h"
 #include "qhip_internal.h"
@@ -47,64 +48,21 @@ __global__ void k_embed(const int8_t *wte, const float *s, int dm, const int *d_
 }
 
 // One block per row: rmsnorm.c:7-21 then the activation quantization of qmatmul.
-// Thread t holds elements [t*CM, t*CM + CM) (NT*CM >= kpad); the sequential
-// float sum of the squares (the reference's loop order) is evaluated exactly
-// by qd::seq_sum_nonneg.
+// Thread t holds elements [t*CM, t*CM + CM) (NT*CM >= kpad).
 template <int NT, int CM>
 __global__ __launch_bounds__(NT) void k_rmsnorm_quant(const float *x, int dm, const float *gamma, float eps,
                                                        int8_t *qa, int kpad, float *as) {
-  static_assert(CM % 4 == 0, "chunk of whole 16-byte words");
   __shared__ float red[NT / 64];
   __shared__ qd::SeqScratch seq;
   const int row = blockIdx.x;
-  const float *xr = x + (size_t)row * dm;
   const int j0 = threadIdx.x * CM;
-  float v[CM], sq[CM], gm[CM];
-  if (j0 + CM <= dm && (dm & 3) == 0) {
-#pragma unroll
-    for (int c = 0; c < CM; c += 4) {
-      const float4 t = *reinterpret_cast<const float4 *>(xr + j0 + c);
-      const float4 u = *reinterpret_cast<const float4 *>(gamma + j0 + c);   // in flight during the sum
-      v[c] = t.x; v[c + 1] = t.y; v[c + 2] = t.z; v[c + 3] = t.w;
-      gm[c] = u.x; gm[c + 1] = u.y; gm[c + 2] = u.z; gm[c + 3] = u.w;
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < CM; c++) {
-      v[c] = j0 + c < dm ? xr[j0 + c] : 0.0f;
-      gm[c] = j0 + c < dm ? gamma[j0 + c] : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < CM; c++) sq[c] = v[c] * v[c];
-  float ms = qd::seq_sum_nonneg<NT, CM>(sq, dm, seq, [&](int i) { return xr[i] * xr[i]; });   // rmsnorm.c:15
-  const float inv_n = 1.0f / (float)dm;
-  ms *= inv_n;
-  const float r = 1.0f / sqrtf(ms + eps);
-  float mx = 0.0f;
-#pragma unroll
-  for (int c = 0; c < CM; c++) {
-    v[c] = j0 + c < dm ? v[c] * r * gm[c] : 0.0f;
-    mx = fmaxf(mx, fabsf(v[c]));
-  }
-  mx = qd::wave_max_f32(mx);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = red[0];
-#pragma unroll
-  for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
-  const float a_s = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+  float y[CM];
+  const float a_s = qd::rmsnorm_row<NT, CM>(x + (size_t)row * dm, dm, gamma, eps, y, red, seq);
   const float inv = 1.0f / a_s;
   int8_t *qr = qa + (size_t)row * kpad;
 #pragma unroll
-  for (int c = 0; c < CM; c += 4) {
-    if (j0 + c < kpad) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int e = 0; e < 4; e++) w |= (uint32_t)(uint8_t)(int8_t)qd::quant_i8(v[c + e], inv) << (8 * e);
-      *reinterpret_cast<uint32_t *>(qr + j0 + c) = w;
-    }
-  }
+  for (int c = 0; c < CM; c += 4)
+    if (j0 + c < kpad) *reinterpret_cast<uint32_t *>(qr + j0 + c) = qd::quant_word(y, c, inv);
   if (threadIdx.x == 0) as[row] = a_s;
 }
 
@@ -252,39 +210,6 @@ __global__ void k_pf_rope_append(const float *qkv, int H, int KVH, int hd, const
   }
 }
 
-// First index of the maximum (sampler.c:8-21), then advance the position.
-__global__ __launch_bounds__(1024) void k_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out,
-                                                         int max_seq) {
-  __shared__ float bv[16];
-  __shared__ int bi[16];
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  for (int j = threadIdx.x; j < n; j += blockDim.x) {
-    const float a = v[j];
-    if (idx == 0x7fffffff || a > best) { best = a; idx = j; }   // a thread's first element, then strict >
-  }
-  // combine: larger value wins, equal values keep the lower index
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(idx, o, 64);
-    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-  }
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane == 0) { bv[w] = best; bi[w] = idx; }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float b = bv[0];
-    int bi0 = bi[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); i++)
-      if (bv[i] > b || (bv[i] == b && bi[i] < bi0)) { b = bv[i]; bi0 = bi[i]; }
-    const int pos = d_state[0];
-    if (pos < max_seq) d_out[pos] = bi0;
-    if (pos + 1 >= d_state[1] && pos + 1 <= max_seq) d_in[pos + 1] = bi0;
-    d_state[0] = pos + 1;
-  }
-}
-
 // matrix.c:354-374 on the reference's row-major (K, N) layout: one thread per column.
 __global__ void k_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
@@ -359,11 +284,6 @@ int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, 
                         const float *sin_t, int p0, float *q_out, float *kc, float *vc, int max_seq) {
   QH_LAUNCH(QK_PF_OTHER, k_pf_rope_append, dim3(n_heads + 2 * n_kv, R), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t,
             sin_t, p0, q_out, kc, vc, max_seq);
-  return 0;
-}
-
-int qhip_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out, int max_seq) {
-  QH_LAUNCH(QK_ARGMAX, k_argmax_advance, dim3(1), dim3(1024), 0, v, n, d_in, d_state, d_out, max_seq);
   return 0;
 }
 

@@ -15,7 +15,10 @@
 //          (llama.c:583-587) and each block records max |out| for the quantizer.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "qdev_math.h"
+#include "qdev_norm.h"
 #include "qhip.h"
 #include "qhip_internal.h"
 
@@ -49,14 +52,19 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
 // PRO = 1: the activation arrives unquantized (v, n values, with per-block
 // maxima of |v| in vbm); every block quantizes it itself (quant.c:66-78, the
 // operations of k_quant_blocks) into LDS while its first weights are in flight.
+// PRO = 2: the activation is the residual stream v (n values) before its
+// rmsnorm (gain vbm, epsilon eps); every block normalizes and quantizes it
+// itself (the operations of k_rmsnorm_quant) while its first weights are in
+// flight.
 template <int MODE, int KCH, int R, int PRO>
 __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float *as_p, const int8_t *W,
                                                   const float *ws, int N, int kpad, float *out, const float *bias,
                                                   float *bm, int *bi, const float *v, int n, const float *vbm,
-                                                  int nvbm) {
+                                                  int nvbm, float eps) {
   __shared__ float red[4];
   __shared__ int redi[4];
   __shared__ __attribute__((aligned(16))) int8_t qsh[PRO ? KCH * 1024 : 16];
+  __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
   float best = -INFINITY;
   int besti = 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -69,7 +77,18 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   }
   v4i a[KCH];
   float as;
-  if (PRO) {
+  if constexpr (PRO == 2) {
+    constexpr int CM = 4 * KCH;                      // 256 threads x CM values = kpad
+    float y[CM];
+    as = qd::rmsnorm_row<256, CM>(v, n, vbm, eps, y, red, seq);
+    const float inv = 1.0f / as;
+#pragma unroll
+    for (int c = 0; c < CM; c += 4)
+      *reinterpret_cast<uint32_t *>(qsh + threadIdx.x * CM + c) = qd::quant_word(y, c, inv);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+  } else if (PRO == 1) {
     float mx = 0.0f;
     for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
     mx = qd::wave_max_f32(mx);
@@ -301,23 +320,38 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
 }
 
+// Output channels per wave: the SwiGLU GEMV that normalizes its own input takes
+// 6 (gate, up) pairs, so that at the 8B shape its blocks are resident together
+// and each block's prologue runs once.
+constexpr int rows_per_wave(int mode, int pro) { return pro == 2 && mode == MODE_SWIGLU ? 6 : 2; }
+
 template <int MODE, int PRO>
 int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws, int N, int kpad, float *out,
-           const float *bias, float *bm, int *bi, const float *v, int n, const float *vbm, int nvbm) {
-  constexpr int R = 2;
+           const float *bias, float *bm, int *bi, const float *v, int n, const float *vbm, int nvbm, float eps) {
+  constexpr int R = rows_per_wave(MODE, PRO);
   const dim3 grid((N + 4 * R - 1) / (4 * R));
 #define QG(KCH)                                                                                             \
   QH_LAUNCH(cls, (k_gemv_dec<MODE, KCH, R, PRO>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi, \
-            v, n, vbm, nvbm)
-  switch (kpad) {
-    case 2048: QG(2); return 0;
-    case 4096: QG(4); return 0;
-    case 8192: QG(8); return 0;
-    case 14336: QG(14); return 0;
-    default:
-      if (PRO) return qh::fail_msg("gemv: fused quantization needs kpad 2048/4096/8192/14336");
-      QH_LAUNCH(cls, k_gemv_dec_any<MODE>, dim3((N + 3) / 4), dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi);
-      return 0;
+            v, n, vbm, nvbm, eps)
+  if constexpr (PRO == 2) {                          // 256 threads x 4*KCH values of the row
+    switch (kpad) {
+      case 2048: QG(2); return 0;
+      case 4096: QG(4); return 0;
+      case 8192: QG(8); return 0;
+      default: return qh::fail_msg("gemv: fused rmsnorm needs kpad 2048/4096/8192");
+    }
+  } else {
+    switch (kpad) {
+      case 2048: QG(2); return 0;
+      case 4096: QG(4); return 0;
+      case 8192: QG(8); return 0;
+      case 14336: QG(14); return 0;
+      default:
+        if (PRO) return qh::fail_msg("gemv: fused quantization needs kpad 2048/4096/8192/14336");
+        QH_LAUNCH(cls, k_gemv_dec_any<MODE>, dim3((N + 3) / 4), dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm,
+                  bi);
+        return 0;
+    }
   }
 #undef QG
 }
@@ -335,10 +369,10 @@ extern "C" int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *a
                              int N, int kpad, float *out, const float *bias, float *bm, int *bi) {
   if (kpad % 16) return qh::fail_msg("gemv: kpad must be a multiple of 16");
   switch (mode) {
-    case MODE_PLAIN: return launch<MODE_PLAIN, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
-    case MODE_RESID: return launch<MODE_RESID, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
-    case MODE_SWIGLU: return launch<MODE_SWIGLU, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
-    case MODE_HEAD: return launch<MODE_HEAD, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0);
+    case MODE_PLAIN: return launch<MODE_PLAIN, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0, 0.0f);
+    case MODE_RESID: return launch<MODE_RESID, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0, 0.0f);
+    case MODE_SWIGLU: return launch<MODE_SWIGLU, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0, 0.0f);
+    case MODE_HEAD: return launch<MODE_HEAD, 0>(cls, qa, as, W, ws, N, kpad, out, bias, bm, bi, NULL, 0, NULL, 0, 0.0f);
     default: return qh::fail_msg("gemv: bad mode");
   }
 }
@@ -348,7 +382,26 @@ extern "C" int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *a
 extern "C" int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vbm, int nvbm, const int8_t *W,
                                  const float *ws, int N, int kpad, float *out) {
   if (kpad % 16 || n > kpad) return qh::fail_msg("gemv_resid_q: bad shape");
-  return launch<MODE_RESID, 1>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, NULL, NULL, v, n, vbm, nvbm);
+  return launch<MODE_RESID, 1>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, NULL, NULL, v, n, vbm, nvbm, 0.0f);
+}
+
+// SwiGLU GEMV whose activation is rmsnorm(x) quantized, formed inside every
+// block (replaces qhip_rmsnorm_quant + mode 2).
+extern "C" int qhip_gemv_swiglu_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+                                     const float *ws, int N, int kpad, float *out, float *bm) {
+  if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_swiglu_norm: unsupported shape");
+  return launch<MODE_SWIGLU, 2>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, bm, NULL, x, dm, gamma, 0, eps);
+}
+
+// Shapes qhip_gemv_swiglu_norm supports.
+extern "C" int qhip_gemv_norm_ok(int kpad, int dm) {
+  return (kpad == 2048 || kpad == 4096 || kpad == 8192) && dm > 0 && dm <= kpad;
+}
+
+// Number of per-block maxima qhip_gemv_swiglu_norm writes.
+extern "C" int qhip_gemv_norm_blocks(int N) {
+  constexpr int per_block = 4 * rows_per_wave(MODE_SWIGLU, 2);
+  return (N + per_block - 1) / per_block;
 }
 
 // Shapes qhip_gemv_resid_q supports.

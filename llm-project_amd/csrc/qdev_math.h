@@ -173,18 +173,35 @@ __device__ __forceinline__ int quant_i8(float v, float inv) {
 }
 
 // ---------------------------------------------------------------------------
-// wave64 reductions
+// wave64 reductions through DPP lane moves (no LDS round trips): within each
+// row of 16 lanes by swaps at distance 1 and 2 (quad_perm) and the half-row and
+// row mirrors, then across the four rows by reading lanes 0, 16, 32 and 48.
+// Every lane receives the result.
 // ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_mov<0xB1>(v);      // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);      // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);     // row_half_mirror
+  v += dpp_mov<0x140>(v);     // row_mirror
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 }  // namespace qd

@@ -41,22 +41,25 @@
 
 namespace qd {
 
-constexpr int kSeqMaxHard = 512;           // hard steps held in LDS
+constexpr int kSeqMaxHard = 512;           // hard steps held in LDS (kSeqMaxHard / waves per wave)
 constexpr int kSeqMaxWaves = 16;           // blocks of up to 1024 threads
 
 struct SeqScratch {
-  float wf[kSeqMaxWaves];
-  float wm[kSeqMaxWaves];
-  unsigned wk[kSeqMaxWaves];
-  int wh[kSeqMaxWaves];
-  int wg[kSeqMaxWaves];
-  int4 hs[kSeqMaxHard];          // hard step: k prefix before it, index, term bits, grid after it
-  unsigned ktot;
-  int nhard;
+  float wf[kSeqMaxWaves];        // per wave: predicted total of its terms
+  float wm[kSeqMaxWaves];        //           largest term
+  unsigned wk[kSeqMaxWaves];     //           total of its k (mod 2^32)
+  int wh[kSeqMaxWaves];          //           hard steps
+  int wg[kSeqMaxWaves];          //           grid of the run continuing past its last step
+  int wgi[kSeqMaxWaves];         //           grid of its first step if that step is easy, else -1
+  int4 hs[kSeqMaxHard];          // hard steps by wave: k prefix within the wave, index, term bits, grid after it
   int bad;
-  int fell;
   float result;
 };
+
+// Lane i receives lane i-1's value, lane 0 receives 0 (DPP wave_shr:1).
+__device__ __forceinline__ unsigned seq_shr1(unsigned x) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x138, 0xf, 0xf, true);
+}
 
 // Wave inclusive scan by DPP row shifts and row broadcasts (32-bit lanes).
 __device__ __forceinline__ unsigned seq_dpp_u(unsigned x, int sel) {
@@ -96,6 +99,13 @@ __device__ __forceinline__ int seq_wave_scan(int x) {
   return x;
 }
 
+// Inclusive scan within the first row of 16 lanes (row_shr only).
+__device__ __forceinline__ unsigned seq_row_scan(unsigned x) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) x += seq_dpp_u(x, k);
+  return x;
+}
+
 // grid of a float p >= 0 (see above)
 __device__ __forceinline__ int seq_grid(float p) { return max((int)(__float_as_uint(p) >> 23), 1); }
 
@@ -111,12 +121,15 @@ __device__ float seq_serial(int n, Term term) {
 // of the NT-thread block (NT = blockDim.x, a multiple of 64, at most 1024) holds
 // terms t*CM .. t*CM+CM-1 in a[], zero past n; n <= NT*CM.  term(i) returns term
 // i again, for the rare fallback.  All threads must call it; all get the result.
-// info (optional, written by thread 0): number of hard steps, 1 if the fallback ran.
+// Three block barriers; S may be used again by the next call without another.
+// info (optional, written by one thread): number of hard steps, 1 if the
+// fallback ran.
 template <int NT, int CM, typename Term>
 __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term term, int *info = nullptr) {
   static_assert(NT % 64 == 0 && NT / 64 <= kSeqMaxWaves, "block size");
   static_assert(CM >= 1 && CM <= 32, "terms per thread");
   constexpr int NW = NT / 64;
+  constexpr int HCAP = kSeqMaxHard / NW;           // hard steps recorded per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // 1. predicted partial sum at the start of this thread's chunk (any order will
@@ -132,117 +145,154 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
     loc = (q[0] + q[1]) + (q[2] + q[3]);
   }
   const float xin = seq_wave_scan(loc);
-  const float min_ = seq_wave_scan_max(cmx);
-  const float mprev = __shfl_up(min_, 1, 64);
-  if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = min_; }
+  const float mex = seq_wave_scan_max(__uint_as_float(seq_shr1(__float_as_uint(cmx))));   // exclusive
+  if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = fmaxf(mex, cmx); }
   if (tid == 0) S.bad = 0;
   __syncthreads();
-  float P0 = xin - loc, M0 = lane ? mprev : 0.0f;
+  float P0 = xin - loc, M0 = mex;
 #pragma unroll
   for (int w = 0; w < NW - 1; w++)
     if (w < wave) { P0 += S.wf[w]; M0 = fmaxf(M0, S.wm[w]); }
 
-  // classify; rho: 16 standard deviations of the rounding error a sequential sum
+  // 2. classify; rho: 16 standard deviations of the rounding error a sequential sum
   // of i terms accumulates (each below half a unit in the last place), plus the
-  // error of the float scan that forms the prediction
+  // error of the float scan that forms the prediction.  kp[c] is the k total of
+  // this thread's steps before step c.
   const float rho = 0x1p-20f * __builtin_amdgcn_sqrtf((float)((tid + 1) * CM + 2)) + 0x1p-17f;
   const float lo = 1.0f - rho, hi = 1.0f + rho;
-  float P = P0, L = M0;
   unsigned ks = 0, hardmask = 0;
   int nh = 0, gin = -1, gout = 1;
-  int kk[CM], gh[CM];
-#pragma unroll
-  for (int c = 0; c < CM; c++) {
-    const float Pn = P + a[c];
-    const int g0 = seq_grid(fmaxf(P * lo, L));
-    L = fmaxf(L, a[c]);
-    const int g1 = seq_grid(Pn * hi);
-    const float t = fminf(ldexpf(a[c], 150 - g0), 0x1p30f);
-    const bool easy = (g0 == g1) && (__builtin_amdgcn_fractf(t) != 0.5f);
-    kk[c] = easy ? (int)__builtin_rintf(t) : 0;
-    ks += (unsigned)kk[c];
-    nh += easy ? 0 : 1;
-    hardmask |= easy ? 0u : (1u << c);
-    if (c == 0) gin = easy ? g0 : -1;
-    gh[c] = seq_grid(fmaxf(Pn * lo, L));               // grid after this step, if it is hard
-    gout = easy ? g0 : gh[c];                          // grid of the run continuing past this step
-    P = Pn;
-  }
-
-  // 2. scans of the k totals and hard counts; exchange of boundary grids
-  // (k totals are kept modulo 2^32: only differences within one run are used,
-  // and a run on grid g adds at most 2^23 units)
-  const unsigned kin = seq_wave_scan(ks);
-  const int hin = seq_wave_scan(nh);
-  const int gprev_lane = __shfl_up(gout, 1, 64);
-  if (lane == 63) { S.wk[wave] = kin; S.wh[wave] = hin; S.wg[wave] = gout; }
-  __syncthreads();
-  unsigned kb = kin - ks, ktot = 0;
-  int hb = hin - nh, htot = 0;
-#pragma unroll
-  for (int w = 0; w < NW; w++) {
-    const unsigned wk = S.wk[w];
-    const int wh = S.wh[w];
-    if (w < wave) { kb += wk; hb += wh; }
-    ktot += wk;
-    htot += wh;
-  }
-  const int gprev = lane ? gprev_lane : (wave ? S.wg[wave - 1] : 1);
-  if (gin >= 0 && gin != gprev) S.bad = 1;
-  if (htot > kSeqMaxHard) {
-    if (tid == 0) {
-      S.result = seq_serial(n, term);
-      if (info) { info[0] = htot; info[1] = 1; }
-    }
-    __syncthreads();
-    const float r = S.result;
-    __syncthreads();
-    return r;
-  }
-
-  // 3. hard steps in order: k prefix before the step, its index, the term and
-  // the grid after it
-  if (nh) {
-    unsigned kp = kb;
-    int m = hb;
+  unsigned kp[CM];
+  int gh[CM];
+  const int gA = seq_grid(fmaxf(P0 * lo, M0)), gB = seq_grid((P0 + loc) * hi);
+  if (__all(gA == gB)) {
+    // every chunk of the wave is predicted on one grid: only exact ties are hard
 #pragma unroll
     for (int c = 0; c < CM; c++) {
-      if ((hardmask >> c) & 1u) {
-        S.hs[m] = make_int4((int)kp, threadIdx.x * CM + c, __float_as_int(a[c]), gh[c]);
-        m++;
-      } else {
-        kp += (unsigned)kk[c];
-      }
+      const float t = fminf(ldexpf(a[c], 150 - gA), 0x1p30f);
+      const bool tie = __builtin_amdgcn_fractf(t) == 0.5f;
+      kp[c] = ks;
+      ks += tie ? 0u : (unsigned)__builtin_rintf(t);
+      nh += tie ? 1 : 0;
+      hardmask |= tie ? (1u << c) : 0u;
+      gh[c] = gA;
+    }
+    gin = (hardmask & 1u) ? -1 : gA;
+    gout = gA;
+  } else {
+    float P = P0, L = M0;
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+      const float Pn = P + a[c];
+      const int g0 = seq_grid(fmaxf(P * lo, L));
+      L = fmaxf(L, a[c]);
+      const int g1 = seq_grid(Pn * hi);
+      const float t = fminf(ldexpf(a[c], 150 - g0), 0x1p30f);
+      const bool easy = (g0 == g1) && (__builtin_amdgcn_fractf(t) != 0.5f);
+      kp[c] = ks;
+      ks += easy ? (unsigned)__builtin_rintf(t) : 0u;
+      nh += easy ? 0 : 1;
+      hardmask |= easy ? 0u : (1u << c);
+      if (c == 0) gin = easy ? g0 : -1;
+      gh[c] = seq_grid(fmaxf(Pn * lo, L));               // grid after this step, if it is hard
+      gout = easy ? g0 : gh[c];                          // grid of the run continuing past this step
+      P = Pn;
     }
   }
+
+  // 3. wave scans of the k totals and hard counts, the boundary check between
+  // lanes, and the hard steps recorded in the wave's region in order (k totals
+  // are kept modulo 2^32: only differences within one run are used, and a run
+  // on grid g adds at most 2^23 units)
+  const unsigned kin = seq_wave_scan(ks);
+  const int hin = seq_wave_scan(nh);
+  const int gprev = (int)seq_shr1((unsigned)gout);
+  if (lane > 0 && gin >= 0 && gin != gprev) S.bad = 1;
+  if (nh && hin <= HCAP) {
+    const unsigned kb = kin - ks;
+    int m = wave * HCAP + hin - nh;
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+      const bool h = (hardmask >> c) & 1u;
+      if (h) S.hs[m] = make_int4((int)(kb + kp[c]), tid * CM + c, __float_as_int(a[c]), gh[c]);
+      m += h ? 1 : 0;
+    }
+  }
+  if (lane == 63) { S.wk[wave] = kin; S.wh[wave] = hin; S.wg[wave] = gout; }
+  if (lane == 0) S.wgi[wave] = gin;
   __syncthreads();
 
-  // 4. the walk, with the proof of every run.  Wave 0 takes the hard steps 64 at
-  // a time: lane i prepares run m = base + i (the run before hard step m; run
-  // htot is the tail) and its exact total, the serial part adds only run totals
-  // and hard terms (lane i records the partial sum its run starts from), and the
+  // 4. wave 0: the waves' offsets, the boundary checks between waves, and the
+  // walk with the proof of every run.  The hard steps are taken 64 at a time:
+  // lane i prepares run m = base + i (the run before hard step m; run htot is
+  // the tail) and its exact total, the serial part adds only run totals and
+  // hard terms (lane i records the partial sum its run starts from), and the
   // runs are then proven in parallel.
   if (wave == 0) {
+    const unsigned wk_l = lane < NW ? S.wk[lane] : 0u;
+    const int wh_l = lane < NW ? S.wh[lane] : 0;
+    const int wg_prev = lane >= 1 && lane < NW ? S.wg[lane - 1] : 1;
+    const int wgi_l = lane < NW ? S.wgi[lane] : -1;
+    const unsigned koff_l = seq_row_scan(wk_l) - wk_l;            // lanes 0..NW-1
+    const int hoff_l = (int)(seq_row_scan((unsigned)wh_l) - (unsigned)wh_l);
+    const unsigned ktot = (unsigned)__builtin_amdgcn_readlane((int)(koff_l + wk_l), NW - 1);
+    const int htot = __builtin_amdgcn_readlane(hoff_l + wh_l, NW - 1);
+    bool ok = S.bad == 0 && !__any(lane < NW && (wh_l > HCAP || (wgi_l >= 0 && wgi_l != wg_prev)));
+    int hoff_s[NW], wh_s[NW];
+    unsigned koff_s[NW];
+#pragma unroll
+    for (int v = 0; v < NW; v++) {
+      hoff_s[v] = __builtin_amdgcn_readlane(hoff_l, v);
+      wh_s[v] = __builtin_amdgcn_readlane(wh_l, v);
+      koff_s[v] = (unsigned)__builtin_amdgcn_readlane((int)koff_l, v);
+    }
     float s = 0.0f;
-    bool ok = S.bad == 0;
-    for (int base = 0; base <= htot; base += 64) {
+    for (int base = 0; ok && base <= htot; base += 64) {
       const int m = base + lane;
-      // this lane's hard step (or the tail) and the one before it
-      const int4 cur = m < htot ? S.hs[m] : make_int4((int)ktot, NT * CM, 0, 1);
-      const int4 prv = m > 0 && m <= htot ? S.hs[m - 1] : make_int4(0, -1, 0, 1);
+      // the waves holding this lane's hard step (or the tail) and the one before it
+      int rc = m, rp = m - 1;
+      unsigned kc = 0, kpv = 0;
+#pragma unroll
+      for (int v = 0; v < NW; v++) {
+        const bool sc = wh_s[v] > 0 && m >= hoff_s[v], sp = wh_s[v] > 0 && m - 1 >= hoff_s[v];
+        rc = sc ? v * HCAP + m - hoff_s[v] : rc;
+        kc = sc ? koff_s[v] : kc;
+        rp = sp ? v * HCAP + m - 1 - hoff_s[v] : rp;
+        kpv = sp ? koff_s[v] : kpv;
+      }
+      int4 cur = make_int4((int)ktot, NT * CM, 0, 1), prv = make_int4(0, -1, 0, 1);
+      if (m < htot) {
+        cur = S.hs[rc];
+        cur.x = (int)((unsigned)cur.x + kc);
+      }
+      if (m > 0 && m <= htot) {
+        prv = S.hs[rp];
+        prv.x = (int)((unsigned)prv.x + kpv);
+      }
       const unsigned K = (unsigned)cur.x - (unsigned)prv.x;
       const int gp = prv.w;
       const bool live = m <= htot && cur.y > prv.y + 1;   // run m has steps
-      const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;
-      const float ah = __int_as_float(cur.z);
+      const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;   // 0 past the tail: adds nothing
+      const float ah = __int_as_float(cur.z);                     // 0 from the tail on
       const int cnt = min(64, htot + 1 - base);
       float st = 0.0f;
-      for (int i = 0; i < cnt; i++) {
-        const float Ti = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(T), i));
-        const float ai = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ah), i));
-        st = lane == i ? s : st;
-        s = s + Ti;
-        s = s + ai;
+      // batches of 8 steps with constant lane indices (the reads are not
+      // serialized behind scalar index arithmetic); steps past cnt add +0
+#pragma unroll
+      for (int b = 0; b < 8; b++) {
+        if (8 * b >= cnt) break;
+        float Ti[8], ai[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          Ti[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(T), 8 * b + u));
+          ai[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ah), 8 * b + u));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          st = lane == 8 * b + u ? s : st;
+          s = s + Ti[u];
+          s = s + ai[u];
+        }
       }
       const float top = __uint_as_float((unsigned)(gp + 1) << 23);
       const bool bad = live && !(K <= (1u << 23) && seq_grid(st) == gp && T <= top - st);
@@ -255,9 +305,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
     }
   }
   __syncthreads();
-  const float r = S.result;
-  __syncthreads();
-  return r;
+  return S.result;
 }
 
 }  // namespace qd

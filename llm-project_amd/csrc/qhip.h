@@ -112,12 +112,15 @@ int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vbm, int nvbm
                       int N, int kpad, float *out);
 int qhip_gemv_fused_ok(int kpad);
 int qhip_gemv_blocks(int N, int kpad);
+// SwiGLU GEMV (mode 2) whose activation is rmsnorm(x; gamma, eps) quantized,
+// formed in each block from the dm values of x; kpad in {2048, 4096, 8192}
+// (qhip_gemv_norm_ok).  It writes qhip_gemv_norm_blocks(N) per-block maxima.
+int qhip_gemv_swiglu_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+                          const float *ws, int N, int kpad, float *out, float *bm);
+int qhip_gemv_norm_ok(int kpad, int dm);
+int qhip_gemv_norm_blocks(int N);
 // Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
 int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as);
-// first index of the maximum (sampler.c:8-21) of v -> d_out[pos]; when pos + 1 is
-// past the staged inputs (d_state[1]) it also becomes d_in[pos + 1]; then
-// d_state[0] = pos + 1.  pos = d_state[0].
-int qhip_argmax_advance(const float *v, int n, int *d_in, int *d_state, int *d_out, int max_seq);
 
 // Many-row int8 GEMM on MFMA (k_gemm.hip): out[i][j] for i < M, j < N from
 // activation rows A [M][kpad] and weight rows W [N][kpad] (SwiGLU: [2N][kpad]),

@@ -13,6 +13,7 @@ enum {
 
 namespace qh {
 hipStream_t stream();
+int num_cus();            // compute units of the device (set by qhip_init)
 int fail(const char *what, hipError_t e);
 int fail_msg(const char *msg);
 int check_launch(const char *what);

@@ -14,6 +14,7 @@
 namespace {
 hipStream_t g_stream = nullptr;
 int g_ready = 0;
+int g_ncu = 0;
 thread_local char g_err[512] = "";
 std::mutex g_init_mu;
 
@@ -35,6 +36,7 @@ hipEvent_t take_event() {
 
 namespace qh {
 hipStream_t stream() { return g_stream; }
+int num_cus() { return g_ncu; }
 
 int fail(const char *what, hipError_t e) {
   snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
@@ -79,6 +81,8 @@ int qhip_init(void) {
   if ((e = hipSetDevice(0)) != hipSuccess) return fail("hipSetDevice", e);
   if ((e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking)) != hipSuccess)
     return fail("hipStreamCreate", e);
+  if ((e = hipDeviceGetAttribute(&g_ncu, hipDeviceAttributeMultiprocessorCount, 0)) != hipSuccess || g_ncu <= 0)
+    return fail("hipDeviceGetAttribute(multiprocessor count)", e);
   g_ready = 1;
   return 0;
 }

@@ -543,6 +543,9 @@ void llama_kv_free(LlamaKV *kv) {
 static int enqueue_step(const QDev *d, const KVDev *kd) {
   const int *dpos = &d->d_state[0];
   const size_t per = (size_t)d->max_seq * d->kvd;
+  const int nbo = qhip_attention_nbm(d->H, d->hd);
+  const int fuse_o = qhip_gemv_fused_ok(d->kp_qd), fuse_gu = qhip_gemv_norm_ok(d->kp_dm, d->dm);
+  const int nbh = fuse_gu ? qhip_gemv_norm_blocks(d->dff) : qhip_gemv_blocks(d->dff, d->kp_dm);
   int rc = qhip_embed(d->wte, d->wte_s, d->dm, d->d_in, d->d_state, d->x);
   for (int l = 0; l < d->L && !rc; l++) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
@@ -550,17 +553,21 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
     rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
     rc |= qhip_rope_append(d->qkv, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, dpos, d->q, kc, vc, d->max_seq);
     rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o, d->obm);
-    if (qhip_gemv_fused_ok(d->kp_qd)) {        // o quantized inside the Wo GEMV
-      rc |= qhip_gemv_resid_q(6, d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->wo[l], d->so[l], d->dm,
-                              d->kp_qd, d->x);
+    if (fuse_o) {        // o quantized inside the Wo GEMV
+      rc |= qhip_gemv_resid_q(6, d->o, d->qd, d->obm, nbo, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x);
     } else {
-      rc |= qhip_quant_blocks(d->o, d->qd, d->obm, qhip_attention_nbm(d->H, d->hd), d->qa, d->kp_qd, d->as);
+      rc |= qhip_quant_blocks(d->o, d->qd, d->obm, nbo, d->qa, d->kp_qd, d->as);
       rc |= qhip_gemv_dec(1, 6, d->qa, d->as, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, NULL, NULL);
     }
-    rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
-    rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
+    if (fuse_gu) {       // rmsnorm inside the gate|up GEMV
+      rc |= qhip_gemv_swiglu_norm(7, d->x, d->dm, d->g_ffn[l], d->eps, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu,
+                                  d->hbm);
+    } else {
+      rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
+      rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
+    }
     // (h is quantized by its own kernel: every down block quantizing d_ff values costs more than it saves)
-    rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, qhip_gemv_blocks(d->dff, d->kp_dm), d->qa, d->kp_ff, d->as);
+    rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, nbh, d->qa, d->kp_ff, d->as);
     rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
   }
   if (!rc) rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_final, d->eps, d->qa, d->kp_dm, d->as);
