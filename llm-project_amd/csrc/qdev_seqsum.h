@@ -275,9 +275,11 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
       const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;   // 0 past the tail: adds nothing
       const float ah = __int_as_float(cur.z);                     // 0 from the tail on
       const int cnt = min(64, htot + 1 - base);
-      float st = 0.0f;
-      // batches of 8 steps with constant lane indices (the reads are not
-      // serialized behind scalar index arithmetic); steps past cnt add +0
+      // Batches of 8 steps with constant lane indices; steps past cnt add +0.
+      // The partial sum before each step is shifted into a lane register (lane
+      // 0 takes it, every other lane takes its neighbour's), so after c steps
+      // lane j holds the sum before step c-1-j.
+      int sh = 0, c = 0;
 #pragma unroll
       for (int b = 0; b < 8; b++) {
         if (8 * b >= cnt) break;
@@ -289,11 +291,13 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-          st = lane == 8 * b + u ? s : st;
+          sh = __builtin_amdgcn_update_dpp(__float_as_int(s), sh, 0x138, 0xf, 0xf, false);   // wave_shr:1
           s = s + Ti[u];
           s = s + ai[u];
         }
+        c += 8;
       }
+      const float st = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * ((c - 1 - lane) & 63), sh));
       const float top = __uint_as_float((unsigned)(gp + 1) << 23);
       const bool bad = live && !(K <= (1u << 23) && seq_grid(st) == gp && T <= top - st);
       ok = ok && !__any(bad);
