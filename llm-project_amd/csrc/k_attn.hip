@@ -407,28 +407,31 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 constexpr int kPfKeys = 128;          // keys per scores block, one per thread
 constexpr int kPfRows = 16;           // query rows per scores / PV block
 constexpr int kPfTile = 32;           // keys per PV tile
+constexpr int kPvRows = 8;            // query rows per PV block
 constexpr int kPfMaxRows = 512;       // rows per attention pass (bounds the scratch)
 
-// Block (KV head, 16 query rows, 128 keys): thread t owns key j0 + t and every
-// (head, row) pair of the block as a sequential chain over d.  The pairs go 8 at
-// a time; the K row streams through registers 16 dims at a time while the 8
-// chains advance together (their independent adds hide each other's latency);
-// q comes from LDS as broadcast reads.  A compiler barrier per chunk keeps the
-// loads of later chunks from being hoisted (they would need hundreds of VGPRs).
+// Block (KV head, 16 query rows, 256 keys): thread t owns keys j0 + t and
+// j0 + 128 + t and, for both, every (head, row) pair of the block as a
+// sequential chain over d.  The pairs go 8 at a time, 16 chains per thread
+// (their independent adds hide each other's latency).  q comes from LDS as
+// broadcast reads, each feeding both keys (the LDS return path, not the VALU,
+// would bound one key per thread); the K rows stream from global memory 16
+// dims at a time, the next chunk in flight while the current one is added.
 constexpr int kPfChains = 8;
+constexpr int kPfKeysPerBlock = 2 * kPfKeys;
 
 template <int HD>
 __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
                                                          int KVH, int max_seq, float scale, float *w, int Tp) {
   static_assert(HD % 16 == 0, "K rows stream in 16-dim chunks");
-  constexpr int NQ = HD / 4;
+  constexpr int NQ = HD / 4, NCH = NQ / 4;
   extern __shared__ __attribute__((aligned(16))) float qsh[];        // [G * kPfRows][HD]
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows, j0 = blockIdx.z * kPfKeys;
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows, j0 = blockIdx.z * kPfKeysPerBlock;
   const int G = H / KVH;
   const int rend = min(R, r0 + kPfRows);
   const int jvis = p0 + rend - 1;                                    // last key any row here sees
   if (j0 > jvis) return;                                             // uniform for the block
-  const int t = threadIdx.x, j = j0 + t;
+  const int t = threadIdx.x, ja = j0 + t, jb = j0 + kPfKeys + t;
   const int npair = G * kPfRows;                                     // a multiple of 16
   for (int idx = t; idx < npair * HD; idx += kPfKeys) {
     const int pair = idx / HD, d = idx % HD;
@@ -436,35 +439,49 @@ __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const flo
     qsh[idx] = q[(size_t)r * H * HD + (size_t)(kvh * G + g) * HD + d];
   }
   __syncthreads();
-  const float4 *krow = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(j, jvis)) * HD);
+  const float4 *ka = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(ja, jvis)) * HD);
+  const float4 *kb = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(jb, jvis)) * HD);
 #pragma unroll 1
   for (int c0 = 0; c0 < npair; c0 += kPfChains) {
-    float acc[kPfChains];
+    float acca[kPfChains], accb[kPfChains];
 #pragma unroll
-    for (int c = 0; c < kPfChains; c++) acc[c] = 0.0f;
+    for (int c = 0; c < kPfChains; c++) acca[c] = accb[c] = 0.0f;
     const float4 *qb = reinterpret_cast<const float4 *>(qsh + (size_t)c0 * HD);
-#pragma unroll 1
-    for (int dc = 0; dc < NQ; dc += 4) {
-      float4 kr[4];
+    float4 xa[4], xb[4], na[4], nb[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) kr[i] = krow[dc + i];
+    for (int i = 0; i < 4; i++) { xa[i] = ka[i]; xb[i] = kb[i]; }
+#pragma unroll 1
+    for (int ch = 0; ch < NCH; ch++) {
+      const int dc = 4 * ch;
+      if (ch + 1 < NCH) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) { na[i] = ka[dc + 4 + i]; nb[i] = kb[dc + 4 + i]; }
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
 #pragma unroll
         for (int c = 0; c < kPfChains; c++) {
           const float4 qv = qb[c * NQ + dc + i];
-          acc[c] += qv.x * kr[i].x;
-          acc[c] += qv.y * kr[i].y;
-          acc[c] += qv.z * kr[i].z;
-          acc[c] += qv.w * kr[i].w;
+          acca[c] += qv.x * xa[i].x;
+          accb[c] += qv.x * xb[i].x;
+          acca[c] += qv.y * xa[i].y;
+          accb[c] += qv.y * xb[i].y;
+          acca[c] += qv.z * xa[i].z;
+          accb[c] += qv.z * xb[i].z;
+          acca[c] += qv.w * xa[i].w;
+          accb[c] += qv.w * xb[i].w;
         }
       }
       asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 4; i++) { xa[i] = na[i]; xb[i] = nb[i]; }
     }
 #pragma unroll
     for (int c = 0; c < kPfChains; c++) {
       const int pair = c0 + c, g = pair / kPfRows, r = r0 + pair % kPfRows;
-      if (r < R && j <= p0 + r) w[((size_t)(kvh * G + g) * R + r) * Tp + j] = acc[c] * scale;
+      float *wr = w + ((size_t)(kvh * G + g) * R + r) * Tp;
+      if (r < R && ja <= p0 + r) wr[ja] = acca[c] * scale;
+      if (r < R && jb <= p0 + r) wr[jb] = accb[c] * scale;
     }
   }
 }
@@ -508,64 +525,124 @@ __global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int 
   else pf_softmax_row<NT, 32>(row, T, m, seq);
 }
 
-// Block (KV head, 16 query rows): thread (g, d) owns the 16 chains o[r][h][d]
-// (h = kvh*G + g), each a sequential sum over its row's visible keys.  V and
-// weight tiles of 32 keys are staged in LDS; weights are broadcast reads.
-template <int HD>
-__global__ __launch_bounds__(1024) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
-                                                int max_seq, int Tp, float *o) {
-  __shared__ __attribute__((aligned(16))) float vs[kPfTile][HD];
-  __shared__ __attribute__((aligned(16))) float wsh[8][kPfRows][kPfTile];
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows;
-  const int G = H / KVH;
-  const int rend = min(R, r0 + kPfRows);
-  const int g = threadIdx.x / HD, d = threadIdx.x % HD;
+// Block (KV head, 8 query rows): thread (g, dd) owns the 16 chains o[r][h][d]
+// for d = dd and dd + HD/2 (h = kvh*G + g), each a sequential sum over its
+// row's visible keys.  V and weight tiles of kPfTile keys are staged in LDS,
+// double-buffered: the next tile's global reads are in flight while the current
+// one is added.  Weights are broadcast reads, each feeding both dims.  Keys a
+// row does not see contribute nothing: in the tiles on the causal diagonal
+// their products are replaced by +0 bitwise (adding +0 leaves a chain
+// unchanged), and weights of unseen keys are stored as 0.
+template <int HD, int G>
+__global__ __launch_bounds__(G * HD / 2) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
+                                                      int max_seq, int Tp, float *o) {
+  static_assert(HD % 8 == 0, "two dims per thread, float4 V words");
+  constexpr int HH = HD / 2;
+  constexpr int nthr = G * HH;
+  constexpr int VW = kPfTile * HD / 4;                               // float4 words of a V tile
+  constexpr int WW = G * kPvRows * kPfTile / 4;                      // float4 words of a weight tile
+  constexpr int VU = (VW + nthr - 1) / nthr, WU = (WW + nthr - 1) / nthr;   // words per thread
+  __shared__ __attribute__((aligned(16))) float vs[2][kPfTile][HD];
+  __shared__ __attribute__((aligned(16))) float wsh[2][G][kPvRows][kPfTile];
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPvRows;
+  const int rend = min(R, r0 + kPvRows);
+  const int g = threadIdx.x / HH, dd = threadIdx.x % HH;
   const int h = kvh * G + g;
   const int kend = p0 + rend;                                        // keys 0 .. kend-1 are used
-  float acc[kPfRows];
+  const float *Vh = vc + (size_t)kvh * max_seq * HD;
+
+  // one tile's global words for this thread: V words i = tid + nthr*u, weight words likewise
+  float4 rv[VU], rw[WU];
+  auto fetch = [&](int k0) {
 #pragma unroll
-  for (int c = 0; c < kPfRows; c++) acc[c] = 0.0f;
-  for (int k0 = 0; k0 < kend; k0 += kPfTile) {
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < kPfTile * HD; idx += blockDim.x) {
-      const int key = k0 + idx / HD;
-      vs[idx / HD][idx % HD] = key < kend ? vc[((size_t)kvh * max_seq + key) * HD + idx % HD] : 0.0f;
+    for (int u = 0; u < VU; u++) {
+      const int i = threadIdx.x + nthr * u;
+      const int key = k0 + i / (HD / 4);
+      rv[u] = (i < VW && key < kend) ? *reinterpret_cast<const float4 *>(Vh + (size_t)key * HD + 4 * (i % (HD / 4)))
+                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    for (int idx = threadIdx.x; idx < G * kPfRows * kPfTile; idx += blockDim.x) {
-      const int gg = idx / (kPfRows * kPfTile), rr = (idx / kPfTile) % kPfRows, kk = idx % kPfTile;
-      const int r = r0 + rr, key = k0 + kk;
-      wsh[gg][rr][kk] = (r < R && key <= p0 + r) ? w[((size_t)(kvh * G + gg) * R + r) * Tp + key] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < WU; u++) {
+      const int i = threadIdx.x + nthr * u;
+      float4 v4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (i < WW) {
+        const int gg = i / (kPvRows * kPfTile / 4), rr = (i / (kPfTile / 4)) % kPvRows, kq = 4 * (i % (kPfTile / 4));
+        const int r = r0 + rr, key = k0 + kq;
+        if (r < R && key <= p0 + r) {                                // this word holds a seen key
+          const float4 t4 = *reinterpret_cast<const float4 *>(w + ((size_t)(kvh * G + gg) * R + r) * Tp + key);
+          v4.x = t4.x;
+          v4.y = key + 1 <= p0 + r ? t4.y : 0.0f;
+          v4.z = key + 2 <= p0 + r ? t4.z : 0.0f;
+          v4.w = key + 3 <= p0 + r ? t4.w : 0.0f;
+        }
+      }
+      rw[u] = v4;
     }
-    __syncthreads();
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+      const int i = threadIdx.x + nthr * u;
+      if (i < VW) *reinterpret_cast<float4 *>(&vs[buf][i / (HD / 4)][4 * (i % (HD / 4))]) = rv[u];
+    }
+#pragma unroll
+    for (int u = 0; u < WU; u++) {
+      const int i = threadIdx.x + nthr * u;
+      if (i < WW) reinterpret_cast<float4 *>(&wsh[buf][0][0][0])[i] = rw[u];
+    }
+  };
+
+  float acc[kPvRows][2];
+#pragma unroll
+  for (int c = 0; c < kPvRows; c++) acc[c][0] = acc[c][1] = 0.0f;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int k0 = 0, buf = 0; k0 < kend; k0 += kPfTile, buf ^= 1) {
+    if (k0 + kPfTile < kend) fetch(k0 + kPfTile);
     const bool full = k0 + kPfTile <= p0 + r0 + 1;                   // every key here is seen by every row
     if (full) {
-#pragma unroll 4
+#pragma unroll 2
       for (int kk = 0; kk < kPfTile; kk += 4) {
-        float v[4];
+        float va[4], vb[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = vs[kk + u][d];
+        for (int u = 0; u < 4; u++) { va[u] = vs[buf][kk + u][dd]; vb[u] = vs[buf][kk + u][dd + HH]; }
 #pragma unroll
-        for (int c = 0; c < kPfRows; c++) {
-          const float4 wv = *reinterpret_cast<const float4 *>(&wsh[g][c][kk]);
-          acc[c] += wv.x * v[0];
-          acc[c] += wv.y * v[1];
-          acc[c] += wv.z * v[2];
-          acc[c] += wv.w * v[3];
+        for (int c = 0; c < kPvRows; c++) {
+          const float4 wv = *reinterpret_cast<const float4 *>(&wsh[buf][g][c][kk]);
+          acc[c][0] += wv.x * va[0];
+          acc[c][1] += wv.x * vb[0];
+          acc[c][0] += wv.y * va[1];
+          acc[c][1] += wv.y * vb[1];
+          acc[c][0] += wv.z * va[2];
+          acc[c][1] += wv.z * vb[2];
+          acc[c][0] += wv.w * va[3];
+          acc[c][1] += wv.w * vb[3];
         }
       }
     } else {
       for (int kk = 0; kk < kPfTile; kk++) {
         const int key = k0 + kk;
-        const float v = vs[kk][d];
+        const float va = vs[buf][kk][dd], vb = vs[buf][kk][dd + HH];
 #pragma unroll
-        for (int c = 0; c < kPfRows; c++)
-          if (key <= p0 + r0 + c) acc[c] += wsh[g][c][kk] * v;          // row r0 + c sees keys <= p0 + r0 + c
+        for (int c = 0; c < kPvRows; c++) {
+          const float wv = wsh[buf][g][c][kk];
+          const bool seen = key <= p0 + r0 + c;                        // row r0 + c sees keys <= p0 + r0 + c
+          acc[c][0] += pv_mask(wv * va, seen);
+          acc[c][1] += pv_mask(wv * vb, seen);
+        }
       }
     }
+    if (k0 + kPfTile < kend) stash(buf ^ 1);
+    __syncthreads();
   }
 #pragma unroll
-  for (int c = 0; c < kPfRows; c++)
-    if (r0 + c < R) o[(size_t)(r0 + c) * H * HD + (size_t)h * HD + d] = acc[c];
+  for (int c = 0; c < kPvRows; c++)
+    if (r0 + c < R) {
+      float *orow = o + (size_t)(r0 + c) * H * HD + (size_t)h * HD;
+      orow[dd] = acc[c][0];
+      orow[dd + HH] = acc[c][1];
+    }
 }
 
 template <int HD>
@@ -573,14 +650,20 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
                  float scale, float *w, float *o) {
   const int G = H / KVH, Tp = (max_seq + 3) & ~3;
   const int Tmax = p0 + R;
-  const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeys - 1) / kPfKeys);
+  const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeysPerBlock - 1) / kPfKeysPerBlock);
   QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
             max_seq, scale, w, Tp);
   if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
   else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
   else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
-  QH_LAUNCH(QK_PF_ATTN, k_pf_pv<HD>, dim3(KVH, (R + kPfRows - 1) / kPfRows), dim3(G * HD), 0, w, vc, R, p0, H, KVH,
-            max_seq, Tp, o);
+  const dim3 pgrid(KVH, (R + kPvRows - 1) / kPvRows);
+  switch (G) {
+    case 1: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 1>), pgrid, dim3(HD / 2), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
+    case 2: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 2>), pgrid, dim3(HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
+    case 4: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 4>), pgrid, dim3(2 * HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
+    case 8: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 8>), pgrid, dim3(4 * HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
+    default: return qh::fail_msg("pf_attention: query heads per KV head must be 1, 2, 4 or 8");
+  }
   return 0;
 }
 
