@@ -265,7 +265,7 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
 template <int CM>
 __device__ __forceinline__ void pv_block(const float *scores, const float *bmax, const float *vc, int T, int h,
                                          int kvh, int hd, int max_seq, int nch, float *o, float *obm, float *lds,
-                                         float *red, qd::SeqScratch &seq) {
+                                         float *red, qd::SeqScratch &seq, const uint64_t *tab) {
   const int d0 = blockIdx.y * kChains, tid = threadIdx.x;
   const int wcap = (max_seq + kTile - 1) / kTile * kTile;
   float *W = lds;
@@ -304,8 +304,9 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   // 2. softmax weights
   m = block_max<kPvThreads>(m, red);
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m) : 0.0f;
-  const float sum = qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m); });
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m, tab) : 0.0f;
+  const float sum =
+      qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m, tab); });
   const float inv = 1.0f / sum;
 #pragma unroll
   for (int c = 0; c < CM; c += 4)
@@ -389,13 +390,15 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   extern __shared__ float lds[];
   __shared__ float red[kPvThreads / 64];
   __shared__ qd::SeqScratch seq;
+  __shared__ uint64_t tab[32];
+  qd::exp_table_to_lds(tab);                             // published by the block max's barrier
   const int h = head_of_block(blockIdx.x, H, KVH);
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
-  if (T <= kPvThreads * 4) pv_block<4>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
-  else if (T <= kPvThreads * 8) pv_block<8>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
-  else if (T <= kPvThreads * 16) pv_block<16>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
-  else pv_block<32>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq);
+  if (T <= kPvThreads * 4) pv_block<4>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else if (T <= kPvThreads * 8) pv_block<8>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else if (T <= kPvThreads * 16) pv_block<16>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else pv_block<32>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
 }
 
 // ---------------------------------------------------------------------------
@@ -404,14 +407,14 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 // (the same sums in the same order).  Scratch w[h][r][Tp] holds the scores and
 // then, in place, the softmax weights.
 // ---------------------------------------------------------------------------
-constexpr int kPfKeys = 128;          // keys per scores block, one per thread
+constexpr int kPfKeys = 256;          // threads per scores block (two keys each)
 constexpr int kPfRows = 16;           // query rows per scores / PV block
 constexpr int kPfTile = 32;           // keys per PV tile
 constexpr int kPvRows = 8;            // query rows per PV block
 constexpr int kPfMaxRows = 512;       // rows per attention pass (bounds the scratch)
 
-// Block (KV head, 16 query rows, 256 keys): thread t owns keys j0 + t and
-// j0 + 128 + t and, for both, every (head, row) pair of the block as a
+// Block (KV head, 16 query rows, 512 keys): thread t owns keys j0 + t and
+// j0 + 256 + t and, for both, every (head, row) pair of the block as a
 // sequential chain over d.  The pairs go 8 at a time, 16 chains per thread
 // (their independent adds hide each other's latency).  q comes from LDS as
 // broadcast reads, each feeding both keys (the LDS return path, not the VALU,
@@ -490,12 +493,12 @@ __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const flo
 // forms e_j for j in [t*CM, t*CM + CM), the block evaluates their sequential
 // sum exactly, w_j = e_j * (1 / S) in place.
 template <int NT, int CM>
-__device__ __forceinline__ void pf_softmax_row(float *row, int T, float m, qd::SeqScratch &seq) {
+__device__ __forceinline__ void pf_softmax_row(float *row, int T, float m, qd::SeqScratch &seq, const uint64_t *tab) {
   const int j0 = threadIdx.x * CM;
   float e[CM];
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(row[j0 + c] - m) : 0.0f;
-  const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m); });
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(row[j0 + c] - m, tab) : 0.0f;
+  const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m, tab); });
   const float inv = 1.0f / sum;
 #pragma unroll
   for (int c = 0; c < CM; c++)
@@ -506,23 +509,23 @@ template <int NT>
 __global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int Tp) {
   __shared__ qd::SeqScratch seq;
   __shared__ float red[NT / 64];
+  __shared__ uint64_t tab[32];
+  qd::exp_table_to_lds(tab);
   const int r = blockIdx.x, h = blockIdx.y;
   const int T = p0 + r + 1;
   float *row = w + ((size_t)h * R + r) * Tp;
   float m = -INFINITY;
   for (int j = threadIdx.x; j < T; j += NT) m = fmaxf(m, row[j]);
   m = qd::wave_max_f32(m);
-  if (NT > 64) {
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = red[0];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();                                   // also publishes the exp table
+  m = red[0];
 #pragma unroll
-    for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
-  }
-  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, m, seq);
-  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, m, seq);
-  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, m, seq);
-  else pf_softmax_row<NT, 32>(row, T, m, seq);
+  for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
+  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, m, seq, tab);
+  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, m, seq, tab);
+  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, m, seq, tab);
+  else pf_softmax_row<NT, 32>(row, T, m, seq, tab);
 }
 
 // Block (KV head, 8 query rows): thread (g, dd) owns the 16 chains o[r][h][d]

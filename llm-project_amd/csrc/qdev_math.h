@@ -30,7 +30,9 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+// tab: the table above, or a copy of it (an LDS copy saves a memory round trip
+// per value when many values are formed); the result does not depend on it.
+__device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2Tab) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {                       // |x| >= 88, inf or nan
@@ -49,7 +51,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= Shift;
   const double r = __builtin_fma(InvLn2N, xd, -kd);
-  const uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+  const uint64_t t = tab[ki & 31] + (ki << 47);
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(C0, r, C1);
   const double r2 = r * r;
@@ -57,6 +59,11 @@ __device__ __forceinline__ float expf_glibc(float x) {
   y = __builtin_fma(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+// Copies the table into LDS (dst: 32 entries); the caller synchronizes.
+__device__ __forceinline__ void exp_table_to_lds(uint64_t *dst) {
+  if (threadIdx.x < 32) dst[threadIdx.x] = kExp2Tab[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
