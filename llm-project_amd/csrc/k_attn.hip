@@ -149,30 +149,73 @@ __device__ __forceinline__ float score_row_dot(const float *qh, const float *ks,
 // that group: G x 128 threads, thread (g, t) computes head kvh*G + g at position
 // j0 + t, and the K tile is copied into LDS once for all of them.  With n_kv a
 // multiple of 8, consecutive KV heads also fall on different XCDs.
-template <int HD>
-__global__ __launch_bounds__(1024) void k_attn_scores(const float *q, const float *kc, const int *d_pos, int H,
+// ROPE: q, k and v of the current position arrive unrotated in qkv (the QKV
+// GEMV's output, H + 2 n_kv heads of hd); every block rotates its G query heads
+// into LDS (rope.c:48-68, the table holding cos and sin of position * inv_freq),
+// and the block holding position pos rotates k, uses it for its own row and
+// appends k and v to the cache (llama.c:551-552), which the later kernels read.
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc, float *vc, const int *d_pos, int H,
                                                        int KVH, int hd, int max_seq, float scale, float *scores,
-                                                       float *bmax, int nch) {
-  __shared__ __attribute__((aligned(16))) float qs[HD ? 4 : 8 * 512];
+                                                       float *bmax, int nch, const float *cos_t,
+                                                       const float *sin_t) {
+  __shared__ __attribute__((aligned(16))) float qs[8 * (HD ? HD : 512)];
   __shared__ __attribute__((aligned(16))) float ks[HD ? kScoreBlock * HD : 4];
+  __shared__ __attribute__((aligned(16))) float kcur[HD ? HD : 512];
   __shared__ float red[16];
   const int kvh = blockIdx.x, c = blockIdx.y;
   const int G = H / KVH;
-  const int T = *d_pos + 1;
+  const int pos = *d_pos, T = pos + 1;
   if (c * kScoreBlock >= T) return;                      // uniform for the block
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x / kScoreBlock), t = threadIdx.x % kScoreBlock;
   const int h = kvh * G + g;
   const int j0 = c * kScoreBlock, j = j0 + t;
-  const float *Kh = kc + (size_t)kvh * max_seq * hd;
-  float dot;
-  if (HD) {
-    score_copy_rows<HD ? HD : 128>(Kh, j0, T, ks, j0 + kScoreBlock <= T, (int)(blockDim.x >> 6));
-    __syncthreads();                                     // the copies (vmcnt)
-    dot = score_row_dot<HD ? HD : 128>(q + (size_t)h * HD, ks, t);
+  const bool last = j0 + kScoreBlock >= T;               // this block holds position pos
+  float *Kh = kc + (size_t)kvh * max_seq * hd;
+  const int half = hd >> 1;
+  if (HD) score_copy_rows<HD ? HD : 128>(Kh, j0, T, ks, j0 + kScoreBlock <= T, (int)(blockDim.x >> 6));
+  // the group's query heads into LDS (rotated when ROPE)
+  if (ROPE) {
+    const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
+    for (int i = threadIdx.x; i < G * half; i += blockDim.x) {
+      const int gg = i / half, k = i % half;
+      const float *xh = q + (size_t)(kvh * G + gg) * hd;
+      const float cs = ct[k], sn = st[k];
+      const float x1 = xh[k], x2 = xh[k + half];
+      qs[gg * hd + k] = x1 * cs - x2 * sn;
+      qs[gg * hd + k + half] = x2 * cs + x1 * sn;
+    }
+    if (last) {
+      const float *kh = q + (size_t)(H + kvh) * hd, *vh = q + (size_t)(H + KVH + kvh) * hd;
+      float *kdst = Kh + (size_t)pos * hd, *vdst = vc + ((size_t)kvh * max_seq + pos) * hd;
+      for (int k = threadIdx.x; k < half; k += blockDim.x) {
+        const float cs = ct[k], sn = st[k];
+        const float x1 = kh[k], x2 = kh[k + half];
+        const float y1 = x1 * cs - x2 * sn, y2 = x2 * cs + x1 * sn;
+        kcur[k] = y1;
+        kcur[k + half] = y2;
+        kdst[k] = y1;
+        kdst[k + half] = y2;
+      }
+      for (int d = threadIdx.x; d < hd; d += blockDim.x) vdst[d] = vh[d];
+    }
   } else {
     for (int d = threadIdx.x; d < G * hd; d += blockDim.x) qs[d] = q[(size_t)kvh * G * hd + d];
+  }
+  __syncthreads();                                       // q, the current k row, the K tile copies (vmcnt)
+  if (HD && ROPE && last) {                              // the current row into its (skewed) place in the tile
+    constexpr int CPR = (HD ? HD : 128) / 4;
+    const int rr = pos - j0;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x)
+      ks[rr * hd + 4 * (((d >> 2) + (rr & 7)) & (CPR - 1)) + (d & 3)] = kcur[d];
     __syncthreads();
-    dot = j < T ? score_dot_any(qs + g * hd, Kh + (size_t)j * hd, hd) : 0.0f;
+  }
+  float dot;
+  if (HD) {
+    dot = score_row_dot<HD ? HD : 128>(qs + g * hd, ks, t);
+  } else {
+    const float *kr = (ROPE && j == pos) ? kcur : Kh + (size_t)min(j, pos) * hd;
+    dot = j < T ? score_dot_any(qs + g * hd, kr, hd) : 0.0f;
   }
   float s = -INFINITY;
   if (j < T) {
@@ -678,8 +721,10 @@ size_t pv_lds_bytes(int max_seq) {
 
 }  // namespace
 
-extern "C" int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads,
-                              int n_kv, int hd, int max_seq, float scale, float *scores, float *o, float *obm) {
+namespace {
+template <bool ROPE>
+int attention(const float *q, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv, int hd, int max_seq,
+              float scale, const float *cos_t, const float *sin_t, float *scores, float *o, float *obm) {
   const int nch = (max_seq + kScoreBlock - 1) / kScoreBlock;
   float *bmax = scores + (size_t)n_heads * max_seq;
   const size_t pv_lds = pv_lds_bytes(max_seq);
@@ -695,22 +740,35 @@ extern "C" int qhip_attention(const float *q, const float *kc, const float *vc, 
   }
   const int G = n_heads / n_kv;
   if (G * kScoreBlock > 1024 || G * hd > 512 * 8) return qh::fail_msg("attention: more than 8 query heads per KV head");
+  if (hd > 512 || (hd & 1)) return qh::fail_msg("attention: head_dim must be even and at most 512");
   const dim3 sgrid(n_kv, nch);
   const dim3 sblock(G * kScoreBlock);
-  if (hd > 512) return qh::fail_msg("attention: head_dim above 512");
   switch (hd) {
     case 128:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<128>, sgrid, sblock, 0, q, kc, d_pos, n_heads, n_kv, hd,
-                max_seq, scale, scores, bmax, nch);
+      QH_LAUNCH(QK_ATTN, (k_attn_scores<128, ROPE>), sgrid, sblock, 0, q, kc, vc, d_pos, n_heads, n_kv, hd, max_seq,
+                scale, scores, bmax, nch, cos_t, sin_t);
       break;
     default:
-      QH_LAUNCH(QK_ATTN, k_attn_scores<0>, sgrid, sblock, 0, q, kc, d_pos, n_heads, n_kv, hd,
-                max_seq, scale, scores, bmax, nch);
+      QH_LAUNCH(QK_ATTN, (k_attn_scores<0, ROPE>), sgrid, sblock, 0, q, kc, vc, d_pos, n_heads, n_kv, hd, max_seq,
+                scale, scores, bmax, nch, cos_t, sin_t);
       break;
   }
   QH_LAUNCH(QK_ATTN_PV, k_attn_pv, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores, bmax,
             vc, d_pos, n_heads, n_kv, hd, max_seq, nch, o, obm);
   return 0;
+}
+}  // namespace
+
+extern "C" int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads,
+                              int n_kv, int hd, int max_seq, float scale, float *scores, float *o, float *obm) {
+  return attention<false>(q, const_cast<float *>(kc), const_cast<float *>(vc), d_pos, n_heads, n_kv, hd, max_seq,
+                          scale, nullptr, nullptr, scores, o, obm);
+}
+
+extern "C" int qhip_attention_rope(const float *qkv, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv,
+                                   int hd, int max_seq, float scale, const float *cos_t, const float *sin_t,
+                                   float *scores, float *o, float *obm) {
+  return attention<true>(qkv, kc, vc, d_pos, n_heads, n_kv, hd, max_seq, scale, cos_t, sin_t, scores, o, obm);
 }
 
 // Number of per-block maxima qhip_attention writes to obm.

@@ -96,6 +96,12 @@ size_t qhip_attention_scratch(int n_heads, int max_seq);
 int qhip_attention(const float *q, const float *kc, const float *vc, const int *d_pos,
                    int n_heads, int n_kv, int hd, int max_seq, float scale, float *scores,
                    float *o, float *obm);
+// qhip_attention with RoPE and the cache append folded in: q, k, v of position
+// pos = *d_pos arrive unrotated in qkv (n_heads + 2 n_kv heads); k (rotated)
+// and v are appended to the cache at pos (what qhip_rope_append does).
+int qhip_attention_rope(const float *qkv, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv, int hd,
+                        int max_seq, float scale, const float *cos_t, const float *sin_t, float *scores, float *o,
+                        float *obm);
 int qhip_attention_nbm(int n_heads, int hd);
 // Decode GEMV with one activation row (k_gemv.hip): mode 0 plain (+bias), 1
 // residual add, 2 SwiGLU over gate rows [0,N) and up rows [N,2N) writing h and

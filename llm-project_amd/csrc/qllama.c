@@ -551,8 +551,8 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
     rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
     rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
-    rc |= qhip_rope_append(d->qkv, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, dpos, d->q, kc, vc, d->max_seq);
-    rc |= qhip_attention(d->q, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->scores, d->o, d->obm);
+    rc |= qhip_attention_rope(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos,
+                              d->rope_sin, d->scores, d->o, d->obm);
     if (fuse_o) {        // o quantized inside the Wo GEMV
       rc |= qhip_gemv_resid_q(6, d->o, d->qd, d->obm, nbo, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x);
     } else {
