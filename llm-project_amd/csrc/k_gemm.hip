@@ -13,8 +13,8 @@
 // Operands are K-contiguous (activation rows [M][kpad], weight rows [N][kpad]).
 // A 256-thread block computes a 128 x 128 tile of C (SWIGLU: 64 outputs from 64
 // gate and the 64 matching up rows) in K steps of 64 bytes: both tiles are
-// staged through double-buffered LDS with 80-byte rows (conflict-free 16-byte
-// fragment reads), and each wave computes 64 x 64 with 4 x 4
+// staged through double-buffered LDS in a swizzled layout (conflict-free 16-byte
+// fragment reads and writes), and each wave computes 64 x 64 with 4 x 4
 // v_mfma_i32_16x16x64_i8.  Fragment layout (checked on gfx950): lane l holds
 // row l % 16 and bytes 16 * (l / 16) .. +15 of the 64 K values; result element
 // r of lane l is C[4 * (l / 16) + r][l % 16].
@@ -31,7 +31,12 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 enum { GM_PLAIN = 0, GM_RESID = 1, GM_SWIGLU = 2 };
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int SROW = BK + 16;               // staged row stride in bytes
+
+// Byte offset of 16-byte chunk c of staged row r: rows are 64 bytes, and the
+// chunk index is XORed with bits 1-2 of the row, so that the 16-byte accesses of
+// 16 consecutive rows (a fragment read) and of 4 consecutive rows x 4 chunks
+// (a staging write) fall in distinct bank groups.
+__device__ __forceinline__ int stage_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 3)) << 4); }
 
 // Block b -> (M tile, N tile): the row tiles of one weight tile run on one XCD
 // (workgroups are dealt to the 8 XCDs round-robin by index), so a weight tile
@@ -46,8 +51,8 @@ template <int MODE>
 __global__ __launch_bounds__(256) void k_gemm_i8(const int8_t *A, const float *as, const int8_t *W, const float *ws,
                                                  int M, int N, int kpad, float *out, int ldo, const float *bias,
                                                  int mt_count, int nt_count) {
-  __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * SROW];
-  __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * SROW];
+  __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * BK];
   int mtile, ntile;
   gemm_tile(blockIdx.x, mt_count, mtile, ntile);
   if (ntile >= nt_count) return;                                   // uniform for the block
@@ -65,7 +70,7 @@ __global__ __launch_bounds__(256) void k_gemm_i8(const int8_t *A, const float *a
   for (int i = 0; i < 2; i++) {
     const int c = tid + 256 * i, row = c >> 2;
     part[i] = c & 3;
-    soff[i] = row * SROW + part[i] * 16;
+    soff[i] = stage_off(row, part[i]);
     ga[i] = A + (size_t)min(m0 + row, M - 1) * kpad + part[i] * 16;
     int wrow;
     if (MODE == GM_SWIGLU) wrow = row < 64 ? min(n0 + row, N - 1) : N + min(n0 + row - 64, N - 1);
@@ -96,9 +101,9 @@ __global__ __launch_bounds__(256) void k_gemm_i8(const int8_t *A, const float *a
   int arow[4], brow[4];
 #pragma unroll
   for (int t = 0; t < 4; t++) {
-    arow[t] = (wm * 64 + t * 16 + (lane & 15)) * SROW + (lane >> 4) * 16;
+    arow[t] = stage_off(wm * 64 + t * 16 + (lane & 15), lane >> 4);
     const int bl = MODE == GM_SWIGLU ? (t < 2 ? wn * 32 + t * 16 : 64 + wn * 32 + (t - 2) * 16) : wn * 64 + t * 16;
-    brow[t] = (bl + (lane & 15)) * SROW + (lane >> 4) * 16;
+    brow[t] = stage_off(bl + (lane & 15), lane >> 4);
   }
 
   v4i acc[4][4];
