@@ -533,19 +533,51 @@ __global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const flo
 }
 
 // Softmax weights of one (head, row) (llama.c:557-572): NT threads, thread t
-// forms e_j for j in [t*CM, t*CM + CM), the block evaluates their sequential
-// sum exactly, w_j = e_j * (1 / S) in place.
+// holds the scores j in [t*CM, t*CM + CM) in registers (one read of the row),
+// the block takes their maximum, forms e_j, evaluates their sequential sum
+// exactly, and writes w_j = e_j * (1 / S) in place.
 template <int NT, int CM>
-__device__ __forceinline__ void pf_softmax_row(float *row, int T, float m, qd::SeqScratch &seq, const uint64_t *tab) {
+__device__ __forceinline__ void pf_softmax_row(float *row, int T, qd::SeqScratch &seq, float *red,
+                                               const uint64_t *tab) {
+  static_assert(CM % 4 == 0, "whole float4 words");
   const int j0 = threadIdx.x * CM;
   float e[CM];
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(row[j0 + c] - m, tab) : 0.0f;
+  for (int c = 0; c < CM; c += 4) {                  // rows are 16-byte aligned (Tp % 4 == 0)
+    float4 t = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (j0 + c + 4 <= T) t = *reinterpret_cast<const float4 *>(row + j0 + c);
+    else if (j0 + c < T) {
+      t.x = row[j0 + c];
+      if (j0 + c + 1 < T) t.y = row[j0 + c + 1];
+      if (j0 + c + 2 < T) t.z = row[j0 + c + 2];
+    }
+    e[c] = t.x; e[c + 1] = t.y; e[c + 2] = t.z; e[c + 3] = t.w;
+  }
+  float m = e[0];
+#pragma unroll
+  for (int c = 1; c < CM; c++) m = fmaxf(m, e[c]);
+  m = qd::wave_max_f32(m);
+  if constexpr (NT > 64) {
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
+  }
+#pragma unroll
+  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m, tab) : 0.0f;
   const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m, tab); });
   const float inv = 1.0f / sum;
 #pragma unroll
-  for (int c = 0; c < CM; c++)
-    if (j0 + c < T) row[j0 + c] = e[c] * inv;
+  for (int c = 0; c < CM; c += 4) {
+    if (j0 + c + 4 <= T) {
+      *reinterpret_cast<float4 *>(row + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (j0 + c + u < T) row[j0 + c + u] = e[c + u] * inv;
+    }
+  }
 }
 
 template <int NT>
@@ -554,21 +586,14 @@ __global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int 
   __shared__ float red[NT / 64];
   __shared__ uint64_t tab[32];
   qd::exp_table_to_lds(tab);
+  __syncthreads();                                   // publishes the exp table
   const int r = blockIdx.x, h = blockIdx.y;
   const int T = p0 + r + 1;
   float *row = w + ((size_t)h * R + r) * Tp;
-  float m = -INFINITY;
-  for (int j = threadIdx.x; j < T; j += NT) m = fmaxf(m, row[j]);
-  m = qd::wave_max_f32(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();                                   // also publishes the exp table
-  m = red[0];
-#pragma unroll
-  for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
-  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, m, seq, tab);
-  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, m, seq, tab);
-  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, m, seq, tab);
-  else pf_softmax_row<NT, 32>(row, T, m, seq, tab);
+  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, seq, red, tab);
+  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, seq, red, tab);
+  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, seq, red, tab);
+  else pf_softmax_row<NT, 32>(row, T, seq, red, tab);
 }
 
 // Block (KV head, 8 query rows): thread (g, dd) owns the 16 chains o[r][h][d]

@@ -56,7 +56,9 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
 // rmsnorm (gain vbm, epsilon eps); every block normalizes and quantizes it
 // itself (the operations of k_rmsnorm_quant) while its first weights are in
 // flight.
-template <int MODE, int KCH, int R, int PRO>
+// NS: weight rows (pairs, for SWIGLU) held in registers; rows r+1 .. r+NS-1 are
+// in flight while row r is reduced.
+template <int MODE, int KCH, int R, int PRO, int NS>
 __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float *as_p, const int8_t *W,
                                                   const float *ws, int N, int kpad, float *out, const float *bias,
                                                   float *bm, int *bi, const float *v, int n, const float *vbm,
@@ -70,10 +72,13 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j0 = (blockIdx.x * 4 + wave) * R;
   float hmax = 0.0f;
-  v4i w[KCH], u[KCH];
-  if (j0 < N) {                                      // weights first: in flight during the prologue
-    load_row(w, W + (size_t)j0 * kpad, lane);
-    if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j0) * kpad, lane);
+  v4i w[NS][KCH], u[NS][KCH];
+#pragma unroll
+  for (int r = 0; r < NS; r++) {                     // weights first: in flight during the prologue
+    if (r < R && j0 + r < N) {
+      load_row(w[r], W + (size_t)(j0 + r) * kpad, lane);
+      if (MODE == MODE_SWIGLU) load_row(u[r], W + (size_t)(N + j0 + r) * kpad, lane);
+    }
   }
   v4i a[KCH];
   float as;
@@ -137,12 +142,12 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   for (int r = 0; r < R; r++) {
     const int j = j0 + r;
     if (j >= N) break;
-    const int accw = dot_row(w, a);
+    const int accw = dot_row(w[r % NS], a);
     int accu = 0;
-    if (MODE == MODE_SWIGLU) accu = dot_row(u, a);
-    if (r + 1 < R && j + 1 < N) {                    // next channel's weights in flight
-      load_row(w, W + (size_t)(j + 1) * kpad, lane);
-      if (MODE == MODE_SWIGLU) load_row(u, W + (size_t)(N + j + 1) * kpad, lane);
+    if (MODE == MODE_SWIGLU) accu = dot_row(u[r % NS], a);
+    if (r + NS < R && j + NS < N) {                  // the slot takes row r + NS
+      load_row(w[r % NS], W + (size_t)(j + NS) * kpad, lane);
+      if (MODE == MODE_SWIGLU) load_row(u[r % NS], W + (size_t)(N + j + NS) * kpad, lane);
     }
     const int sw = qd::wave_sum_i32(accw);
     if (MODE == MODE_SWIGLU) {
@@ -320,19 +325,26 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
 }
 
-// Output channels per wave: the SwiGLU GEMV that normalizes its own input takes
-// 6 (gate, up) pairs, so that at the 8B shape its blocks are resident together
-// and each block's prologue runs once.
-constexpr int rows_per_wave(int mode, int pro) { return pro == 2 && mode == MODE_SWIGLU ? 6 : 2; }
+// Output channels per wave.  The GEMVs that normalize their own input take
+// several, so that at the 8B shape their blocks are resident together and each
+// block's prologue runs once: 6 (gate, up) pairs for SwiGLU, 4 rows for QKV.
+constexpr int rows_per_wave(int mode, int pro) { return pro == 2 ? (mode == MODE_SWIGLU ? 6 : 4) : 2; }
+
+// Weight rows in registers (measured at the 8B shape): two where that keeps
+// every wave resident (the 14336-wide down projection, the QKV GEMV with its
+// prologue), else one.
+constexpr int weight_slots(int mode, int pro, int kch) {
+  return (pro == 0 && kch == 14) || (pro == 2 && mode != MODE_SWIGLU) ? 2 : 1;
+}
 
 template <int MODE, int PRO>
 int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const float *ws, int N, int kpad, float *out,
            const float *bias, float *bm, int *bi, const float *v, int n, const float *vbm, int nvbm, float eps) {
   constexpr int R = rows_per_wave(MODE, PRO);
   const dim3 grid((N + 4 * R - 1) / (4 * R));
-#define QG(KCH)                                                                                             \
-  QH_LAUNCH(cls, (k_gemv_dec<MODE, KCH, R, PRO>), grid, dim3(256), 0, qa, as, W, ws, N, kpad, out, bias, bm, bi, \
-            v, n, vbm, nvbm, eps)
+#define QG(KCH)                                                                                                    \
+  QH_LAUNCH(cls, (k_gemv_dec<MODE, KCH, R, PRO, weight_slots(MODE, PRO, KCH)>), grid, dim3(256), 0, qa, as, W, ws, N, \
+            kpad, out, bias, bm, bi, v, n, vbm, nvbm, eps)
   if constexpr (PRO == 2) {                          // 256 threads x 4*KCH values of the row
     switch (kpad) {
       case 2048: QG(2); return 0;
@@ -402,6 +414,14 @@ extern "C" int qhip_gemv_norm_ok(int kpad, int dm) {
 extern "C" int qhip_gemv_norm_blocks(int N) {
   constexpr int per_block = 4 * rows_per_wave(MODE_SWIGLU, 2);
   return (N + per_block - 1) / per_block;
+}
+
+// Plain (QKV) GEMV whose activation is rmsnorm(x) quantized, formed inside
+// every block (replaces qhip_rmsnorm_quant + mode 0).
+extern "C" int qhip_gemv_plain_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+                                    const float *ws, int N, int kpad, float *out, const float *bias) {
+  if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_plain_norm: unsupported shape");
+  return launch<MODE_PLAIN, 2>(cls, NULL, NULL, W, ws, N, kpad, out, bias, NULL, NULL, x, dm, gamma, 0, eps);
 }
 
 // Shapes qhip_gemv_resid_q supports.

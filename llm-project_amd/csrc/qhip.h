@@ -124,6 +124,10 @@ int qhip_gemv_blocks(int N, int kpad);
 int qhip_gemv_swiglu_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
                           const float *ws, int N, int kpad, float *out, float *bm);
 int qhip_gemv_norm_ok(int kpad, int dm);
+// Plain GEMV (mode 0, QKV) whose activation is rmsnorm(x; gamma, eps) quantized,
+// formed in each block like qhip_gemv_swiglu_norm's; same shapes.
+int qhip_gemv_plain_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+                         const float *ws, int N, int kpad, float *out, const float *bias);
 int qhip_gemv_norm_blocks(int N);
 // Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
 int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as);

@@ -549,8 +549,13 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
   int rc = qhip_embed(d->wte, d->wte_s, d->dm, d->d_in, d->d_state, d->x);
   for (int l = 0; l < d->L && !rc; l++) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
-    rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
-    rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
+    if (fuse_gu) {       // rmsnorm inside the QKV GEMV
+      rc |= qhip_gemv_plain_norm(2, d->x, d->dm, d->g_attn[l], d->eps, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm,
+                                 d->qkv, d->bqkv[l]);
+    } else {
+      rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
+      rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
+    }
     rc |= qhip_attention_rope(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos,
                               d->rope_sin, d->scores, d->o, d->obm);
     if (fuse_o) {        // o quantized inside the Wo GEMV
