@@ -20,14 +20,14 @@ import re
 import sys
 
 COPY_KERNEL = "k_copy_v4"
-# decode GEMV call sites at the 8B shape: template <MODE, KCH, R, PRO>
-# (PRO = 1: the activation is quantized inside the kernel)
+# decode GEMV call sites at the 8B shape: template <MODE, KCH, R, PRO, NS>
+# (PRO 2: the kernel normalizes its own input; PRO 1: it quantizes its input)
 GEMV_SITES = {
-    "k_gemv_dec<0, 4, 2, 0>": "gemv_qkv",
-    "k_gemv_dec<1, 4, 2, 1>": "gemv_o",
-    "k_gemv_dec<2, 4, 2, 0>": "gemv_gate_up",
-    "k_gemv_dec<1, 14, 2, 0>": "gemv_down",
-    "k_gemv_dec<3, 4, 2, 0>": "gemv_head",
+    "k_gemv_dec<0, 4, 4, 2, 2>": "gemv_qkv",
+    "k_gemv_dec<1, 4, 2, 1, 1>": "gemv_o",
+    "k_gemv_dec<2, 4, 6, 2, 1>": "gemv_gate_up",
+    "k_gemv_dec<1, 14, 2, 0, 2>": "gemv_down",
+    "k_gemv_dec<3, 4, 2, 0, 1>": "gemv_head",
 }
 
 
