@@ -148,33 +148,6 @@ __global__ __launch_bounds__(256) void k_gemv(const int8_t *qa, const float *as,
   }
 }
 
-// rope.c:48-68 with cos/sin from the host tables at position pos; blocks
-// [0, H) rotate query heads into q_out, [H, H+KVH) rotate key heads into the
-// cache, [H+KVH, H+2KVH) copy value heads into the cache.
-__global__ void k_rope_append(const float *qkv, int H, int KVH, int hd, const float *cos_t, const float *sin_t,
-                              const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
-  const int pos = *d_pos;
-  const int half = hd >> 1;
-  const int b = blockIdx.x;
-  const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
-  if (b < H + KVH) {
-    const bool isq = b < H;
-    const float *xh = qkv + (isq ? (size_t)b * hd : (size_t)H * hd + (size_t)(b - H) * hd);
-    float *dst = isq ? q_out + (size_t)b * hd : kc + ((size_t)(b - H) * max_seq + pos) * hd;
-    for (int k = threadIdx.x; k < half; k += blockDim.x) {
-      const float c = ct[k], s = st[k];
-      const float x1 = xh[k], x2 = xh[k + half];
-      dst[k] = x1 * c - x2 * s;
-      dst[k + half] = x2 * c + x1 * s;
-    }
-  } else {
-    const int h = b - H - KVH;
-    const float *vh = qkv + (size_t)(H + KVH) * hd + (size_t)h * hd;
-    float *dst = vc + ((size_t)h * max_seq + pos) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = vh[d];
-  }
-}
-
 // Prompt rows: x[r][j] = (float)wte[ids[r]*dm + j] * scale[j]  (llama.c:534-536)
 __global__ void k_pf_embed(const int8_t *wte, const float *s, int dm, const int *ids, float *x) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
@@ -182,8 +155,9 @@ __global__ void k_pf_embed(const int8_t *wte, const float *s, int dm, const int 
   x[(size_t)r * dm + j] = (float)wte[(size_t)ids[r] * dm + j] * s[j];
 }
 
-// Prompt rows: RoPE at position p0 + r (rope.c:48-68), q -> q_out row r, k and v
-// appended to the cache at p0 + r; the operations of k_rope_append.
+// Prompt rows: RoPE at position p0 + r (rope.c:48-68) with cos/sin from the host
+// tables; blocks [0, H) rotate query heads into q_out row r, [H, H+KVH) rotate
+// key heads into the cache at p0 + r, [H+KVH, H+2KVH) copy value heads there.
 __global__ void k_pf_rope_append(const float *qkv, int H, int KVH, int hd, const float *cos_t, const float *sin_t,
                                  int p0, float *q_out, float *kc, float *vc, int max_seq) {
   const int r = blockIdx.y, pos = p0 + r;
@@ -265,13 +239,6 @@ int qhip_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W, cons
     QH_LAUNCH(cls, k_gemv, dim3((N + 3) / 4), dim3(256), 0, qa + (size_t)m0 * kpad, as + m0,
               r, W, ws, N, kpad, out + (size_t)m0 * N, bias, residual);
   }
-  return 0;
-}
-
-int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const float *cos_t, const float *sin_t,
-                     const int *d_pos, float *q_out, float *kc, float *vc, int max_seq) {
-  QH_LAUNCH(QK_ROPE, k_rope_append, dim3(n_heads + 2 * n_kv), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t, sin_t,
-            d_pos, q_out, kc, vc, max_seq);
   return 0;
 }
 

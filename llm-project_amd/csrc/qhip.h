@@ -84,11 +84,6 @@ int qhip_swiglu_quant(const float *gu, int rows, int dff, int8_t *qa, int kpad, 
 // cls names the call site for event timing (QK_* in qhip_internal.h, 12 = other)
 int qhip_gemv(const int8_t *qa, const float *as, int rows, const int8_t *W, const float *ws,
               int N, int kpad, float *out, const float *bias, int residual, int cls);
-// RoPE from host-built tables (rope.c:48-68) on q and k of qkv = [q | k | v];
-// q -> q_out, k and v appended to the per-layer cache [n_kv][max_seq][hd] at *d_pos.
-int qhip_rope_append(const float *qkv, int n_heads, int n_kv, int hd, const float *cos_t,
-                     const float *sin_t, const int *d_pos, float *q_out, float *kc, float *vc,
-                     int max_seq);
 // decode attention over cache rows 0..*d_pos (llama.c:554-576); scores must hold
 // qhip_attention_scratch(n_heads, max_seq) floats
 size_t qhip_attention_scratch(int n_heads, int max_seq);
@@ -98,7 +93,8 @@ int qhip_attention(const float *q, const float *kc, const float *vc, const int *
                    float *o, float *obm);
 // qhip_attention with RoPE and the cache append folded in: q, k, v of position
 // pos = *d_pos arrive unrotated in qkv (n_heads + 2 n_kv heads); k (rotated)
-// and v are appended to the cache at pos (what qhip_rope_append does).
+// and v are appended to the per-layer cache [n_kv][max_seq][hd] at pos; RoPE uses
+// the host-built tables (rope.c:48-68).
 int qhip_attention_rope(const float *qkv, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv, int hd,
                         int max_seq, float scale, const float *cos_t, const float *sin_t, float *scores, float *o,
                         float *obm);
