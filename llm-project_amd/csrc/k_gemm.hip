@@ -11,14 +11,23 @@
 //   SWIGLU gate j and up j -> h = (g * (1 / (1 + expf(-g)))) * u  (llama.c:583-587)
 //
 // Operands are K-contiguous (activation rows [M][kpad], weight rows [N][kpad]).
-// A 256-thread block computes a 128 x 128 tile of C (SWIGLU: 64 outputs from 64
-// gate and the 64 matching up rows) in K steps of 64 bytes: both tiles are
-// staged through double-buffered LDS in a swizzled layout (conflict-free 16-byte
-// fragment reads and writes), and each wave computes 64 x 64 with 4 x 4
-// v_mfma_i32_16x16x64_i8.  Fragment layout (checked on gfx950): lane l holds
-// row l % 16 and bytes 16 * (l / 16) .. +15 of the 64 K values; result element
-// r of lane l is C[4 * (l / 16) + r][l % 16].
+// Two kernels, both in K steps of 64 bytes through LDS:
+//  - k_gemm_i8_pipe (kpad % 64 == 0): block tiles of 128 x 128 or 256 x 128 (SWIGLU:
+//    half the columns are gate rows, half the matching up rows), 8 waves of
+//    v_mfma_i32_32x32x32_i8 (the 16x16x64 form runs at half its rate on gfx950).
+//    Both operand tiles are copied straight from global memory into LDS
+//    (global_load_lds, no staging registers), three or four K steps ahead.
+//  - k_gemm_i8 (other K): 128 x 128 tiles staged through registers into
+//    double-buffered LDS, 4 waves of 4 x 4 v_mfma_i32_16x16x64_i8; chunks past
+//    kpad are zero.
+// Fragment layouts (checked on gfx950): 16x16x64: lane l holds row l % 16 and
+// bytes 16 * (l / 16) .. +15 of the 64 K values, result element r of lane l is
+// C[4 * (l / 16) + r][l % 16]; 32x32x32: lane l holds row l % 32 and bytes
+// 16 * (l / 32) .. +15 of 32 K values, result element e of lane l is
+// C[8 * (e / 4) + 4 * (l / 32) + e % 4][l % 32].
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "qdev_math.h"
 #include "qhip.h"
@@ -27,6 +36,7 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 enum { GM_PLAIN = 0, GM_RESID = 1, GM_SWIGLU = 2 };
 
@@ -167,9 +177,235 @@ __global__ __launch_bounds__(256) void k_gemm_i8(const int8_t *A, const float *a
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined variant for kpad % 64 == 0: the same tiles, fragments and epilogues,
+// but both operand tiles go straight from global memory into LDS
+// (global_load_lds, 16 bytes per lane, no staging registers), NSTAGE K steps
+// deep.  Wave instruction i of a tile fills LDS slots 64i .. 64i+63 of 16 bytes;
+// slot s holds chunk (s % 4) ^ ((r >> 1) % 4) of row r = s / 4, i.e. the lane
+// fetches the global chunk that the swizzled layout puts there.  The waits
+// before each step's barrier name only the step's own loads (vmcnt of the
+// later stages stay in flight); the barrier itself is s_barrier without a
+// fence, which would drain every outstanding load.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// Staged layout of the pipelined kernel: 64-byte rows, 16-byte chunk c of row r
+// at slot c ^ swz32(r).  The fragment reads of v_mfma_i32_32x32x32_i8 take one
+// chunk of 32 consecutive rows per half-wave; with the XOR of row bits (1^3,
+// 2^4) the lanes the LDS serves together hit distinct banks (measured: the
+// bits-1,2 swizzle of the register-staged kernel leaves 2-way conflicts here).
+__device__ __forceinline__ int swz32(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | ((((r >> 2) ^ (r >> 4)) & 1) << 1); }
+__device__ __forceinline__ int stage_off32(int r, int c) { return r * BK + ((c ^ swz32(r)) << 4); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void block_sync_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Block tile TM x TN, waves WM x WN, each wave (TM/WM) x (TN/WN) from 32 x 32
+// v_mfma_i32_32x32x32_i8 blocks: RB row blocks x 2 column blocks (SWIGLU: the
+// wave's 32 gate columns and the matching 32 up columns).
+template <int MODE, int TM, int TN, int WM, int WN, int NSTAGE>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, const float *as, const int8_t *W,
+                                                              const float *ws, int M, int N, int kpad, float *out,
+                                                              int ldo, const float *bias, int mt_count, int nt_count) {
+  static_assert(NSTAGE == 3 || NSTAGE == 4, "pipeline depth");
+  constexpr int NWAVE = WM * WN, RB = TM / WM / 32;
+  static_assert(TN == 64 * WN, "two 32-column blocks per wave");
+  static_assert(TM % (16 * NWAVE) == 0 && TN % (16 * NWAVE) == 0, "whole wave instructions per tile");
+  constexpr int LA = TM / 16 / NWAVE, LB = TN / 16 / NWAVE;        // 1 KiB copies per wave and stage
+  constexpr int LPS = LA + LB;                                       // vmcnt per stage
+  // one LDS buffer per stage and operand, as distinct variables: the compiler
+  // then knows which copies in flight write which buffer
+  __shared__ __attribute__((aligned(16))) int8_t sA0[TM * BK], sA1[TM * BK], sA2[TM * BK], sA3[NSTAGE > 3 ? TM * BK : 16];
+  __shared__ __attribute__((aligned(16))) int8_t sB0[TN * BK], sB1[TN * BK], sB2[TN * BK], sB3[NSTAGE > 3 ? TN * BK : 16];
+  int mtile, ntile;
+  gemm_tile(blockIdx.x, mt_count, mtile, ntile);
+  if (ntile >= nt_count) return;                                   // uniform for the block
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int m0 = mtile * TM;
+  constexpr int NOUT = MODE == GM_SWIGLU ? TN / 2 : TN;
+  const int n0 = ntile * NOUT;
+
+  // this lane's global chunks: wave instructions wave*LA + i of the A tile and
+  // wave*LB + i of the B tile
+  const int8_t *ga[LA], *gb[LB];
+#pragma unroll
+  for (int i = 0; i < LA; i++) {
+    const int slot = (wave * LA + i) * 64 + lane, row = slot >> 2;
+    const int c = (slot & 3) ^ swz32(row);
+    ga[i] = A + (size_t)min(m0 + row, M - 1) * kpad + c * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int slot = (wave * LB + i) * 64 + lane, row = slot >> 2;
+    const int c = (slot & 3) ^ swz32(row);
+    int wrow;
+    if (MODE == GM_SWIGLU) wrow = row < TN / 2 ? min(n0 + row, N - 1) : N + min(n0 + row - TN / 2, N - 1);
+    else wrow = min(n0 + row, N - 1);
+    gb[i] = W + (size_t)wrow * kpad + c * 16;
+  }
+  const int nk = kpad / BK;
+  auto bufA = [&](auto st) -> int8_t * {
+    if constexpr (decltype(st)::value == 0) return sA0;
+    else if constexpr (decltype(st)::value == 1) return sA1;
+    else if constexpr (decltype(st)::value == 2) return sA2;
+    else return sA3;
+  };
+  auto bufB = [&](auto st) -> int8_t * {
+    if constexpr (decltype(st)::value == 0) return sB0;
+    else if constexpr (decltype(st)::value == 1) return sB1;
+    else if constexpr (decltype(st)::value == 2) return sB2;
+    else return sB3;
+  };
+  auto issue = [&](auto st, int kt) {
+    const int k0 = kt * BK;
+    int8_t *da = bufA(st), *db = bufB(st);
+#pragma unroll
+    for (int i = 0; i < LA; i++)
+      __builtin_amdgcn_global_load_lds((const void *)(ga[i] + k0), (lds_ptr_t)(da + (wave * LA + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; i++)
+      __builtin_amdgcn_global_load_lds((const void *)(gb[i] + k0), (lds_ptr_t)(db + (wave * LB + i) * 1024), 16, 0, 0);
+  };
+
+  // fragments of v_mfma_i32_32x32x32_i8: lane l supplies row l % 32 and bytes
+  // 16 * (l / 32) .. +15 of a 32-byte K half, i.e. chunk 2 * kh + l / 32 of the
+  // 64-byte staged row; result element e of lane l is
+  // C[8 * (e / 4) + 4 * (l / 32) + e % 4][l % 32] (checked on gfx950)
+  int arow[RB][2], brow[2][2];
+#pragma unroll
+  for (int kh = 0; kh < 2; kh++) {
+#pragma unroll
+    for (int t = 0; t < RB; t++) arow[t][kh] = stage_off32(wm * (TM / WM) + t * 32 + (lane & 31), 2 * kh + (lane >> 5));
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int bl = MODE == GM_SWIGLU ? t * (TN / 2) + wn * 32 : wn * 64 + t * 32;
+      brow[t][kh] = stage_off32(bl + (lane & 31), 2 * kh + (lane >> 5));
+    }
+  }
+
+  v16i acc[RB][2];
+#pragma unroll
+  for (int a = 0; a < RB; a++)
+#pragma unroll
+    for (int b = 0; b < 2; b++) acc[a][b] = (v16i){};
+
+  // step kt from stage ST: wait for its copies, barrier, refill stage ST-1 with
+  // step kt + NSTAGE - 1, multiply
+  auto step = [&](auto st, int kt) {
+    constexpr int ST = decltype(st)::value;
+    const int later = min(NSTAGE - 2, nk - 1 - kt);      // steps issued after kt
+    if (later >= NSTAGE - 2) wait_vmcnt<LPS * (NSTAGE - 2)>();
+    else if (NSTAGE > 3 && later == 1) wait_vmcnt<LPS>();
+    else wait_vmcnt<0>();
+    block_sync_lds();                   // every wave's copies of step kt have landed; step kt-1 is consumed
+    if (kt + NSTAGE - 1 < nk) issue(std::integral_constant<int, (ST + NSTAGE - 1) % NSTAGE>(), kt + NSTAGE - 1);
+    // fragment reads in asm, with their own waits: the compiler would otherwise
+    // wait for every copy in flight before reading an LDS buffer it cannot
+    // tell apart from the ones being filled
+    const unsigned la = (unsigned)(uintptr_t)bufA(st), lb = (unsigned)(uintptr_t)bufB(st);
+    v4i fa[RB][2], fb[2][2];
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+#pragma unroll
+      for (int t = 0; t < 2; t++) asm volatile("ds_read_b128 %0, %1" : "=v"(fb[t][kh]) : "v"(lb + brow[t][kh]));
+#pragma unroll
+      for (int t = 0; t < RB; t++) asm volatile("ds_read_b128 %0, %1" : "=v"(fa[t][kh]) : "v"(la + arow[t][kh]));
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      // the kh = 0 fragments are the first 2 + RB reads issued
+      if (kh == 0) __builtin_amdgcn_s_waitcnt(0xC07F | ((2 + RB) << 8));
+      else __builtin_amdgcn_s_waitcnt(0xC07F);
+#pragma unroll
+      for (int t = 0; t < 2; t++) asm volatile("" : "+v"(fb[t][kh]));
+#pragma unroll
+      for (int t = 0; t < RB; t++) asm volatile("" : "+v"(fa[t][kh]));
+#pragma unroll
+      for (int a = 0; a < RB; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+          acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[a][kh], fb[b][kh], acc[a][b], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);   // the kh = 0 products go before the wait for the kh = 1 reads
+    }
+  };
+
+  issue(std::integral_constant<int, 0>(), 0);
+  if (1 < nk) issue(std::integral_constant<int, 1>(), 1);
+  if (NSTAGE > 3 && 2 < nk) issue(std::integral_constant<int, (NSTAGE > 3 ? 2 : 0)>(), 2);
+  for (int kt = 0; kt < nk; kt += NSTAGE) {
+    step(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+    if (kt + 2 < nk) step(std::integral_constant<int, 2>(), kt + 2);
+    if (NSTAGE > 3 && kt + 3 < nk) step(std::integral_constant<int, (NSTAGE > 3 ? 3 : 0)>(), kt + 3);
+  }
+
+  // epilogue (the decode GEMV's operations and order)
+#pragma unroll
+  for (int a = 0; a < RB; a++) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int i = m0 + wm * (TM / WM) + a * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      if (i >= M) continue;
+      const float asi = as[i];
+      if (MODE == GM_SWIGLU) {
+        const int j = n0 + wn * 32 + (lane & 31);
+        if (j < N) {
+          const float g = (asi * ws[j]) * (float)acc[a][0][e];
+          const float up = (asi * ws[N + j]) * (float)acc[a][1][e];
+          const float s = 1.0f / (1.0f + qd::expf_glibc(-g));
+          out[(size_t)i * ldo + j] = (g * s) * up;
+        }
+      } else {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const int j = n0 + wn * 64 + b * 32 + (lane & 31);
+          if (j < N) {
+            const float c = (asi * ws[j]) * (float)acc[a][b][e];
+            float *o = out + (size_t)i * ldo + j;
+            if (MODE == GM_RESID) *o = *o + c;
+            else *o = bias ? c + bias[j] : c;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, int TM, int TN, int WM, int WN, int NS>
+int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N, int kpad, float *out,
+                int ldo, const float *bias, int cls) {
+  const int nout = MODE == GM_SWIGLU ? TN / 2 : TN;
+  const int mt = (M + TM - 1) / TM, nt = (N + nout - 1) / nout;
+  const int blocks = 8 * mt * ((nt + 7) / 8);
+  QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS>), dim3(blocks), dim3(64 * WM * WN), 0, A, as, W, ws, M, N,
+            kpad, out, ldo, bias, mt, nt);
+  return 0;
+}
+
+// Tile choice (measured at the 8B prefill shapes, M = 2048): 256 x 128 blocks for
+// the wide gate|up GEMM and for long K; 128 x 128 blocks of 8 waves otherwise.
+// K not a multiple of 64 takes the register-staged kernel.
 template <int MODE>
 int launch(const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N, int kpad, float *out,
            int ldo, const float *bias, int cls) {
+  if (kpad % BK == 0) {
+    if (MODE == GM_SWIGLU || (MODE == GM_RESID && kpad >= 8192))
+      return launch_pipe<MODE, 256, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
+    if (MODE == GM_RESID) return launch_pipe<MODE, 128, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
+    return launch_pipe<MODE, 128, 128, 4, 2, 4>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
+  }
   const int nout = MODE == GM_SWIGLU ? BN / 2 : BN;
   const int mt = (M + BM - 1) / BM, nt = (N + nout - 1) / nout;
   const int blocks = 8 * mt * ((nt + 7) / 8);
