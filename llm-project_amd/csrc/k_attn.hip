@@ -41,22 +41,15 @@ constexpr int kPWaves = kProducers / 64;    // 7
 constexpr int kGroups = kTile / 4;          // groups of 4 positions per tile
 constexpr int kGSlots = (kGroups + kPWaves - 1) / kPWaves;   // 5 groups per producer lane
 
-// Barrier for LDS hand-offs only: waits for this wave's LDS operations
-// (lgkmcnt(0)) and then for the other waves, but leaves global loads in flight.
-// __syncthreads() would also drain every outstanding global load (its fence
-// covers global memory), which would cancel the producers' V prefetch.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);        // vmcnt(63) expcnt(7) lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-}
+__device__ __forceinline__ void lds_barrier() { qd::lds_sync(); }
 
 template <int NT>
 __device__ __forceinline__ float block_max(float m, float *red) {
   m = qd::wave_max_f32(m);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __syncthreads();
+  qd::lds_sync();
   if (lane == 0) red[w] = m;
-  __syncthreads();
+  qd::lds_sync();
   float r = red[0];
 #pragma unroll
   for (int i = 1; i < NT / 64; i++) r = fmaxf(r, red[i]);
@@ -241,12 +234,12 @@ __device__ __forceinline__ int head_of_block(int x, int H, int KVH) { return (x 
 // offset of each slot is fixed (vo) and the tile adds one scalar, so a load
 // costs one add of address arithmetic; the whole offset is in the range-checked
 // vector operand, so tiles past the last one (the prefetch runs ahead), rows
-// past max_seq and the slots of wave 0 (which has none, but issues the same
-// loads so that every wave's memory counter runs alike) read as 0 without
-// touching memory.  Rows in [T, max_seq) and columns >= hd are zeroed by the
+// past max_seq and unused slots read as 0 without touching memory.  Wave 0 (the
+// chains) issues none.  Rows in [T, max_seq) and columns >= hd are zeroed by the
 // producer.
 __device__ __forceinline__ void pv_load(float (&v)[kGSlots][4], __amdgpu_buffer_rsrc_t rs, const int (&vo)[kGSlots],
                                         int t, int ntile, int hd) {
+  if (threadIdx.x < 64) return;                                   // wave 0: no slots
   const int tb = t < ntile ? t * kTile * hd * 4 : 0x40000000;   // tiles past the last: no memory traffic
 #pragma unroll
   for (int g = 0; g < kGSlots; g++)
@@ -355,7 +348,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   for (int c = 0; c < CM; c += 4)
     if (j0 + c < wcap)
       *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
-  __syncthreads();
+  qd::lds_sync();
 
   // 3. the chains
   if (tid < 64) {

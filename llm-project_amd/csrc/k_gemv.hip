@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
 #pragma unroll
     for (int c = 0; c < CM; c += 4)
       *reinterpret_cast<uint32_t *>(qsh + threadIdx.x * CM + c) = qd::quant_word(y, c, inv);
-    __syncthreads();
+    qd::lds_sync();                                  // the first weights stay in flight
 #pragma unroll
     for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
   } else if (PRO == 1) {
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
     for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
     mx = qd::wave_max_f32(mx);
     if (lane == 0) red[wave] = mx;
-    __syncthreads();
+    qd::lds_sync();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
     const float inv = 1.0f / as;
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
       }
       *reinterpret_cast<v4i *>(qsh + k0) = pk;
     }
-    __syncthreads();
+    qd::lds_sync();
 #pragma unroll
     for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
   } else {

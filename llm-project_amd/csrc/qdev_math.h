@@ -61,6 +61,12 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2
   return (float)y;
 }
 
+// Block barrier for LDS hand-offs: waits for this wave's LDS operations and then
+// for the other waves, leaving global loads in flight (__syncthreads() waits for
+// every outstanding global load too, which would stall any prefetch across it).
+// The memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Copies the table into LDS (dst: 32 entries); the caller synchronizes.
 __device__ __forceinline__ void exp_table_to_lds(uint64_t *dst) {
   if (threadIdx.x < 32) dst[threadIdx.x] = kExp2Tab[threadIdx.x];

@@ -64,7 +64,7 @@ __device__ __forceinline__ float rmsnorm_apply(const float *xr, int n, float eps
   }
   mx = wave_max_f32(mx);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
+  lds_sync();
   mx = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);

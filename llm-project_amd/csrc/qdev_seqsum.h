@@ -39,6 +39,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "qdev_math.h"
+
 namespace qd {
 
 constexpr int kSeqMaxHard = 512;           // hard steps held in LDS (kSeqMaxHard / waves per wave)
@@ -121,7 +123,8 @@ __device__ float seq_serial(int n, Term term) {
 // of the NT-thread block (NT = blockDim.x, a multiple of 64, at most 1024) holds
 // terms t*CM .. t*CM+CM-1 in a[], zero past n; n <= NT*CM.  term(i) returns term
 // i again, for the rare fallback.  All threads must call it; all get the result.
-// Three block barriers; S may be used again by the next call without another.
+// Three block barriers (LDS only: global loads in flight stay in flight); S may be
+// used again by the next call without another.
 // info (optional, written by one thread): number of hard steps, 1 if the
 // fallback ran.
 template <int NT, int CM, typename Term>
@@ -148,7 +151,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   const float mex = seq_wave_scan_max(__uint_as_float(seq_shr1(__float_as_uint(cmx))));   // exclusive
   if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = fmaxf(mex, cmx); }
   if (tid == 0) S.bad = 0;
-  __syncthreads();
+  lds_sync();
   float P0 = xin - loc, M0 = mex;
 #pragma unroll
   for (int w = 0; w < NW - 1; w++)
@@ -220,7 +223,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   }
   if (lane == 63) { S.wk[wave] = kin; S.wh[wave] = hin; S.wg[wave] = gout; }
   if (lane == 0) S.wgi[wave] = gin;
-  __syncthreads();
+  lds_sync();
 
   // 4. wave 0: the waves' offsets, the boundary checks between waves, and the
   // walk with the proof of every run.  The hard steps are taken 64 at a time:
@@ -308,7 +311,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
       if (info) { info[0] = htot; info[1] = !ok; }
     }
   }
-  __syncthreads();
+  lds_sync();
   return S.result;
 }
 
