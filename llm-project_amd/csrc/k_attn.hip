@@ -445,9 +445,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 // ---------------------------------------------------------------------------
 constexpr int kPfKeys = 256;          // threads per scores block (two keys each)
 constexpr int kPfRows = 16;           // query rows per scores / PV block
-constexpr int kPfTile = 32;           // keys per PV tile
 constexpr int kPvRows = 8;            // query rows per PV block
-constexpr int kPfMaxRows = 512;       // rows per attention pass (bounds the scratch)
+constexpr size_t kPfScratchBytes = (size_t)1 << 30;   // score scratch per attention pass (bounds the rows of a pass)
 
 // Block (KV head, 16 query rows, 512 keys): thread t owns keys j0 + t and
 // j0 + 256 + t and, for both, every (head, row) pair of the block as a
@@ -589,130 +588,116 @@ __global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int 
   else pf_softmax_row<NT, 32>(row, T, seq, red, tab);
 }
 
-// Block (KV head, 8 query rows): thread (g, dd) owns the 16 chains o[r][h][d]
-// for d = dd and dd + HD/2 (h = kvh*G + g), each a sequential sum over its
-// row's visible keys.  V and weight tiles of kPfTile keys are staged in LDS,
-// double-buffered: the next tile's global reads are in flight while the current
-// one is added.  Weights are broadcast reads, each feeding both dims.  Keys a
-// row does not see contribute nothing: in the tiles on the causal diagonal
-// their products are replaced by +0 bitwise (adding +0 leaves a chain
-// unchanged), and weights of unseen keys are stored as 0.
-template <int HD, int G>
-__global__ __launch_bounds__(G * HD / 2) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
-                                                      int max_seq, int Tp, float *o) {
-  static_assert(HD % 8 == 0, "two dims per thread, float4 V words");
-  constexpr int HH = HD / 2;
-  constexpr int nthr = G * HH;
-  constexpr int VW = kPfTile * HD / 4;                               // float4 words of a V tile
-  constexpr int WW = G * kPvRows * kPfTile / 4;                      // float4 words of a weight tile
-  constexpr int VU = (VW + nthr - 1) / nthr, WU = (WW + nthr - 1) / nthr;   // words per thread
-  __shared__ __attribute__((aligned(16))) float vs[2][kPfTile][HD];
-  __shared__ __attribute__((aligned(16))) float wsh[2][G][kPvRows][kPfTile];
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPvRows;
-  const int rend = min(R, r0 + kPvRows);
-  const int g = threadIdx.x / HH, dd = threadIdx.x % HH;
-  const int h = kvh * G + g;
-  const int kend = p0 + rend;                                        // keys 0 .. kend-1 are used
-  const float *Vh = vc + (size_t)kvh * max_seq * HD;
+// Block (KV head, 8 query rows), one wave per query head of the group: lane l
+// owns dims 2l, 2l+1 (HD = 128) or dim l (HD <= 64) and, for each, the chains of
+// the block's 8 rows over their visible keys, in key order.  The weights of a
+// group of 4 keys are the same for every lane, so they come through scalar
+// loads (the weight scratch is read-only here); V rows stream through per-lane
+// loads, two groups ahead.  No LDS and no barriers.  Keys a row does not see
+// contribute +0 (bitwise masks on the groups at the causal diagonal).
+typedef float f8v __attribute__((ext_vector_type(8)));
+typedef const __attribute__((address_space(4))) float cfloat_t;
+typedef const __attribute__((address_space(4))) f8v cf8v_t;
 
-  // one tile's global words for this thread: V words i = tid + nthr*u, weight words likewise
-  float4 rv[VU], rw[WU];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int u = 0; u < VU; u++) {
-      const int i = threadIdx.x + nthr * u;
-      const int key = k0 + i / (HD / 4);
-      rv[u] = (i < VW && key < kend) ? *reinterpret_cast<const float4 *>(Vh + (size_t)key * HD + 4 * (i % (HD / 4)))
-                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-#pragma unroll
-    for (int u = 0; u < WU; u++) {
-      const int i = threadIdx.x + nthr * u;
-      float4 v4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (i < WW) {
-        const int gg = i / (kPvRows * kPfTile / 4), rr = (i / (kPfTile / 4)) % kPvRows, kq = 4 * (i % (kPfTile / 4));
-        const int r = r0 + rr, key = k0 + kq;
-        if (r < R && key <= p0 + r) {                                // this word holds a seen key
-          const float4 t4 = *reinterpret_cast<const float4 *>(w + ((size_t)(kvh * G + gg) * R + r) * Tp + key);
-          v4.x = t4.x;
-          v4.y = key + 1 <= p0 + r ? t4.y : 0.0f;
-          v4.z = key + 2 <= p0 + r ? t4.z : 0.0f;
-          v4.w = key + 3 <= p0 + r ? t4.w : 0.0f;
-        }
-      }
-      rw[u] = v4;
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < VU; u++) {
-      const int i = threadIdx.x + nthr * u;
-      if (i < VW) *reinterpret_cast<float4 *>(&vs[buf][i / (HD / 4)][4 * (i % (HD / 4))]) = rv[u];
-    }
-#pragma unroll
-    for (int u = 0; u < WU; u++) {
-      const int i = threadIdx.x + nthr * u;
-      if (i < WW) reinterpret_cast<float4 *>(&wsh[buf][0][0][0])[i] = rw[u];
-    }
-  };
+constexpr int kPvKeys = 8;                                           // keys per group (one 32-byte scalar load per row)
 
-  float acc[kPvRows][2];
+// V values of keys k0 .. k0+7 for this lane (keys clamped to kend - 1).
+template <int DPL>
+__device__ __forceinline__ void pf_pv_vload(const float *Vh, int HD, int k0, int kend, float (&v)[kPvKeys][DPL]) {
 #pragma unroll
-  for (int c = 0; c < kPvRows; c++) acc[c][0] = acc[c][1] = 0.0f;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int k0 = 0, buf = 0; k0 < kend; k0 += kPfTile, buf ^= 1) {
-    if (k0 + kPfTile < kend) fetch(k0 + kPfTile);
-    const bool full = k0 + kPfTile <= p0 + r0 + 1;                   // every key here is seen by every row
-    if (full) {
-#pragma unroll 2
-      for (int kk = 0; kk < kPfTile; kk += 4) {
-        float va[4], vb[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) { va[u] = vs[buf][kk + u][dd]; vb[u] = vs[buf][kk + u][dd + HH]; }
-#pragma unroll
-        for (int c = 0; c < kPvRows; c++) {
-          const float4 wv = *reinterpret_cast<const float4 *>(&wsh[buf][g][c][kk]);
-          acc[c][0] += wv.x * va[0];
-          acc[c][1] += wv.x * vb[0];
-          acc[c][0] += wv.y * va[1];
-          acc[c][1] += wv.y * vb[1];
-          acc[c][0] += wv.z * va[2];
-          acc[c][1] += wv.z * vb[2];
-          acc[c][0] += wv.w * va[3];
-          acc[c][1] += wv.w * vb[3];
-        }
-      }
+  for (int u = 0; u < kPvKeys; u++) {
+    const float *row = Vh + (size_t)min(k0 + u, kend - 1) * HD;
+    if constexpr (DPL == 2) {
+      const float2 t = *reinterpret_cast<const float2 *>(row);
+      v[u][0] = t.x;
+      v[u][1] = t.y;
     } else {
-      for (int kk = 0; kk < kPfTile; kk++) {
-        const int key = k0 + kk;
-        const float va = vs[buf][kk][dd], vb = vs[buf][kk][dd + HH];
+      v[u][0] = *row;
+    }
+  }
+}
+
+// The adds of one group: every key seen by every row (MASK false) or masked
+// per (row, key) at the causal diagonal.
+template <bool MASK, int DPL>
+__device__ __forceinline__ void pf_pv_group(float (&acc)[kPvRows][DPL], const float (&v)[kPvKeys][DPL],
+                                          const f8v (&wv)[kPvRows], int k0, int rlast0) {
 #pragma unroll
-        for (int c = 0; c < kPvRows; c++) {
-          const float wv = wsh[buf][g][c][kk];
-          const bool seen = key <= p0 + r0 + c;                        // row r0 + c sees keys <= p0 + r0 + c
-          acc[c][0] += pv_mask(wv * va, seen);
-          acc[c][1] += pv_mask(wv * vb, seen);
-        }
+  for (int u = 0; u < kPvKeys; u++) {
+#pragma unroll
+    for (int c = 0; c < kPvRows; c++) {
+      const float wk = wv[c][u];
+#pragma unroll
+      for (int e = 0; e < DPL; e++) {
+        const float p = wk * v[u][e];
+        acc[c][e] += MASK ? pv_mask(p, k0 + u <= rlast0 + c) : p;
       }
     }
-    if (k0 + kPfTile < kend) stash(buf ^ 1);
-    __syncthreads();
   }
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
+                                               int max_seq, int Tp, float *o) {
+  static_assert(HD == 128 || HD <= 64, "two dims per lane at 128, one below");
+  constexpr int DPL = HD == 128 ? 2 : 1;
+  const int G = H / KVH;
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPvRows;
+  const int g = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  const int h = kvh * G + g;
+  const int rend = min(R, r0 + kPvRows);
+  const int kend = p0 + rend;                                        // keys 0 .. kend-1 are used
+  const int rlast0 = p0 + r0;                                        // last key row r0 sees
+  const int dfirst = DPL * lane;
+  const bool lane_ok = dfirst < HD;
+  const float *Vh = vc + (size_t)kvh * max_seq * HD + (lane_ok ? dfirst : 0);
+  cfloat_t *wr[kPvRows];
+#pragma unroll
+  for (int c = 0; c < kPvRows; c++) wr[c] = (cfloat_t *)(w + ((size_t)h * R + min(r0 + c, R - 1)) * Tp);
+  const int klast = (kend - 1) / kPvKeys * kPvKeys;                  // group starts are clamped to it
+
+  float acc[kPvRows][DPL];
 #pragma unroll
   for (int c = 0; c < kPvRows; c++)
-    if (r0 + c < R) {
-      float *orow = o + (size_t)(r0 + c) * H * HD + (size_t)h * HD;
-      orow[dd] = acc[c][0];
-      orow[dd + HH] = acc[c][1];
-    }
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[c][e] = 0.0f;
+  // three V register sets in rotation: group k in set k % 3, requested two
+  // groups before it is added
+  float v0[kPvKeys][DPL], v1[kPvKeys][DPL], v2[kPvKeys][DPL];
+  f8v wv[kPvRows];
+  pf_pv_vload<DPL>(Vh, HD, 0, kend, v0);
+  pf_pv_vload<DPL>(Vh, HD, min(kPvKeys, klast), kend, v1);
+  auto run = [&](int k, const float (&v)[kPvKeys][DPL]) {
+#pragma unroll
+    for (int c = 0; c < kPvRows; c++) wv[c] = *(cf8v_t *)(wr[c] + k);
+    if (k + kPvKeys <= rlast0 + 1) pf_pv_group<false, DPL>(acc, v, wv, k, rlast0);
+    else pf_pv_group<true, DPL>(acc, v, wv, k, rlast0);
+  };
+  for (int k0 = 0; k0 < kend; k0 += 3 * kPvKeys) {
+    pf_pv_vload<DPL>(Vh, HD, min(k0 + 2 * kPvKeys, klast), kend, v2);
+    run(k0, v0);
+    if (k0 + kPvKeys >= kend) break;
+    pf_pv_vload<DPL>(Vh, HD, min(k0 + 3 * kPvKeys, klast), kend, v0);
+    run(k0 + kPvKeys, v1);
+    if (k0 + 2 * kPvKeys >= kend) break;
+    pf_pv_vload<DPL>(Vh, HD, min(k0 + 4 * kPvKeys, klast), kend, v1);
+    run(k0 + 2 * kPvKeys, v2);
+  }
+  if (lane_ok) {
+#pragma unroll
+    for (int c = 0; c < kPvRows; c++)
+      if (r0 + c < R) {
+        float *orow = o + (size_t)(r0 + c) * H * HD + (size_t)h * HD + dfirst;
+        if constexpr (DPL == 2) *reinterpret_cast<float2 *>(orow) = make_float2(acc[c][0], acc[c][1]);
+        else *orow = acc[c][0];
+      }
+  }
 }
 
 template <int HD>
 int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int H, int KVH, int max_seq,
                  float scale, float *w, float *o) {
-  const int G = H / KVH, Tp = (max_seq + 3) & ~3;
+  const int G = H / KVH, Tp = (max_seq + 7) & ~7;          // rows of whole 32-byte words
   const int Tmax = p0 + R;
   const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeysPerBlock - 1) / kPfKeysPerBlock);
   QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
@@ -721,13 +706,7 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
   else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
   else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
   const dim3 pgrid(KVH, (R + kPvRows - 1) / kPvRows);
-  switch (G) {
-    case 1: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 1>), pgrid, dim3(HD / 2), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
-    case 2: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 2>), pgrid, dim3(HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
-    case 4: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 4>), pgrid, dim3(2 * HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
-    case 8: QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, 8>), pgrid, dim3(4 * HD), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o); break;
-    default: return qh::fail_msg("pf_attention: query heads per KV head must be 1, 2, 4 or 8");
-  }
+  QH_LAUNCH(QK_PF_ATTN, k_pf_pv<HD>, pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
   return 0;
 }
 
@@ -797,15 +776,27 @@ extern "C" size_t qhip_attention_scratch(int n_heads, int max_seq) {
   return (size_t)n_heads * max_seq + (size_t)n_heads * ((max_seq + kScoreBlock - 1) / kScoreBlock);
 }
 
+// Rows per attention pass: as many as the scratch budget holds (whole prompts of
+// the model shapes here: 2048 rows at the 8B shape take 671 MB), so that every
+// kernel of the pass has work for the whole chip.
+static int pf_pass_rows(int R, int n_heads, int max_seq) {
+  const size_t row_bytes = (size_t)n_heads * (size_t)((max_seq + 7) & ~7) * 4;
+  size_t cap = kPfScratchBytes / row_bytes;
+  if (cap < 64) cap = 64;
+  cap -= cap % 16;
+  return R < (int)cap ? R : (int)cap;
+}
+
 // Causal attention of R prompt rows (R may exceed one pass: rows are taken
-// kPfMaxRows at a time, each pass seeing every earlier position).
+// pf_pass_rows at a time, each pass seeing every earlier position).
 extern "C" int qhip_pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads,
                                  int n_kv, int hd, int max_seq, float scale, float *ws, float *o) {
   const int G = n_heads / n_kv;
   if (G < 1 || G > 8 || G * hd > 1024) return qh::fail_msg("pf_attention: unsupported head grouping");
   if (p0 + R > max_seq || max_seq > 16384) return qh::fail_msg("pf_attention: positions out of range");
-  for (int c0 = 0; c0 < R; c0 += kPfMaxRows) {
-    const int rr = min(kPfMaxRows, R - c0);
+  const int pass = pf_pass_rows(R, n_heads, max_seq);
+  for (int c0 = 0; c0 < R; c0 += pass) {
+    const int rr = min(pass, R - c0);
     const float *qc = q + (size_t)c0 * n_heads * hd;
     float *oc = o + (size_t)c0 * n_heads * hd;
     int rc;
@@ -822,5 +813,5 @@ extern "C" int qhip_pf_attention(const float *q, const float *kc, const float *v
 
 // Floats of scratch qhip_pf_attention needs.
 extern "C" size_t qhip_pf_attention_scratch(int R, int n_heads, int max_seq) {
-  return (size_t)n_heads * (size_t)(R < kPfMaxRows ? R : kPfMaxRows) * (size_t)((max_seq + 3) & ~3);
+  return (size_t)n_heads * (size_t)pf_pass_rows(R, n_heads, max_seq) * (size_t)((max_seq + 7) & ~7);
 }
