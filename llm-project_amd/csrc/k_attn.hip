@@ -443,86 +443,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 // (the same sums in the same order).  Scratch w[h][r][Tp] holds the scores and
 // then, in place, the softmax weights.
 // ---------------------------------------------------------------------------
-constexpr int kPfKeys = 256;          // threads per scores block (two keys each)
-constexpr int kPfRows = 16;           // query rows per scores / PV block
 constexpr int kPvRows = 8;            // query rows per PV block
 constexpr size_t kPfScratchBytes = (size_t)1 << 30;   // score scratch per attention pass (bounds the rows of a pass)
-
-// Block (KV head, 16 query rows, 512 keys): thread t owns keys j0 + t and
-// j0 + 256 + t and, for both, every (head, row) pair of the block as a
-// sequential chain over d.  The pairs go 8 at a time, 16 chains per thread
-// (their independent adds hide each other's latency).  q comes from LDS as
-// broadcast reads, each feeding both keys (the LDS return path, not the VALU,
-// would bound one key per thread); the K rows stream from global memory 16
-// dims at a time, the next chunk in flight while the current one is added.
-constexpr int kPfChains = 8;
-constexpr int kPfKeysPerBlock = 2 * kPfKeys;
-
-template <int HD>
-__global__ __launch_bounds__(kPfKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
-                                                         int KVH, int max_seq, float scale, float *w, int Tp) {
-  static_assert(HD % 16 == 0, "K rows stream in 16-dim chunks");
-  constexpr int NQ = HD / 4, NCH = NQ / 4;
-  extern __shared__ __attribute__((aligned(16))) float qsh[];        // [G * kPfRows][HD]
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPfRows, j0 = blockIdx.z * kPfKeysPerBlock;
-  const int G = H / KVH;
-  const int rend = min(R, r0 + kPfRows);
-  const int jvis = p0 + rend - 1;                                    // last key any row here sees
-  if (j0 > jvis) return;                                             // uniform for the block
-  const int t = threadIdx.x, ja = j0 + t, jb = j0 + kPfKeys + t;
-  const int npair = G * kPfRows;                                     // a multiple of 16
-  for (int idx = t; idx < npair * HD; idx += kPfKeys) {
-    const int pair = idx / HD, d = idx % HD;
-    const int g = pair / kPfRows, r = min(r0 + pair % kPfRows, R - 1);
-    qsh[idx] = q[(size_t)r * H * HD + (size_t)(kvh * G + g) * HD + d];
-  }
-  __syncthreads();
-  const float4 *ka = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(ja, jvis)) * HD);
-  const float4 *kb = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(jb, jvis)) * HD);
-#pragma unroll 1
-  for (int c0 = 0; c0 < npair; c0 += kPfChains) {
-    float acca[kPfChains], accb[kPfChains];
-#pragma unroll
-    for (int c = 0; c < kPfChains; c++) acca[c] = accb[c] = 0.0f;
-    const float4 *qb = reinterpret_cast<const float4 *>(qsh + (size_t)c0 * HD);
-    float4 xa[4], xb[4], na[4], nb[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) { xa[i] = ka[i]; xb[i] = kb[i]; }
-#pragma unroll 1
-    for (int ch = 0; ch < NCH; ch++) {
-      const int dc = 4 * ch;
-      if (ch + 1 < NCH) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) { na[i] = ka[dc + 4 + i]; nb[i] = kb[dc + 4 + i]; }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-#pragma unroll
-        for (int c = 0; c < kPfChains; c++) {
-          const float4 qv = qb[c * NQ + dc + i];
-          acca[c] += qv.x * xa[i].x;
-          accb[c] += qv.x * xb[i].x;
-          acca[c] += qv.y * xa[i].y;
-          accb[c] += qv.y * xb[i].y;
-          acca[c] += qv.z * xa[i].z;
-          accb[c] += qv.z * xb[i].z;
-          acca[c] += qv.w * xa[i].w;
-          accb[c] += qv.w * xb[i].w;
-        }
-      }
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int i = 0; i < 4; i++) { xa[i] = na[i]; xb[i] = nb[i]; }
-    }
-#pragma unroll
-    for (int c = 0; c < kPfChains; c++) {
-      const int pair = c0 + c, g = pair / kPfRows, r = r0 + pair % kPfRows;
-      float *wr = w + ((size_t)(kvh * G + g) * R + r) * Tp;
-      if (r < R && ja <= p0 + r) wr[ja] = acca[c] * scale;
-      if (r < R && jb <= p0 + r) wr[jb] = accb[c] * scale;
-    }
-  }
-}
 
 // Softmax weights of one (head, row) (llama.c:557-572): NT threads, thread t
 // holds the scores j in [t*CM, t*CM + CM) in registers (one read of the row),
@@ -694,14 +616,103 @@ __global__ __launch_bounds__(512) void k_pf_pv(const float *w, const float *vc, 
   }
 }
 
+// Scores with the K row in registers: block (KV head, 16 query rows, 256 keys);
+// lane t of wave v owns key j0 + 64v + t and holds its whole K row.  For every
+// (head, row) pair of the block the dot over d is formed in order; 4 pairs go
+// together (4 independent chains per lane), their q values wave-uniform in
+// scalar registers, 8 dims per scalar load.  Waves whose keys are all past the
+// block's last visible key stop at once; no LDS, no barriers.
+constexpr int kPsKeys = 256, kPsRows = 16, kPsPairs = 4, kPsDims = 8;
+
+// q of 8 dims of the 4 pairs into scalar registers, issued where it stands (asm,
+// immediate offset D floats); scalar loads may return out of order, so the
+// wait for a chunk is a full one.
+template <int D>
+__device__ __forceinline__ void ps_sload(f8v (&qq)[kPsPairs], cfloat_t *const (&qp)[kPsPairs]) {
+#pragma unroll
+  for (int u = 0; u < kPsPairs; u++) asm volatile("s_load_dwordx8 %0, %1, %2" : "=s"(qq[u]) : "s"(qp[u]), "i"(4 * D));
+}
+
+// The accumulators pass through the wait, so that the adds before it stay
+// before it (and their q registers are free again).
+__device__ __forceinline__ void ps_swait(f8v (&qq)[kPsPairs], float (&acc)[kPsPairs]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+s"(qq[0]), "+s"(qq[1]), "+s"(qq[2]), "+s"(qq[3]), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),
+                 "+v"(acc[3]));
+}
+
+// Chunk D of the 4 chains (q already waited for in cur); the next chunk is
+// requested before these adds and waited for after them.
+template <int HD, int D>
+__device__ __forceinline__ void ps_chunk(cfloat_t *const (&qp)[kPsPairs], const float (&k)[HD], float (&acc)[kPsPairs],
+                                         f8v (&cur)[kPsPairs], f8v (&nxt)[kPsPairs]) {
+  if constexpr (D + kPsDims < HD) ps_sload<D + kPsDims>(nxt, qp);
+#pragma unroll
+  for (int e = 0; e < kPsDims; e++)
+#pragma unroll
+    for (int u = 0; u < kPsPairs; u++) acc[u] += cur[u][e] * k[D + e];
+  if constexpr (D + kPsDims < HD) {
+    ps_swait(nxt, acc);
+    ps_chunk<HD, D + kPsDims>(qp, k, acc, nxt, cur);
+  }
+}
+
+template <int HD, int D>
+__device__ __forceinline__ void ps_chunks(cfloat_t *const (&qp)[kPsPairs], const float (&k)[HD], float (&acc)[kPsPairs]) {
+  f8v qa[kPsPairs], qb[kPsPairs];
+  ps_sload<0>(qa, qp);
+  ps_swait(qa, acc);
+  ps_chunk<HD, 0>(qp, k, acc, qa, qb);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kPsKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
+                                                         int KVH, int max_seq, float scale, float *w, int Tp) {
+  static_assert(HD % kPsDims == 0, "whole scalar loads of q");
+  const int kvh = blockIdx.x, r0 = blockIdx.y * kPsRows, j0 = blockIdx.z * kPsKeys;
+  const int G = H / KVH;
+  const int rend = min(R, r0 + kPsRows);
+  const int jvis = p0 + rend - 1;                                    // last key any row here sees
+  const int jw = j0 + 64 * __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (jw > jvis) return;                                             // uniform for the wave
+  const int j = jw + (threadIdx.x & 63);
+  float k[HD];
+  {
+    const float4 *kr = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(j, jvis)) * HD);
+#pragma unroll
+    for (int i = 0; i < HD / 4; i++) {
+      const float4 t = kr[i];
+      k[4 * i] = t.x; k[4 * i + 1] = t.y; k[4 * i + 2] = t.z; k[4 * i + 3] = t.w;
+    }
+  }
+  const int npair = G * kPsRows;
+#pragma unroll 1
+  for (int c0 = 0; c0 < npair; c0 += kPsPairs) {
+    cfloat_t *qp[kPsPairs];
+#pragma unroll
+    for (int u = 0; u < kPsPairs; u++) {
+      const int pair = c0 + u, g = pair / kPsRows, r = min(r0 + pair % kPsRows, R - 1);
+      qp[u] = (cfloat_t *)(q + (size_t)r * H * HD + (size_t)(kvh * G + g) * HD);
+    }
+    float acc[kPsPairs];
+#pragma unroll
+    for (int u = 0; u < kPsPairs; u++) acc[u] = 0.0f;
+    ps_chunks<HD, 0>(qp, k, acc);
+#pragma unroll
+    for (int u = 0; u < kPsPairs; u++) {
+      const int pair = c0 + u, g = pair / kPsRows, r = r0 + pair % kPsRows;
+      if (r < R && j <= p0 + r) w[((size_t)(kvh * G + g) * R + r) * Tp + j] = acc[u] * scale;
+    }
+  }
+}
+
 template <int HD>
 int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int H, int KVH, int max_seq,
                  float scale, float *w, float *o) {
   const int G = H / KVH, Tp = (max_seq + 7) & ~7;          // rows of whole 32-byte words
   const int Tmax = p0 + R;
-  const dim3 sgrid(KVH, (R + kPfRows - 1) / kPfRows, (Tmax + kPfKeysPerBlock - 1) / kPfKeysPerBlock);
-  QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPfKeys), (size_t)G * kPfRows * HD * 4, q, kc, R, p0, H, KVH,
-            max_seq, scale, w, Tp);
+  const dim3 sgrid(KVH, (R + kPsRows - 1) / kPsRows, (Tmax + kPsKeys - 1) / kPsKeys);
+  QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
   if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
   else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
   else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
