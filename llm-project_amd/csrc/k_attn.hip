@@ -479,7 +479,7 @@ __device__ __forceinline__ void pf_softmax_row(float *row, int T, qd::SeqScratch
     for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
   }
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m, tab) : 0.0f;
+  for (int c = 0; c < CM; c++) e[c] = qd::expf_glibc(e[c] - m, tab);   // -inf past T: +0
   const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m, tab); });
   const float inv = 1.0f / sum;
 #pragma unroll

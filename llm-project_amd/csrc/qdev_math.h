@@ -32,15 +32,16 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
 
 // tab: the table above, or a copy of it (an LDS copy saves a memory round trip
 // per value when many values are formed); the result does not depend on it.
+//
+// The special cases of |x| >= 88 (glibc's abstop >= 0x42b branch) are applied
+// by selects after the main path, which every lane evaluates (its table index
+// is masked, so any input is safe there): -inf and x < -0x1.9fe368p6 give +0,
+// x > 0x1.62e42ep6 gives +inf, NaN and +inf give x + x; every other input,
+// those with 88 <= |x| in between included, takes the main path's value, as in
+// glibc.  No branch, so that many values in a wave cost no divergence.
 __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2Tab) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= 0x42bu) {                       // |x| >= 88, inf or nan
-    if (ux == 0xff800000u) return 0.0f;         // -inf
-    if (abstop >= 0x7f8u) return x + x;         // +inf, nan
-    if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);   // overflow
-    if (x < -0x1.9fe368p6f) return 0.0f;                           // underflow
-  }
   const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double Shift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -58,7 +59,11 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2
   double y = __builtin_fma(C2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  return (float)y;
+  float res = (float)y;
+  res = x < -0x1.9fe368p6f ? 0.0f : res;                            // underflow, -inf
+  res = x > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : res;     // overflow, +inf
+  res = abstop >= 0x7f8u && ux != 0xff800000u ? x + x : res;        // nan, +inf
+  return res;
 }
 
 // Block barrier for LDS hand-offs: waits for this wave's LDS operations and then
