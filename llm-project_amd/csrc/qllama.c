@@ -658,8 +658,8 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
 
 static int pf_supported(const QDev *d) {
   const int G = d->H / d->KVH;
-  return (d->hd == 128 || d->hd == 64 || d->hd == 48) && (G == 1 || G == 2 || G == 4 || G == 8) &&
-         G * d->hd <= 1024 && d->dff <= 32768;
+  return (d->hd == 128 || d->hd == 64 || d->hd == 48) && G >= 1 && G <= 8 && G * d->hd <= 1024 &&
+         d->dff <= 32768;
 }
 
 static int pf_alloc(QDev *d, int rows) {

@@ -355,6 +355,8 @@ int or_model_synth(OrModel *m, const int32_t cfg[8], float rope_base, float eps,
   size_t biggest = (size_t)m->vocab * dm;
   size_t ff = (size_t)dm * m->d_ff;
   if (ff > biggest) biggest = ff;
+  size_t qo = (size_t)dm * m->n_heads * m->head_dim;     // Wq and Wo when n_heads*head_dim > d_model
+  if (qo > biggest) biggest = qo;
   float *buf = (float*)malloc(biggest * sizeof(float));
   if (!buf) return 1;
   synth_qt(&m->wte, buf, seed, 0);

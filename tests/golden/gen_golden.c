@@ -238,6 +238,7 @@ static void build_model(QLlamaModel *m, const E2E *e, uint64_t seed) {
   m->head_dim = c[5]; m->d_ff = c[6]; m->max_seq = c[7]; m->rope_base = e->base; m->eps = 1e-5f;
   const int dm = c[1], qd = c[3] * c[5], kvd = c[4] * c[5], ff = c[6], L = c[2];
   size_t big = (size_t)c[0] * dm; if ((size_t)dm * ff > big) big = (size_t)dm * ff;
+  if ((size_t)dm * qd > big) big = (size_t)dm * qd;
   float *buf = malloc(big * sizeof(float));
   m->wte = qtensor_create(c[0], dm);
   synth_q(&m->wte, buf, seed, 0);

@@ -163,6 +163,51 @@ def test_e2e_8b_batched_prefill_matches_reference(Q):
     _big_prefill(Q, "8b")
 
 
+# Batched prefill over head groupings G = H/KVH, head sizes and cache lengths
+# the model fixtures do not reach, against the oracle's decode steps:
+# (vocab, dim, layers, H, KVH, hd, hidden, max_seq, prompt length).
+PF_SHAPES = [
+    (512, 512, 2, 8, 8, 64, 1024, 333, 330),     # G=1; cache rows not a multiple of 8
+    (512, 1024, 2, 8, 4, 128, 2048, 600, 520),   # G=2
+    (512, 384, 2, 6, 2, 48, 768, 320, 317),      # G=3
+    (512, 768, 2, 8, 2, 128, 1536, 300, 290),    # G=4 with dim != H*hd
+    (512, 1024, 2, 16, 2, 64, 1536, 400, 397),   # G=8
+    (512, 1024, 1, 8, 1, 128, 1024, 300, 297),   # G=8 at hd 128: 1024 lanes per block
+    (512, 512, 1, 16, 2, 64, 512, 16384, 1100),  # two attention passes (1 GiB of scores each)
+]
+
+
+@pytest.mark.parametrize("shape", PF_SHAPES, ids=lambda s: f"H{s[3]}kv{s[4]}hd{s[5]}T{s[7]}")
+def test_batched_prefill_groupings_match_oracle(Q, shape):
+    """The prompt in two batched pieces (the second starting at an unaligned
+    position), then decode steps from the cache they left: every logit vector
+    equals the oracle's after the same tokens, bit for bit."""
+    cfg, n = list(shape[:8]), shape[8]
+    ids = O.prompt(n, 77, cfg[0])
+    cut = 37
+    log(f"prefill {cfg}: {n} prompt tokens in pieces of {cut} and {n - cut}")
+    ref = O.Model(cfg, 10000.0, seed=4321)
+    m = Q.Model.synth(cfg, 10000.0, seed=4321)
+    try:
+        assert m.hash() == ref.hash()
+        ref_cut = None
+        for i, t in enumerate(ids):
+            lg = ref.step(t)
+            if i == cut - 1:
+                ref_cut = lg.copy()
+        assert bits_equal(m.prefill(ids[:cut]), ref_cut)
+        lg = m.prefill(ids[cut:]).copy()
+        assert bits_equal(lg, ref.logits)
+        t = int(np.argmax(lg))
+        for _ in range(min(3, cfg[7] - n)):
+            a = m.step(t).copy()
+            assert bits_equal(a, ref.step(t))
+            t = int(np.argmax(a))
+    finally:
+        m.close()
+        ref.close()
+
+
 def test_decode_rejects_position_past_max_seq(Q):
     # the reference leaves this to its callers (main.c:663); the library checks
     # it on the host before any device work: run in a child so the abort is seen

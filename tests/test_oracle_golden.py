@@ -226,6 +226,25 @@ def test_generator_math_is_accurate():
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
 
 
+def test_synth_weights_when_attention_is_wider_than_the_model():
+    """n_heads*head_dim above d_model (and above vocab and d_ff): every weight
+    of the synthetic model is syn_fill's stream for its id, quantized per
+    column -- the attention projections included."""
+    cfg = [64, 64, 1, 8, 2, 32, 64, 16]
+    dm, qd, kvd, ff = 64, 8 * 32, 2 * 32, 64
+    m = O.Model(cfg, 10000.0, seed=5)
+    try:
+        b = m.m.blocks[0]
+        for qt, rows, cols, tid in ((b.Wq, dm, qd, 2), (b.Wk, dm, kvd, 3), (b.Wv, dm, kvd, 4),
+                                    (b.Wo, qd, dm, 8), (b.Wgate, dm, ff, 10), (b.Wdown, ff, dm, 12)):
+            q, s = O.quantize(O.synth(rows * cols, 5, tid, 0.02).reshape(rows, cols))
+            assert (qt.rows, qt.cols) == (rows, cols)
+            assert np.array_equal(np.ctypeslib.as_array(qt.q, (rows * cols,)), q.ravel())
+            assert_bits(np.ctypeslib.as_array(qt.scale, (cols,)), s)
+    finally:
+        m.close()
+
+
 # ---- llama.c:528-600 end to end --------------------------------------------
 def _e2e(name):
     meta = golden_json(f"e2e_{name}")
