@@ -14,12 +14,15 @@
 // Kernel 1 (k_attn_scores): grid (H, ceil(max_seq/128)); one thread per (head,
 //   position) computes dot_j and s_j; the block's K rows are copied into LDS
 //   with direct global-to-LDS loads; each block writes its maximum.
-// Kernel 2 (k_attn_pv): grid (H, ceil(hd/64)), 512 threads.  All threads form
+// Kernel 2 (k_attn_pv): grid (H, ceil(hd/16)), 512 threads.  All threads form
 //   the head's softmax weights in LDS (each thread a run of consecutive
-//   positions, in registers).  Then wave 0 owns 64 output chains o_d while waves
-//   1-7 stream V tiles of 128 positions, three tiles ahead, and store the
-//   products w_j * V_jd as [d][j] tiles (double-buffered in LDS), so that the
-//   chain lane reads four consecutive positions with one 16-byte LDS read.
+//   positions, in registers).  Then lanes 0-15 of wave 0 own 16 output chains
+//   o_d while waves 1-7 stream V tiles of 128 positions, three tiles ahead, and
+//   store the products w_j * V_jd as [d][j] tiles (double-buffered in LDS), so
+//   that the chain lane reads four consecutive positions with one 16-byte LDS
+//   read.  Sixteen chains per block spread a head's V stream over hd/16 CUs:
+//   the rate at which one CU brings in V rows, not the chain, bounded wider
+//   blocks.
 #include <hip/hip_runtime.h>
 
 #include "qdev_math.h"
@@ -34,12 +37,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kScoreBlock = 128;        // positions per scores block
 constexpr int kTile = 128;                  // positions per PV tile
 constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
-constexpr int kChains = 64;                 // output dims per PV block (wave 0's lanes)
+constexpr int kChains = 16;                 // output dims per PV block (lanes 0-15 of wave 0)
 constexpr int kPvThreads = 512;
 constexpr int kProducers = kPvThreads - 64;
 constexpr int kPWaves = kProducers / 64;    // 7
+constexpr int kUnits = kPWaves * (64 / kChains);             // 28 producer units of kChains lanes
 constexpr int kGroups = kTile / 4;          // groups of 4 positions per tile
-constexpr int kGSlots = (kGroups + kPWaves - 1) / kPWaves;   // 5 groups per producer lane
+constexpr int kGSlots = (kGroups + kUnits - 1) / kUnits;     // 2 groups per producer lane
 
 __device__ __forceinline__ void lds_barrier() { qd::lds_sync(); }
 
@@ -228,8 +232,9 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc,
 // L2, and each KV head's V rows are fetched from HBM once per XCD.
 __device__ __forceinline__ int head_of_block(int x, int H, int KVH) { return (x % KVH) * (H / KVH) + x / KVH; }
 
-// V values of tile t for this producer lane: slot g covers positions
-// t*kTile + 4*(pw + kPWaves*g) + 0..3 at column d0 + (pid & 63).  The loads go
+// V values of tile t for this producer lane (unit u = pid / kChains, column
+// dd = pid % kChains): slot g covers positions t*kTile + 4*(u + kUnits*g) + 0..3
+// at column d0 + dd.  The loads go
 // through a buffer resource over this KV head's rows [0, max_seq): the lane's
 // offset of each slot is fixed (vo) and the tile adds one scalar, so a load
 // costs one add of address arithmetic; the whole offset is in the range-checked
@@ -259,19 +264,19 @@ __device__ __forceinline__ float pv_mask(float p, bool keep) {
 
 __device__ __forceinline__ void pv_produce(float *B, const float *W, const float (&v)[kGSlots][4], int t, int T,
                                            bool cols_full, bool col_ok, int pid) {
-  const int pw = pid >> 6, dd = pid & 63;
+  const int u = pid / kChains, dd = pid % kChains;
   const bool full = cols_full && (t + 1) * kTile <= T;
   float4 w[kGSlots];
 #pragma unroll
   for (int g = 0; g < kGSlots; g++) {
-    const int grp = pw + kPWaves * g;
-    if (kPWaves * (g + 1) <= kGroups || grp < kGroups)         // compile-time true except the last slot
+    const int grp = u + kUnits * g;
+    if (kUnits * (g + 1) <= kGroups || grp < kGroups)          // compile-time true except the last slot
       w[g] = *reinterpret_cast<const float4 *>(W + t * kTile + 4 * grp);
   }
 #pragma unroll
   for (int g = 0; g < kGSlots; g++) {
-    const int grp = pw + kPWaves * g;
-    if (kPWaves * (g + 1) <= kGroups || grp < kGroups) {
+    const int grp = u + kUnits * g;
+    if (kUnits * (g + 1) <= kGroups || grp < kGroups) {
       const int jb = t * kTile + 4 * grp;
       float4 p;
       p.x = w[g].x * v[g][0];
@@ -325,12 +330,12 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const float *Vh = vc + (size_t)kvh * max_seq * hd;
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void *)Vh, (short)0, max_seq * hd * 4, 0x00020000);
-  const bool cols_full = d0 + kChains <= hd, col_ok = d0 + (pid & 63) < hd;
+  const bool cols_full = d0 + kChains <= hd, col_ok = d0 + pid % kChains < hd;
   int vo[kGSlots];
 #pragma unroll
   for (int g = 0; g < kGSlots; g++) {
-    const int grp = (pid >> 6) + kPWaves * g;
-    vo[g] = tid >= 64 && grp < kGroups ? (4 * grp * hd + d0 + (pid & 63)) * 4 : 0x40000000;   // else: no traffic
+    const int grp = pid / kChains + kUnits * g;
+    vo[g] = tid >= 64 && grp < kGroups ? (4 * grp * hd + d0 + pid % kChains) * 4 : 0x40000000;   // else: no traffic
   }
   float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
   pv_load(r0, vrs, vo, 0, ntile, hd);
@@ -351,14 +356,15 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   qd::lds_sync();
 
   // 3. the chains
-  if (tid < 64) {
+  if (tid < 64) {                 // lanes past kChains repeat the last chain and store nothing
     const int d = d0 + tid;
+    const int crow = tid < kChains ? tid : kChains - 1;
     float acc = 0.0f;
     for (int t = 0; t < ntile; t++) {
       lds_barrier();
       // tile t: four groups of eight 16-byte reads, the next group in flight
       // while the current one is added
-      const float4 *Pt = reinterpret_cast<const float4 *>(P + (t & 1) * kChains * kTS + tid * kTS);
+      const float4 *Pt = reinterpret_cast<const float4 *>(P + (t & 1) * kChains * kTS + crow * kTS);
       constexpr int GR = 8, NG = kTile / 4 / GR;
       float4 buf[2][GR];
 #pragma unroll
@@ -380,9 +386,10 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (d < hd) o[(size_t)h * hd + d] = acc;
+    const bool own = tid < kChains && d < hd;
+    if (own) o[(size_t)h * hd + d] = acc;
     if (obm) {                 // max |o| of this block, for the activation quantizer
-      const float mo = qd::wave_max_f32(d < hd ? fabsf(acc) : 0.0f);
+      const float mo = qd::wave_max_f32(own ? fabsf(acc) : 0.0f);
       if (tid == 0) obm[(size_t)h * gridDim.y + blockIdx.y] = mo;
     }
   } else {
