@@ -138,9 +138,37 @@ void dequantize_int8_percol(const signed char *q, const float *scale, int rows, 
 // matrix.c:370-374  acc[j] = sum_k qa[k] * qw[k*N + j]  (host arrays, computed on the GPU)
 void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, int32_t *acc);
 
+// sampler.h:12-31.  Inside the reference's build this takes the place of
+// sampler.h (which, included first, supplies Rng itself).
+#ifndef SAMPLER_H
+#define SAMPLER_H
+typedef struct {
+  unsigned long long state;
+} Rng;
+#endif
+// sampler.c:24-29 / 40-45 (host: xorshift64, top 53 bits to a float in [0, 1))
+Rng rng_create(unsigned long long seed);
+float rng_uniform(Rng *r);
+// sampler.c:8-21  First index of the largest logit of row `row` (host Tensor of
+// shape (rows, vocab)); evaluated on the GPU.
+int sample_argmax(const Tensor *logits, int row);
+// sampler.c:54-143  Temperature + top-k + top-p sampling of row `row` (host
+// Tensor), evaluated on the GPU with the reference's arithmetic: the same token
+// and the same advance of *rng (none when temperature <= 0, which is greedy).
+int sample_token(const Tensor *logits, int row, float temperature, int top_k, float top_p, Rng *rng);
+
 // ---------------------------------------------------------------------------
 // Additive entry points
 // ---------------------------------------------------------------------------
+
+// Sampled generation kept on the device (the loop of main.c:663-667): n_steps
+// times, sample a token from the logits of the last token this model processed
+// (sample_token's arithmetic, rng state advanced on the device), record it in
+// out[i] and feed it at position kv->len.  Needs kv->len >= 1 (a prompt or a
+// decode step before it) and kv->len + n_steps <= max_seq.  *rng is advanced as
+// n_steps calls of sample_token would.  Returns 0 on success.
+int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float temperature, int top_k, float top_p,
+                     Rng *rng, int *out);
 
 // Prompt ingestion: n tokens at positions kv->len .. kv->len+n-1.  Same result
 // as n calls of q_llama_decode_step (main.c:662); logits are those of the last
@@ -161,6 +189,11 @@ int q_llama_model_synth(QLlamaModel *out, const int32_t cfg[8], float rope_base,
 // Order-independent digest of every int8 tensor and scale vector, in the
 // reference's (rows, cols) indexing; equal to the generator's CPU digest.
 uint64_t q_llama_model_hash(const QLlamaModel *m);
+
+// Write the model as an 'LLMQ' v2 checkpoint that q_llama_model_load (and the
+// reference's loader, llama.c:603-657) reads back: the int8 byte order of the
+// reference's writer (tools/convert_llama.py:73-97).  Returns 0 on success.
+int q_llama_model_save(const QLlamaModel *m, const char *path);
 
 // Copy a device QTensor back to host memory in the reference's layout (quant.h:22-27):
 // q (rows, cols) row-major int8 and scale (cols).  Counterpart of the loader's

@@ -27,6 +27,12 @@ int         qhip_h2d_async(void *dst, const void *host_src, size_t n);  // pinne
 int         qhip_d2h_async(void *host_dst, const void *src, size_t n);
 int         qhip_d2d_async(void *dst, const void *src, size_t n);
 int         qhip_fill_zero(void *p, size_t n);           // kernel, capture-safe
+// Staged upload from any host memory (a mapped file, say) through two pinned
+// buffers of `chunk` bytes: qhip_upload returns once src may be reused, the copy
+// itself completes in stream order; qhip_upload_end waits for all of it.
+int         qhip_upload_begin(size_t chunk);
+int         qhip_upload(void *dst, const void *host_src, size_t n);
+int         qhip_upload_end(void);
 int         qhip_sync(void);
 void       *qhip_stream(void);
 
@@ -143,6 +149,18 @@ int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, 
 int qhip_pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads, int n_kv,
                       int hd, int max_seq, float scale, float *ws, float *o);
 size_t qhip_pf_attention_scratch(int R, int n_heads, int max_seq);
+
+// Token sampling on the device (k_sample.hip).  qhip_sample: temperature > 0,
+// top-k, top-p over one row of V logits (sampler.c:54-143) with the xorshift64
+// state *rng advanced on the device; scratch holds qhip_sample_scratch(V) bytes.
+// qhip_argmax_row: first index of the maximum (sampler.c:8-21).  Both write the
+// token to *tok; with d_state (decode state [pos, fill_end]) they also record it
+// as the output of position d_state[0]-1 and the input of position d_state[0].
+size_t qhip_sample_scratch(int V);
+int qhip_sample(const float *logits, int V, float temperature, int top_k, float top_p, void *scratch,
+                size_t scratch_bytes, unsigned long long *rng, int *tok, int *d_in, const int *d_state, int *d_out,
+                int max_seq);
+int qhip_argmax_row(const float *logits, int V, int *tok, int *d_in, const int *d_state, int *d_out, int max_seq);
 
 // reference-layout column accumulate (matrix.c:354-374) for qacc_columns
 int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);

@@ -6,6 +6,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "qhip.h"
@@ -143,6 +144,76 @@ int qhip_d2d_async(void *dst, const void *src, size_t n) {
   if (!n) return 0;
   hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, g_stream);
   return e == hipSuccess ? 0 : fail("device copy", e);
+}
+
+// Staged upload: two pinned buffers; the CPU fills one (several threads for
+// large chunks: the source is often a freshly mapped file, whose page faults
+// dominate) while the DMA of the other is in flight.
+namespace {
+struct Stager {
+  void *buf[2] = {nullptr, nullptr};
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  bool busy[2] = {false, false};
+  size_t chunk = 0;
+  int next = 0;
+} g_up;
+
+void par_copy(void *dst, const void *src, size_t n) {
+  const size_t kMinPart = (size_t)8 << 20;
+  const int parts = n >= 4 * kMinPart ? 4 : 1;
+  if (parts == 1) { memcpy(dst, src, n); return; }
+  std::vector<std::thread> th;
+  const size_t per = (n + parts - 1) / parts;
+  for (int i = 0; i < parts; i++) {
+    const size_t o = per * (size_t)i, c = o >= n ? 0 : (n - o < per ? n - o : per);
+    if (c) th.emplace_back([=] { memcpy((char *)dst + o, (const char *)src + o, c); });
+  }
+  for (auto &t : th) t.join();
+}
+}  // namespace
+
+int qhip_upload_begin(size_t chunk) {
+  if (qhip_init()) return 1;
+  if (g_up.buf[0]) return fail_msg("upload already in progress");
+  g_up.chunk = chunk;
+  g_up.next = 0;
+  for (int b = 0; b < 2; b++) {
+    hipError_t e = hipHostMalloc(&g_up.buf[b], chunk, hipHostMallocDefault);
+    if (e != hipSuccess) return fail("hipHostMalloc (upload staging)", e);
+    if ((e = hipEventCreateWithFlags(&g_up.ev[b], hipEventDisableTiming)) != hipSuccess)
+      return fail("hipEventCreate (upload staging)", e);
+    g_up.busy[b] = false;
+  }
+  return 0;
+}
+
+int qhip_upload(void *dst, const void *src, size_t n) {
+  if (!g_up.buf[0]) return fail_msg("upload not begun");
+  for (size_t o = 0; o < n; o += g_up.chunk) {
+    const size_t c = n - o < g_up.chunk ? n - o : g_up.chunk;
+    const int b = g_up.next;
+    hipError_t e;
+    if (g_up.busy[b] && (e = hipEventSynchronize(g_up.ev[b])) != hipSuccess) return fail("upload wait", e);
+    par_copy(g_up.buf[b], (const char *)src + o, c);
+    if ((e = hipMemcpyAsync((char *)dst + o, g_up.buf[b], c, hipMemcpyHostToDevice, g_stream)) != hipSuccess)
+      return fail("upload copy", e);
+    if ((e = hipEventRecord(g_up.ev[b], g_stream)) != hipSuccess) return fail("upload record", e);
+    g_up.busy[b] = true;
+    g_up.next ^= 1;
+  }
+  return 0;
+}
+
+int qhip_upload_end(void) {
+  int rc = g_up.buf[0] ? qhip_sync() : 0;
+  for (int b = 0; b < 2; b++) {
+    if (g_up.buf[b]) (void)hipHostFree(g_up.buf[b]);
+    if (g_up.ev[b]) (void)hipEventDestroy(g_up.ev[b]);
+    g_up.buf[b] = nullptr;
+    g_up.ev[b] = nullptr;
+    g_up.busy[b] = false;
+  }
+  return rc;
 }
 
 int qhip_sync(void) {

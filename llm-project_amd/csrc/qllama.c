@@ -14,6 +14,11 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <sys/types.h>
+#include <unistd.h>
 
 #define LLMQ_MAGIC   0x514D4C4Cu   // llama.c:193
 #define LLMA_VERSION 2u            // llama.c:194
@@ -366,87 +371,100 @@ uint64_t q_llama_model_hash(const QLlamaModel *m) {
 }
 
 // ---------------------------------------------------------------------------
-// Loading: LLMQ v2 (llama.c:603-657 byte order)
+// Loading: LLMQ v2 (llama.c:603-657 byte order).  The file is mapped, each
+// tensor is streamed to HBM through double-buffered pinned staging with async
+// copies, and int8 matrices are transposed into the NK layout on the device.
 // ---------------------------------------------------------------------------
-// Read one int8 tensor (cols f32 scales, then rows*cols int8 row-major) into the
-// device, in the requested layout.
-static int read_q(FILE *f, int rows, int cols, int layout_nk, int kpad, int8_t *dq, float *ds,
-                  void *stage, void *dtmp) {
-  float *sc = (float*)stage;
-  if (fread(sc, sizeof(float), (size_t)cols, f) != (size_t)cols) return 1;
-  if (qhip_h2d(ds, sc, (size_t)cols * 4)) return 2;
-  const size_t n = (size_t)rows * cols;
-  int8_t *dst = layout_nk ? (int8_t*)dtmp : dq;
-  // stream the int8 body through the staging buffer
-  const size_t chunk = (size_t)64 << 20;
-  for (size_t o = 0; o < n; o += chunk) {
-    size_t c = n - o < chunk ? n - o : chunk;
-    if (fread(stage, 1, c, f) != c) return 1;
-    if (qhip_h2d(dst + o, stage, c)) return 2;
-  }
-  if (layout_nk && qhip_transpose_kn_to_nk((const int8_t*)dtmp, rows, cols, kpad, dq)) return 2;
+typedef struct {
+  const uint8_t *p;     // mapped file
+  size_t size, off;
+} FileCur;
+
+static const void *cur_take(FileCur *c, size_t n) {
+  if (c->size - c->off < n) return NULL;
+  const void *r = c->p + c->off;
+  c->off += n;
+  return r;
+}
+
+// One int8 tensor: cols f32 scales, then rows*cols int8 row-major (llama.c:603-608).
+// 1 = truncated, 2 = device error.
+static int read_q(FileCur *c, int rows, int cols, int layout_nk, int kpad, int8_t *dq, float *ds, int8_t *dtmp) {
+  const void *sc = cur_take(c, (size_t)cols * 4);
+  const void *body = cur_take(c, (size_t)rows * cols);
+  if (!sc || !body) return 1;
+  if (qhip_upload(ds, sc, (size_t)cols * 4)) return 2;
+  if (qhip_upload(layout_nk ? dtmp : dq, body, (size_t)rows * cols)) return 2;
+  if (layout_nk && qhip_transpose_kn_to_nk(dtmp, rows, cols, kpad, dq)) return 2;
   return 0;
 }
 
-static int read_f(FILE *f, float *dst, int n, void *stage) {
-  if (fread(stage, sizeof(float), (size_t)n, f) != (size_t)n) return 1;
-  return qhip_h2d(dst, stage, (size_t)n * 4) ? 2 : 0;
+static int read_f(FileCur *c, float *dst, int n) {
+  const void *v = cur_take(c, (size_t)n * 4);
+  if (!v) return 1;
+  return qhip_upload(dst, v, (size_t)n * 4) ? 2 : 0;
 }
 
 int q_llama_model_load(const char *path, QLlamaModel *out) {
-  FILE *f = fopen(path, "rb");
-  if (!f) { fprintf(stderr, "Error: cannot open '%s' for reading\n", path); return 1; }
+  int fd = open(path, O_RDONLY);
+  if (fd < 0) { fprintf(stderr, "Error: cannot open '%s' for reading\n", path); return 1; }
+  struct stat stt;
+  if (fstat(fd, &stt) != 0) { fprintf(stderr, "Error: cannot open '%s' for reading\n", path); close(fd); return 1; }
+  const size_t fsize = (size_t)stt.st_size;
+  const size_t hdr = 2 * sizeof(uint32_t) + 8 * sizeof(int32_t) + 2 * sizeof(float);
   uint32_t header[2];
   int32_t cfg[8];
   float fcfg[2];
-  if (fread(header, sizeof(uint32_t), 2, f) != 2 || fread(cfg, sizeof(int32_t), 8, f) != 8 ||
-      fread(fcfg, sizeof(float), 2, f) != 2) {
+  if (fsize < hdr || pread(fd, header, sizeof header, 0) != (ssize_t)sizeof header ||
+      pread(fd, cfg, sizeof cfg, 8) != (ssize_t)sizeof cfg || pread(fd, fcfg, sizeof fcfg, 40) != (ssize_t)sizeof fcfg) {
     fprintf(stderr, "Error: '%s' is truncated (bad header)\n", path);
-    fclose(f); return 1;
+    close(fd); return 1;
   }
   if (header[0] != LLMQ_MAGIC || header[1] != LLMA_VERSION) {
     fprintf(stderr, "Error: '%s' is not a v%u int8 LLMQ checkpoint\n", path, LLMA_VERSION);
-    fclose(f); return 1;
+    close(fd); return 1;
   }
   if (!config_valid(cfg)) {
     fprintf(stderr, "Error: '%s' has an invalid/unsupported config\n", path);
-    fclose(f); return 1;
+    close(fd); return 1;
   }
   if (!config_supported(cfg)) {
     fprintf(stderr, "Error: '%s' has a config this GPU build does not support\n", path);
-    fclose(f); return 1;
+    close(fd); return 1;
   }
-  if (model_alloc(out, cfg, fcfg[0], fcfg[1])) { fclose(f); return 1; }
+  void *map = mmap(NULL, fsize, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (map == MAP_FAILED) { fprintf(stderr, "Error: cannot map '%s'\n", path); return 1; }
+  (void)posix_madvise(map, fsize, POSIX_MADV_SEQUENTIAL);
+  if (model_alloc(out, cfg, fcfg[0], fcfg[1])) { munmap(map, fsize); return 1; }
   QDev *d = (QDev*)out->dev;
-  size_t big = (size_t)d->vocab * d->dm;
-  if ((size_t)d->dm * d->dff > big) big = (size_t)d->dm * d->dff;
+  size_t big = (size_t)d->dm * d->dff;                 // largest NK matrix staged for the transpose
   if ((size_t)d->qd * d->dm > big) big = (size_t)d->qd * d->dm;
-  const size_t stage_n = (size_t)64 << 20;
-  void *stage = malloc(stage_n > (size_t)d->vocab * 4 ? stage_n : (size_t)d->vocab * 4);
-  void *dtmp = qhip_malloc(big);
-  int rc = (!stage || !dtmp) ? 2 : 0;
+  if ((size_t)d->vocab * d->dm > big) big = (size_t)d->vocab * d->dm;
+  int8_t *dtmp = (int8_t*)qhip_malloc(big);
+  FileCur c = {(const uint8_t*)map, fsize, hdr};
+  int rc = (!dtmp || qhip_upload_begin((size_t)32 << 20)) ? 2 : 0;
   const int kp = d->kp_dm;
-  if (!rc) rc = read_q(f, d->vocab, d->dm, 0, d->dm, d->wte, d->wte_s, stage, dtmp);
+  if (!rc) rc = read_q(&c, d->vocab, d->dm, 0, d->dm, d->wte, d->wte_s, dtmp);
   for (int l = 0; l < d->L && !rc; l++) {
-    rc = read_f(f, d->g_attn[l], d->dm, stage);
-    if (!rc) rc = read_q(f, d->dm, d->qd, 1, kp, d->wqkv[l], d->sqkv[l], stage, dtmp);
-    if (!rc) rc = read_q(f, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)d->qd * kp, d->sqkv[l] + d->qd, stage, dtmp);
-    if (!rc) rc = read_q(f, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)(d->qd + d->kvd) * kp,
-                         d->sqkv[l] + d->qd + d->kvd, stage, dtmp);
-    if (!rc) rc = read_f(f, d->bqkv[l], d->qd, stage);
-    if (!rc) rc = read_f(f, d->bqkv[l] + d->qd, d->kvd, stage);
-    if (!rc) rc = read_f(f, d->bqkv[l] + d->qd + d->kvd, d->kvd, stage);
-    if (!rc) rc = read_q(f, d->qd, d->dm, 1, d->kp_qd, d->wo[l], d->so[l], stage, dtmp);
-    if (!rc) rc = read_f(f, d->g_ffn[l], d->dm, stage);
-    if (!rc) rc = read_q(f, d->dm, d->dff, 1, kp, d->wgu[l], d->sgu[l], stage, dtmp);
-    if (!rc) rc = read_q(f, d->dm, d->dff, 1, kp, d->wgu[l] + (size_t)d->dff * kp, d->sgu[l] + d->dff, stage, dtmp);
-    if (!rc) rc = read_q(f, d->dff, d->dm, 1, d->kp_ff, d->wd[l], d->sd[l], stage, dtmp);
+    rc = read_f(&c, d->g_attn[l], d->dm);
+    if (!rc) rc = read_q(&c, d->dm, d->qd, 1, kp, d->wqkv[l], d->sqkv[l], dtmp);
+    if (!rc) rc = read_q(&c, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)d->qd * kp, d->sqkv[l] + d->qd, dtmp);
+    if (!rc) rc = read_q(&c, d->dm, d->kvd, 1, kp, d->wqkv[l] + (size_t)(d->qd + d->kvd) * kp,
+                         d->sqkv[l] + d->qd + d->kvd, dtmp);
+    if (!rc) rc = read_f(&c, d->bqkv[l], d->qd);
+    if (!rc) rc = read_f(&c, d->bqkv[l] + d->qd, d->kvd);
+    if (!rc) rc = read_f(&c, d->bqkv[l] + d->qd + d->kvd, d->kvd);
+    if (!rc) rc = read_q(&c, d->qd, d->dm, 1, d->kp_qd, d->wo[l], d->so[l], dtmp);
+    if (!rc) rc = read_f(&c, d->g_ffn[l], d->dm);
+    if (!rc) rc = read_q(&c, d->dm, d->dff, 1, kp, d->wgu[l], d->sgu[l], dtmp);
+    if (!rc) rc = read_q(&c, d->dm, d->dff, 1, kp, d->wgu[l] + (size_t)d->dff * kp, d->sgu[l] + d->dff, dtmp);
+    if (!rc) rc = read_q(&c, d->dff, d->dm, 1, d->kp_ff, d->wd[l], d->sd[l], dtmp);
   }
-  if (!rc) rc = read_f(f, d->g_final, d->dm, stage);
-  if (!rc) rc = read_q(f, d->dm, d->vocab, 1, kp, d->head, d->head_s, stage, dtmp);
-  if (!rc && qhip_sync()) rc = 2;
-  fclose(f);
-  free(stage);
+  if (!rc) rc = read_f(&c, d->g_final, d->dm);
+  if (!rc) rc = read_q(&c, d->dm, d->vocab, 1, kp, d->head, d->head_s, dtmp);
+  if (qhip_upload_end() && !rc) rc = 2;
+  munmap(map, fsize);
   qhip_free(dtmp);
   if (rc) {
     if (rc == 1) fprintf(stderr, "Error: '%s' is truncated (bad weights)\n", path);
@@ -454,6 +472,52 @@ int q_llama_model_load(const char *path, QLlamaModel *out) {
     q_llama_model_free(out);
     return 1;
   }
+  return 0;
+}
+
+// The writer's side of the same format (tools/convert_llama.py:73-97 with
+// int8=True): every int8 matrix as cols f32 scales then rows*cols int8 bytes.
+static int write_q(FILE *f, const QTensor *t, int8_t *qh, float *sh) {
+  if (q_llama_tensor_export(t, (signed char*)qh, sh)) return 1;
+  return fwrite(sh, 4, (size_t)t->cols, f) != (size_t)t->cols ||
+         fwrite(qh, 1, (size_t)t->rows * t->cols, f) != (size_t)t->rows * t->cols;
+}
+
+static int write_f(FILE *f, const float *dev, int n, float *sh) {
+  if (qhip_d2h(sh, dev, (size_t)n * 4)) return 1;
+  return fwrite(sh, 4, (size_t)n, f) != (size_t)n;
+}
+
+int q_llama_model_save(const QLlamaModel *m, const char *path) {
+  const QDev *d = m ? (const QDev*)m->dev : NULL;
+  if (!d) { fprintf(stderr, "Error: q_llama_model_save: model not on the GPU\n"); return 1; }
+  FILE *f = fopen(path, "wb");
+  if (!f) { fprintf(stderr, "Error: cannot open '%s' for writing\n", path); return 1; }
+  size_t big = (size_t)d->vocab * d->dm;
+  if ((size_t)d->dm * d->dff > big) big = (size_t)d->dm * d->dff;
+  if ((size_t)d->qd * d->dm > big) big = (size_t)d->qd * d->dm;
+  size_t nf = (size_t)d->vocab;
+  if ((size_t)d->dff > nf) nf = (size_t)d->dff;
+  if ((size_t)d->nqkv > nf) nf = (size_t)d->nqkv;
+  int8_t *qh = (int8_t*)malloc(big);
+  float *sh = (float*)malloc(nf * 4);
+  const uint32_t header[2] = {LLMQ_MAGIC, LLMA_VERSION};
+  const int32_t cfg[8] = {m->vocab, m->d_model, m->n_layers, m->n_heads, m->n_kv, m->head_dim, m->d_ff, m->max_seq};
+  const float fcfg[2] = {m->rope_base, m->eps};
+  int rc = !qh || !sh || fwrite(header, 4, 2, f) != 2 || fwrite(cfg, 4, 8, f) != 8 || fwrite(fcfg, 4, 2, f) != 2;
+  if (!rc) rc = write_q(f, &m->wte, qh, sh);
+  for (int l = 0; l < m->n_layers && !rc; l++) {
+    const QLlamaBlock *b = &m->blocks[l];
+    rc = write_f(f, d->g_attn[l], d->dm, sh) || write_q(f, &b->Wq, qh, sh) || write_q(f, &b->Wk, qh, sh) ||
+         write_q(f, &b->Wv, qh, sh) || write_f(f, d->bqkv[l], d->qd, sh) ||
+         write_f(f, d->bqkv[l] + d->qd, d->kvd, sh) || write_f(f, d->bqkv[l] + d->qd + d->kvd, d->kvd, sh) ||
+         write_q(f, &b->Wo, qh, sh) || write_f(f, d->g_ffn[l], d->dm, sh) || write_q(f, &b->Wgate, qh, sh) ||
+         write_q(f, &b->Wup, qh, sh) || write_q(f, &b->Wdown, qh, sh);
+  }
+  if (!rc) rc = write_f(f, d->g_final, d->dm, sh) || write_q(f, &m->lm_head, qh, sh);
+  if (fclose(f) != 0) rc = 1;
+  free(qh); free(sh);
+  if (rc) { fprintf(stderr, "Error: writing '%s' failed\n", path); return 1; }
   return 0;
 }
 
@@ -750,6 +814,125 @@ int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_
   if (out && qhip_d2h_async(d->h_stage, d->d_out + pos, (size_t)n_steps * sizeof(int))) return 1;
   if (qhip_sync()) return 1;
   if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
+  kv->len += n_steps;
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Sampling (sampler.h).  The RNG is the reference's host xorshift64; the
+// sampling arithmetic runs on the device (k_sample.hip), which also holds the
+// RNG state inside q_llama_generate.
+// ---------------------------------------------------------------------------
+Rng rng_create(unsigned long long seed) {            // sampler.c:24-29
+  Rng r;
+  r.state = seed ? seed : 0x9E3779B97F4A7C15ULL;      // the all-zero state is a fixed point
+  return r;
+}
+
+float rng_uniform(Rng *r) {                           // sampler.c:31-45
+  unsigned long long x = r->state;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  r->state = x;
+  return (float)((x >> 11) * (1.0 / 9007199254740992.0));
+}
+
+// Process-wide sampler buffers, grown to the largest vocabulary seen.
+typedef struct {
+  int V;
+  float *row;                   // device copy of a host logits row
+  void *scratch;                // qhip_sample_scratch(V)
+  size_t bytes;
+  unsigned long long *rng;      // device RNG state, then the token (tok)
+  int *tok;
+  unsigned long long *h;        // pinned: [0] RNG state, [1] token
+} SmpBuf;
+static SmpBuf g_smp;
+
+static int smp_reserve(int V) {
+  if (g_smp.scratch && g_smp.V >= V) return 0;
+  if (qhip_init()) return 1;
+  qhip_sync();
+  qhip_free(g_smp.row); qhip_free(g_smp.scratch); qhip_free(g_smp.rng);
+  g_smp.row = NULL; g_smp.scratch = NULL; g_smp.rng = NULL; g_smp.tok = NULL; g_smp.V = 0;
+  g_smp.bytes = qhip_sample_scratch(V);
+  g_smp.row = (float*)qhip_malloc((size_t)V * 4);
+  g_smp.scratch = qhip_malloc(g_smp.bytes);
+  g_smp.rng = (unsigned long long*)qhip_malloc(256);
+  if (!g_smp.h) g_smp.h = (unsigned long long*)qhip_host_alloc(2 * sizeof(unsigned long long));
+  if (!g_smp.row || !g_smp.scratch || !g_smp.rng || !g_smp.h) return 1;
+  g_smp.tok = (int*)(g_smp.rng + 1);
+  g_smp.V = V;
+  return 0;
+}
+
+static int smp_row(const Tensor *logits, int row, int *V) {
+  if (!logits || !logits->data || !logits->shape || logits->ndim < 2 || row < 0 || row >= logits->shape[0] ||
+      logits->shape[1] <= 0) {
+    fprintf(stderr, "Error: sample: logits must be a (rows, vocab) host tensor and row in range\n");
+    abort();
+  }
+  *V = logits->shape[1];
+  if (smp_reserve(*V)) return 1;
+  return qhip_h2d(g_smp.row, logits->data + (size_t)row * *V, (size_t)*V * 4);
+}
+
+int sample_argmax(const Tensor *logits, int row) {
+  int V = 0;
+  if (smp_row(logits, row, &V) || qhip_argmax_row(g_smp.row, V, g_smp.tok, NULL, NULL, NULL, 0) ||
+      qhip_d2h_async(&g_smp.h[1], g_smp.tok, sizeof(int)) || qhip_sync())
+    die("sample_argmax");
+  int t;
+  memcpy(&t, &g_smp.h[1], sizeof t);
+  return t;
+}
+
+int sample_token(const Tensor *logits, int row, float temperature, int top_k, float top_p, Rng *rng) {
+  if (temperature <= 0.0f) return sample_argmax(logits, row);     // greedy, RNG untouched
+  int V = 0;
+  if (smp_row(logits, row, &V)) die("sample_token");
+  g_smp.h[0] = rng->state;
+  if (qhip_h2d_async(g_smp.rng, &g_smp.h[0], 8) ||
+      qhip_sample(g_smp.row, V, temperature, top_k, top_p, g_smp.scratch, g_smp.bytes, g_smp.rng, g_smp.tok, NULL,
+                  NULL, NULL, 0) ||
+      qhip_d2h_async(&g_smp.h[0], g_smp.rng, 16) || qhip_sync())
+    die("sample_token");
+  rng->state = g_smp.h[0];
+  int t;
+  memcpy(&t, &g_smp.h[1], sizeof t);
+  return t;
+}
+
+int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float temperature, int top_k, float top_p,
+                     Rng *rng, int *out) {
+  if (n_steps <= 0) return 0;
+  check_step(m, kv, NULL, 0, n_steps, "q_llama_generate");
+  if (kv->len < 1 || !rng) {
+    fprintf(stderr, "Error: q_llama_generate: needs a processed token (kv->len >= 1) and an Rng\n");
+    return 1;
+  }
+  const QDev *d = (const QDev*)m->dev;
+  KVDev *kd = (KVDev*)kv->dev;
+  if (smp_reserve(d->vocab)) return 1;
+  const int pos = kv->len;
+  // position state: the next input goes to pos, and every position from pos on
+  // takes the sampled token
+  d->h_stage[0] = pos; d->h_stage[1] = pos;
+  g_smp.h[0] = rng->state;
+  if (qhip_h2d_async(d->d_state, d->h_stage, 2 * sizeof(int)) || qhip_h2d_async(g_smp.rng, &g_smp.h[0], 8)) return 1;
+  for (int i = 0; i < n_steps; i++) {
+    const int rc = temperature > 0.0f
+        ? qhip_sample(d->logits, d->vocab, temperature, top_k, top_p, g_smp.scratch, g_smp.bytes, g_smp.rng,
+                      g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq)
+        : qhip_argmax_row(d->logits, d->vocab, g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq);
+    if (rc || run_steps(d, kd, 1)) return 1;
+  }
+  if (qhip_d2h_async(g_smp.h, g_smp.rng, 8)) return 1;
+  if (out && qhip_d2h_async(d->h_stage, d->d_out + pos - 1, (size_t)n_steps * sizeof(int))) return 1;
+  if (qhip_sync()) return 1;
+  if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
+  rng->state = g_smp.h[0];
   kv->len += n_steps;
   return 0;
 }

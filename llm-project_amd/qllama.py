@@ -50,6 +50,10 @@ class QLlamaBlock(C.Structure):
                 ("b_v", Tensor)] + [(n, QTensor) for n in ("Wq", "Wk", "Wv", "Wo", "Wgate", "Wup", "Wdown")]
 
 
+class Rng(C.Structure):
+    _fields_ = [("state", C.c_ulonglong)]        # sampler.h:15-17
+
+
 class QLlamaModel(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("vocab", "d_model", "n_layers", "n_heads", "n_kv", "head_dim",
                                        "d_ff", "max_seq")] + \
@@ -91,7 +95,16 @@ def lib():
         L.quantize_int8_percol.argtypes = [P(C.c_float), C.c_int, C.c_int, P(C.c_int8), P(C.c_float)]
         L.dequantize_int8_percol.argtypes = [P(C.c_int8), P(C.c_float), C.c_int, C.c_int, P(C.c_float)]
         L.qacc_columns.argtypes = [P(C.c_int8), P(C.c_int8), C.c_int, C.c_int, P(C.c_int32)]
+        L.q_llama_model_save.argtypes = [P(QLlamaModel), C.c_char_p]
         L.q_llama_tensor_export.argtypes = [P(QTensor), P(C.c_int8), P(C.c_float)]
+        L.rng_create.argtypes = [C.c_ulonglong]
+        L.rng_create.restype = Rng
+        L.rng_uniform.argtypes = [P(Rng)]
+        L.rng_uniform.restype = C.c_float
+        L.sample_argmax.argtypes = [P(Tensor), C.c_int]
+        L.sample_token.argtypes = [P(Tensor), C.c_int, C.c_float, C.c_int, C.c_float, P(Rng)]
+        L.q_llama_generate.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, C.c_float, C.c_int, C.c_float, P(Rng),
+                                       P(C.c_int)]
         L.qllama_device_count.restype = C.c_int
         L.qllama_device_sync.restype = C.c_int
         L.qllama_test_expf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
@@ -170,6 +183,19 @@ class Model:
             raise RuntimeError("q_llama_generate_greedy failed")
         return list(out)
 
+    def save(self, path):
+        """Write an LLMQ v2 checkpoint (q_llama_model_save)."""
+        if lib().q_llama_model_save(C.byref(self.m), os.fsencode(path)) != 0:
+            raise RuntimeError(f"q_llama_model_save failed for {path}")
+
+    def generate(self, n, temperature, top_k, top_p, rng):
+        """n sampled tokens (q_llama_generate); rng is an Rng, advanced in place."""
+        out = (C.c_int * n)()
+        if lib().q_llama_generate(C.byref(self.m), C.byref(self.kv), n, temperature, top_k, top_p,
+                                  C.byref(rng), out) != 0:
+            raise RuntimeError("q_llama_generate failed")
+        return list(out)
+
     def close(self):
         if self.m.dev:
             lib().llama_kv_free(C.byref(self.kv))
@@ -181,6 +207,22 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+# ---- sampler.h API ----------------------------------------------------------
+def rng_create(seed):
+    return lib().rng_create(seed)
+
+
+def sample_token(logits, temperature, top_k, top_p, rng, row=0):
+    """sample_token on a (rows, vocab) float32 array (sampled on the GPU); rng advances in place."""
+    a = np.ascontiguousarray(logits, np.float32).reshape(-1, logits.shape[-1])
+    return int(lib().sample_token(C.byref(host_tensor(a)), row, temperature, top_k, top_p, C.byref(rng)))
+
+
+def sample_argmax(logits, row=0):
+    a = np.ascontiguousarray(logits, np.float32).reshape(-1, logits.shape[-1])
+    return int(lib().sample_argmax(C.byref(host_tensor(a)), row))
 
 
 # ---- quant.h API ------------------------------------------------------------

@@ -289,6 +289,72 @@ int or_argmax(const float *r, int n) {
   return best;
 }
 
+// sampler.c:24-45: xorshift64 state, seed 0 replaced by a fixed odd constant;
+// a draw is the top 53 bits scaled to [0, 1) in double, narrowed to float.
+uint64_t or_rng_create(uint64_t seed) { return seed ? seed : 0x9E3779B97F4A7C15ULL; }
+
+float or_rng_uniform(uint64_t *state) {
+  uint64_t x = *state;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  *state = x;
+  return (float)((double)(x >> 11) * (1.0 / 9007199254740992.0));
+}
+
+typedef struct { float p; int idx; } OrProb;
+
+// Probability descending, then index ascending: the order a stable sort by
+// probability leaves the index-ordered array in (sampler.c:82 sorts with
+// glibc's qsort, a merge sort for arrays of this size, which is stable).
+static int or_prob_cmp(const void *a, const void *b) {
+  const OrProb *x = (const OrProb*)a, *y = (const OrProb*)b;
+  if (x->p != y->p) return x->p < y->p ? 1 : -1;
+  return (x->idx > y->idx) - (x->idx < y->idx);
+}
+
+// sampler.c:54-143
+int or_sample_token(const float *l, int V, float temperature, int top_k, float top_p, uint64_t *state) {
+  if (temperature <= 0.0f) return or_argmax(l, V);
+  float max_l = l[0];
+  for (int j = 1; j < V; j++) if (l[j] > max_l) max_l = l[j];
+  OrProb *pi = (OrProb*)malloc((size_t)V * sizeof(OrProb));
+  if (!pi) abort();
+  float sum = 0.0f;
+  for (int j = 0; j < V; j++) {
+    const float e = expf((l[j] - max_l) / temperature);
+    pi[j].p = e;
+    pi[j].idx = j;
+    sum += e;
+  }
+  for (int j = 0; j < V; j++) pi[j].p /= sum;
+  qsort(pi, (size_t)V, sizeof(OrProb), or_prob_cmp);
+  int keep = V;
+  if (top_k > 0 && top_k < keep) keep = top_k;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    float cum = 0.0f;
+    int kp = 0;
+    for (int i = 0; i < keep; i++) {
+      cum += pi[i].p;
+      kp++;
+      if (cum >= top_p) break;
+    }
+    keep = kp;
+  }
+  if (keep < 1) keep = 1;
+  float z = 0.0f;
+  for (int i = 0; i < keep; i++) z += pi[i].p;
+  const float u = or_rng_uniform(state) * z;
+  int chosen = pi[keep - 1].idx;
+  float acc = 0.0f;
+  for (int i = 0; i < keep; i++) {
+    acc += pi[i].p;
+    if (u <= acc) { chosen = pi[i].idx; break; }
+  }
+  free(pi);
+  return chosen;
+}
+
 // ---------------------------------------------------------------------------
 // Model construction.
 // ---------------------------------------------------------------------------

@@ -55,6 +55,10 @@ void or_gqa_forward(const float *Q, const float *K, const float *V, int n, int H
 void or_attn_decode(const float *q, const float *kc, const float *vc, int kvd, int pos,
                     int n_heads, int n_kv, int hd, float *sc, float *o);
 int  or_argmax(const float *r, int n);
+// sampler.c:24-45 (state in, state out) and sampler.c:54-143
+uint64_t or_rng_create(uint64_t seed);
+float or_rng_uniform(uint64_t *state);
+int  or_sample_token(const float *l, int V, float temperature, int top_k, float top_p, uint64_t *state);
 
 // Model from the seeded generator (synth.h), quantized as llama.c:490-511 does.
 int  or_model_synth(OrModel *m, const int32_t cfg[8], float rope_base, float eps,

@@ -8,6 +8,10 @@
 //   gen_golden <outdir> ops        quantizer, qmatmul, rmsnorm, rope, attention
 //   gen_golden <outdir> gqa8192    decode attention at context 8192 (slow)
 //   gen_golden <outdir> e2e <name> tiny | 1b | 8b greedy token streams
+//   gen_golden <outdir> llmqhash <file>   load an LLMQ file with the reference's
+//                                  q_llama_model_load and print its digest
+//   gen_golden <outdir> sample     sample_token draws, and the `llama` command's
+//                                  sampled loop (main.c:658-669) on the tiny model
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -350,8 +354,92 @@ static void run_e2e(const E2E *e) {
   free(seq); free(lh); free(amax); tensor_free(&logits); llama_kv_free(&kv); q_llama_model_free(&m);
 }
 
+// ---------------------------------------------------------------------------
+// Sampling: sample_token (sampler.c:54-143) on rows regenerated by the tests
+// from the seeded generator, and the `llama` command's sampled generation loop.
+// ---------------------------------------------------------------------------
+// Row kinds: 0 = N(0, sigma) values; 1 = the same rounded to quarters (many exact
+// ties, so the order of equal probabilities matters).
+static void sample_row(float *r, int V, uint64_t tid, double sigma, int kind) {
+  syn_fill(r, (size_t)V, 77, tid, sigma);
+  if (kind == 1)
+    for (int j = 0; j < V; j++) r[j] = rintf(r[j] * 4.0f) / 4.0f;
+}
+
+typedef struct { float t; int k; float p; } SParams;
+
+static void fx_sample(FILE *js) {
+  const struct { int V; uint64_t tid; double sigma; int kind; } rows[5] = {
+      {32000, 1, 1.0, 0}, {32000, 2, 1.0, 1}, {128256, 3, 1.3, 0}, {128256, 4, 4.0, 1}, {1000, 5, 0.05, 0}};
+  const SParams ps[9] = {{0.8f, 40, 0.95f}, {1.0f, 0, 0.9f}, {1.0f, 0, 1.0f}, {0.5f, 5, 0.0f}, {1.5f, 1000, 0.5f},
+                         {1.0f, 1, 1.0f}, {0.0f, 40, 0.95f}, {2.0f, 0, 0.99f}, {0.7f, 200000, 0.3f}};
+  fprintf(js, "  \"sample_cases\": [\n");
+  int first = 1;
+  for (int ri = 0; ri < 5; ri++) {
+    const int V = rows[ri].V;
+    Tensor L = mat(1, V);
+    sample_row(L.data, V, rows[ri].tid, rows[ri].sigma, rows[ri].kind);
+    for (int pi = 0; pi < 9; pi++) {
+      Rng rng = rng_create(1000 + 10 * ri + pi);
+      int tok[8];
+      for (int d = 0; d < 8; d++) tok[d] = sample_token(&L, 0, ps[pi].t, ps[pi].k, ps[pi].p, &rng);
+      fprintf(js, "%s    {\"V\": %d, \"tid\": %llu, \"sigma\": %.2f, \"kind\": %d, \"t\": %.9g, \"k\": %d, "
+                  "\"p\": %.9g, \"seed\": %d, \"tokens\": [",
+              first ? "" : ",\n", V, (unsigned long long)rows[ri].tid, rows[ri].sigma, rows[ri].kind,
+              (double)ps[pi].t, ps[pi].k, (double)ps[pi].p, 1000 + 10 * ri + pi);
+      for (int d = 0; d < 8; d++) fprintf(js, "%s%d", d ? "," : "", tok[d]);
+      fprintf(js, "], \"state\": \"%016llx\"}", (unsigned long long)rng.state);
+      first = 0;
+    }
+    tensor_free(&L);
+  }
+  fprintf(js, "\n  ],\n");
+  // rng_uniform's first values from a few seeds (seed 0 maps to the fixed constant)
+  fprintf(js, "  \"uniform\": [");
+  const unsigned long long seeds[3] = {0, 1, 1234};
+  for (int i = 0; i < 3; i++) {
+    Rng r = rng_create(seeds[i]);
+    fprintf(js, "%s[%llu", i ? ", " : "", seeds[i]);
+    for (int d = 0; d < 4; d++) { float u = rng_uniform(&r); uint32_t b; memcpy(&b, &u, 4); fprintf(js, ", %u", b); }
+    fprintf(js, "]");
+  }
+  fprintf(js, "],\n");
+}
+
+// The LLMQ branch of the `llama` command (main.c:658-669) on the tiny model:
+// rng_create(1234) once, then per input line: kv.len = 0, the prompt through
+// q_llama_decode_step, and n_new sampled tokens (T 0.8, top-k 40, top-p 0.95).
+static void fx_cli(FILE *js) {
+  QLlamaModel m;
+  build_model(&m, &CASES[0], 1234);
+  LlamaKV kv = q_llama_kv_create(&m);
+  Tensor logits = mat(1, m.vocab);
+  Rng rng = rng_create(1234);
+  const int lens[2] = {20, 7}, n_new = 40;
+  int *seq = malloc(sizeof(int) * (size_t)m.max_seq);
+  fprintf(js, "  \"cli\": {\"model\": \"tiny\", \"seed\": 1234, \"n_new\": %d, \"lines\": [\n", n_new);
+  for (int li = 0; li < 2; li++) {
+    int n = lens[li];
+    syn_prompt(seq, n, 4321 + li, m.vocab);
+    fprintf(js, "%s    {\"prompt\": [", li ? ",\n" : "");
+    for (int i = 0; i < n; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+    kv.len = 0;
+    for (int i = 0; i < n; i++) q_llama_decode_step(&m, &kv, seq[i], &logits);
+    fprintf(js, "], \"gen\": [");
+    for (int s = 0; s < n_new && n < m.max_seq; s++) {
+      int nxt = sample_token(&logits, 0, 0.8f, 40, 0.95f, &rng);
+      seq[n++] = nxt;
+      fprintf(js, "%s%d", s ? "," : "", nxt);
+      q_llama_decode_step(&m, &kv, nxt, &logits);
+    }
+    fprintf(js, "]}");
+  }
+  fprintf(js, "\n  ]},\n");
+  free(seq); tensor_free(&logits); llama_kv_free(&kv); q_llama_model_free(&m);
+}
+
 int main(int argc, char **argv) {
-  if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|e2e <name>\n"); return 2; }
+  if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|sample|e2e <name>\n"); return 2; }
   OUT = argv[1];
   if (!strcmp(argv[2], "ops")) {
     char path[1024]; snprintf(path, sizeof path, "%s/ops.json", OUT);
@@ -379,6 +467,23 @@ int main(int argc, char **argv) {
     gqa_case(3, 8192, js);
     fprintf(js, "  \"done\": true\n}\n");
     fclose(js);
+    return 0;
+  }
+  if (!strcmp(argv[2], "sample")) {
+    char path[1024]; snprintf(path, sizeof path, "%s/sample.json", OUT);
+    FILE *js = fopen(path, "w");
+    fprintf(js, "{\n");
+    fx_sample(js);
+    fx_cli(js);
+    fprintf(js, "  \"done\": true\n}\n");
+    fclose(js);
+    return 0;
+  }
+  if (!strcmp(argv[2], "llmqhash") && argc > 3) {
+    QLlamaModel m;
+    if (q_llama_model_load(argv[3], &m) != 0) return 1;
+    printf("%016llx\n", (unsigned long long)model_hash(&m));
+    q_llama_model_free(&m);
     return 0;
   }
   if (!strcmp(argv[2], "e2e") && argc > 3) {

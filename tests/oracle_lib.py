@@ -5,6 +5,7 @@ module.  The restatement it loads follows the reference file:line cited at each
 function in oracle/oracle.c.
 """
 import ctypes as C
+import struct
 import os
 import numpy as np
 
@@ -82,6 +83,11 @@ def lib():
         L.or_expf_mismatches.argtypes = [C.c_uint32, C.c_uint32, fp]
         L.or_expf_mismatches.restype = C.c_longlong
         L.or_set_threads.argtypes = [C.c_int]
+        L.or_rng_create.argtypes = [C.c_uint64]
+        L.or_rng_create.restype = C.c_uint64
+        L.or_rng_uniform.argtypes = [C.POINTER(C.c_uint64)]
+        L.or_rng_uniform.restype = C.c_float
+        L.or_sample_token.argtypes = [fp, C.c_int, C.c_float, C.c_int, C.c_float, C.POINTER(C.c_uint64)]
         L.or_get_threads.restype = C.c_int
         L.syn_key.argtypes = [C.c_uint64, C.c_uint64]
         L.syn_key.restype = C.c_uint64
@@ -206,6 +212,66 @@ def gqa_forward(Q, K, V, H, KVH, hd):
     lib().or_gqa_forward(fptr(np.ascontiguousarray(Q, np.float32)), fptr(np.ascontiguousarray(K, np.float32)),
                          fptr(np.ascontiguousarray(V, np.float32)), n, H, KVH, hd, fptr(att), fptr(O))
     return O
+
+
+def rng_create(seed):
+    return int(lib().or_rng_create(seed))
+
+
+def rng_uniform(state):
+    """(draw, new state)"""
+    st = C.c_uint64(state)
+    u = lib().or_rng_uniform(C.byref(st))
+    return u, st.value
+
+
+def sample_token(l, temperature, top_k, top_p, state):
+    """(token, new state) of sampler.c:54-143 on the float32 row l."""
+    l = np.ascontiguousarray(l, np.float32)
+    st = C.c_uint64(state)
+    t = lib().or_sample_token(fptr(l), l.size, temperature, top_k, top_p, C.byref(st))
+    return int(t), st.value
+
+
+def sample_row(V, tid, sigma, kind):
+    """The logits rows of the sampler fixtures: generator values, kind 1 rounded to quarters."""
+    r = synth(V, 77, tid, sigma)
+    if kind == 1:
+        r = (np.rint(r * np.float32(4.0)) / np.float32(4.0)).astype(np.float32)
+    return r
+
+
+def write_llmq(model, path):
+    """Write an oracle Model as an 'LLMQ' v2 checkpoint: the byte order of the
+    reference's reader (llama.c:603-657) and writer (tools/convert_llama.py:73-97):
+    header, 8 config ints, rope base and eps, then per tensor either f32 values
+    or (int8 matrices) the cols f32 scales followed by the rows*cols int8 bytes."""
+    m = model.m
+
+    def f32(ptr, n):
+        return np.ctypeslib.as_array(ptr, shape=(n,)).astype("<f4").tobytes()
+
+    def qt(t):
+        return (np.ctypeslib.as_array(t.scale, shape=(t.cols,)).astype("<f4").tobytes() +
+                np.ctypeslib.as_array(t.q, shape=(t.rows * t.cols,)).tobytes())
+
+    dm, qd, kvd = m.d_model, m.n_heads * m.head_dim, m.n_kv * m.head_dim
+    with open(path, "wb") as f:
+        f.write(struct.pack("<II", 0x514D4C4C, 2))
+        f.write(struct.pack("<8i", m.vocab, m.d_model, m.n_layers, m.n_heads, m.n_kv, m.head_dim, m.d_ff,
+                            m.max_seq))
+        f.write(struct.pack("<2f", m.rope_base, m.eps))
+        f.write(qt(m.wte))
+        for l in range(m.n_layers):
+            b = m.blocks[l]
+            f.write(f32(b.attn_norm, dm))
+            f.write(qt(b.Wq)); f.write(qt(b.Wk)); f.write(qt(b.Wv))
+            f.write(f32(b.b_q, qd)); f.write(f32(b.b_k, kvd)); f.write(f32(b.b_v, kvd))
+            f.write(qt(b.Wo))
+            f.write(f32(b.ffn_norm, dm))
+            f.write(qt(b.Wgate)); f.write(qt(b.Wup)); f.write(qt(b.Wdown))
+        f.write(f32(m.final_norm, dm))
+        f.write(qt(m.lm_head))
 
 
 class Model:

@@ -119,3 +119,25 @@ def test_load_without_gpu_fails_cleanly(tmp_path, capfd):
     _write(p, (0x514D4C4C, 2), GOOD_CFG, (10000.0, 1e-5))
     rc, err = _load_rc(p, capfd)
     assert rc != 0 and "Error:" in err
+
+
+# ---- the `llama` command drop-in (host-side behaviour only) -------------------
+CLI = os.path.join(ROOT, "llm-project_amd", "qllama-cli")
+
+
+@pytest.mark.skipif(not os.path.exists(CLI), reason="qllama-cli not built")
+def test_cli_usage_and_refusals(tmp_path):
+    r = subprocess.run([CLI], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
+    r = subprocess.run([CLI, "llama"], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
+    r = subprocess.run([CLI, "llama", str(tmp_path / "missing.bin")], capture_output=True, text=True)
+    assert r.returncode == 1 and "cannot open" in r.stderr
+    tiny = tmp_path / "tiny.bin"
+    tiny.write_bytes(b"LL")
+    r = subprocess.run([CLI, "llama", str(tiny)], capture_output=True, text=True)
+    assert r.returncode == 1 and "too small" in r.stderr
+    llma = tmp_path / "f32.bin"
+    _write(llma, (0x414D4C4C, 2), GOOD_CFG, (10000.0, 1e-5))
+    r = subprocess.run([CLI, "llama", str(llma)], capture_output=True, text=True)
+    assert r.returncode == 1 and "not an LLMQ" in r.stderr
