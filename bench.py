@@ -138,6 +138,9 @@ def main():
     ap.add_argument("--config", default="8b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=None)
     ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--sampled-steps", type=int, default=32,
+                    help="decode steps with on-device sampling (T 0.8, top-k 40, top-p 0.95: the llama "
+                         "command's settings), timed after the greedy ones")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -153,9 +156,10 @@ def main():
     Q = load_qllama()
     cfg, base, tied, prefill = CONFIGS[args.config]
     P = args.prefill if args.prefill is not None else prefill
-    W, K, NP = args.warmup, args.steps, args.profile_steps
-    if P + W + K + NP > cfg[7]:
-        sys.exit(f"bench.py: prefill {P} + warmup {W} + steps {K} + profile {NP} exceeds max_seq {cfg[7]}")
+    W, K, NP, NS = args.warmup, args.steps, args.profile_steps, args.sampled_steps
+    if P + W + K + NP + NS + (2 if NS else 0) > cfg[7]:
+        sys.exit(f"bench.py: prefill {P} + warmup {W} + steps {K} + profile {NP} + sampled {NS} "
+                 f"exceeds max_seq {cfg[7]}")
 
     t0 = time.perf_counter()
     gm = Q.Model.synth(cfg, base, seed=1234, tied=tied)
@@ -198,6 +202,18 @@ def main():
         gm.generate_greedy(tok, NP)
         prof = Q.profile_read()
         Q.profile(False)
+    # sampled decode (sample_token's arithmetic on the device between the steps)
+    sampled = None
+    if NS:
+        rng = Q.rng_create(1234)
+        gm.generate(2, 0.8, 40, 0.95, rng)          # allocates the sampler's buffers
+        Q.lib().qllama_device_sync()
+        t0 = time.perf_counter()
+        gm.generate(NS, 0.8, 40, 0.95, rng)
+        Q.lib().qllama_device_sync()
+        t_s = time.perf_counter() - t0
+        sampled = {"tok_s": round(NS / t_s, 3), "steps": NS, "temperature": 0.8, "top_k": 40, "top_p": 0.95,
+                   "ms_per_step": round(1e3 * t_s / NS, 4)}
     if args.calib_copy_mib:
         Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
         if Q.lib().qllama_test_copy(args.calib_copy_mib << 20) != 0:
@@ -256,6 +272,7 @@ def main():
         "decode_hbm_roofline_frac": round(step_frac, 4),
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
+        "sampled_decode": sampled,
         "prefill_roofline": pf_roof,
         "prefill_s": round(t_prefill, 4),
         "model_build_s": round(t_build, 3),

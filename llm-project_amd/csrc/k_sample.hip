@@ -3,12 +3,17 @@
 // bit for bit.
 //
 // Order of work for one logits row of V values (temperature > 0):
-//   k_smp_probs   one block: max, e_j = expf((l_j - max) / T), the sequential
-//                 float sum of the e_j evaluated exactly (qdev_seqsum.h, in
-//                 chunks whose first term carries the previous partial sum),
-//                 then p_j = e_j / sum (a true division, as sampler.c:79).
-//   radix sort    (p, index) pairs by p descending.  The sort is stable, so equal
-//                 probabilities keep ascending index order: the order the
+//   k_smp_bmax, k_smp_exp   blockwise: max, e_j = expf((l_j - max) / T)
+//   k_smp_sum     one block: the sequential float sum of the e_j evaluated
+//                 exactly (qdev_seqsum.h, in chunks whose first term carries the
+//                 previous partial sum); p_j = e_j / sum (a true division,
+//                 sampler.c:79) is formed where it is used.
+//   top-k <= 64   each block selects the 64 largest (p, index) keys of its 1024
+//                 by a bitwise search for the 64th largest; one block selects
+//                 the 64 largest of those (the global top-k is among the blocks'
+//                 top-k) and one wave sorts them.
+//   otherwise     a radix sort of all (p, index) pairs by p descending.  Both
+//                 orders are p descending, then index ascending: the order the
 //                 reference's qsort (glibc's merge sort, stable) leaves them in.
 //   k_smp_pick    one wave: keep = top-k, then the top-p cut over the running
 //                 sum, the kept mass z, u = uniform * z from the xorshift64
@@ -39,33 +44,173 @@ __device__ float block_max(float v, float *red) {
   return m;
 }
 
-// p[j] = expf((l[j] - max_l) / temperature) / sum  (sampler.c:68-79)
-__global__ __launch_bounds__(kNT) void k_smp_probs(const float *l, int V, float temperature, float *p) {
-  __shared__ qd::SeqScratch S;
-  __shared__ float red[kNT / 64];
-  const int tid = threadIdx.x;
+constexpr int kSlice = 1024;   // logits per block in the blockwise kernels (256 threads x 4)
+constexpr int kTopC = 64;      // candidates each block passes to the top-k merge
+constexpr int kMergeCap = 8192;
+
+// Per-block maximum of the logits.
+__global__ __launch_bounds__(256) void k_smp_bmax(const float *l, int V, float *bm) {
+  __shared__ float red[4];
+  const int j0 = blockIdx.x * kSlice + threadIdx.x;
   float mx = -INFINITY;
-  for (int j = tid; j < V; j += kNT) mx = fmaxf(mx, l[j]);
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+    if (j0 + 256 * r < V) mx = fmaxf(mx, l[j0 + 256 * r]);
   mx = block_max(mx, red);
-  for (int j = tid; j < V; j += kNT) p[j] = qd::expf_glibc((l[j] - mx) / temperature);
-  __syncthreads();
-  // sum = ((0 + e_0) + e_1) + ... in chunks of kNT*kCM terms; after the first
-  // chunk, term 0 of a chunk is the partial sum so far ((0 + s) = s exactly).
+  if (threadIdx.x == 0) bm[blockIdx.x] = mx;
+}
+
+// e[j] = expf((l[j] - max_l) / temperature)  (sampler.c:68-76); max_l from the
+// per-block maxima (a maximum does not depend on the order it is taken in).
+__global__ __launch_bounds__(256) void k_smp_exp(const float *l, int V, float temperature, const float *bm, int nb,
+                                                 float *e) {
+  __shared__ float red[4];
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < nb; i += 256) mx = fmaxf(mx, bm[i]);
+  mx = block_max(mx, red);
+  const int j0 = blockIdx.x * kSlice + threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int j = j0 + 256 * r;
+    if (j < V) e[j] = qd::expf_glibc((l[j] - mx) / temperature);
+  }
+}
+
+// *S = ((0 + e_0) + e_1) + ... + e_{V-1} in float (sampler.c:76), evaluated exactly
+// in chunks of kSumNT*kCM terms; after the first chunk, term 0 of a chunk is the
+// partial sum so far ((0 + s) = s exactly).  Four waves, so that each wave may
+// record up to 128 hard steps (the first chunk's partial sums cross many
+// binades early on) before the exact-sum walk has to fall back to the loop.
+constexpr int kSumNT = 256;
+__global__ __launch_bounds__(kSumNT) void k_smp_sum(const float *e, int V, float *S_out) {
+  __shared__ qd::SeqScratch S;
+  const int tid = threadIdx.x;
   float s = 0.0f;
   for (int base = 0, off = 0; base < V; off = 1) {
-    const int nnew = min(V - base, kNT * kCM - off), n = nnew + off;
+    const int nnew = min(V - base, kSumNT * kCM - off), n = nnew + off;
     const float s0 = s;
     const int b0 = base, o0 = off;
     float a[kCM];
 #pragma unroll
     for (int c = 0; c < kCM; c++) {
       const int q = tid * kCM + c;
-      a[c] = q < n ? (q < o0 ? s0 : p[b0 + q - o0]) : 0.0f;
+      a[c] = q < n ? (q < o0 ? s0 : e[b0 + q - o0]) : 0.0f;
     }
-    s = qd::seq_sum_nonneg<kNT, kCM>(a, n, S, [=](int i) { return i < o0 ? s0 : p[b0 + i - o0]; });
+    s = qd::seq_sum_nonneg<kSumNT, kCM>(a, n, S, [=](int i) { return i < o0 ? s0 : e[b0 + i - o0]; });
     base += nnew;
   }
-  for (int j = tid; j < V; j += kNT) p[j] = p[j] / s;
+  if (tid == 0) S_out[0] = s;
+}
+
+// p[j] = e[j] / S  (sampler.c:79)
+__global__ __launch_bounds__(256) void k_smp_div(const float *e, int V, const float *S, float *p) {
+  const float s = S[0];
+  const int j0 = blockIdx.x * kSlice + threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int j = j0 + 256 * r;
+    if (j < V) p[j] = e[j] / s;
+  }
+}
+
+// Sort key of (p, j): probability descending, then index ascending (the order
+// of a stable sort by probability, sampler.c:82).  p >= 0, so its bits order
+// like its values; 0 never is a real key (j < 2^31).
+__device__ __forceinline__ unsigned long long prob_key(float p, int j) {
+  return ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)(0xffffffffu - (unsigned)j);
+}
+
+// Sum of one int per thread over the block; red holds 2 * (NT / 64) ints and
+// alternates halves between calls (parity), so one barrier per call suffices.
+template <int NT>
+__device__ __forceinline__ int block_count(int n, int *red, int parity) {
+  n = qd::wave_sum_i32(n);
+  int *r = red + parity * (NT / 64);
+  if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = n;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) t += r[w];
+  return t;
+}
+
+// The K largest of the block's keys (NK per thread; nonzero keys are distinct, 0
+// is an empty slot), written unordered to out[0 .. K-1] with K = min(want, number
+// of nonzero keys): the K-th largest key is found bit by bit from the top (the
+// largest T with at least K keys >= T), then the keys >= T are gathered.
+template <int NT, int NK>
+__device__ int block_top(const unsigned long long (&k)[NK], int want, unsigned long long *out, int *red, int *cnt) {
+  int nz = 0;
+#pragma unroll
+  for (int i = 0; i < NK; i++) nz += k[i] != 0ull;
+  const int K = min(want, block_count<NT>(nz, red, 0));
+  unsigned long long T = 0;
+  if (K > 0) {
+    for (int b = 63; b >= 0; b--) {
+      const unsigned long long c = T | (1ull << b);
+      int n = 0;
+#pragma unroll
+      for (int i = 0; i < NK; i++) n += k[i] >= c;
+      if (block_count<NT>(n, red, b & 1) >= K) T = c;
+    }
+  }
+  if (threadIdx.x == 0) *cnt = 0;
+  __syncthreads();
+  if (K > 0) {
+#pragma unroll
+    for (int i = 0; i < NK; i++)
+      if (k[i] >= T) out[atomicAdd(cnt, 1)] = k[i];
+  }
+  __syncthreads();
+  return K;
+}
+
+// Per block: p = e / S over its slice and the slice's kTopC largest keys
+// (unordered; empty slots 0).
+__global__ __launch_bounds__(256) void k_smp_topk_block(const float *e, int V, const float *S,
+                                                        unsigned long long *cand) {
+  __shared__ unsigned long long top[kTopC];
+  __shared__ int red[8], cnt;
+  const float sum = S[0];
+  const int j0 = blockIdx.x * kSlice + threadIdx.x;
+  unsigned long long k[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int j = j0 + 256 * r;
+    k[r] = j < V ? prob_key(e[j] / sum, j) : 0ull;
+  }
+  const int K = block_top<256, 4>(k, kTopC, top, red, &cnt);
+  if (threadIdx.x < kTopC) cand[(size_t)blockIdx.x * kTopC + threadIdx.x] = (int)threadIdx.x < K ? top[threadIdx.x] : 0ull;
+}
+
+// The kTopC largest of n candidate keys, as sorted (p, index) pairs: selected by
+// block_top, then ordered by one wave's bitonic network (descending).
+__global__ __launch_bounds__(kNT) void k_smp_topk_merge(const unsigned long long *cand, int n, float *ps, int *is) {
+  constexpr int NK = kMergeCap / kNT;
+  __shared__ unsigned long long top[kTopC];
+  __shared__ int red[2 * (kNT / 64)], cnt;
+  unsigned long long k[NK];
+#pragma unroll
+  for (int i = 0; i < NK; i++) {
+    const int c = (int)threadIdx.x + kNT * i;
+    k[i] = c < n ? cand[c] : 0ull;
+  }
+  const int K = block_top<kNT, NK>(k, kTopC, top, red, &cnt);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    unsigned long long x = lane < K ? top[lane] : 0ull;
+    for (int kk = 2; kk <= 64; kk <<= 1) {
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        const unsigned long long y = __shfl_xor(x, j, 64);
+        const bool desc = (lane & kk) == 0, lower = (lane & j) == 0;
+        x = (desc == lower) ? (x > y ? x : y) : (x < y ? x : y);
+      }
+    }
+    if (lane < K) {
+      ps[lane] = __uint_as_float((unsigned)(x >> 32));
+      is[lane] = (int)(0xffffffffu - (unsigned)x);
+    }
+  }
 }
 
 // First index of the maximum (sampler.c:8-21).  Optional decode-state update as
@@ -172,13 +317,49 @@ size_t sort_temp_bytes(int V) {
   return e == hipSuccess ? bytes : 0;
 }
 
+int nblocks(int V) { return (V + kSlice - 1) / kSlice; }
+
+// Scratch layout: e, p, sorted p, indices, sorted indices (V each), block maxima,
+// the sum, top-k candidates, then the radix sort's temporary storage.
+struct Layout {
+  float *e, *p, *ps, *bm, *S;
+  int *idx, *is;
+  unsigned long long *cand;
+  void *temp;
+  size_t temp_bytes, total;
+};
+
+Layout layout(void *base, int V) {
+  Layout L{};
+  uint8_t *b = static_cast<uint8_t *>(base);
+  const size_t slot = al256((size_t)V * 4), nb = (size_t)nblocks(V);
+  size_t o = 0;
+  L.e = reinterpret_cast<float *>(b + o); o += slot;
+  L.p = reinterpret_cast<float *>(b + o); o += slot;
+  L.ps = reinterpret_cast<float *>(b + o); o += slot;
+  L.idx = reinterpret_cast<int *>(b + o); o += slot;
+  L.is = reinterpret_cast<int *>(b + o); o += slot;
+  L.bm = reinterpret_cast<float *>(b + o); o += al256(nb * 4);
+  L.S = reinterpret_cast<float *>(b + o); o += 256;
+  L.cand = reinterpret_cast<unsigned long long *>(b + o); o += al256(nb * kTopC * 8);
+  L.temp = b + o;
+  L.temp_bytes = al256(sort_temp_bytes(V));
+  L.total = o + L.temp_bytes;
+  return L;
+}
+
 }  // namespace
 
-// Scratch of qhip_sample for rows of V logits: p, sorted p, indices, sorted
-// indices and the radix sort's temporary storage.
+// Scratch of qhip_sample for rows of V logits.
 extern "C" size_t qhip_sample_scratch(int V) {
   if (V <= 0) return 0;
-  return 4 * al256((size_t)V * 4) + al256(sort_temp_bytes(V));
+  return layout(nullptr, V).total;
+}
+
+// Whether qhip_sample takes the top-k path for these arguments: its kernels are
+// all this library's (no library sort), so the launches can be graph-captured.
+extern "C" int qhip_sample_topk_path(int V, int top_k) {
+  return top_k >= 1 && top_k <= kTopC && V > 0 && (size_t)nblocks(V) * kTopC <= (size_t)kMergeCap;
 }
 
 extern "C" int qhip_sample(const float *logits, int V, float temperature, int top_k, float top_p, void *scratch,
@@ -186,18 +367,25 @@ extern "C" int qhip_sample(const float *logits, int V, float temperature, int to
                            int *d_out, int max_seq) {
   if (V <= 0 || !(temperature > 0.0f)) return qh::fail_msg("sample: needs V > 0 and temperature > 0");
   if (scratch_bytes < qhip_sample_scratch(V)) return qh::fail_msg("sample: scratch too small");
-  uint8_t *b = static_cast<uint8_t *>(scratch);
-  const size_t slot = al256((size_t)V * 4);
-  float *p = reinterpret_cast<float *>(b), *ps = reinterpret_cast<float *>(b + slot);
-  int *idx = reinterpret_cast<int *>(b + 2 * slot), *is = reinterpret_cast<int *>(b + 3 * slot);
-  void *temp = b + 4 * slot;
-  size_t temp_bytes = scratch_bytes - 4 * slot;
-  QH_LAUNCH(QK_OTHER, k_smp_probs, dim3(1), dim3(kNT), 0, logits, V, temperature, p);
-  QH_LAUNCH(QK_OTHER, k_smp_iota, dim3((V + 255) / 256), dim3(256), 0, idx, V);
-  hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(temp, temp_bytes, p, ps, idx, is, V, 0, 32, qh::stream());
-  if (e != hipSuccess) return qh::fail("sample: radix sort", e);
-  QH_LAUNCH(QK_OTHER, k_smp_pick, dim3(1), dim3(64), 0, ps, is, V, top_k, top_p, rng, tok, d_in, d_state, d_out,
-            max_seq);
+  const Layout L = layout(scratch, V);
+  const int nb = nblocks(V);
+  QH_LAUNCH(QK_OTHER, k_smp_bmax, dim3(nb), dim3(256), 0, logits, V, L.bm);
+  QH_LAUNCH(QK_OTHER, k_smp_exp, dim3(nb), dim3(256), 0, logits, V, temperature, L.bm, nb, L.e);
+  QH_LAUNCH(QK_OTHER, k_smp_sum, dim3(1), dim3(kSumNT), 0, L.e, V, L.S);
+  if (qhip_sample_topk_path(V, top_k)) {
+    // the top_k <= kTopC largest of all V are among the kTopC largest of each block
+    QH_LAUNCH(QK_OTHER, k_smp_topk_block, dim3(nb), dim3(256), 0, L.e, V, L.S, L.cand);
+    QH_LAUNCH(QK_OTHER, k_smp_topk_merge, dim3(1), dim3(kNT), 0, L.cand, nb * kTopC, L.ps, L.is);
+  } else {
+    QH_LAUNCH(QK_OTHER, k_smp_div, dim3(nb), dim3(256), 0, L.e, V, L.S, L.p);
+    QH_LAUNCH(QK_OTHER, k_smp_iota, dim3((V + 255) / 256), dim3(256), 0, L.idx, V);
+    size_t tb = L.temp_bytes;
+    hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(L.temp, tb, L.p, L.ps, L.idx, L.is, V, 0, 32,
+                                                                qh::stream());
+    if (e != hipSuccess) return qh::fail("sample: radix sort", e);
+  }
+  QH_LAUNCH(QK_OTHER, k_smp_pick, dim3(1), dim3(64), 0, L.ps, L.is, V, top_k, top_p, rng, tok, d_in, d_state,
+            d_out, max_seq);
   return 0;
 }
 

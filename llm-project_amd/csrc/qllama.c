@@ -63,6 +63,11 @@ typedef struct {
   float *kbase, *vbase;
   void *graph;
   const void *graph_owner;
+  // sampled step (sampler kernels, then the decode step) for one parameter set
+  void *sgraph;
+  const void *sgraph_owner, *sgraph_scratch;
+  float sg_t, sg_p;
+  int sg_k;
 } KVDev;
 
 static int config_valid(const int32_t *cfg) {
@@ -593,6 +598,7 @@ void llama_kv_free(LlamaKV *kv) {
   if (kd) {
     qhip_sync();
     if (kd->graph) qhip_graph_destroy(kd->graph);
+    if (kd->sgraph) qhip_graph_destroy(kd->sgraph);
     qhip_free(kd->kbase); qhip_free(kd->vbase);
     free(kd);
   } else if (kv->k && kv->v) {
@@ -904,6 +910,39 @@ int sample_token(const Tensor *logits, int row, float temperature, int top_k, fl
   return t;
 }
 
+// One sampled token: the sampler writes it as the input of position d_state[0],
+// then the decode step runs it.
+static int enqueue_sampled(const QDev *d, const KVDev *kd, float temperature, int top_k, float top_p) {
+  const int rc = temperature > 0.0f
+      ? qhip_sample(d->logits, d->vocab, temperature, top_k, top_p, g_smp.scratch, g_smp.bytes, g_smp.rng,
+                    g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq)
+      : qhip_argmax_row(d->logits, d->vocab, g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq);
+  return rc || enqueue_step(d, kd);
+}
+
+// n sampled tokens: one graph replay each when every launch of the step is this
+// library's own (qhip_sample_topk_path), else eager launches.
+static int run_sampled_steps(const QDev *d, KVDev *kd, int n, float temperature, int top_k, float top_p) {
+  const int capturable = temperature <= 0.0f || qhip_sample_topk_path(d->vocab, top_k);
+  if (profiling || !capturable || getenv("QLLAMA_NO_GRAPH")) {
+    for (int i = 0; i < n; i++) if (enqueue_sampled(d, kd, temperature, top_k, top_p)) return 1;
+    return 0;
+  }
+  if (!kd->sgraph || kd->sgraph_owner != (const void*)d || kd->sgraph_scratch != g_smp.scratch ||
+      kd->sg_t != temperature || kd->sg_k != top_k || kd->sg_p != top_p) {
+    if (kd->sgraph) { qhip_graph_destroy(kd->sgraph); kd->sgraph = NULL; }
+    if (qhip_capture_begin()) return 1;
+    int rc = enqueue_sampled(d, kd, temperature, top_k, top_p);
+    void *g = NULL;
+    if (qhip_capture_end(&g) || rc) return 1;
+    kd->sgraph = g;
+    kd->sgraph_owner = d; kd->sgraph_scratch = g_smp.scratch;
+    kd->sg_t = temperature; kd->sg_k = top_k; kd->sg_p = top_p;
+  }
+  for (int i = 0; i < n; i++) if (qhip_graph_launch(kd->sgraph)) return 1;
+  return 0;
+}
+
 int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float temperature, int top_k, float top_p,
                      Rng *rng, int *out) {
   if (n_steps <= 0) return 0;
@@ -921,13 +960,7 @@ int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float tempe
   d->h_stage[0] = pos; d->h_stage[1] = pos;
   g_smp.h[0] = rng->state;
   if (qhip_h2d_async(d->d_state, d->h_stage, 2 * sizeof(int)) || qhip_h2d_async(g_smp.rng, &g_smp.h[0], 8)) return 1;
-  for (int i = 0; i < n_steps; i++) {
-    const int rc = temperature > 0.0f
-        ? qhip_sample(d->logits, d->vocab, temperature, top_k, top_p, g_smp.scratch, g_smp.bytes, g_smp.rng,
-                      g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq)
-        : qhip_argmax_row(d->logits, d->vocab, g_smp.tok, d->d_in, d->d_state, d->d_out, d->max_seq);
-    if (rc || run_steps(d, kd, 1)) return 1;
-  }
+  if (run_sampled_steps(d, kd, n_steps, temperature, top_k, top_p)) return 1;
   if (qhip_d2h_async(g_smp.h, g_smp.rng, 8)) return 1;
   if (out && qhip_d2h_async(d->h_stage, d->d_out + pos - 1, (size_t)n_steps * sizeof(int))) return 1;
   if (qhip_sync()) return 1;

@@ -42,6 +42,21 @@ def test_sample_token_matches_reference(Q):
         assert rng.state == int(c["state"], 16), ci
 
 
+@pytest.mark.parametrize("V,k", [(131072, 64), (131072, 65), (131073, 40), (131073, 64), (50, 60), (50, 10),
+                                 (1025, 64), (5000, 1)])
+def test_sample_token_paths_match_oracle(Q, V, k):
+    """Both device paths (blockwise top-k when top_k <= 64 and V <= 131072, the
+    full radix sort otherwise) against the oracle, at and around the switch."""
+    for kind in (0, 1):
+        row = O.sample_row(V, 40 + kind, 1.0, kind)
+        rng = Q.rng_create(11)
+        st = O.rng_create(11)
+        for _ in range(6):
+            t = Q.sample_token(row.reshape(1, -1), 0.9, k, 0.97, rng)
+            r, st = O.sample_token(row, 0.9, k, 0.97, st)
+            assert t == r and rng.state == st, (V, k, kind)
+
+
 def test_sample_argmax_first_index(Q):
     for tid in range(4):
         row = O.sample_row(128256 if tid % 2 else 32000, 30 + tid, 1.0, 1).reshape(1, -1)
@@ -82,6 +97,32 @@ def test_generate_in_pieces_equals_one_call(Q):
         r = Q.rng_create(5)
         b = m.generate(10, 1.1, 0, 0.9, r) + m.generate(1, 1.1, 0, 0.9, r) + m.generate(13, 1.1, 0, 0.9, r)
         assert a == b
+        # the same through the captured sampled step (top-k path), with a change of
+        # parameters in between (a second capture) and back
+        m.reset(0)
+        m.prefill(prompt, want_logits=False)
+        a = m.generate(24, 0.8, 40, 0.95, Q.rng_create(6))
+        m.reset(0)
+        m.prefill(prompt, want_logits=False)
+        r = Q.rng_create(6)
+        b = m.generate(7, 0.8, 40, 0.95, r)
+        b += m.generate(5, 0.8, 40, 0.95, r)
+        b += m.generate(12, 0.8, 40, 0.95, r)
+        assert a == b
+        # oracle: the same draws from the oracle's decode steps and sampler
+        ref = O.Model(TINY, 10000.0, seed=1234)
+        try:
+            for t in prompt:
+                lg = ref.step(t)
+            st = O.rng_create(6)
+            c = []
+            for _ in range(24):
+                t, st = O.sample_token(lg, 0.8, 40, 0.95, st)
+                c.append(t)
+                lg = ref.step(t)
+            assert a == c
+        finally:
+            ref.close()
         # greedy through the sampler path equals the decode graph's argmax
         m.reset(0)
         m.prefill(prompt, want_logits=False)
