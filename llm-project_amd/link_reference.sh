@@ -12,7 +12,9 @@
 #             go away; llama_kv_create zeroes the new device handle
 #   matrix.c  qacc_columns (matrix.c:370-374) goes away (the library exports it)
 #   quant.c   is not compiled (the library exports its functions)
-# and links -lqllama.  The line numbers are those of the reference revision this
+# and links -lqllama.  With GPU_SAMPLER=1 in the environment sampler.c is not
+# compiled either: the library's sample_token / sample_argmax / rng_create /
+# rng_uniform (same results, computed on the GPU) serve every caller.  The line numbers are those of the reference revision this
 # library was built against; the script checks each anchor before editing.
 set -euo pipefail
 SRC=${1:?usage: link_reference.sh SRC DEST}
@@ -47,8 +49,10 @@ sed -i '17d' "$DEST/llama.h"
 sed -i '447,657d; 290,294d; 276a\  kv.dev = NULL;' "$DEST/llama.c"
 sed -i '370,374d' "$DEST/matrix.c"
 
+DROP='s/quant\.o//'
+[ "${GPU_SAMPLER:-0}" = 1 ] && DROP='s/quant\.o//; s/sampler\.o//'
 make -C "$DEST" transformer \
   CFLAGS="-std=c11 -O3 -march=native -Wall -pthread -I$INC" \
-  OBJS="$(make -s -C "$DEST" -p -n 2>/dev/null | sed -n 's/^OBJS *= *//p' | head -1 | sed 's/quant\.o//')" \
+  OBJS="$(make -s -C "$DEST" -p -n 2>/dev/null | sed -n 's/^OBJS *= *//p' | head -1 | sed "$DROP")" \
   LDLIBS="-lm -pthread -L$HERE -lqllama -Wl,-rpath,$HERE"
 echo "link_reference.sh: built $DEST/transformer against $HERE/libqllama.so"
