@@ -543,6 +543,126 @@ void or_decode_step(const OrModel *m, OrKV *kv, int token, float *logits) {
 }
 
 // ---------------------------------------------------------------------------
+// fp32 (LLMA) path: llama.c:296-362 with the f32 matmul of matrix.c:178-190.
+// ---------------------------------------------------------------------------
+// One row of matrix.c:178-190: c[j] = ((0 + a_0*W_0j) + a_1*W_1j) + ..., k outer,
+// j inner (every c[j] sums in k order; products rounded before the add).
+void or_matmul_row(const float *a, const float *W, int K, int N, float *c) {
+  for (int j = 0; j < N; j++) c[j] = 0.0f;
+  for (int k = 0; k < K; k++) {
+    const float ak = a[k];
+    const float *Wk = &W[(size_t)k * N];
+    for (int j = 0; j < N; j++) c[j] += ak * Wk[j];
+  }
+}
+
+int or_fmodel_synth(OrFModel *m, const int32_t cfg[8], float rope_base, float eps, uint64_t seed, int tied) {
+  memset(m, 0, sizeof *m);
+  m->vocab = cfg[0]; m->d_model = cfg[1]; m->n_layers = cfg[2]; m->n_heads = cfg[3]; m->n_kv = cfg[4];
+  m->head_dim = cfg[5]; m->d_ff = cfg[6]; m->max_seq = cfg[7]; m->rope_base = rope_base; m->eps = eps;
+  const size_t dm = (size_t)m->d_model, qd = (size_t)m->n_heads * m->head_dim, kvd = (size_t)m->n_kv * m->head_dim;
+  const size_t ff = (size_t)m->d_ff, V = (size_t)m->vocab;
+  const int L = m->n_layers;
+  m->blocks = (OrFBlock*)calloc((size_t)L, sizeof(OrFBlock));
+  m->wte = (float*)malloc(V * dm * 4);
+  m->lm_head = (float*)malloc(V * dm * 4);
+  m->final_norm = (float*)malloc(dm * 4);
+  if (!m->blocks || !m->wte || !m->lm_head || !m->final_norm) return 1;
+  syn_fill(m->wte, V * dm, seed, 0, 0.02);
+  for (size_t j = 0; j < dm; j++) m->final_norm[j] = 1.0f;
+  for (int l = 0; l < L; l++) {
+    OrFBlock *b = &m->blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    b->attn_norm = (float*)malloc(dm * 4); b->ffn_norm = (float*)malloc(dm * 4);
+    b->b_q = (float*)calloc(qd, 4); b->b_k = (float*)calloc(kvd, 4); b->b_v = (float*)calloc(kvd, 4);
+    b->Wq = (float*)malloc(dm * qd * 4); b->Wk = (float*)malloc(dm * kvd * 4); b->Wv = (float*)malloc(dm * kvd * 4);
+    b->Wo = (float*)malloc(qd * dm * 4);
+    b->Wgate = (float*)malloc(dm * ff * 4); b->Wup = (float*)malloc(dm * ff * 4); b->Wdown = (float*)malloc(ff * dm * 4);
+    if (!b->attn_norm || !b->ffn_norm || !b->b_q || !b->b_k || !b->b_v || !b->Wq || !b->Wk || !b->Wv || !b->Wo ||
+        !b->Wgate || !b->Wup || !b->Wdown) return 1;
+    for (size_t j = 0; j < dm; j++) { b->attn_norm[j] = 1.0f; b->ffn_norm[j] = 1.0f; }
+    syn_fill(b->Wq, dm * qd, seed, t0 + 1, 0.02);
+    syn_fill(b->Wk, dm * kvd, seed, t0 + 2, 0.02);
+    syn_fill(b->Wv, dm * kvd, seed, t0 + 3, 0.02);
+    syn_fill(b->Wo, qd * dm, seed, t0 + 7, 0.02);
+    syn_fill(b->Wgate, dm * ff, seed, t0 + 9, 0.02);
+    syn_fill(b->Wup, dm * ff, seed, t0 + 10, 0.02);
+    syn_fill(b->Wdown, ff * dm, seed, t0 + 11, 0.02);
+  }
+  if (tied) {      // lm_head[k][v] = wte[v][k]
+    for (size_t v = 0; v < V; v++)
+      for (size_t k = 0; k < dm; k++) m->lm_head[k * V + v] = m->wte[v * dm + k];
+  } else {
+    syn_fill(m->lm_head, dm * V, seed, 2 + 12 * (uint64_t)L, 0.02);
+  }
+  return 0;
+}
+
+void or_fmodel_free(OrFModel *m) {
+  if (m->blocks) {
+    for (int l = 0; l < m->n_layers; l++) {
+      OrFBlock *b = &m->blocks[l];
+      free(b->attn_norm); free(b->ffn_norm); free(b->b_q); free(b->b_k); free(b->b_v);
+      free(b->Wq); free(b->Wk); free(b->Wv); free(b->Wo); free(b->Wgate); free(b->Wup); free(b->Wdown);
+    }
+  }
+  free(m->blocks); free(m->wte); free(m->lm_head); free(m->final_norm);
+  memset(m, 0, sizeof *m);
+}
+
+int or_fkv_create(OrKV *kv, const OrFModel *m) {
+  kv->n_layers = m->n_layers; kv->max_seq = m->max_seq;
+  kv->kv_dim = m->n_kv * m->head_dim; kv->len = 0;
+  size_t n = (size_t)m->n_layers * m->max_seq * kv->kv_dim;
+  kv->k = (float*)malloc(n * sizeof(float));
+  kv->v = (float*)malloc(n * sizeof(float));
+  return (kv->k && kv->v) ? 0 : 1;
+}
+
+// llama.c:296-362 (swiglu.c:31-41 for the feed-forward)
+void or_f32_decode_step(const OrFModel *m, OrKV *kv, int token, float *logits) {
+  const int dm = m->d_model, hd = m->head_dim, dff = m->d_ff;
+  const int qd = m->n_heads * hd, kvd = m->n_kv * hd;
+  const int pos = kv->len;
+  float *x = (float*)calloc((size_t)dm, 4), *xn = (float*)calloc((size_t)dm, 4);
+  float *q = (float*)calloc((size_t)qd, 4), *k = (float*)calloc((size_t)kvd, 4), *v = (float*)calloc((size_t)kvd, 4);
+  float *o = (float*)calloc((size_t)qd, 4), *ao = (float*)calloc((size_t)dm, 4), *hn = (float*)calloc((size_t)dm, 4);
+  float *f = (float*)calloc((size_t)dm, 4), *g = (float*)calloc((size_t)dff, 4), *u = (float*)calloc((size_t)dff, 4);
+  float *sc = (float*)malloc((size_t)(pos + 1) * 4);
+  for (int j = 0; j < dm; j++) x[j] = m->wte[(size_t)token * dm + j];
+  for (int l = 0; l < m->n_layers; l++) {
+    const OrFBlock *b = &m->blocks[l];
+    float *kc = &kv->k[(size_t)l * kv->max_seq * kvd];
+    float *vc = &kv->v[(size_t)l * kv->max_seq * kvd];
+    or_rmsnorm(x, 1, dm, b->attn_norm, m->eps, xn);
+    or_matmul_row(xn, b->Wq, dm, qd, q); for (int j = 0; j < qd; j++) q[j] = q[j] + b->b_q[j];
+    or_matmul_row(xn, b->Wk, dm, kvd, k); for (int j = 0; j < kvd; j++) k[j] = k[j] + b->b_k[j];
+    or_matmul_row(xn, b->Wv, dm, kvd, v); for (int j = 0; j < kvd; j++) v[j] = v[j] + b->b_v[j];
+    or_rope_heads_pos(q, 1, qd, m->n_heads, m->rope_base, pos);
+    or_rope_heads_pos(k, 1, kvd, m->n_kv, m->rope_base, pos);
+    memcpy(&kc[(size_t)pos * kvd], k, (size_t)kvd * 4);
+    memcpy(&vc[(size_t)pos * kvd], v, (size_t)kvd * 4);
+    or_attn_decode(q, kc, vc, kvd, pos, m->n_heads, m->n_kv, hd, sc, o);
+    or_matmul_row(o, b->Wo, qd, dm, ao);
+    for (int j = 0; j < dm; j++) x[j] += ao[j];
+    or_rmsnorm(x, 1, dm, b->ffn_norm, m->eps, hn);
+    or_matmul_row(hn, b->Wgate, dm, dff, g);
+    or_matmul_row(hn, b->Wup, dm, dff, u);
+    for (int j = 0; j < dff; j++) {
+      const float z = g[j];
+      const float s = 1.0f / (1.0f + expf(-z));
+      g[j] = (z * s) * u[j];
+    }
+    or_matmul_row(g, b->Wdown, dff, dm, f);
+    for (int j = 0; j < dm; j++) x[j] += f[j];
+  }
+  or_rmsnorm(x, 1, dm, m->final_norm, m->eps, hn);
+  or_matmul_row(hn, m->lm_head, dm, m->vocab, logits);
+  kv->len = pos + 1;
+  free(sc); free(x); free(xn); free(q); free(k); free(v); free(o); free(ao); free(hn); free(f); free(g); free(u);
+}
+
+// ---------------------------------------------------------------------------
 // Checker for the device expf: counts inputs start..start+count-1 (as float bit
 // patterns) where got[] differs bitwise from this host's libm expf (the function
 // llama.c:567,585 call).  NaN results compare equal to NaN.

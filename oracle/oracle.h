@@ -73,6 +73,29 @@ int  or_kv_create(OrKV *kv, const OrModel *m);
 void or_kv_free(OrKV *kv);
 void or_decode_step(const OrModel *m, OrKV *kv, int token, float *logits);
 
+// fp32 (LLMA) model, reference layout: every matrix (rows = in, cols = out) f32
+// row-major (llama.h:19-37, 58-66).
+typedef struct {
+  float *attn_norm, *ffn_norm, *b_q, *b_k, *b_v;
+  float *Wq, *Wk, *Wv, *Wo, *Wgate, *Wup, *Wdown;
+} OrFBlock;
+
+typedef struct {
+  int vocab, d_model, n_layers, n_heads, n_kv, head_dim, d_ff, max_seq;
+  float rope_base, eps;
+  float *wte;
+  OrFBlock *blocks;
+  float *final_norm;
+  float *lm_head;
+} OrFModel;
+
+void or_matmul_row(const float *a, const float *W, int K, int N, float *c);
+// Weights N(0, 0.02) from the generator with the int8 model's tensor ids, not quantized.
+int  or_fmodel_synth(OrFModel *m, const int32_t cfg[8], float rope_base, float eps, uint64_t seed, int tied);
+void or_fmodel_free(OrFModel *m);
+int  or_fkv_create(OrKV *kv, const OrFModel *m);
+void or_f32_decode_step(const OrFModel *m, OrKV *kv, int token, float *logits);
+
 // Bitwise mismatches of got[i] against the host libm expf at bit pattern start+i.
 long long or_expf_mismatches(uint32_t start, uint32_t count, const float *got);
 

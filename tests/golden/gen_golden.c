@@ -10,6 +10,10 @@
 //   gen_golden <outdir> e2e <name> tiny | 1b | 8b greedy token streams
 //   gen_golden <outdir> llmqhash <file>   load an LLMQ file with the reference's
 //                                  q_llama_model_load and print its digest
+//   gen_golden <outdir> e2e_f32 <name>   tiny | mid: greedy streams of the fp32
+//                                  LLMA path (llama_decode_step, llama.c:296-362)
+//   gen_golden <outdir> llmahash <file>   load an LLMA file with llama_model_load
+//                                  and print its digest
 //   gen_golden <outdir> sample     sample_token draws, and the `llama` command's
 //                                  sampled loop (main.c:658-669) on the tiny model
 #include <math.h>
@@ -438,6 +442,100 @@ static void fx_cli(FILE *js) {
   free(seq); tensor_free(&logits); llama_kv_free(&kv); q_llama_model_free(&m);
 }
 
+// ---------------------------------------------------------------------------
+// fp32 (LLMA) path: the generator's N(0, 0.02) weights, not quantized.
+// ---------------------------------------------------------------------------
+typedef struct { const char *name; int32_t cfg[8]; float base; int tied, prompt, gen; } E2EF;
+static const E2EF FCASES[2] = {
+  {"tiny", {32000, 288, 6, 6, 2, 48, 768, 256}, 10000.0f, 0, 32, 32},
+  {"mid", {32000, 1024, 4, 16, 4, 64, 2816, 256}, 500000.0f, 1, 40, 24},
+};
+
+static void build_fmodel(LlamaModel *m, const E2EF *e, uint64_t seed) {
+  const int32_t *c = e->cfg;
+  *m = llama_model_create(c[0], c[1], c[2], c[3], c[4], c[5], c[6], c[7], e->base, 1e-5f);
+  const int dm = c[1], L = c[2];
+  syn_fill(m->wte.data, (size_t)c[0] * dm, seed, 0, 0.02);
+  for (int l = 0; l < L; l++) {
+    LlamaBlock *b = &m->blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l;
+    for (int j = 0; j < dm; j++) { b->attn_norm.data[j] = 1.0f; b->ffn_norm.data[j] = 1.0f; }
+    memset(b->b_q.data, 0, b->b_q.size * 4); memset(b->b_k.data, 0, b->b_k.size * 4);
+    memset(b->b_v.data, 0, b->b_v.size * 4);
+    syn_fill(b->Wq.data, b->Wq.size, seed, t0 + 1, 0.02);
+    syn_fill(b->Wk.data, b->Wk.size, seed, t0 + 2, 0.02);
+    syn_fill(b->Wv.data, b->Wv.size, seed, t0 + 3, 0.02);
+    syn_fill(b->Wo.data, b->Wo.size, seed, t0 + 7, 0.02);
+    syn_fill(b->Wgate.data, b->Wgate.size, seed, t0 + 9, 0.02);
+    syn_fill(b->Wup.data, b->Wup.size, seed, t0 + 10, 0.02);
+    syn_fill(b->Wdown.data, b->Wdown.size, seed, t0 + 11, 0.02);
+  }
+  for (int j = 0; j < dm; j++) m->final_norm.data[j] = 1.0f;
+  if (e->tied) {
+    for (int v = 0; v < c[0]; v++)
+      for (int k = 0; k < dm; k++) m->lm_head.data[(size_t)k * c[0] + v] = m->wte.data[(size_t)v * dm + k];
+  } else {
+    syn_fill(m->lm_head.data, m->lm_head.size, seed, 2 + 12 * (uint64_t)L, 0.02);
+  }
+}
+
+// Digest of every tensor of an fp32 model in the canonical order (llama.c:198-219).
+static uint64_t fmodel_hash(const LlamaModel *m) {
+  uint64_t h = syn_hash_f32(m->wte.data, m->wte.size, 0);
+  for (int l = 0; l < m->n_layers; l++) {
+    const LlamaBlock *b = &m->blocks[l];
+    const Tensor *t[12] = {&b->attn_norm, &b->Wq, &b->Wk, &b->Wv, &b->b_q, &b->b_k, &b->b_v, &b->Wo,
+                           &b->ffn_norm, &b->Wgate, &b->Wup, &b->Wdown};
+    for (int i = 0; i < 12; i++) h = h * 31 + syn_hash_f32(t[i]->data, t[i]->size, 0);
+  }
+  h = h * 31 + syn_hash_f32(m->final_norm.data, m->final_norm.size, 0);
+  return h * 31 + syn_hash_f32(m->lm_head.data, m->lm_head.size, 0);
+}
+
+static void run_e2e_f32(const E2EF *e) {
+  const uint64_t seed = 1234;
+  LlamaModel m;
+  build_fmodel(&m, e, seed);
+  LlamaKV kv = llama_kv_create(&m);
+  Tensor logits = mat(1, m.vocab);
+  const int P = e->prompt, G = e->gen;
+  int *seq = malloc(sizeof(int) * (size_t)m.max_seq);
+  uint64_t *lh = malloc(sizeof(uint64_t) * (size_t)(P + G));
+  syn_prompt(seq, P, seed, m.vocab);
+  kv.len = 0;
+  for (int i = 0; i < P; i++) {
+    llama_decode_step(&m, &kv, seq[i], &logits);
+    lh[i] = syn_hash_f32(logits.data, (size_t)m.vocab, 0);
+  }
+  char nm[128]; long sv[1] = {m.vocab};
+  snprintf(nm, sizeof nm, "e2e_f32_%s_logits_prompt_last", e->name);
+  npy_f32(nm, logits.data, 1, sv);
+  int n = P;
+  for (int s = 0; s < G; s++) {
+    int nxt = sample_argmax(&logits, 0);
+    seq[n++] = nxt;
+    llama_decode_step(&m, &kv, nxt, &logits);
+    lh[P + s] = syn_hash_f32(logits.data, (size_t)m.vocab, 0);
+  }
+  snprintf(nm, sizeof nm, "e2e_f32_%s_logits_final", e->name);
+  npy_f32(nm, logits.data, 1, sv);
+  char path[1024]; snprintf(path, sizeof path, "%s/e2e_f32_%s.json", OUT, e->name);
+  FILE *js = fopen(path, "w");
+  fprintf(js, "{\n  \"name\": \"%s\", \"seed\": %llu, \"cfg\": [%d,%d,%d,%d,%d,%d,%d,%d],\n", e->name,
+          (unsigned long long)seed, e->cfg[0], e->cfg[1], e->cfg[2], e->cfg[3], e->cfg[4], e->cfg[5], e->cfg[6],
+          e->cfg[7]);
+  fprintf(js, "  \"rope_base\": %.1f, \"eps\": 1e-5, \"tied\": %d,\n", e->base, e->tied);
+  fprintf(js, "  \"model_hash\": \"%016llx\",\n  \"prompt\": [", (unsigned long long)fmodel_hash(&m));
+  for (int i = 0; i < P; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"gen\": [");
+  for (int i = P; i < n; i++) fprintf(js, "%s%d", i > P ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"logit_hashes\": [");
+  for (int i = 0; i < P + G; i++) fprintf(js, "%s\"%016llx\"", i ? "," : "", (unsigned long long)lh[i]);
+  fprintf(js, "]\n}\n");
+  fclose(js);
+  free(seq); free(lh); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
+}
+
 int main(int argc, char **argv) {
   if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|sample|e2e <name>\n"); return 2; }
   OUT = argv[1];
@@ -484,6 +582,16 @@ int main(int argc, char **argv) {
     if (q_llama_model_load(argv[3], &m) != 0) return 1;
     printf("%016llx\n", (unsigned long long)model_hash(&m));
     q_llama_model_free(&m);
+    return 0;
+  }
+  if (!strcmp(argv[2], "e2e_f32") && argc > 3) {
+    for (int i = 0; i < 2; i++) if (!strcmp(argv[3], FCASES[i].name)) { run_e2e_f32(&FCASES[i]); return 0; }
+  }
+  if (!strcmp(argv[2], "llmahash") && argc > 3) {
+    LlamaModel m;
+    if (llama_model_load(argv[3], &m) != 0) return 1;
+    printf("%016llx\n", (unsigned long long)fmodel_hash(&m));
+    llama_model_free(&m);
     return 0;
   }
   if (!strcmp(argv[2], "e2e") && argc > 3) {

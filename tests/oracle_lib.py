@@ -35,6 +35,20 @@ class OrModel(C.Structure):
                 ("final_norm", C.POINTER(C.c_float)), ("lm_head", OrQT)]
 
 
+class OrFBlock(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in
+                ("attn_norm", "ffn_norm", "b_q", "b_k", "b_v", "Wq", "Wk", "Wv", "Wo", "Wgate", "Wup", "Wdown")]
+
+
+class OrFModel(C.Structure):
+    _fields_ = [("vocab", C.c_int), ("d_model", C.c_int), ("n_layers", C.c_int),
+                ("n_heads", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("d_ff", C.c_int), ("max_seq", C.c_int),
+                ("rope_base", C.c_float), ("eps", C.c_float),
+                ("wte", C.POINTER(C.c_float)), ("blocks", C.POINTER(OrFBlock)),
+                ("final_norm", C.POINTER(C.c_float)), ("lm_head", C.POINTER(C.c_float))]
+
+
 class OrKV(C.Structure):
     _fields_ = [("n_layers", C.c_int), ("max_seq", C.c_int), ("kv_dim", C.c_int),
                 ("len", C.c_int), ("k", C.POINTER(C.c_float)), ("v", C.POINTER(C.c_float))]
@@ -83,6 +97,12 @@ def lib():
         L.or_expf_mismatches.argtypes = [C.c_uint32, C.c_uint32, fp]
         L.or_expf_mismatches.restype = C.c_longlong
         L.or_set_threads.argtypes = [C.c_int]
+        L.or_matmul_row.argtypes = [fp, fp, C.c_int, C.c_int, fp]
+        L.or_fmodel_synth.argtypes = [C.POINTER(OrFModel), C.POINTER(C.c_int32), C.c_float, C.c_float,
+                                      C.c_uint64, C.c_int]
+        L.or_fmodel_free.argtypes = [C.POINTER(OrFModel)]
+        L.or_fkv_create.argtypes = [C.POINTER(OrKV), C.POINTER(OrFModel)]
+        L.or_f32_decode_step.argtypes = [C.POINTER(OrFModel), C.POINTER(OrKV), C.c_int, fp]
         L.or_rng_create.argtypes = [C.c_uint64]
         L.or_rng_create.restype = C.c_uint64
         L.or_rng_uniform.argtypes = [C.POINTER(C.c_uint64)]
@@ -239,6 +259,81 @@ def sample_row(V, tid, sigma, kind):
     if kind == 1:
         r = (np.rint(r * np.float32(4.0)) / np.float32(4.0)).astype(np.float32)
     return r
+
+
+def matmul_row(a, W):
+    """matrix.c:178-190 for one row: a (K,), W (K, N) f32."""
+    a = np.ascontiguousarray(a, np.float32)
+    W = np.ascontiguousarray(W, np.float32)
+    c = np.empty(W.shape[1], np.float32)
+    lib().or_matmul_row(fptr(a), fptr(W), W.shape[0], W.shape[1], fptr(c))
+    return c
+
+
+class FModel:
+    """Oracle fp32 (LLMA) model from the generator (weights not quantized)."""
+
+    def __init__(self, cfg, rope_base, eps=1e-5, seed=1234, tied=False):
+        self.m = OrFModel()
+        if lib().or_fmodel_synth(C.byref(self.m), (C.c_int32 * 8)(*cfg), rope_base, eps, seed, int(tied)) != 0:
+            raise MemoryError("oracle fp32 model allocation failed")
+        self.kv = OrKV()
+        if lib().or_fkv_create(C.byref(self.kv), C.byref(self.m)) != 0:
+            raise MemoryError("oracle kv allocation failed")
+        self.vocab = cfg[0]
+        self.logits = np.zeros(self.vocab, np.float32)
+
+    def tensors(self):
+        """(name, array view) in the canonical LLMA order (llama.c:198-219)."""
+        m = self.m
+        dm, qd, kvd, ff, V = m.d_model, m.n_heads * m.head_dim, m.n_kv * m.head_dim, m.d_ff, m.vocab
+        A = lambda p, *shape: np.ctypeslib.as_array(p, shape=shape)
+        out = [("wte", A(m.wte, V, dm))]
+        for l in range(m.n_layers):
+            b = m.blocks[l]
+            out += [("attn_norm", A(b.attn_norm, dm)), ("Wq", A(b.Wq, dm, qd)), ("Wk", A(b.Wk, dm, kvd)),
+                    ("Wv", A(b.Wv, dm, kvd)), ("b_q", A(b.b_q, qd)), ("b_k", A(b.b_k, kvd)),
+                    ("b_v", A(b.b_v, kvd)), ("Wo", A(b.Wo, qd, dm)), ("ffn_norm", A(b.ffn_norm, dm)),
+                    ("Wgate", A(b.Wgate, dm, ff)), ("Wup", A(b.Wup, dm, ff)), ("Wdown", A(b.Wdown, ff, dm))]
+        return out + [("final_norm", A(m.final_norm, dm)), ("lm_head", A(m.lm_head, dm, V))]
+
+    def hash(self):
+        """The fixtures' digest: h = h*31 + hash of each tensor, canonical order."""
+        h = 0
+        for i, (_, t) in enumerate(self.tensors()):
+            d = hash_f32(t)
+            h = d if i == 0 else (h * 31 + d) & 0xFFFFFFFFFFFFFFFF
+        return h
+
+    def write_llma(self, path):
+        """An 'LLMA' v2 checkpoint (llama.c:234-262): header, config, then every
+        tensor's f32 values in the canonical order."""
+        m = self.m
+        with open(path, "wb") as f:
+            f.write(struct.pack("<II", 0x414D4C4C, 2))
+            f.write(struct.pack("<8i", m.vocab, m.d_model, m.n_layers, m.n_heads, m.n_kv, m.head_dim, m.d_ff,
+                                m.max_seq))
+            f.write(struct.pack("<2f", m.rope_base, m.eps))
+            for _, t in self.tensors():
+                f.write(t.astype("<f4").tobytes())
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def step(self, token):
+        lib().or_f32_decode_step(C.byref(self.m), C.byref(self.kv), token, fptr(self.logits))
+        return self.logits
+
+    def close(self):
+        if self.m.blocks:
+            lib().or_kv_free(C.byref(self.kv))
+            lib().or_fmodel_free(C.byref(self.m))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def write_llmq(model, path):
