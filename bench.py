@@ -130,6 +130,93 @@ def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
                       f"{med * 1e3:.1f} ms, oracle/liboracle with {nthreads} threads"}
 
 
+def f32_host_model(Q, cfg, base, tied, seed=1234):
+    """A reference LlamaModel (host f32) with N(0, 0.02) weights from numpy, norms 1,
+    biases 0, in the canonical tensor order (llama.c:198-219)."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    rng = np.random.default_rng(seed)
+
+    def w(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+    one = np.ones(dm, np.float32)
+    wte = w(vocab, dm)
+    t = [("wte", wte)]
+    for _ in range(L):
+        t += [("attn_norm", one), ("Wq", w(dm, qd)), ("Wk", w(dm, kvd)), ("Wv", w(dm, kvd)),
+              ("b_q", np.zeros(qd, np.float32)), ("b_k", np.zeros(kvd, np.float32)), ("b_v", np.zeros(kvd, np.float32)),
+              ("Wo", w(qd, dm)), ("ffn_norm", one), ("Wgate", w(dm, ff)), ("Wup", w(dm, ff)), ("Wdown", w(ff, dm))]
+    t += [("final_norm", one), ("lm_head", np.ascontiguousarray(wte.T) if tied else w(dm, vocab))]
+    return Q.host_model(cfg, base, 1e-5, t)
+
+
+def f32_bytes(cfg, t):
+    """HBM bytes of one fp32 decode token at context t: every weight once (f32),
+    the KV rows read and the new row written."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    w = L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab
+    return 4 * w + L * (2 * kvd * 4 * t + 2 * kvd * 4)
+
+
+def main_f32(args, Q, cfg, base, tied, P):
+    """The fp32 (LLMA) decode path: llama_decode_step per token (host logits, as in
+    the reference), after P prompt tokens fed the same way."""
+    W, K, NP = args.warmup, args.steps, args.profile_steps
+    if P + W + K + NP > cfg[7]:
+        sys.exit("bench.py: prompt + warmup + steps + profile exceeds max_seq")
+    t0 = time.perf_counter()
+    host = f32_host_model(Q, cfg, base, tied)
+    t_host = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    m = Q.FModel(host)                                   # uploads the weights
+    t_up = time.perf_counter() - t0
+    ids = list(np.random.default_rng(1234).integers(0, cfg[0], P + 1))
+    for t in ids[:P]:
+        lg = m.step(int(t))
+    tok = int(np.argmax(lg)) if P else int(ids[P])
+    for _ in range(W):
+        tok = int(np.argmax(m.step(tok)))
+    pos0 = m.pos
+    t0 = time.perf_counter()
+    for _ in range(K):
+        tok = int(np.argmax(m.step(tok)))
+    t_dec = time.perf_counter() - t0
+    prof = {}
+    if NP:
+        Q.profile(True)
+        for _ in range(NP):
+            tok = int(np.argmax(m.step(tok)))
+        prof = Q.profile_read()
+        Q.profile(False)
+    m.close()
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    gb = {"gemv_qkv": (L, 4 * dm * (qd + 2 * kvd)), "gemv_o": (L, 4 * qd * dm), "gemv_gate_up": (L, 8 * dm * ff),
+          "gemv_down": (L, 4 * ff * dm), "gemv_head": (1, 4 * dm * vocab)}
+    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
+    gemv_bytes = sum(n * b for n, b in gb.values())
+    step_bytes = statistics.mean(f32_bytes(cfg, pos0 + 1 + i) for i in range(K))
+    achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9 if gemv_ms else None
+    line = {
+        "metric": f"fp32 LLMA decode tok/s, {args.config}-shape (1 GPU)",
+        "value": round(K / t_dec, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(1e3 * t_dec / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (numpy N(0,0.02) f32 weights; uniform-random prompt ids)",
+        "config": {"workload": f"{args.config}-shape fp32 LLaMA greedy decode (llama_decode_step, host logits) "
+                               f"after {P} prompt tokens", "cfg": cfg, "context_timed": [pos0 + 1, pos0 + K]},
+        "decode_hbm_roofline_frac": round(step_bytes / (t_dec / K) / (HBM_PEAK_GBS * 1e9), 4),
+        "decode_bytes_per_token": int(step_bytes),
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_f32 (f32 GEMV, k-order chains, all call sites)",
+                     "achieved": round(achieved, 1) if achieved else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None},
+        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
+        "host_model_s": round(t_host, 2), "upload_s": round(t_up, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +233,8 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (the scale reference "
                          "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--path", default="int8", choices=["int8", "f32"],
+                    help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -156,6 +245,8 @@ def main():
     Q = load_qllama()
     cfg, base, tied, prefill = CONFIGS[args.config]
     P = args.prefill if args.prefill is not None else prefill
+    if args.path == "f32":
+        return main_f32(args, Q, cfg, base, tied, args.prefill if args.prefill is not None else 64)
     W, K, NP, NS = args.warmup, args.steps, args.profile_steps, args.sampled_steps
     if P + W + K + NP + NS + (2 if NS else 0) > cfg[7]:
         sys.exit(f"bench.py: prefill {P} + warmup {W} + steps {K} + profile {NP} + sampled {NS} "

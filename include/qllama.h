@@ -138,6 +138,16 @@ void dequantize_int8_percol(const signed char *q, const float *scale, int rows, 
 // matrix.c:370-374  acc[j] = sum_k qa[k] * qw[k*N + j]  (host arrays, computed on the GPU)
 void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, int32_t *acc);
 
+// llama.c:275-288 / 296-362  The fp32 (LLMA) decode step on the GPU, for the
+// reference's host LlamaModel (llama.h:58-66).  The first cache made for a model
+// uploads a device copy of its weights (found again by the model's weight
+// pointers); the copy is freed with the last of its caches (llama_kv_free).
+// Weight changes made on the host afterwards are seen by caches created later.
+// logits: host (1, vocab).  Every output sums in the reference's order, so the
+// logits are the reference's bit for bit.
+LlamaKV llama_kv_create(const LlamaModel *m);
+void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logits);
+
 // sampler.h:12-31.  Inside the reference's build this takes the place of
 // sampler.h (which, included first, supplies Rng itself).
 #ifndef SAMPLER_H

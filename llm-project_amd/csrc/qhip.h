@@ -26,6 +26,7 @@ int         qhip_d2h(void *host_dst, const void *src, size_t n);        // synch
 int         qhip_h2d_async(void *dst, const void *host_src, size_t n);  // pinned src
 int         qhip_d2h_async(void *host_dst, const void *src, size_t n);
 int         qhip_d2d_async(void *dst, const void *src, size_t n);
+int         qhip_copy2d_d2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height);
 int         qhip_fill_zero(void *p, size_t n);           // kernel, capture-safe
 // Staged upload from any host memory (a mapped file, say) through two pinned
 // buffers of `chunk` bytes: qhip_upload returns once src may be reused, the copy
@@ -162,6 +163,18 @@ int qhip_sample(const float *logits, int V, float temperature, int top_k, float 
                 size_t scratch_bytes, unsigned long long *rng, int *tok, int *d_in, const int *d_state, int *d_out,
                 int max_seq);
 int qhip_argmax_row(const float *logits, int V, int *tok, int *d_in, const int *d_state, int *d_out, int max_seq);
+
+// fp32 (LLMA) decode path (k_gemv_f32.hip).  qhip_gemv_f32: out[j] = c[j] (+bias[j])
+// or out[j] += c[j] with c = x (K) times W (K, N), every c[j] summed in k order
+// (matrix.c:178-190); W in the panel layout qhip_to_panels_f32 writes (from the
+// reference's row-major (K, N); qhip_panels_f32_size floats); K <= qhip_gemv_f32_max_k().
+size_t qhip_panels_f32_size(int K, int N);
+int qhip_to_panels_f32(const float *src, int K, int N, float *dst);
+int qhip_gemv_f32(int residual, int cls, const float *x, int K, const float *W, int N, float *out, const float *bias);
+int qhip_gemv_f32_max_k(void);
+int qhip_embed_f32(const float *wte, int dm, const int *d_in, const int *d_state, float *x);
+int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y);
+int qhip_swiglu_f32(const float *gu, int dff, float *h);
 
 // reference-layout column accumulate (matrix.c:354-374) for qacc_columns
 int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);

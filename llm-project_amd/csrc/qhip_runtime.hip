@@ -216,6 +216,12 @@ int qhip_upload_end(void) {
   return rc;
 }
 
+int qhip_copy2d_d2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height) {
+  if (!width || !height) return 0;
+  hipError_t e = hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToDevice, g_stream);
+  return e == hipSuccess ? 0 : fail("2-D device copy", e);
+}
+
 int qhip_sync(void) {
   if (!g_ready) return 0;
   hipError_t e = hipStreamSynchronize(g_stream);

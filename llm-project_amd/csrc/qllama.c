@@ -68,6 +68,7 @@ typedef struct {
   const void *sgraph_owner, *sgraph_scratch;
   float sg_t, sg_p;
   int sg_k;
+  struct FDev *fdev;   // fp32 caches: the device model they belong to
 } KVDev;
 
 static int config_valid(const int32_t *cfg) {
@@ -593,6 +594,9 @@ LlamaKV q_llama_kv_create(const QLlamaModel *m) {
   return kv;
 }
 
+struct FDev;
+static void fdev_release(struct FDev *f);
+
 void llama_kv_free(LlamaKV *kv) {
   KVDev *kd = (KVDev*)kv->dev;
   if (kd) {
@@ -600,6 +604,7 @@ void llama_kv_free(LlamaKV *kv) {
     if (kd->graph) qhip_graph_destroy(kd->graph);
     if (kd->sgraph) qhip_graph_destroy(kd->sgraph);
     qhip_free(kd->kbase); qhip_free(kd->vbase);
+    if (kd->fdev) fdev_release(kd->fdev);
     free(kd);
   } else if (kv->k && kv->v) {
     for (int l = 0; l < kv->n_layers; l++) { free(kv->k[l]); free(kv->v[l]); }
@@ -822,6 +827,253 @@ int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_
   if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
   kv->len += n_steps;
   return 0;
+}
+
+// ---------------------------------------------------------------------------
+// fp32 (LLMA) decode path: llama_kv_create / llama_decode_step of llama.c:275-362
+// on the GPU.  The caller keeps the reference's host LlamaModel; the first cache
+// created for it uploads a device copy (looked up by the model's weight
+// pointers), which lives as long as a cache of it does.  Weights are read at
+// that point: host changes made afterwards are seen by caches created later.
+// Device layout: every matrix keeps the reference's (K, N) row-major order (the
+// GEMV reads a row's columns contiguously); Wq|Wk|Wv and Wgate|Wup are joined
+// column-wise into one matrix each, so one launch serves each pair.
+// ---------------------------------------------------------------------------
+typedef struct FDev {
+  const void *key_wte, *key_blocks;      // identity of the host model
+  int refs;
+  int vocab, dm, L, H, KVH, hd, dff, max_seq, qd, kvd, nqkv;
+  float eps, attn_scale;
+  uint8_t *blob;
+  float **wqkv, **bqkv, **wo, **wgu, **wd, **g_attn, **g_ffn;
+  float *wte, *head, *g_final, *rope_cos, *rope_sin;
+  float *x, *xn, *qkv, *o, *gu, *h, *logits, *scores;
+  int *d_state, *d_in;
+  int *h_stage;
+} FDev;
+
+#define FDEV_MAX 16
+static FDev *g_fdev[FDEV_MAX];
+
+static void fdev_free(FDev *f) {
+  if (!f) return;
+  qhip_free(f->blob);
+  qhip_host_free(f->h_stage);
+  free(f->wqkv); free(f->bqkv); free(f->wo); free(f->wgu); free(f->wd); free(f->g_attn); free(f->g_ffn);
+  free(f);
+}
+
+static void fdev_release(FDev *f) {
+  if (--f->refs > 0) return;
+  for (int i = 0; i < FDEV_MAX; i++) if (g_fdev[i] == f) g_fdev[i] = NULL;
+  qhip_sync();
+  fdev_free(f);
+}
+
+static FDev *fdev_find(const LlamaModel *m) {
+  for (int i = 0; i < FDEV_MAX; i++)
+    if (g_fdev[i] && g_fdev[i]->key_wte == (const void*)m->wte.data && g_fdev[i]->key_blocks == (const void*)m->blocks)
+      return g_fdev[i];
+  return NULL;
+}
+
+// The host-built RoPE tables (rope.c:58-61 with the host libm).
+static int rope_upload(float *dcos, float *dsin, int max_seq, int hd, float base) {
+  const int half = hd / 2;
+  float *ct = (float*)malloc((size_t)max_seq * half * sizeof(float));
+  float *st = (float*)malloc((size_t)max_seq * half * sizeof(float));
+  if (!ct || !st) { free(ct); free(st); return 1; }
+  for (int pos = 0; pos < max_seq; pos++)
+    for (int k = 0; k < half; k++) {
+      float inv_freq = powf(base, -2.0f * (float)k / (float)hd);
+      float ang = (float)pos * inv_freq;
+      ct[(size_t)pos * half + k] = cosf(ang);
+      st[(size_t)pos * half + k] = sinf(ang);
+    }
+  int rc = qhip_h2d(dcos, ct, (size_t)max_seq * half * 4) | qhip_h2d(dsin, st, (size_t)max_seq * half * 4);
+  free(ct); free(st);
+  return rc;
+}
+
+static FDev *fdev_upload(const LlamaModel *m) {
+  const int32_t cfg[8] = {m->vocab, m->d_model, m->n_layers, m->n_heads, m->n_kv, m->head_dim, m->d_ff, m->max_seq};
+  if (!config_valid(cfg) || !config_supported(cfg) || m->d_model > qhip_gemv_f32_max_k() ||
+      m->n_heads * m->head_dim > qhip_gemv_f32_max_k() || m->d_ff > qhip_gemv_f32_max_k()) {
+    fprintf(stderr, "Error: llama_kv_create: config not supported by the GPU fp32 path\n");
+    return NULL;
+  }
+  if (qhip_init() != 0) { fprintf(stderr, "Error: no usable GPU: %s\n", qhip_last_error()); return NULL; }
+  int slot = -1;
+  for (int i = 0; i < FDEV_MAX && slot < 0; i++) if (!g_fdev[i]) slot = i;
+  if (slot < 0) { fprintf(stderr, "Error: llama_kv_create: too many fp32 models on the GPU\n"); return NULL; }
+  FDev *f = (FDev*)calloc(1, sizeof(FDev));
+  if (!f) return NULL;
+  f->key_wte = m->wte.data; f->key_blocks = m->blocks;
+  f->vocab = m->vocab; f->dm = m->d_model; f->L = m->n_layers; f->H = m->n_heads; f->KVH = m->n_kv;
+  f->hd = m->head_dim; f->dff = m->d_ff; f->max_seq = m->max_seq; f->eps = m->eps;
+  f->qd = f->H * f->hd; f->kvd = f->KVH * f->hd; f->nqkv = f->qd + 2 * f->kvd;
+  f->attn_scale = 1.0f / sqrtf((float)f->hd);                      // llama.c:301
+  const int L = f->L;
+  const size_t dm = (size_t)f->dm, qd = (size_t)f->qd, kvd = (size_t)f->kvd, nqkv = (size_t)f->nqkv;
+  const size_t dff = (size_t)f->dff, V = (size_t)f->vocab;
+  f->wqkv = calloc(L, sizeof(float*)); f->bqkv = calloc(L, sizeof(float*)); f->wo = calloc(L, sizeof(float*));
+  f->wgu = calloc(L, sizeof(float*)); f->wd = calloc(L, sizeof(float*)); f->g_attn = calloc(L, sizeof(float*));
+  f->g_ffn = calloc(L, sizeof(float*));
+  if (!f->wqkv || !f->bqkv || !f->wo || !f->wgu || !f->wd || !f->g_attn || !f->g_ffn) { fdev_free(f); return NULL; }
+  size_t off = 0, *lo = (size_t*)calloc((size_t)L * 7, sizeof(size_t));
+  if (!lo) { fdev_free(f); return NULL; }
+#define FTAKE(n) (off += al256((n) * 4), off - al256((n) * 4))
+#define PAN(K, N) qhip_panels_f32_size((int)(K), (int)(N))
+  for (int l = 0; l < L; l++) {
+    lo[l * 7 + 0] = FTAKE(PAN(dm, nqkv)); lo[l * 7 + 1] = FTAKE(nqkv); lo[l * 7 + 2] = FTAKE(PAN(qd, dm));
+    lo[l * 7 + 3] = FTAKE(PAN(dm, 2 * dff)); lo[l * 7 + 4] = FTAKE(PAN(dff, dm));
+    lo[l * 7 + 5] = FTAKE(dm); lo[l * 7 + 6] = FTAKE(dm);
+  }
+  const size_t o_wte = FTAKE(V * dm), o_head = FTAKE(PAN(dm, V)), o_gf = FTAKE(dm);
+#undef PAN
+  const size_t o_cos = FTAKE((size_t)f->max_seq * (f->hd / 2)), o_sin = FTAKE((size_t)f->max_seq * (f->hd / 2));
+  const size_t o_x = FTAKE(dm), o_xn = FTAKE(dm), o_qkv = FTAKE(nqkv), o_o = FTAKE(qd), o_gu = FTAKE(2 * dff);
+  const size_t o_h = FTAKE(dff), o_lg = FTAKE(V), o_sc = FTAKE(qhip_attention_scratch(f->H, f->max_seq));
+  const size_t o_st = FTAKE(16), o_in = FTAKE((size_t)f->max_seq + 1);
+#undef FTAKE
+  size_t big = dm * V;                                   // row-major staging of the largest matrix
+  if (dm * 2 * dff > big) big = dm * 2 * dff;
+  if (dm * nqkv > big) big = dm * nqkv;
+  if (qd * dm > big) big = qd * dm;
+  f->blob = (uint8_t*)qhip_malloc(off);
+  f->h_stage = (int*)qhip_host_alloc(64);
+  float *tmp = (float*)qhip_malloc(big * 4);
+  size_t big2 = dm * (qd > dff ? qd : dff);                // one part of a joined matrix
+  float *tmp2 = (float*)qhip_malloc(big2 * 4);
+  if (!f->blob || !f->h_stage || !tmp || !tmp2) {
+    fprintf(stderr, "Error: device allocation of %zu bytes failed: %s\n", off, qhip_last_error());
+    qhip_free(tmp); qhip_free(tmp2); free(lo); fdev_free(f); return NULL;
+  }
+  uint8_t *b = f->blob;
+  for (int l = 0; l < L; l++) {
+    f->wqkv[l] = (float*)(b + lo[l * 7 + 0]); f->bqkv[l] = (float*)(b + lo[l * 7 + 1]);
+    f->wo[l] = (float*)(b + lo[l * 7 + 2]); f->wgu[l] = (float*)(b + lo[l * 7 + 3]);
+    f->wd[l] = (float*)(b + lo[l * 7 + 4]); f->g_attn[l] = (float*)(b + lo[l * 7 + 5]);
+    f->g_ffn[l] = (float*)(b + lo[l * 7 + 6]);
+  }
+  free(lo);
+  f->wte = (float*)(b + o_wte); f->head = (float*)(b + o_head); f->g_final = (float*)(b + o_gf);
+  f->rope_cos = (float*)(b + o_cos); f->rope_sin = (float*)(b + o_sin);
+  f->x = (float*)(b + o_x); f->xn = (float*)(b + o_xn); f->qkv = (float*)(b + o_qkv); f->o = (float*)(b + o_o);
+  f->gu = (float*)(b + o_gu); f->h = (float*)(b + o_h); f->logits = (float*)(b + o_lg);
+  f->scores = (float*)(b + o_sc); f->d_state = (int*)(b + o_st); f->d_in = (int*)(b + o_in);
+  int rc = qhip_upload_begin((size_t)32 << 20);
+  // every matrix is staged row-major in tmp, then rewritten in the GEMV's panel
+  // layout; two matrices (K, n1), (K, n2) are first joined column-wise in tmp
+#define PART(src, K, ld, coloff, n) \
+  (qhip_upload((float*)tmp2, (src)->data, (size_t)(K) * (n) * 4) || \
+   qhip_copy2d_d2d(tmp + (coloff), (ld) * 4, tmp2, (n) * 4, (n) * 4, (K)))
+  rc = rc || qhip_upload(f->wte, m->wte.data, V * dm * 4) || qhip_upload(f->g_final, m->final_norm.data, dm * 4) ||
+       qhip_upload(tmp, m->lm_head.data, dm * V * 4) || qhip_to_panels_f32(tmp, (int)dm, (int)V, f->head);
+  for (int l = 0; l < L && !rc; l++) {
+    const LlamaBlock *a = &m->blocks[l];
+    rc = PART(&a->Wq, dm, nqkv, 0, qd) || PART(&a->Wk, dm, nqkv, qd, kvd) || PART(&a->Wv, dm, nqkv, qd + kvd, kvd) ||
+         qhip_to_panels_f32(tmp, (int)dm, (int)nqkv, f->wqkv[l]) ||
+         PART(&a->Wgate, dm, 2 * dff, 0, dff) || PART(&a->Wup, dm, 2 * dff, dff, dff) ||
+         qhip_to_panels_f32(tmp, (int)dm, (int)(2 * dff), f->wgu[l]) ||
+         qhip_upload(tmp, a->Wo.data, qd * dm * 4) || qhip_to_panels_f32(tmp, (int)qd, (int)dm, f->wo[l]) ||
+         qhip_upload(tmp, a->Wdown.data, dff * dm * 4) || qhip_to_panels_f32(tmp, (int)dff, (int)dm, f->wd[l]) ||
+         qhip_upload(f->bqkv[l], a->b_q.data, qd * 4) || qhip_upload(f->bqkv[l] + qd, a->b_k.data, kvd * 4) ||
+         qhip_upload(f->bqkv[l] + qd + kvd, a->b_v.data, kvd * 4) ||
+         qhip_upload(f->g_attn[l], a->attn_norm.data, dm * 4) || qhip_upload(f->g_ffn[l], a->ffn_norm.data, dm * 4);
+  }
+#undef PART
+  if (qhip_upload_end()) rc = 1;
+  qhip_free(tmp); qhip_free(tmp2);
+  if (!rc) rc = rope_upload(f->rope_cos, f->rope_sin, f->max_seq, f->hd, m->rope_base) ||
+                qhip_fill_zero(f->d_in, ((size_t)f->max_seq + 1) * 4) || qhip_fill_zero(f->d_state, 64) ||
+                qhip_sync();
+  if (rc) {
+    fprintf(stderr, "Error: upload of the fp32 model failed: %s\n", qhip_last_error());
+    fdev_free(f); return NULL;
+  }
+  g_fdev[slot] = f;
+  return f;
+}
+
+// llama.c:296-362 for the token at d_in[d_state[0]]
+static int enqueue_step_f32(const FDev *f, const KVDev *kd) {
+  const size_t per = (size_t)f->max_seq * f->kvd;
+  int rc = qhip_embed_f32(f->wte, f->dm, f->d_in, f->d_state, f->x);
+  for (int l = 0; l < f->L && !rc; l++) {
+    float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
+    rc |= qhip_rmsnorm_f32(f->x, f->dm, f->g_attn[l], f->eps, f->xn);
+    rc |= qhip_gemv_f32(0, 2, f->xn, f->dm, f->wqkv[l], f->nqkv, f->qkv, f->bqkv[l]);
+    rc |= qhip_attention_rope(f->qkv, kc, vc, f->d_state, f->H, f->KVH, f->hd, f->max_seq, f->attn_scale,
+                              f->rope_cos, f->rope_sin, f->scores, f->o, NULL);
+    rc |= qhip_gemv_f32(1, 6, f->o, f->qd, f->wo[l], f->dm, f->x, NULL);
+    rc |= qhip_rmsnorm_f32(f->x, f->dm, f->g_ffn[l], f->eps, f->xn);
+    rc |= qhip_gemv_f32(0, 7, f->xn, f->dm, f->wgu[l], 2 * f->dff, f->gu, NULL);
+    rc |= qhip_swiglu_f32(f->gu, f->dff, f->h);
+    rc |= qhip_gemv_f32(1, 9, f->h, f->dff, f->wd[l], f->dm, f->x, NULL);
+  }
+  if (!rc) rc |= qhip_rmsnorm_f32(f->x, f->dm, f->g_final, f->eps, f->xn);
+  if (!rc) rc |= qhip_gemv_f32(0, 10, f->xn, f->dm, f->head, f->vocab, f->logits, NULL);
+  return rc;
+}
+
+// llama.c:275-288: a device cache; the model's device copy is made (or shared)
+LlamaKV llama_kv_create(const LlamaModel *m) {
+  LlamaKV kv;
+  memset(&kv, 0, sizeof kv);
+  FDev *f = fdev_find(m);
+  if (!f) f = fdev_upload(m);
+  if (!f) abort();
+  KVDev *kd = (KVDev*)calloc(1, sizeof(KVDev));
+  kv.n_layers = m->n_layers; kv.max_seq = m->max_seq; kv.kv_dim = m->n_kv * m->head_dim; kv.len = 0;
+  kv.k = (float**)malloc((size_t)m->n_layers * sizeof(float*));
+  kv.v = (float**)malloc((size_t)m->n_layers * sizeof(float*));
+  const size_t per = (size_t)m->max_seq * kv.kv_dim;
+  if (!kd || !kv.k || !kv.v) { fprintf(stderr, "Error: out of memory (kv)\n"); abort(); }
+  kd->kbase = (float*)qhip_malloc((size_t)m->n_layers * per * 4);
+  kd->vbase = (float*)qhip_malloc((size_t)m->n_layers * per * 4);
+  if (!kd->kbase || !kd->vbase) die("llama_kv_create");
+  for (int l = 0; l < m->n_layers; l++) { kv.k[l] = kd->kbase + (size_t)l * per; kv.v[l] = kd->vbase + (size_t)l * per; }
+  kd->fdev = f;
+  f->refs++;
+  kv.dev = kd;
+  return kv;
+}
+
+// llama.c:296-362 on the GPU; logits (1, vocab) in host memory.
+void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logits) {
+  KVDev *kd = kv ? (KVDev*)kv->dev : NULL;
+  FDev *f = kd ? kd->fdev : NULL;
+  if (!m || !f || f != fdev_find(m)) {
+    fprintf(stderr, "Error: llama_decode_step: the cache was not made by llama_kv_create for this model\n");
+    abort();
+  }
+  if (kv->len < 0 || kv->len >= f->max_seq || token < 0 || token >= f->vocab) {
+    fprintf(stderr, "Error: llama_decode_step: position %d / token %d out of range\n", kv->len, token);
+    abort();
+  }
+  int *h = f->h_stage;
+  h[0] = kv->len; h[1] = kv->len + 1; h[2] = token;
+  int rc = qhip_h2d_async(f->d_state, h, 2 * sizeof(int)) || qhip_h2d_async(f->d_in + kv->len, h + 2, sizeof(int));
+  if (!rc) {
+    if (profiling || getenv("QLLAMA_NO_GRAPH")) {
+      rc = enqueue_step_f32(f, kd);
+    } else {
+      if (!kd->graph || kd->graph_owner != (const void*)f) {
+        if (kd->graph) { qhip_graph_destroy(kd->graph); kd->graph = NULL; }
+        void *g = NULL;
+        rc = qhip_capture_begin();
+        if (!rc) {
+          const int e = enqueue_step_f32(f, kd);
+          rc = qhip_capture_end(&g) || e;
+        }
+        if (!rc) { kd->graph = g; kd->graph_owner = f; }
+      }
+      if (!rc) rc = qhip_graph_launch(kd->graph);
+    }
+  }
+  if (rc || qhip_d2h_async(logits->data, f->logits, (size_t)f->vocab * 4) || qhip_sync()) die("llama_decode_step");
+  kv->len += 1;
 }
 
 // ---------------------------------------------------------------------------

@@ -97,6 +97,9 @@ def lib():
         L.qacc_columns.argtypes = [P(C.c_int8), P(C.c_int8), C.c_int, C.c_int, P(C.c_int32)]
         L.q_llama_model_save.argtypes = [P(QLlamaModel), C.c_char_p]
         L.q_llama_tensor_export.argtypes = [P(QTensor), P(C.c_int8), P(C.c_float)]
+        L.llama_kv_create.argtypes = [P(LlamaModel)]
+        L.llama_kv_create.restype = LlamaKV
+        L.llama_decode_step.argtypes = [P(LlamaModel), P(LlamaKV), C.c_int, P(Tensor)]
         L.rng_create.argtypes = [C.c_ulonglong]
         L.rng_create.restype = Rng
         L.rng_uniform.argtypes = [P(Rng)]
@@ -201,6 +204,73 @@ class Model:
             lib().llama_kv_free(C.byref(self.kv))
             lib().q_llama_model_free(C.byref(self.m))
             self.m.dev = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- fp32 (LLMA) path -----------------------------------------------------------
+def host_model(cfg, rope_base, eps, tensors):
+    """A reference LlamaModel (host memory) over float32 arrays given in the
+    canonical order of llama.c:198-219 as (name, array) pairs; the arrays are
+    kept alive by the returned object."""
+    keep = []
+
+    def T(a):
+        a = np.ascontiguousarray(a, np.float32)
+        keep.append(a)
+        t = host_tensor(a)
+        keep.append(t._keep)
+        return t
+
+    m = LlamaModel()
+    (m.vocab, m.d_model, m.n_layers, m.n_heads, m.n_kv, m.head_dim, m.d_ff, m.max_seq) = cfg
+    m.rope_base, m.eps = rope_base, eps
+    it = iter(tensors)
+    m.wte = T(next(it)[1])
+    blocks = (LlamaBlock * cfg[2])()
+    for l in range(cfg[2]):
+        b = blocks[l]
+        b.d_model, b.n_heads, b.n_kv, b.head_dim, b.d_ff = cfg[1], cfg[3], cfg[4], cfg[5], cfg[6]
+        b.rope_base, b.eps = rope_base, eps
+        for name in ("attn_norm", "Wq", "Wk", "Wv", "b_q", "b_k", "b_v", "Wo", "ffn_norm", "Wgate", "Wup", "Wdown"):
+            n, a = next(it)
+            assert n == name, (n, name)
+            setattr(b, name, T(a))
+    m.blocks = blocks
+    m.final_norm = T(next(it)[1])
+    m.lm_head = T(next(it)[1])
+    m._keep = (keep, blocks)
+    return m
+
+
+class FModel:
+    """fp32 decode on the GPU (llama_kv_create / llama_decode_step) of a host LlamaModel."""
+
+    def __init__(self, host):
+        self.m = host
+        self.kv = lib().llama_kv_create(C.byref(self.m))
+        self.logits = np.zeros((1, host.vocab), np.float32)
+        self._lt = host_tensor(self.logits)
+
+    @property
+    def pos(self):
+        return self.kv.len
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def step(self, token):
+        lib().llama_decode_step(C.byref(self.m), C.byref(self.kv), int(token), C.byref(self._lt))
+        return self.logits[0]
+
+    def close(self):
+        if self.kv.dev:
+            lib().llama_kv_free(C.byref(self.kv))
+            self.kv.dev = None
 
     def __del__(self):
         try:

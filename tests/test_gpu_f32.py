@@ -1,0 +1,105 @@
+"""GPU fp32 (LLMA) decode path through the C ABI (llama_kv_create /
+llama_decode_step) against the fixtures the compiled reference wrote
+(gen_golden e2e_f32) and against the oracle's k-order matmul.  Bar: token
+streams and logits bit-exact (north-star tolerance reported too)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import qlib
+from conftest import golden, golden_json
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def Q():
+    q = qlib.load()
+    assert q.lib().qllama_device_count() > 0, "no GPU visible to the HIP library"
+    return q
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def gpu_model(Q, ref, cfg, base):
+    return Q.FModel(Q.host_model(cfg, base, 1e-5, ref.tensors()))
+
+
+@pytest.mark.parametrize("name", ["tiny", "mid"])
+def test_f32_decode_matches_reference(Q, name):
+    meta = golden_json(f"e2e_f32_{name}")
+    ref = O.FModel(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    try:
+        assert ref.hash() == int(meta["model_hash"], 16)
+        g = gpu_model(Q, ref, meta["cfg"], meta["rope_base"])
+        try:
+            hashes = [int(h, 16) for h in meta["logit_hashes"]]
+            P = len(meta["prompt"])
+            for i, t in enumerate(meta["prompt"]):
+                log(f"{name} prompt step {i}")
+                lg = g.step(t)
+                assert O.hash_f32(lg) == hashes[i], i
+            np.testing.assert_allclose(lg, golden(f"e2e_f32_{name}_logits_prompt_last"), atol=1e-3, rtol=1e-4)
+            assert np.array_equal(bits(lg), bits(golden(f"e2e_f32_{name}_logits_prompt_last")))
+            for s, t in enumerate(meta["gen"]):
+                assert int(np.argmax(lg)) == t, s
+                lg = g.step(t)
+                assert O.hash_f32(lg) == hashes[P + s], P + s
+            assert np.array_equal(bits(lg), bits(golden(f"e2e_f32_{name}_logits_final")))
+        finally:
+            g.close()
+    finally:
+        ref.close()
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 1024), (300, 17), (1000, 130), (129, 16)])
+def test_f32_gemv_rows_match_oracle(Q, shape):
+    """The fp32 GEMV at (K, N) through a one-layer model whose down projection
+    has K inputs and whose head has N outputs: every step's logits bit for bit
+    against the oracle (k-order chains over partial tiles, partial column
+    blocks, the 14336-input down projection of the 8B shape)."""
+    K, N = shape
+    dm = 16 * ((K + 15) // 16) if K % 16 else K
+    cfg = [N if N >= 16 else 16, min(dm, 4096), 1, 4, 2, 32, max(K, 64), 32]
+    ref = O.FModel(cfg, 10000.0, seed=7)
+    try:
+        g = gpu_model(Q, ref, cfg, 10000.0)
+        try:
+            for t in [1, 5, 2, 9]:
+                r = ref.step(t % cfg[0]).copy()
+                o = g.step(t % cfg[0]).copy()
+                assert np.array_equal(bits(o), bits(r)), shape
+        finally:
+            g.close()
+    finally:
+        ref.close()
+
+
+def test_two_caches_share_one_device_copy(Q):
+    meta = golden_json("e2e_f32_tiny")
+    ref = O.FModel(meta["cfg"], meta["rope_base"], seed=meta["seed"])
+    try:
+        host = Q.host_model(meta["cfg"], meta["rope_base"], 1e-5, ref.tensors())
+        a, b = Q.FModel(host), Q.FModel(host)
+        try:
+            la = [a.step(t).copy() for t in meta["prompt"][:6]]
+            a.close()                                    # b keeps the device copy alive
+            lb = [b.step(t).copy() for t in meta["prompt"][:6]]
+            for x, y in zip(la, lb):
+                assert np.array_equal(bits(x), bits(y))
+            b.reset(0)
+            assert np.array_equal(bits(b.step(meta["prompt"][0])), bits(la[0]))
+        finally:
+            a.close()
+            b.close()
+    finally:
+        ref.close()
