@@ -7,9 +7,9 @@
 #             which brings LlamaKV with its device handle, QTensor, QLlamaModel
 #             and the quantized prototypes; the old quantized section
 #             (llama.h:108-140) and #include "quant.h" (llama.h:17) go away
-#   llama.c   the quantized section (llama.c:447-657) and llama_kv_free
-#             (llama.c:290-294, which the library also serves for fp32 caches)
-#             go away; llama_kv_create zeroes the new device handle
+#   llama.c   the quantized section (llama.c:447-657) and the fp32 cache and
+#             decode step (llama_kv_create, llama_kv_free, llama_decode_step,
+#             llama.c:275-362) go away: the library serves both paths on the GPU
 #   matrix.c  qacc_columns (matrix.c:370-374) goes away (the library exports it)
 #   quant.c   is not compiled (the library exports its functions)
 # and links -lqllama.  With GPU_SAMPLER=1 in the environment sampler.c is not
@@ -38,15 +38,17 @@ check llama.h 94 'typedef struct {'
 check llama.h 99 '} LlamaKV;'
 check llama.h 114 'typedef struct {'
 check llama.h 140 'LlamaKV q_llama_kv_create(const QLlamaModel *m);'
-check llama.c 276 'LlamaKV kv;'
+check llama.c 275 'LlamaKV llama_kv_create(const LlamaModel *m) {'
 check llama.c 290 'void llama_kv_free(LlamaKV *kv) {'
+check llama.c 296 'void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logits) {'
+check llama.c 362 '}'
 check llama.c 447 'static QLlamaBlock q_block_create('
 check matrix.c 370 'void qacc_columns('
 
 # edits from the bottom up so the earlier line numbers stay valid
 sed -i '108,140d; 94,99c #include "qllama.h"' "$DEST/llama.h"
 sed -i '17d' "$DEST/llama.h"
-sed -i '447,657d; 290,294d; 276a\  kv.dev = NULL;' "$DEST/llama.c"
+sed -i '447,657d; 275,362d' "$DEST/llama.c"
 sed -i '370,374d' "$DEST/matrix.c"
 
 DROP='s/quant\.o//'

@@ -1,5 +1,5 @@
-// qllama_cli.c - the reference's `transformer llama` command for int8 LLMQ
-// checkpoints (main.c:624-671), running on the MI355X library.
+// qllama_cli.c - the reference's `transformer llama` command for LLMQ (int8) and
+// LLMA (f32) checkpoints (main.c:624-702), running on the MI355X library.
 //
 //   qllama-cli llama <checkpoint.bin> [n_new=40]
 //
@@ -12,8 +12,10 @@
 // ends with "gen: <prompt and generated ids>".  The prompt goes through
 // q_llama_prefill (equal to the reference's per-token q_llama_decode_step
 // calls) and each token through q_llama_generate (sampling and the next decode
-// step on the device).  'LLMA' f32 checkpoints and the tokenizer text mode are
-// not part of this build: they are reported and refused.
+// step on the device).  'LLMA' (f32) checkpoints take the command's f32 branch
+// (main.c:686-700): the file is read into a host LlamaModel, and
+// llama_kv_create / llama_decode_step / sample_token run on the GPU.  The
+// tokenizer text mode is not part of this build: it is reported and refused.
 #define _POSIX_C_SOURCE 200809L
 #include <stdint.h>
 #include <stdio.h>
@@ -43,10 +45,126 @@ static void print_gen(const int *seq, int n) {
   fflush(stdout);
 }
 
+// ---- the f32 branch -------------------------------------------------------------
+static Tensor host_tensor(int r, int c) {   // (r, c), or (r) when c == 0; zero-filled
+  Tensor t;
+  const size_t n = (size_t)r * (c ? c : 1);
+  t.data = (float*)calloc(n, sizeof(float));
+  t.grad = NULL;
+  t.ndim = c ? 2 : 1;
+  t.shape = (int*)malloc(2 * sizeof(int));
+  if (!t.data || !t.shape) { fprintf(stderr, "Error: out of memory\n"); exit(EXIT_FAILURE); }
+  t.shape[0] = r; t.shape[1] = c;
+  t.size = n;
+  return t;
+}
+
+static void free_tensor(Tensor *t) { free(t->data); free(t->shape); t->data = NULL; t->shape = NULL; }
+
+static void free_model(LlamaModel *m) {
+  free_tensor(&m->wte); free_tensor(&m->final_norm); free_tensor(&m->lm_head);
+  for (int l = 0; l < m->n_layers && m->blocks; l++) {
+    LlamaBlock *b = &m->blocks[l];
+    Tensor *t[12] = {&b->attn_norm, &b->Wq, &b->Wk, &b->Wv, &b->b_q, &b->b_k, &b->b_v, &b->Wo,
+                     &b->ffn_norm, &b->Wgate, &b->Wup, &b->Wdown};
+    for (int i = 0; i < 12; i++) free_tensor(t[i]);
+  }
+  free(m->blocks); m->blocks = NULL;
+}
+
+// An 'LLMA' v2 file into a host LlamaModel: header, config, then every tensor's
+// f32 values in the canonical order (llama.c:198-219, 388-437).
+static int load_llma(const char *path, LlamaModel *m) {
+  FILE *f = fopen(path, "rb");
+  if (!f) { fprintf(stderr, "Error: cannot open '%s' for reading\n", path); return 1; }
+  uint32_t header[2];
+  int32_t c[8];
+  float fc[2];
+  if (fread(header, 4, 2, f) != 2 || fread(c, 4, 8, f) != 8 || fread(fc, 4, 2, f) != 2) {
+    fprintf(stderr, "Error: '%s' is truncated (bad header)\n", path);
+    fclose(f); return 1;
+  }
+  if (header[0] != 0x414D4C4Cu || header[1] != 2u) {
+    fprintf(stderr, "Error: '%s' is not a v2 LLMA checkpoint\n", path);
+    fclose(f); return 1;
+  }
+  for (int i = 0; i < 8; i++)
+    if (c[i] <= 0 || c[i] > 1000000 || (i == 4 && c[3] % c[4])) {
+      fprintf(stderr, "Error: '%s' has an invalid/unsupported config\n", path);
+      fclose(f); return 1;
+    }
+  memset(m, 0, sizeof *m);
+  m->vocab = c[0]; m->d_model = c[1]; m->n_layers = c[2]; m->n_heads = c[3]; m->n_kv = c[4];
+  m->head_dim = c[5]; m->d_ff = c[6]; m->max_seq = c[7]; m->rope_base = fc[0]; m->eps = fc[1];
+  const int dm = c[1], qd = c[3] * c[5], kvd = c[4] * c[5], ff = c[6];
+  m->wte = host_tensor(c[0], dm);
+  m->blocks = (LlamaBlock*)calloc((size_t)c[2], sizeof(LlamaBlock));
+  if (!m->blocks) { fclose(f); return 1; }
+  int ok = fread(m->wte.data, 4, m->wte.size, f) == m->wte.size;
+  for (int l = 0; l < c[2]; l++) {
+    LlamaBlock *b = &m->blocks[l];
+    b->d_model = dm; b->n_heads = c[3]; b->n_kv = c[4]; b->head_dim = c[5]; b->d_ff = ff;
+    b->rope_base = fc[0]; b->eps = fc[1];
+    b->attn_norm = host_tensor(dm, 0); b->Wq = host_tensor(dm, qd); b->Wk = host_tensor(dm, kvd);
+    b->Wv = host_tensor(dm, kvd); b->b_q = host_tensor(qd, 0); b->b_k = host_tensor(kvd, 0);
+    b->b_v = host_tensor(kvd, 0); b->Wo = host_tensor(qd, dm); b->ffn_norm = host_tensor(dm, 0);
+    b->Wgate = host_tensor(dm, ff); b->Wup = host_tensor(dm, ff); b->Wdown = host_tensor(ff, dm);
+    Tensor *t[12] = {&b->attn_norm, &b->Wq, &b->Wk, &b->Wv, &b->b_q, &b->b_k, &b->b_v, &b->Wo,
+                     &b->ffn_norm, &b->Wgate, &b->Wup, &b->Wdown};
+    for (int i = 0; i < 12 && ok; i++) ok = fread(t[i]->data, 4, t[i]->size, f) == t[i]->size;
+  }
+  m->final_norm = host_tensor(dm, 0);
+  m->lm_head = host_tensor(dm, c[0]);
+  if (ok) ok = fread(m->final_norm.data, 4, m->final_norm.size, f) == m->final_norm.size &&
+               fread(m->lm_head.data, 4, m->lm_head.size, f) == m->lm_head.size;
+  fclose(f);
+  if (!ok) {
+    fprintf(stderr, "Error: '%s' is truncated (bad weights)\n", path);
+    free_model(m);
+    return 1;
+  }
+  return 0;
+}
+
+static int run_llama_f32(const char *path, int n_new) {
+  const float temperature = 0.8f;   // main.c:641-644
+  const int top_k = 40;
+  const float top_p = 0.95f;
+  Rng rng = rng_create(1234);
+  char line[8192];
+  LlamaModel m;
+  if (load_llma(path, &m) != 0) return 1;
+  fprintf(stderr, "loaded LLMA (f32, MI355X): vocab %d d_model %d layers %d heads %d kv %d head_dim %d d_ff %d\n",
+          m.vocab, m.d_model, m.n_layers, m.n_heads, m.n_kv, m.head_dim, m.d_ff);
+  LlamaKV kv = llama_kv_create(&m);
+  Tensor logits = host_tensor(1, m.vocab);
+  int *seq = (int*)malloc((size_t)m.max_seq * sizeof(int));
+  if (!seq) { fprintf(stderr, "Error: out of memory\n"); return 1; }
+  while (fgets(line, sizeof(line), stdin)) {
+    int n = parse_ids(line, seq, m.vocab, m.max_seq);
+    if (n == 0) continue;
+    kv.len = 0;
+    for (int i = 0; i < n; i++) llama_decode_step(&m, &kv, seq[i], &logits);
+    for (int s = 0; s < n_new && n < m.max_seq; s++) {
+      int nxt = sample_token(&logits, 0, temperature, top_k, top_p, &rng);
+      seq[n++] = nxt;
+      printf("t %d\n", nxt);
+      fflush(stdout);
+      llama_decode_step(&m, &kv, nxt, &logits);
+    }
+    print_gen(seq, n);
+  }
+  free(seq);
+  free_tensor(&logits);
+  llama_kv_free(&kv);
+  free_model(&m);
+  return 0;
+}
+
 static int run_llama(int argc, char **argv) {
   if (argc < 3) {
     fprintf(stderr, "usage: qllama-cli llama <checkpoint.bin> [n_new=40]\n"
-                    "  LLMQ (int8) checkpoint, run on the GPU;\n"
+                    "  LLMQ (int8) or LLMA (f32) checkpoint, run on the GPU;\n"
                     "  reads space-separated token IDs per stdin line; prints 't <id>' per token and 'gen: <ids>'\n");
     return 2;
   }
@@ -64,9 +182,9 @@ static int run_llama(int argc, char **argv) {
     return 1;
   }
   fclose(pf);
+  if (magic == 0x414D4C4Cu) return run_llama_f32(argv[2], n_new);   // 'LLMA'
   if (magic != 0x514D4C4Cu) {   // 'LLMQ'
-    fprintf(stderr, "Error: '%s' is not an LLMQ (int8) checkpoint; f32 LLMA checkpoints are not supported\n",
-            argv[2]);
+    fprintf(stderr, "Error: '%s' is not an LLMA or LLMQ checkpoint\n", argv[2]);
     return 1;
   }
 

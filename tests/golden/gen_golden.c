@@ -536,6 +536,38 @@ static void run_e2e_f32(const E2EF *e) {
   free(seq); free(lh); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
 }
 
+// The LLMA branch of the `llama` command (main.c:686-700) on the tiny fp32 model:
+// a generator of its own (rng_create(1234)), per line kv.len = 0, the prompt
+// through llama_decode_step, n_new sampled tokens.
+static void fx_cli_f32(FILE *js) {
+  LlamaModel m;
+  build_fmodel(&m, &FCASES[0], 1234);
+  LlamaKV kv = llama_kv_create(&m);
+  Tensor logits = mat(1, m.vocab);
+  Rng rng = rng_create(1234);
+  const int lens[2] = {20, 7}, n_new = 40;
+  int *seq = malloc(sizeof(int) * (size_t)m.max_seq);
+  fprintf(js, "  \"cli_f32\": {\"model\": \"tiny\", \"seed\": 1234, \"n_new\": %d, \"lines\": [\n", n_new);
+  for (int li = 0; li < 2; li++) {
+    int n = lens[li];
+    syn_prompt(seq, n, 4321 + li, m.vocab);
+    fprintf(js, "%s    {\"prompt\": [", li ? ",\n" : "");
+    for (int i = 0; i < n; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+    kv.len = 0;
+    for (int i = 0; i < n; i++) llama_decode_step(&m, &kv, seq[i], &logits);
+    fprintf(js, "], \"gen\": [");
+    for (int s = 0; s < n_new && n < m.max_seq; s++) {
+      int nxt = sample_token(&logits, 0, 0.8f, 40, 0.95f, &rng);
+      seq[n++] = nxt;
+      fprintf(js, "%s%d", s ? "," : "", nxt);
+      llama_decode_step(&m, &kv, nxt, &logits);
+    }
+    fprintf(js, "]}");
+  }
+  fprintf(js, "\n  ]},\n");
+  free(seq); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
+}
+
 int main(int argc, char **argv) {
   if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|sample|e2e <name>\n"); return 2; }
   OUT = argv[1];
@@ -573,6 +605,7 @@ int main(int argc, char **argv) {
     fprintf(js, "{\n");
     fx_sample(js);
     fx_cli(js);
+    fx_cli_f32(js);
     fprintf(js, "  \"done\": true\n}\n");
     fclose(js);
     return 0;

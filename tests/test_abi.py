@@ -137,7 +137,15 @@ def test_cli_usage_and_refusals(tmp_path):
     tiny.write_bytes(b"LL")
     r = subprocess.run([CLI, "llama", str(tiny)], capture_output=True, text=True)
     assert r.returncode == 1 and "too small" in r.stderr
+    other = tmp_path / "other.bin"
+    _write(other, (0x12345678, 2), GOOD_CFG, (10000.0, 1e-5))
+    r = subprocess.run([CLI, "llama", str(other)], capture_output=True, text=True)
+    assert r.returncode == 1 and "not an LLMA or LLMQ" in r.stderr
+    # the f32 branch checks the file before any device work (llama.c:388-437 messages)
     llma = tmp_path / "f32.bin"
     _write(llma, (0x414D4C4C, 2), GOOD_CFG, (10000.0, 1e-5))
     r = subprocess.run([CLI, "llama", str(llma)], capture_output=True, text=True)
-    assert r.returncode == 1 and "not an LLMQ" in r.stderr
+    assert r.returncode == 1 and "is truncated (bad weights)" in r.stderr
+    _write(llma, (0x414D4C4C, 3), GOOD_CFG, (10000.0, 1e-5))
+    r = subprocess.run([CLI, "llama", str(llma)], capture_output=True, text=True)
+    assert r.returncode == 1 and "is not a v2 LLMA" in r.stderr

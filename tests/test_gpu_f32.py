@@ -103,3 +103,30 @@ def test_two_caches_share_one_device_copy(Q):
             b.close()
     finally:
         ref.close()
+
+
+def test_cli_f32_branch_matches_reference(Q, tmp_path):
+    """qllama-cli on an LLMA file: the `llama` command's f32 branch (main.c:686-700)
+    with decode and sampling on the GPU, against the compiled reference's loop."""
+    import os
+    import subprocess
+    from conftest import ROOT
+    cli = os.path.join(ROOT, "llm-project_amd", "qllama-cli")
+    S = golden_json("sample")["cli_f32"]
+    meta = golden_json("e2e_f32_tiny")
+    ref = O.FModel(meta["cfg"], meta["rope_base"], seed=S["seed"])
+    try:
+        path = str(tmp_path / "tiny.llma")
+        ref.write_llma(path)
+    finally:
+        ref.close()
+    stdin = "".join(" ".join(str(t) for t in ln["prompt"]) + "\n" for ln in S["lines"])
+    expect = []
+    for ln in S["lines"]:
+        expect += [f"t {t}" for t in ln["gen"]]
+        expect.append("gen: " + " ".join(str(t) for t in ln["prompt"] + ln["gen"]))
+    log("running qllama-cli on an LLMA file")
+    out = subprocess.run([cli, "llama", path, str(S["n_new"])], input=stdin.encode(), capture_output=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr.decode()
+    assert out.stdout.decode().splitlines() == expect
