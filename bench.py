@@ -8,8 +8,12 @@ decode steps.  A "step" is one decode token through the whole model.  Everything
 the timed region touches is already resident in HBM.
 
 Prints one JSON line (rank 0) with decode tok/s, the dominant kernel's roofline
-(the W8A8 GEMV, timed with HIP events on the library's stream) and the CPU
+(the W8A8 GEMV, timed with HIP events on the library's stream), prefill tok/s
+with the MFMA GEMMs' roofline, decode with on-device sampling, and the CPU
 oracle timed on this host's cores on the same weights.
+
+`--path f32` measures the fp32 (LLMA) decode path instead (llama_decode_step on
+a host LlamaModel of numpy N(0, 0.02) weights), with the f32 GEMV's roofline.
 """
 import argparse
 import ctypes as C
