@@ -237,6 +237,9 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (the scale reference "
                          "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--load-check", action="store_true",
+                    help="also time q_llama_model_save and q_llama_model_load of the model through $TMPDIR "
+                         "(writes a checkpoint of the model's size there)")
     ap.add_argument("--path", default="int8", choices=["int8", "f32"],
                     help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
     args = ap.parse_args()
@@ -341,6 +344,29 @@ def main():
                        "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4), "gemm_ms": round(g_ms, 3),
                        "attention_ms": round(a_ms, 3) if a_ms is not None else None}
 
+    load = None
+    if args.load_check:
+        import tempfile
+        d = tempfile.mkdtemp(dir=os.environ.get("TMPDIR"))
+        path = os.path.join(d, "model.llmq")
+        h = gm.hash()
+        t0 = time.perf_counter()
+        gm.save(path)
+        t_save = time.perf_counter() - t0
+        size = os.path.getsize(path)
+        times = []
+        for _ in range(2):                       # the second read finds the file in the page cache
+            t0 = time.perf_counter()
+            m2 = Q.Model.load(path)
+            times.append(time.perf_counter() - t0)
+            ok = m2.hash() == h
+            m2.close()
+            if not ok:
+                raise RuntimeError("loaded weights differ from the saved model")
+        os.remove(path)
+        os.rmdir(d)
+        load = {"bytes": size, "save_s": round(t_save, 3), "load_s": [round(t, 3) for t in times],
+                "load_gbs": [round(size / t / 1e9, 2) for t in times]}
     cpu = None
     if not args.no_cpu_baseline and rank == 0:
         cpu = cpu_baseline(Q, gm, cfg, base, pos_first, args.cpu_seconds)
@@ -368,6 +394,7 @@ def main():
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
         "sampled_decode": sampled,
+        "checkpoint_io": load,
         "prefill_roofline": pf_roof,
         "prefill_s": round(t_prefill, 4),
         "model_build_s": round(t_build, 3),
