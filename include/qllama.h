@@ -147,6 +147,10 @@ void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, in
 // logits are the reference's bit for bit.
 LlamaKV llama_kv_create(const LlamaModel *m);
 void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logits);
+// llama.c:167-186  Logits (seq_len, vocab) of every position of ids (host tensor),
+// on the GPU.  Row i equals the reference's batched forward bit for bit (which
+// equals its decode step at position i); seq_len <= max_seq.
+void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits);
 
 // sampler.h:12-31.  Inside the reference's build this takes the place of
 // sampler.h (which, included first, supplies Rng itself).

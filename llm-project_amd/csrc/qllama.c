@@ -1076,6 +1076,28 @@ void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logi
   kv->len += 1;
 }
 
+// llama.c:167-186: logits (seq_len, vocab) for every position of ids.  Row i of
+// the reference's batched forward is bit-identical to the decode step of ids[i]
+// at position i after ids[0..i-1] (the reference's own check, selftest.c:1144-1178,
+// and the fixtures), so each row is computed by the device decode step on a
+// cache of its own; positions are limited to max_seq.
+void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits) {
+  if (!m || !ids || !logits || !logits->data || seq_len <= 0 || seq_len > m->max_seq) {
+    fprintf(stderr, "Error: llama_model_forward: needs 1 <= seq_len <= max_seq (%d) and a (seq_len, vocab) tensor\n",
+            m ? m->max_seq : 0);
+    abort();
+  }
+  LlamaKV kv = llama_kv_create(m);
+  int shape[2] = {1, m->vocab};
+  for (int i = 0; i < seq_len; i++) {
+    Tensor row = *logits;
+    row.data = logits->data + (size_t)i * m->vocab;
+    row.shape = shape; row.ndim = 2; row.size = (size_t)m->vocab;
+    llama_decode_step(m, &kv, ids[i], &row);
+  }
+  llama_kv_free(&kv);
+}
+
 // ---------------------------------------------------------------------------
 // Sampling (sampler.h).  The RNG is the reference's host xorshift64; the
 // sampling arithmetic runs on the device (k_sample.hip), which also holds the

@@ -100,6 +100,7 @@ def lib():
         L.llama_kv_create.argtypes = [P(LlamaModel)]
         L.llama_kv_create.restype = LlamaKV
         L.llama_decode_step.argtypes = [P(LlamaModel), P(LlamaKV), C.c_int, P(Tensor)]
+        L.llama_model_forward.argtypes = [P(LlamaModel), P(C.c_int), C.c_int, P(Tensor)]
         L.rng_create.argtypes = [C.c_ulonglong]
         L.rng_create.restype = Rng
         L.rng_uniform.argtypes = [P(Rng)]
@@ -266,6 +267,13 @@ class FModel:
     def step(self, token):
         lib().llama_decode_step(C.byref(self.m), C.byref(self.kv), int(token), C.byref(self._lt))
         return self.logits[0]
+
+    def forward(self, ids):
+        """llama_model_forward: (len(ids), vocab) logits of every position."""
+        out = np.zeros((len(ids), self.m.vocab), np.float32)
+        arr = (C.c_int * len(ids))(*ids)
+        lib().llama_model_forward(C.byref(self.m), arr, len(ids), C.byref(host_tensor(out)))
+        return out
 
     def close(self):
         if self.kv.dev:

@@ -507,6 +507,14 @@ static void run_e2e_f32(const E2EF *e) {
     llama_decode_step(&m, &kv, seq[i], &logits);
     lh[i] = syn_hash_f32(logits.data, (size_t)m.vocab, 0);
   }
+  // the batched forward over the same prompt (llama.c:167-186): one row per position
+  uint64_t *fh = malloc(sizeof(uint64_t) * (size_t)P);
+  {
+    Tensor L = mat(P, m.vocab);
+    llama_model_forward(&m, seq, P, &L);
+    for (int i = 0; i < P; i++) fh[i] = syn_hash_f32(L.data + (size_t)i * m.vocab, (size_t)m.vocab, 0);
+    tensor_free(&L);
+  }
   char nm[128]; long sv[1] = {m.vocab};
   snprintf(nm, sizeof nm, "e2e_f32_%s_logits_prompt_last", e->name);
   npy_f32(nm, logits.data, 1, sv);
@@ -531,9 +539,11 @@ static void run_e2e_f32(const E2EF *e) {
   for (int i = P; i < n; i++) fprintf(js, "%s%d", i > P ? "," : "", seq[i]);
   fprintf(js, "],\n  \"logit_hashes\": [");
   for (int i = 0; i < P + G; i++) fprintf(js, "%s\"%016llx\"", i ? "," : "", (unsigned long long)lh[i]);
+  fprintf(js, "],\n  \"forward_hashes\": [");
+  for (int i = 0; i < P; i++) fprintf(js, "%s\"%016llx\"", i ? "," : "", (unsigned long long)fh[i]);
   fprintf(js, "]\n}\n");
   fclose(js);
-  free(seq); free(lh); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
+  free(seq); free(lh); free(fh); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
 }
 
 // The LLMA branch of the `llama` command (main.c:686-700) on the tiny fp32 model:

@@ -62,3 +62,13 @@ def test_llma_writer_round_trips_through_reference_loader(tmp_path):
         assert int(out.stdout.strip(), 16) == m.hash()
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("name", ["tiny", "mid"])
+def test_reference_forward_rows_are_its_decode_steps(name):
+    """The fixtures record the reference's batched forward (llama.c:167-186) over
+    the prompt: each row's digest equals that of its decode step, which is what
+    lets the GPU's llama_model_forward run decode steps."""
+    meta = golden_json(f"e2e_f32_{name}")
+    P = len(meta["prompt"])
+    assert meta["forward_hashes"] == meta["logit_hashes"][:P]

@@ -130,3 +130,20 @@ def test_cli_f32_branch_matches_reference(Q, tmp_path):
                          timeout=120)
     assert out.returncode == 0, out.stderr.decode()
     assert out.stdout.decode().splitlines() == expect
+
+
+@pytest.mark.parametrize("name", ["tiny", "mid"])
+def test_f32_forward_matches_reference(Q, name):
+    """llama_model_forward on the GPU against the reference's batched forward rows."""
+    meta = golden_json(f"e2e_f32_{name}")
+    ref = O.FModel(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    try:
+        g = gpu_model(Q, ref, meta["cfg"], meta["rope_base"])
+        try:
+            L = g.forward(meta["prompt"])
+            assert [f"{O.hash_f32(r):016x}" for r in L] == meta["forward_hashes"]
+            assert g.pos == 0                       # the caller's cache is untouched
+        finally:
+            g.close()
+    finally:
+        ref.close()
