@@ -78,10 +78,11 @@ __global__ __launch_bounds__(256) void k_smp_exp(const float *l, int V, float te
 
 // *S = ((0 + e_0) + e_1) + ... + e_{V-1} in float (sampler.c:76), evaluated exactly
 // in chunks of kSumNT*kCM terms; after the first chunk, term 0 of a chunk is the
-// partial sum so far ((0 + s) = s exactly).  Four waves, so that each wave may
-// record up to 128 hard steps (the first chunk's partial sums cross many
-// binades early on) before the exact-sum walk has to fall back to the loop.
-constexpr int kSumNT = 256;
+// partial sum so far ((0 + s) = s exactly).  Eight waves: each wave may record
+// up to 64 hard steps (the first chunk's partial sums cross many binades early
+// on) before the exact-sum walk has to fall back to the loop; sixteen waves
+// (32 each) fell back on real logits.
+constexpr int kSumNT = 512;
 __global__ __launch_bounds__(kSumNT) void k_smp_sum(const float *e, int V, float *S_out) {
   __shared__ qd::SeqScratch S;
   const int tid = threadIdx.x;
