@@ -398,6 +398,36 @@ static void fx_sample(FILE *js) {
     tensor_free(&L);
   }
   fprintf(js, "\n  ],\n");
+  // edge cases: one entry, all-equal logits, -inf logits, extreme temperatures and
+  // top-k / top-p settings (rows rebuilt by the tests from these recipes)
+  fprintf(js, "  \"edge_cases\": [\n");
+  const struct { const char *row; float t; int k; float p; } ec[15] = {
+      {"V1", 0.8f, 40, 0.95f}, {"V1", 2.0f, 0, 1.0f}, {"flat", 1.0f, 0, 0.5f}, {"flat", 0.7f, 64, 0.3f},
+      {"flat", 1.0f, 4096, 1.0f}, {"plain", 1e-30f, 0, 0.9f}, {"plain", 1e3f, 40, 0.95f}, {"plain", 1.0f, 5000, 0.0f},
+      {"plain", 1.0f, 0, 1e-7f}, {"plain", 1.0f, 0, 0.999999f}, {"plain", 0.9f, -3, 2.0f}, {"ninf", 0.8f, 40, 0.95f},
+      {"ninf", 1.0f, 0, 0.99f}, {"wide", 0.8f, 40, 0.95f}, {"wide", 1.1f, 0, 0.9f}};
+  for (int ci = 0; ci < 15; ci++) {
+    int V = 5000;
+    if (!strcmp(ec[ci].row, "V1")) V = 1;
+    else if (!strcmp(ec[ci].row, "flat")) V = 4096;
+    else if (!strcmp(ec[ci].row, "wide")) V = 131072;
+    Tensor L = mat(1, V);
+    if (V == 1) L.data[0] = 0.25f;
+    else if (V == 4096) for (int j = 0; j < V; j++) L.data[j] = 1.5f;
+    else if (V == 131072) sample_row(L.data, V, 61, 3.0, 1);
+    else {
+      sample_row(L.data, V, 60, 1.0, 0);
+      if (!strcmp(ec[ci].row, "ninf")) for (int j = 0; j < V; j += 3) L.data[j] = -INFINITY;
+    }
+    Rng rng = rng_create(2024);
+    int tok[5];
+    for (int d = 0; d < 5; d++) tok[d] = sample_token(&L, 0, ec[ci].t, ec[ci].k, ec[ci].p, &rng);
+    fprintf(js, "%s    {\"row\": \"%s\", \"t\": %.9g, \"k\": %d, \"p\": %.9g, \"tokens\": [%d,%d,%d,%d,%d], "
+                "\"state\": \"%016llx\"}", ci ? ",\n" : "", ec[ci].row, (double)ec[ci].t, ec[ci].k, (double)ec[ci].p,
+            tok[0], tok[1], tok[2], tok[3], tok[4], (unsigned long long)rng.state);
+    tensor_free(&L);
+  }
+  fprintf(js, "\n  ],\n");
   // rng_uniform's first values from a few seeds (seed 0 maps to the fixed constant)
   fprintf(js, "  \"uniform\": [");
   const unsigned long long seeds[3] = {0, 1, 1234};

@@ -203,3 +203,42 @@ def test_save_load_round_trip_and_truncation(Q, tmp_path, capfd):
         assert "is truncated (bad weights)" in capfd.readouterr().err
     finally:
         m.close()
+
+
+def _edge_rows():
+    r = O.sample_row(5000, 60, 1.0, 0)
+    ninf = r.copy()
+    ninf[::3] = -np.inf                        # expf(-inf) = 0: never kept by top-p, p = 0 otherwise
+    return {
+        "V1": np.array([0.25], np.float32),
+        "flat": np.full(4096, 1.5, np.float32),     # every probability equal: index order decides
+        "plain": r,
+        "ninf": ninf,
+        "wide": O.sample_row(131072, 61, 3.0, 1),   # top-k path at its widest vocabulary
+    }
+
+
+@pytest.mark.parametrize("case", [
+    ("V1", 0.8, 40, 0.95), ("V1", 2.0, 0, 1.0),
+    ("flat", 1.0, 0, 0.5), ("flat", 0.7, 64, 0.3), ("flat", 1.0, 4096, 1.0),
+    ("plain", 1e-30, 0, 0.9), ("plain", 1e3, 40, 0.95), ("plain", 1.0, 5000, 0.0),
+    ("plain", 1.0, 0, 1e-7), ("plain", 1.0, 0, 0.999999), ("plain", 0.9, -3, 2.0),
+    ("ninf", 0.8, 40, 0.95), ("ninf", 1.0, 0, 0.99),
+    ("wide", 0.8, 40, 0.95), ("wide", 1.1, 0, 0.9),
+])
+def test_sample_token_edge_cases_match_oracle(Q, case):
+    name, t, k, p = case
+    row = _edge_rows()[name]
+    rng = Q.rng_create(2024)
+    st = O.rng_create(2024)
+    for _ in range(5):
+        g = Q.sample_token(row.reshape(1, -1), t, k, p, rng)
+        r, st = O.sample_token(row, t, k, p, st)
+        assert g == r and rng.state == st, case
+    # and the compiled reference's draws for the same case
+    ref = [c for c in S["edge_cases"] if c["row"] == name and np.float32(c["t"]) == np.float32(t)
+           and c["k"] == k and np.float32(c["p"]) == np.float32(p)]
+    assert len(ref) == 1
+    rng = Q.rng_create(2024)
+    assert [Q.sample_token(row.reshape(1, -1), t, k, p, rng) for _ in range(5)] == ref[0]["tokens"]
+    assert rng.state == int(ref[0]["state"], 16)

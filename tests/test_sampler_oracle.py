@@ -106,3 +106,28 @@ def test_llmq_writer_round_trips_through_reference_loader(tmp_path):
         assert int(out.stdout.strip(), 16) == m.hash()
     finally:
         m.close()
+
+
+def _edge_row(name):
+    if name == "V1":
+        return np.array([0.25], np.float32)
+    if name == "flat":
+        return np.full(4096, 1.5, np.float32)
+    if name == "wide":
+        return O.sample_row(131072, 61, 3.0, 1)
+    r = O.sample_row(5000, 60, 1.0, 0)
+    if name == "ninf":
+        r[::3] = -np.inf
+    return r
+
+
+@pytest.mark.parametrize("ci", range(len(S["edge_cases"])))
+def test_sample_token_edge_cases_match_reference(ci):
+    c = S["edge_cases"][ci]
+    row = _edge_row(c["row"])
+    st = O.rng_create(2024)
+    toks = []
+    for _ in range(5):
+        t, st = O.sample_token(row, c["t"], c["k"], c["p"], st)
+        toks.append(t)
+    assert toks == c["tokens"] and st == int(c["state"], 16), c
