@@ -147,3 +147,27 @@ def test_f32_forward_matches_reference(Q, name):
             g.close()
     finally:
         ref.close()
+
+
+def test_f32_nonzero_biases_and_gains_match_oracle(Q):
+    """Biases (Qwen-style checkpoints, llama.c:319-321) and norm gains other than 1
+    (rmsnorm.c:18) through the fp32 step, bit for bit against the oracle."""
+    cfg = [3000, 256, 2, 8, 2, 32, 512, 64]
+    ref = O.FModel(cfg, 10000.0, seed=31)
+    try:
+        rng = np.random.default_rng(5)
+        for name, t in ref.tensors():
+            if name in ("b_q", "b_k", "b_v"):
+                t[:] = rng.standard_normal(t.shape).astype(np.float32) * np.float32(0.1)
+            if name in ("attn_norm", "ffn_norm", "final_norm"):
+                t[:] = (1.0 + rng.standard_normal(t.shape) * 0.2).astype(np.float32)
+        g = gpu_model(Q, ref, cfg, 10000.0)
+        try:
+            for t in [3, 17, 2999, 0, 42, 7]:
+                a = g.step(t).copy()
+                b = ref.step(t).copy()
+                assert np.array_equal(bits(a), bits(b)), t
+        finally:
+            g.close()
+    finally:
+        ref.close()

@@ -242,3 +242,38 @@ def test_sample_token_edge_cases_match_oracle(Q, case):
     rng = Q.rng_create(2024)
     assert [Q.sample_token(row.reshape(1, -1), t, k, p, rng) for _ in range(5)] == ref[0]["tokens"]
     assert rng.state == int(ref[0]["state"], 16)
+
+
+def test_int8_nonzero_biases_and_gains_match_oracle(Q, tmp_path):
+    """Biases and norm gains other than 1 through the int8 path: an LLMQ file
+    written from an oracle model whose biases and gains were set, loaded on the
+    GPU, decode steps and a batched prefill bit for bit against the oracle."""
+    cfg = [3000, 256, 2, 8, 2, 32, 512, 64]
+    ref = O.Model(cfg, 10000.0, seed=32)
+    try:
+        rng = np.random.default_rng(6)
+        m = ref.m
+        dm, qd, kvd = cfg[1], cfg[3] * cfg[5], cfg[4] * cfg[5]
+        views = [(m.final_norm, dm, True)]
+        for l in range(cfg[2]):
+            b = m.blocks[l]
+            views += [(b.attn_norm, dm, True), (b.ffn_norm, dm, True), (b.b_q, qd, False), (b.b_k, kvd, False),
+                      (b.b_v, kvd, False)]
+        for ptr, n, gain in views:
+            a = np.ctypeslib.as_array(ptr, shape=(n,))
+            a[:] = ((1.0 + rng.standard_normal(n) * 0.2) if gain else rng.standard_normal(n) * 0.1).astype(np.float32)
+        path = str(tmp_path / "b.llmq")
+        O.write_llmq(ref, path)
+        g = Q.Model.load(path)
+        try:
+            ids = O.prompt(20, 9, cfg[0])
+            for t in ids[:4]:
+                assert np.array_equal(g.step(t).view(np.uint32), ref.step(t).view(np.uint32)), t
+            lg = g.prefill(ids[4:]).copy()                 # batched (16 rows) after 4 decode steps
+            for t in ids[4:]:
+                r = ref.step(t)
+            assert np.array_equal(lg.view(np.uint32), r.view(np.uint32))
+        finally:
+            g.close()
+    finally:
+        ref.close()
