@@ -270,10 +270,24 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float *bv, const in
   __shared__ int si[16];
   float best = -INFINITY;
   int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-    const float v = bv[i];
-    const int k = bidx[i];
-    if (k != 0x7fffffff && (idx == 0x7fffffff || v > best || (v == best && k < idx))) { best = v; idx = k; }
+  // 16 candidates per thread per pass, all requested before any is compared
+  // (one memory round trip per pass instead of one per candidate)
+  constexpr int U = 16;
+  for (int i0 = 0; i0 < nb; i0 += U * (int)blockDim.x) {
+    float v[U];
+    int k[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + u * (int)blockDim.x + (int)threadIdx.x;
+      v[u] = i < nb ? bv[i] : -INFINITY;
+      k[u] = i < nb ? bidx[i] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (k[u] != 0x7fffffff && (idx == 0x7fffffff || v[u] > best || (v[u] == best && k[u] < idx))) {
+        best = v[u];
+        idx = k[u];
+      }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
