@@ -1,8 +1,10 @@
 // qllama.h - C ABI of the MI355X library for the reference's int8 LLaMA decode path.
 //
 // Drop-in for the quantized section of the reference's llama.h (llama.h:114-140),
-// for quant.h (quant.h:15-33) and for qacc_columns (matrix.h:55).  Same names,
-// argument meaning and error behaviour; the difference is where the data lives:
+// for quant.h (quant.h:15-33), for qacc_columns (matrix.h:55), for sampler.h
+// (sampler.h:12-31) and for the fp32 cache / decode step / forward of llama.h
+// (llama.h:80, 101-106).  Same names, argument meaning and error behaviour; the
+// difference is where the data lives:
 //
 //   * QTensor.q / QTensor.scale point to DEVICE memory (MI355X HBM).  q is stored
 //     output-channel major: element (row k, col j) of the reference's (rows, cols)
@@ -16,6 +18,10 @@
 //     reset LlamaKV.len (main.c:661), which this library honours.
 //   * Tensor arguments of qmatmul and the logits of q_llama_decode_step are host
 //     memory, exactly as in the reference.
+//   * The fp32 LlamaModel stays the reference's host structure; the library keeps
+//     a private device copy of its weights for llama_kv_create's caches, and the
+//     logits of llama_decode_step / llama_model_forward and the logits that
+//     sample_token reads are host memory.
 //
 // Errors follow the reference: loaders return nonzero and print "Error: ..." to
 // stderr; void functions print and abort on a device error.  Entry points that
