@@ -240,6 +240,9 @@ def main():
     ap.add_argument("--load-check", action="store_true",
                     help="also time q_llama_model_save and q_llama_model_load of the model through $TMPDIR "
                          "(writes a checkpoint of the model's size there)")
+    ap.add_argument("--full-range", action=argparse.BooleanOptionalAction, default=True,
+                    help="also decode from the prompt to max_seq in one loop per mode (the config's whole "
+                         "decode range)")
     ap.add_argument("--path", default="int8", choices=["int8", "f32"],
                     help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
     args = ap.parse_args()
@@ -255,15 +258,14 @@ def main():
     if args.path == "f32":
         return main_f32(args, Q, cfg, base, tied, args.prefill if args.prefill is not None else 64)
     W, K, NP, NS = args.warmup, args.steps, args.profile_steps, args.sampled_steps
-    if P + W + K + NP + NS + (2 if NS else 0) > cfg[7]:
+    if P + W + K + 2 * NP + NS + (2 if NS else 0) > cfg[7]:
         sys.exit(f"bench.py: prefill {P} + warmup {W} + steps {K} + profile {NP} + sampled {NS} "
                  f"exceeds max_seq {cfg[7]}")
 
     t0 = time.perf_counter()
     gm = Q.Model.synth(cfg, base, seed=1234, tied=tied)
     t_build = time.perf_counter() - t0
-    import oracle_lib as O
-    prompt = O.prompt(P, 1234, cfg[0])
+    prompt = [int(t) for t in np.random.default_rng(1234).integers(0, cfg[0], P)]
 
     # prefill (timed separately, after one untimed ingestion that allocates its buffers)
     if P:
@@ -274,44 +276,81 @@ def main():
     gm.prefill(prompt, want_logits=True)
     Q.lib().qllama_device_sync()
     t_prefill = time.perf_counter() - t0
-    tok = int(np.argmax(gm.logits[0]))
+    first = int(np.argmax(gm.logits[0]))
 
-    # warm-up decode steps (untimed), then exactly K timed steps
-    out = gm.generate_greedy(tok, W) if W else []
-    tok = out[-1] if out else tok
-    Q.lib().qllama_device_sync()
-    pos_first = gm.pos
-    t0 = time.perf_counter()
-    out = gm.generate_greedy(tok, K)
-    Q.lib().qllama_device_sync()
-    t_decode = time.perf_counter() - t0
-    tok = out[-1]
+    def timed_decode(m, tok):
+        """W untimed warm-up steps, then exactly K timed greedy steps on the device."""
+        out = m.generate_greedy(tok, W) if W else []
+        tok = out[-1] if out else tok
+        Q.lib().qllama_device_sync()
+        pos = m.pos
+        t0 = time.perf_counter()
+        out = m.generate_greedy(tok, K)
+        Q.lib().qllama_device_sync()
+        return time.perf_counter() - t0, pos, out[-1]
+
+    def full_range(m):
+        """From the prompt to max_seq in one device loop (the config's whole decode
+        range: 512 steps at contexts 2049..2560 for the 8B shape)."""
+        n = cfg[7] - P
+        if n < 2:
+            return None
+        m.reset(0)
+        m.prefill(prompt, want_logits=True)
+        tok = int(np.argmax(m.logits[0]))
+        Q.lib().qllama_device_sync()
+        t0 = time.perf_counter()
+        m.generate_greedy(tok, n)
+        Q.lib().qllama_device_sync()
+        t = time.perf_counter() - t0
+        bytes_avg = statistics.mean(decode_bytes(cfg, P + 1 + i) for i in range(n))
+        return {"tok_s": round(n / t, 3), "steps": n, "context": [P + 1, P + n],
+                "ms_per_step": round(1e3 * t / n, 4),
+                "hbm_roofline_frac": round(bytes_avg / (t / n) / (HBM_PEAK_GBS * 1e9), 4)}
+
+    def kernel_profile(m, tok):
+        if not NP:
+            return {}
+        Q.profile(True)
+        m.generate_greedy(tok, NP)
+        prof = Q.profile_read()
+        Q.profile(False)
+        return prof
+
+    # exact mode (logits bit-identical to the reference), on the prefilled cache
+    t_exact, pos_first, tok_e = timed_decode(gm, first)
+    prof_exact = kernel_profile(gm, tok_e)
+    # fast mode (split-K attention, tree-ordered norm sums): a second cache on the same weights
+    gf = gm.fork(Q.MODE_FAST)
+    gf.prefill(prompt, want_logits=True)
+    t_decode, pos_fast, tok = timed_decode(gf, int(np.argmax(gf.logits[0])))
+    assert pos_fast == pos_first
+    prof = kernel_profile(gf, tok)
     ms_per_step = 1e3 * t_decode / K
     tok_s = K / t_decode
     # context of each timed step: pos + 1 cached rows
     ctx = [pos_first + 1 + i for i in range(K)]
     step_bytes = statistics.mean(decode_bytes(cfg, t) for t in ctx)
     step_frac = step_bytes / (t_decode / K) / (HBM_PEAK_GBS * 1e9)
-
-    # per-kernel HIP-event timing of the same decode steps (eager launches)
-    prof = {}
-    if NP:
-        Q.profile(True)
-        gm.generate_greedy(tok, NP)
-        prof = Q.profile_read()
-        Q.profile(False)
+    exact_line = {"tok_s": round(K / t_exact, 3), "ms_per_step": round(1e3 * t_exact / K, 4),
+                  "hbm_roofline_frac": round(step_bytes / (t_exact / K) / (HBM_PEAK_GBS * 1e9), 4),
+                  "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof_exact.items())}
+                  if NP else None}
+    full = {"fast": full_range(gf), "exact": full_range(gm)} if args.full_range else None
     # sampled decode (sample_token's arithmetic on the device between the steps)
     sampled = None
     if NS:
+        gf.reset(pos_first + K + NP)
         rng = Q.rng_create(1234)
-        gm.generate(2, 0.8, 40, 0.95, rng)          # allocates the sampler's buffers
+        gf.generate(2, 0.8, 40, 0.95, rng)          # allocates the sampler's buffers
         Q.lib().qllama_device_sync()
         t0 = time.perf_counter()
-        gm.generate(NS, 0.8, 40, 0.95, rng)
+        gf.generate(NS, 0.8, 40, 0.95, rng)
         Q.lib().qllama_device_sync()
         t_s = time.perf_counter() - t0
         sampled = {"tok_s": round(NS / t_s, 3), "steps": NS, "temperature": 0.8, "top_k": 40, "top_p": 0.95,
-                   "ms_per_step": round(1e3 * t_s / NS, 4)}
+                   "ms_per_step": round(1e3 * t_s / NS, 4), "mode": "fast"}
+    gf.close()
     if args.calib_copy_mib:
         Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
         if Q.lib().qllama_test_copy(args.calib_copy_mib << 20) != 0:
@@ -388,9 +427,11 @@ def main():
         "config": {
             "workload": f"{args.config}-shape int8 LLaMA greedy decode after a {P}-token prefill",
             "cfg": cfg, "rope_base": base, "tied": tied, "prefill_tokens": P,
-            "context_timed": [ctx[0], ctx[-1]],
+            "context_timed": [ctx[0], ctx[-1]], "decode_mode": "fast",
         },
         "decode_hbm_roofline_frac": round(step_frac, 4),
+        "decode_exact": exact_line,
+        "decode_full_range": full,
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
         "sampled_decode": sampled,
@@ -400,7 +441,7 @@ def main():
         "model_build_s": round(t_build, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites)",
+            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites, fast-mode decode)",
             "achieved": round(achieved, 1) if achieved else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -125,7 +125,7 @@ int q_llama_model_load(const char *path, QLlamaModel *out);
 void q_llama_model_free(QLlamaModel *m);
 // llama.c:490-511  Quantize a host fp32 model (per output channel) on the GPU.
 QLlamaModel q_llama_quantize_from(const LlamaModel *src);
-// llama.c:513-526  Device KV cache of max_seq positions per layer.
+// llama.c:513-526  Device KV cache of max_seq positions per layer (exact mode).
 LlamaKV q_llama_kv_create(const QLlamaModel *m);
 // llama.c:290-294
 void llama_kv_free(LlamaKV *kv);
@@ -148,7 +148,9 @@ void qacc_columns(const signed char *qa, const signed char *qw, int K, int N, in
 // reference's host LlamaModel (llama.h:58-66).  The first cache made for a model
 // uploads a device copy of its weights (found again by the model's weight
 // pointers); the copy is freed with the last of its caches (llama_kv_free).
-// Weight changes made on the host afterwards are seen by caches created later.
+// The copy is taken when the first live cache of the model is created: host
+// weight changes made while a cache of it lives are not seen until every cache
+// has been freed and a new one is made.
 // logits: host (1, vocab).  Every output sums in the reference's order, so the
 // logits are the reference's bit for bit.
 LlamaKV llama_kv_create(const LlamaModel *m);
@@ -189,6 +191,15 @@ int sample_token(const Tensor *logits, int row, float temperature, int top_k, fl
 // n_steps calls of sample_token would.  Returns 0 on success.
 int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float temperature, int top_k, float top_p,
                      Rng *rng, int *out);
+
+// Decode modes of a KV cache, chosen when it is created.
+#define QLLAMA_MODE_EXACT 0  // every float sum in the reference's order: logits bit-identical to llama.c:528-600
+#define QLLAMA_MODE_FAST  1  // split-K attention with an online-softmax merge and tree-ordered rmsnorm sums;
+                             // the integer GEMV arithmetic is unchanged (greedy streams equal, logits within
+                             // max-abs 1e-3 / relative 1e-4 of the reference on the committed fixtures)
+// q_llama_kv_create (llama.c:513-526) with a decode mode; every entry point that
+// takes the cache then decodes in that mode (prompt ingestion stays exact).
+LlamaKV q_llama_kv_create_mode(const QLlamaModel *m, int mode);
 
 // Prompt ingestion: n tokens at positions kv->len .. kv->len+n-1.  Same result
 // as n calls of q_llama_decode_step (main.c:662); logits are those of the last
@@ -237,6 +248,22 @@ int  qllama_test_expf(uint32_t start, uint32_t count, float *out);
 // reference's cache layout, o (n_heads*hd); all host memory.  For op-level parity.
 int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv,
                        int hd, float *o);
+// The same with a decode mode (QLLAMA_MODE_*) and, for rope_base > 0, the RoPE
+// of the decode step on the device: q and rows T-1 of k and v arrive
+// unrotated; the device rotates q and k (host-libm tables, rope.c:48-68),
+// appends row T-1 to the cache and attends; k_row (n_kv*hd, may be NULL)
+// receives the rotated row as cached.  reps > 0 times that many launches after
+// one warm-up (HIP events on the library stream); *us_per_call receives the mean.
+int  qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv, int hd,
+                          float rope_base, int mode, int reps, float *o, float *k_row, double *us_per_call);
+// One activation row through the decode GEMV that normalizes its own input:
+// rmsnorm (rmsnorm.c:7-21) + activation quantization (quant.c:66-78) formed in
+// every block, then the W8A8 product (quant.c:79-82).  mode 0: out = W->cols
+// values; mode 2: SwiGLU (llama.c:583-587) over gate columns [0, N) and up
+// columns [N, 2N), out = N values of h.  fast = 1 uses the fast decode mode's
+// tree-ordered sum of squares.  W: device QTensor (rows = d_model, NK layout,
+// kpad 2048, 4096 or 8192); x, gamma, out: host.  For parity tests.
+int  qllama_norm_gemv(const float *x, const float *gamma, float eps, const QTensor *W, int mode, int fast, float *out);
 // The device's exact evaluation of the sequential float sum ((0 + a_0) + a_1) + ...
 // of n <= 16384 non-negative terms (the form of rmsnorm.c:15 and llama.c:567):
 // *out = the sum, info[0] = number of serially evaluated steps, info[1] = 1 when

@@ -282,6 +282,11 @@ __global__ void k_kv_relayout(const float *src, int T, int n_kv, int hd, float *
 }
 }  // namespace
 
+extern "C" int qhip_kv_relayout(const float *src, int T, int n_kv, int hd, float *dst) {
+  QH_LAUNCH(QK_OTHER, k_kv_relayout, dim3(4096), dim3(256), 0, src, T, n_kv, hd, dst);
+  return 0;
+}
+
 extern "C" int qllama_test_expf(uint32_t start, uint32_t count, float *out) {
   if (qhip_init()) return 1;
   float *d = (float *)qhip_malloc((size_t)count * 4);

@@ -55,7 +55,7 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
 // PRO = 2: the activation is the residual stream v (n values) before its
 // rmsnorm (gain vbm, epsilon eps); every block normalizes and quantizes it
 // itself (the operations of k_rmsnorm_quant) while its first weights are in
-// flight.
+// flight.  PRO = 3: the same with the fast mode's tree-ordered sum of squares.
 // NS: weight rows (pairs, for SWIGLU) held in registers; rows r+1 .. r+NS-1 are
 // in flight while row r is reduced.
 template <int MODE, int KCH, int R, int PRO, int NS>
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
                                                   const float *ws, int N, int kpad, float *out, const float *bias,
                                                   float *bm, int *bi, const float *v, int n, const float *vbm,
                                                   int nvbm, float eps) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   __shared__ int redi[4];
   __shared__ __attribute__((aligned(16))) int8_t qsh[PRO ? KCH * 1024 : 16];
   __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
@@ -82,10 +82,16 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   }
   v4i a[KCH];
   float as;
-  if constexpr (PRO == 2) {
+  if constexpr (PRO == 2 || PRO == 3) {
     constexpr int CM = 4 * KCH;                      // 256 threads x CM values = kpad
     float y[CM];
-    as = qd::rmsnorm_row<256, CM>(v, n, vbm, eps, y, red, seq);
+    if constexpr (PRO == 2) {
+      as = qd::rmsnorm_row<256, CM>(v, n, vbm, eps, y, red, seq);
+    } else {
+      float gm[CM];
+      qd::rmsnorm_load<CM>(v, n, vbm, y, gm);
+      as = qd::rmsnorm_apply_fast<256, CM>(n, eps, y, gm, red);
+    }
     const float inv = 1.0f / as;
 #pragma unroll
     for (int c = 0; c < CM; c += 4)
@@ -342,13 +348,13 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
 // Output channels per wave.  The GEMVs that normalize their own input take
 // several, so that at the 8B shape their blocks are resident together and each
 // block's prologue runs once: 6 (gate, up) pairs for SwiGLU, 4 rows for QKV.
-constexpr int rows_per_wave(int mode, int pro) { return pro == 2 ? (mode == MODE_SWIGLU ? 6 : 4) : 2; }
+constexpr int rows_per_wave(int mode, int pro) { return pro >= 2 ? (mode == MODE_SWIGLU ? 6 : 4) : 2; }
 
 // Weight rows in registers (measured at the 8B shape): two where that keeps
 // every wave resident (the 14336-wide down projection, the QKV GEMV with its
 // prologue), else one.
 constexpr int weight_slots(int mode, int pro, int kch) {
-  return (pro == 0 && kch == 14) || (pro == 2 && mode != MODE_SWIGLU) ? 2 : 1;
+  return (pro == 0 && kch == 14) || (pro >= 2 && mode != MODE_SWIGLU) ? 2 : 1;
 }
 
 template <int MODE, int PRO>
@@ -359,7 +365,7 @@ int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const fl
 #define QG(KCH)                                                                                                    \
   QH_LAUNCH(cls, (k_gemv_dec<MODE, KCH, R, PRO, weight_slots(MODE, PRO, KCH)>), grid, dim3(256), 0, qa, as, W, ws, N, \
             kpad, out, bias, bm, bi, v, n, vbm, nvbm, eps)
-  if constexpr (PRO == 2) {                          // 256 threads x 4*KCH values of the row
+  if constexpr (PRO >= 2) {                          // 256 threads x 4*KCH values of the row
     switch (kpad) {
       case 2048: QG(2); return 0;
       case 4096: QG(4); return 0;
@@ -413,9 +419,10 @@ extern "C" int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vb
 
 // SwiGLU GEMV whose activation is rmsnorm(x) quantized, formed inside every
 // block (replaces qhip_rmsnorm_quant + mode 2).
-extern "C" int qhip_gemv_swiglu_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
-                                     const float *ws, int N, int kpad, float *out, float *bm) {
+extern "C" int qhip_gemv_swiglu_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps,
+                                     const int8_t *W, const float *ws, int N, int kpad, float *out, float *bm) {
   if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_swiglu_norm: unsupported shape");
+  if (fast) return launch<MODE_SWIGLU, 3>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, bm, NULL, x, dm, gamma, 0, eps);
   return launch<MODE_SWIGLU, 2>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, bm, NULL, x, dm, gamma, 0, eps);
 }
 
@@ -432,9 +439,10 @@ extern "C" int qhip_gemv_norm_blocks(int N) {
 
 // Plain (QKV) GEMV whose activation is rmsnorm(x) quantized, formed inside
 // every block (replaces qhip_rmsnorm_quant + mode 0).
-extern "C" int qhip_gemv_plain_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
-                                    const float *ws, int N, int kpad, float *out, const float *bias) {
+extern "C" int qhip_gemv_plain_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps,
+                                    const int8_t *W, const float *ws, int N, int kpad, float *out, const float *bias) {
   if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_plain_norm: unsupported shape");
+  if (fast) return launch<MODE_PLAIN, 3>(cls, NULL, NULL, W, ws, N, kpad, out, bias, NULL, NULL, x, dm, gamma, 0, eps);
   return launch<MODE_PLAIN, 2>(cls, NULL, NULL, W, ws, N, kpad, out, bias, NULL, NULL, x, dm, gamma, 0, eps);
 }
 

@@ -210,6 +210,19 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
          __builtin_amdgcn_readlane(v, 48);
 }
 
+// Sum over the wave in a fixed order; every lane receives the same bits.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += __int_as_float(dpp_mov<0xB1>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<0x4E>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<0x141>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<0x140>(__float_as_int(v)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
   v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
   v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));

@@ -71,6 +71,40 @@ __device__ __forceinline__ float rmsnorm_apply(const float *xr, int n, float eps
   return (mx > 0.0f) ? mx / 127.0f : 1.0f;
 }
 
+// The fast decode mode's form of rmsnorm_apply: the sum of squares is a fixed-
+// shape tree (per-thread partial sums, then the wave, then the waves in order),
+// so it is deterministic but not the reference's sequential order; everything
+// after it is the same.  red holds 2 * NT/64 floats.
+template <int NT, int CM>
+__device__ __forceinline__ float rmsnorm_apply_fast(int n, float eps, float (&y)[CM], const float (&gm)[CM],
+                                                    float *red) {
+  const int j0 = threadIdx.x * CM;
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CM; c++) ss = __builtin_fmaf(y[c], y[c], ss);      // y is 0 past n
+  ss = wave_sum_f32(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  lds_sync();
+  ss = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) ss += red[w];
+  const float ms = ss * (1.0f / (float)n);
+  const float r = 1.0f / sqrtf(ms + eps);
+  float mx = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CM; c++) {
+    y[c] = j0 + c < n ? y[c] * r * gm[c] : 0.0f;
+    mx = fmaxf(mx, fabsf(y[c]));
+  }
+  mx = wave_max_f32(mx);
+  if ((threadIdx.x & 63) == 0) red[NT / 64 + (threadIdx.x >> 6)] = mx;
+  lds_sync();
+  mx = red[NT / 64];
+#pragma unroll
+  for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[NT / 64 + w]);
+  return (mx > 0.0f) ? mx / 127.0f : 1.0f;
+}
+
 // Both steps: y[] receives this thread's normalized values.
 template <int NT, int CM>
 __device__ __forceinline__ float rmsnorm_row(const float *xr, int n, const float *gamma, float eps, float (&y)[CM],

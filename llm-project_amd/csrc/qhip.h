@@ -43,6 +43,10 @@ int  qhip_capture_end(void **exec);
 int  qhip_graph_launch(void *exec);
 void qhip_graph_destroy(void *exec);
 
+// elapsed time (ms) of the work enqueued between start and stop (HIP events on the stream)
+int  qhip_timer_start(void);
+int  qhip_timer_stop(double *ms);
+
 // per-kernel-class timing with HIP events on the library stream
 int  qhip_profile_enable(int on);
 int  qhip_profile_read(char *names, int names_len, double *ms, long long *count, int max);
@@ -106,6 +110,15 @@ int qhip_attention_rope(const float *qkv, float *kc, float *vc, const int *d_pos
                         int max_seq, float scale, const float *cos_t, const float *sin_t, float *scores, float *o,
                         float *obm);
 int qhip_attention_nbm(int n_heads, int hd);
+// The fast decode mode's attention (k_fattn.hip): split-K over positions with an
+// online-softmax merge, same inputs and outputs as qhip_attention_rope (rope = 1)
+// or qhip_attention (rope = 0, q pre-rotated and row pos already cached); obm
+// receives n_heads maxima of |o| (one per query head).  scratch:
+// qhip_fattn_scratch bytes (the chunks' partial results).
+int qhip_fattn_ok(int n_heads, int n_kv, int hd, int max_seq);
+size_t qhip_fattn_scratch(int n_heads, int n_kv, int hd, int max_seq);
+int qhip_fattn(const float *qkv, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv, int hd, int max_seq,
+               float scale, const float *cos_t, const float *sin_t, int rope, void *scratch, float *o, float *obm);
 // Decode GEMV with one activation row (k_gemv.hip): mode 0 plain (+bias), 1
 // residual add, 2 SwiGLU over gate rows [0,N) and up rows [N,2N) writing h and
 // per-block max |h| into bm (qhip_gemv_blocks(N, kpad) entries).
@@ -124,12 +137,13 @@ int qhip_gemv_blocks(int N, int kpad);
 // SwiGLU GEMV (mode 2) whose activation is rmsnorm(x; gamma, eps) quantized,
 // formed in each block from the dm values of x; kpad in {2048, 4096, 8192}
 // (qhip_gemv_norm_ok).  It writes qhip_gemv_norm_blocks(N) per-block maxima.
-int qhip_gemv_swiglu_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+// fast = 1: the sum of squares in a fixed tree order (the fast decode mode).
+int qhip_gemv_swiglu_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
                           const float *ws, int N, int kpad, float *out, float *bm);
 int qhip_gemv_norm_ok(int kpad, int dm);
 // Plain GEMV (mode 0, QKV) whose activation is rmsnorm(x; gamma, eps) quantized,
 // formed in each block like qhip_gemv_swiglu_norm's; same shapes.
-int qhip_gemv_plain_norm(int cls, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
+int qhip_gemv_plain_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps, const int8_t *W,
                          const float *ws, int N, int kpad, float *out, const float *bias);
 int qhip_gemv_norm_blocks(int N);
 // Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
@@ -175,6 +189,9 @@ int qhip_gemv_f32_max_k(void);
 int qhip_embed_f32(const float *wte, int dm, const int *d_in, const int *d_state, float *x);
 int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y);
 int qhip_swiglu_f32(const float *gu, int dff, float *h);
+
+// cache rows (T, n_kv*hd) in the reference's layout -> [n_kv][T][hd]
+int qhip_kv_relayout(const float *src, int T, int n_kv, int hd, float *dst);
 
 // reference-layout column accumulate (matrix.c:354-374) for qacc_columns
 int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);

@@ -8,7 +8,8 @@
 // Kernel classes for event timing (names in qhip_runtime.hip).
 enum {
   QK_EMBED = 0, QK_RMSNORM, QK_GEMV_QKV, QK_ROPE, QK_ATTN, QK_QUANT, QK_GEMV_O, QK_GEMV_GU,
-  QK_SWIGLU, QK_GEMV_DOWN, QK_GEMV_HEAD, QK_ARGMAX, QK_OTHER, QK_ATTN_PV, QK_PF_GEMM, QK_PF_ATTN, QK_PF_OTHER, QK_NUM_CLASSES
+  QK_SWIGLU, QK_GEMV_DOWN, QK_GEMV_HEAD, QK_ARGMAX, QK_OTHER, QK_ATTN_PV, QK_PF_GEMM, QK_PF_ATTN, QK_PF_OTHER,
+  QK_ATTN_FAST, QK_NUM_CLASSES
 };
 
 namespace qh {

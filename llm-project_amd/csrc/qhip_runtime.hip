@@ -25,7 +25,8 @@ std::vector<ProfRec> g_prof_recs;
 std::vector<hipEvent_t> g_event_pool;
 const char *g_class_names[QK_NUM_CLASSES] = {
     "embed", "rmsnorm_quant", "gemv_qkv", "rope_append", "attn_scores", "quant_rows",
-    "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other", "attn_pv", "pf_gemm", "pf_attn", "pf_other"};
+    "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other", "attn_pv", "pf_gemm", "pf_attn", "pf_other",
+    "attn_fast"};
 
 hipEvent_t take_event() {
   if (!g_event_pool.empty()) { hipEvent_t e = g_event_pool.back(); g_event_pool.pop_back(); return e; }
@@ -299,3 +300,26 @@ int qhip_profile_read(char *names, int names_len, double *ms, long long *count, 
 }
 
 }  // extern "C"
+
+// Wall time of the launches enqueued between qhip_timer_start and qhip_timer_stop
+// on the library stream (HIP events); qhip_timer_stop waits for the stop event.
+namespace {
+hipEvent_t g_t0 = nullptr, g_t1 = nullptr;
+}
+
+extern "C" int qhip_timer_start(void) {
+  if (!g_t0 && (hipEventCreate(&g_t0) != hipSuccess || hipEventCreate(&g_t1) != hipSuccess))
+    return qh::fail_msg("hipEventCreate failed");
+  hipError_t e = hipEventRecord(g_t0, g_stream);
+  return e == hipSuccess ? 0 : qh::fail("hipEventRecord", e);
+}
+
+extern "C" int qhip_timer_stop(double *ms) {
+  hipError_t e = hipEventRecord(g_t1, g_stream);
+  if (e == hipSuccess) e = hipEventSynchronize(g_t1);
+  float t = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t, g_t0, g_t1);
+  if (e != hipSuccess) return qh::fail("timer", e);
+  *ms = t;
+  return 0;
+}

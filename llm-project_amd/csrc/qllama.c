@@ -21,6 +21,7 @@
 #include <unistd.h>
 
 #define LLMQ_MAGIC   0x514D4C4Cu   // llama.c:193
+#define QLLAMA_CLS_OTHER 12        // kernel class "other" of the event timing
 #define LLMA_VERSION 2u            // llama.c:194
 
 static int pad16(int k) { return (k + 15) & ~15; }
@@ -53,6 +54,7 @@ typedef struct {
   int *d_in;         // max_seq + 1 input tokens by position
   int *d_out;        // max_seq argmax ids by position
   int *h_stage;      // pinned staging, max_seq + 2 ints
+  uint64_t gen;      // process-wide generation: identifies this model to the graphs of its caches
   // prompt ingestion (allocated on first use): rows of activations
   int pf_rows;
   float *pf_x, *pf_qkv, *pf_q, *pf_o, *pf_h, *pf_as, *pf_attn;
@@ -61,15 +63,24 @@ typedef struct {
 
 typedef struct {
   float *kbase, *vbase;
+  int mode;            // QLLAMA_MODE_*
+  void *fa_scratch;    // fast mode: split-K attention partials and counters
+  // a captured graph bakes in the device addresses of the model it was made
+  // for; it is reused only while that model (by generation, never by address,
+  // which the allocator may hand out again) and the sampler buffers are the same
   void *graph;
-  const void *graph_owner;
+  uint64_t graph_gen;
   // sampled step (sampler kernels, then the decode step) for one parameter set
   void *sgraph;
-  const void *sgraph_owner, *sgraph_scratch;
+  uint64_t sgraph_gen, sgraph_smp_gen;
   float sg_t, sg_p;
   int sg_k;
   struct FDev *fdev;   // fp32 caches: the device model they belong to
 } KVDev;
+
+// Generations start at 1, so a zeroed KVDev matches no model.
+static uint64_t g_generation = 0;
+static uint64_t next_generation(void) { return ++g_generation; }
 
 static int config_valid(const int32_t *cfg) {
   // Same acceptance rule as llama.c:371-386: positive bounded dims, whole GQA
@@ -86,8 +97,9 @@ static int config_valid(const int32_t *cfg) {
 
 // Shapes the kernels of this build support (beyond the reference's own checks).
 static int config_supported(const int32_t *cfg) {
-  const int dm = cfg[1], hd = cfg[5], ff = cfg[6];
+  const int dm = cfg[1], hd = cfg[5], ff = cfg[6], G = cfg[3] / cfg[4];
   if (hd % 2 != 0 || hd > 512) return 0;
+  if (G > 8 || G * hd > 4096) return 0;  // the decode attention serves up to 8 query heads per KV head
   if (dm > 16384 || ff > 32768 || cfg[3] * hd > 32768) return 0;   // rmsnorm holds a row in one block
   if (cfg[7] > 16384) return 0;          // attention keeps a head's softmax weights in LDS
   return 1;
@@ -127,6 +139,24 @@ static void qdev_free(QDev *d) {
   free(d);
 }
 
+// The host-built RoPE tables (rope.c:58-61 with the host libm).
+static int rope_upload(float *dcos, float *dsin, int max_seq, int hd, float base) {
+  const int half = hd / 2;
+  float *ct = (float*)malloc((size_t)max_seq * half * sizeof(float));
+  float *st = (float*)malloc((size_t)max_seq * half * sizeof(float));
+  if (!ct || !st) { free(ct); free(st); return 1; }
+  for (int pos = 0; pos < max_seq; pos++)
+    for (int k = 0; k < half; k++) {
+      float inv_freq = powf(base, -2.0f * (float)k / (float)hd);
+      float ang = (float)pos * inv_freq;
+      ct[(size_t)pos * half + k] = cosf(ang);
+      st[(size_t)pos * half + k] = sinf(ang);
+    }
+  int rc = qhip_h2d(dcos, ct, (size_t)max_seq * half * 4) | qhip_h2d(dsin, st, (size_t)max_seq * half * 4);
+  free(ct); free(st);
+  return rc;
+}
+
 // Allocate one blob holding every weight and the scratch; fill the QLlamaModel
 // view (config ints, QTensor / Tensor device views).
 static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, float eps) {
@@ -145,6 +175,7 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
   if (d->kp_qd > d->kp_max) d->kp_max = d->kp_qd;
   if (d->kp_ff > d->kp_max) d->kp_max = d->kp_ff;
   d->eps = eps; d->rope_base = rope_base;
+  d->gen = next_generation();
   d->attn_scale = 1.0f / sqrtf((float)d->hd);          // llama.c:532
   const int L = d->L;
   d->wqkv = calloc(L, sizeof(int8_t*)); d->wo = calloc(L, sizeof(int8_t*));
@@ -237,22 +268,7 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
 
   // --- RoPE tables: the expressions of rope.c:58-61, evaluated on the host with
   // the same libm, so the device reads bit-identical cos/sin values.
-  float *ct = (float*)malloc((size_t)d->max_seq * half * sizeof(float));
-  float *st = (float*)malloc((size_t)d->max_seq * half * sizeof(float));
-  if (!ct || !st) { free(ct); free(st); qdev_free(d); return 1; }
-  for (int pos = 0; pos < d->max_seq; pos++) {
-    for (int k = 0; k < half; k++) {
-      float inv_freq = powf(rope_base, -2.0f * (float)k / (float)d->hd);
-      float ang = (float)pos * inv_freq;
-      float c = cosf(ang), s = sinf(ang);
-      ct[(size_t)pos * half + k] = c;
-      st[(size_t)pos * half + k] = s;
-    }
-  }
-  int rc = qhip_h2d(d->rope_cos, ct, (size_t)d->max_seq * half * 4) |
-           qhip_h2d(d->rope_sin, st, (size_t)d->max_seq * half * 4);
-  free(ct); free(st);
-  if (rc) { qdev_free(d); return 1; }
+  if (rope_upload(d->rope_cos, d->rope_sin, d->max_seq, d->hd, rope_base)) { qdev_free(d); return 1; }
 
   // --- API view ---
   m->vocab = d->vocab; m->d_model = d->dm; m->n_layers = L; m->n_heads = d->H;
@@ -576,9 +592,15 @@ QLlamaModel q_llama_quantize_from(const LlamaModel *s) {
 // ---------------------------------------------------------------------------
 // KV cache and decode
 // ---------------------------------------------------------------------------
-LlamaKV q_llama_kv_create(const QLlamaModel *m) {
+LlamaKV q_llama_kv_create(const QLlamaModel *m) { return q_llama_kv_create_mode(m, QLLAMA_MODE_EXACT); }
+
+LlamaKV q_llama_kv_create_mode(const QLlamaModel *m, int mode) {
   LlamaKV kv;
   memset(&kv, 0, sizeof kv);
+  if (mode != QLLAMA_MODE_EXACT && mode != QLLAMA_MODE_FAST) {
+    fprintf(stderr, "Error: q_llama_kv_create_mode: unknown mode %d\n", mode);
+    abort();
+  }
   const QDev *d = (const QDev*)m->dev;
   kv.n_layers = m->n_layers; kv.max_seq = m->max_seq; kv.kv_dim = m->n_kv * m->head_dim; kv.len = 0;
   KVDev *kd = (KVDev*)calloc(1, sizeof(KVDev));
@@ -590,6 +612,12 @@ LlamaKV q_llama_kv_create(const QLlamaModel *m) {
   kd->vbase = (float*)qhip_malloc((size_t)m->n_layers * per * 4);
   if (!kd->kbase || !kd->vbase) die("q_llama_kv_create");
   for (int l = 0; l < m->n_layers; l++) { kv.k[l] = kd->kbase + (size_t)l * per; kv.v[l] = kd->vbase + (size_t)l * per; }
+  kd->mode = mode;
+  if (mode == QLLAMA_MODE_FAST && qhip_fattn_ok(d->H, d->KVH, d->hd, d->max_seq)) {
+    const size_t fb = qhip_fattn_scratch(d->H, d->KVH, d->hd, d->max_seq);
+    kd->fa_scratch = qhip_malloc(fb);
+    if (!kd->fa_scratch || qhip_fill_zero(kd->fa_scratch, fb) || qhip_sync()) die("q_llama_kv_create_mode");
+  }
   kv.dev = kd;
   return kv;
 }
@@ -603,7 +631,7 @@ void llama_kv_free(LlamaKV *kv) {
     qhip_sync();
     if (kd->graph) qhip_graph_destroy(kd->graph);
     if (kd->sgraph) qhip_graph_destroy(kd->sgraph);
-    qhip_free(kd->kbase); qhip_free(kd->vbase);
+    qhip_free(kd->kbase); qhip_free(kd->vbase); qhip_free(kd->fa_scratch);
     if (kd->fdev) fdev_release(kd->fdev);
     free(kd);
   } else if (kv->k && kv->v) {
@@ -615,24 +643,32 @@ void llama_kv_free(LlamaKV *kv) {
 }
 
 // Enqueue one token's work (llama.c:534-594): token at d_in[pos], pos = d_state[0].
+// Exact mode forms every float sum in the reference's order; fast mode
+// (QLLAMA_MODE_FAST) runs the split-K attention with an online-softmax merge and
+// tree-ordered rmsnorm sums, with the same integer GEMV arithmetic.
 static int enqueue_step(const QDev *d, const KVDev *kd) {
   const int *dpos = &d->d_state[0];
   const size_t per = (size_t)d->max_seq * d->kvd;
-  const int nbo = qhip_attention_nbm(d->H, d->hd);
+  const int fast = kd->mode == QLLAMA_MODE_FAST, fa = fast && kd->fa_scratch;
+  const int nbo = fa ? d->H : qhip_attention_nbm(d->H, d->hd);
   const int fuse_o = qhip_gemv_fused_ok(d->kp_qd), fuse_gu = qhip_gemv_norm_ok(d->kp_dm, d->dm);
   const int nbh = fuse_gu ? qhip_gemv_norm_blocks(d->dff) : qhip_gemv_blocks(d->dff, d->kp_dm);
   int rc = qhip_embed(d->wte, d->wte_s, d->dm, d->d_in, d->d_state, d->x);
   for (int l = 0; l < d->L && !rc; l++) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
     if (fuse_gu) {       // rmsnorm inside the QKV GEMV
-      rc |= qhip_gemv_plain_norm(2, d->x, d->dm, d->g_attn[l], d->eps, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm,
-                                 d->qkv, d->bqkv[l]);
+      rc |= qhip_gemv_plain_norm(2, fast, d->x, d->dm, d->g_attn[l], d->eps, d->wqkv[l], d->sqkv[l], d->nqkv,
+                                 d->kp_dm, d->qkv, d->bqkv[l]);
     } else {
       rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
       rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
     }
-    rc |= qhip_attention_rope(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos,
-                              d->rope_sin, d->scores, d->o, d->obm);
+    if (fa)
+      rc |= qhip_fattn(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos, d->rope_sin,
+                       1, kd->fa_scratch, d->o, d->obm);
+    else
+      rc |= qhip_attention_rope(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos,
+                                d->rope_sin, d->scores, d->o, d->obm);
     if (fuse_o) {        // o quantized inside the Wo GEMV
       rc |= qhip_gemv_resid_q(6, d->o, d->qd, d->obm, nbo, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x);
     } else {
@@ -640,8 +676,8 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
       rc |= qhip_gemv_dec(1, 6, d->qa, d->as, d->wo[l], d->so[l], d->dm, d->kp_qd, d->x, NULL, NULL, NULL);
     }
     if (fuse_gu) {       // rmsnorm inside the gate|up GEMV
-      rc |= qhip_gemv_swiglu_norm(7, d->x, d->dm, d->g_ffn[l], d->eps, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu,
-                                  d->hbm);
+      rc |= qhip_gemv_swiglu_norm(7, fast, d->x, d->dm, d->g_ffn[l], d->eps, d->wgu[l], d->sgu[l], d->dff, d->kp_dm,
+                                  d->gu, d->hbm);
     } else {
       rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
       rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
@@ -670,14 +706,15 @@ static int run_steps(const QDev *d, KVDev *kd, int n) {
     for (int i = 0; i < n; i++) if (enqueue_step(d, kd)) return 1;
     return 0;
   }
-  if (!kd->graph || kd->graph_owner != (const void*)d) {
+  if (!kd->graph || kd->graph_gen != d->gen) {
     if (kd->graph) { qhip_graph_destroy(kd->graph); kd->graph = NULL; }
     if (qhip_capture_begin()) return 1;
     int rc = enqueue_step(d, kd);
     void *g = NULL;
-    if (qhip_capture_end(&g) || rc) return 1;
+    rc = qhip_capture_end(&g) || rc;
+    if (rc) { if (g) qhip_graph_destroy(g); return 1; }
     kd->graph = g;
-    kd->graph_owner = d;
+    kd->graph_gen = d->gen;
   }
   for (int i = 0; i < n; i++) if (qhip_graph_launch(kd->graph)) return 1;
   return 0;
@@ -698,6 +735,15 @@ static int stage_inputs(const QDev *d, int pos, const int *ids, int n) {
 static void check_step(const QLlamaModel *m, const LlamaKV *kv, const int *ids, int n_ids, int n_pos,
                        const char *who) {
   if (!m || !m->dev || !kv || !kv->dev) { fprintf(stderr, "Error: %s: model or cache not on the GPU\n", who); abort(); }
+  // a cache serves any model of its own shape (llama.c:513-526 sizes it from the
+  // model); one of another shape would be indexed past its buffers
+  if (((const KVDev*)kv->dev)->fdev || kv->n_layers != m->n_layers || kv->max_seq != m->max_seq ||
+      kv->kv_dim != m->n_kv * m->head_dim) {
+    fprintf(stderr, "Error: %s: the cache (%d layers, max_seq %d, kv_dim %d) does not fit this model "
+            "(%d layers, max_seq %d, kv_dim %d)\n", who, kv->n_layers, kv->max_seq, kv->kv_dim, m->n_layers,
+            m->max_seq, m->n_kv * m->head_dim);
+    abort();
+  }
   if (kv->len < 0 || n_pos < 0 || (long long)kv->len + n_pos > m->max_seq) {
     fprintf(stderr, "Error: %s: position %d + %d exceeds max_seq %d\n", who, kv->len, n_pos, m->max_seq);
     abort();
@@ -841,6 +887,7 @@ int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_
 // ---------------------------------------------------------------------------
 typedef struct FDev {
   const void *key_wte, *key_blocks;      // identity of the host model
+  uint64_t gen;                          // identifies this device copy to the graphs of its caches
   int refs;
   int vocab, dm, L, H, KVH, hd, dff, max_seq, qd, kvd, nqkv;
   float eps, attn_scale;
@@ -877,24 +924,6 @@ static FDev *fdev_find(const LlamaModel *m) {
   return NULL;
 }
 
-// The host-built RoPE tables (rope.c:58-61 with the host libm).
-static int rope_upload(float *dcos, float *dsin, int max_seq, int hd, float base) {
-  const int half = hd / 2;
-  float *ct = (float*)malloc((size_t)max_seq * half * sizeof(float));
-  float *st = (float*)malloc((size_t)max_seq * half * sizeof(float));
-  if (!ct || !st) { free(ct); free(st); return 1; }
-  for (int pos = 0; pos < max_seq; pos++)
-    for (int k = 0; k < half; k++) {
-      float inv_freq = powf(base, -2.0f * (float)k / (float)hd);
-      float ang = (float)pos * inv_freq;
-      ct[(size_t)pos * half + k] = cosf(ang);
-      st[(size_t)pos * half + k] = sinf(ang);
-    }
-  int rc = qhip_h2d(dcos, ct, (size_t)max_seq * half * 4) | qhip_h2d(dsin, st, (size_t)max_seq * half * 4);
-  free(ct); free(st);
-  return rc;
-}
-
 static FDev *fdev_upload(const LlamaModel *m) {
   const int32_t cfg[8] = {m->vocab, m->d_model, m->n_layers, m->n_heads, m->n_kv, m->head_dim, m->d_ff, m->max_seq};
   if (!config_valid(cfg) || !config_supported(cfg) || m->d_model > qhip_gemv_f32_max_k() ||
@@ -909,6 +938,7 @@ static FDev *fdev_upload(const LlamaModel *m) {
   FDev *f = (FDev*)calloc(1, sizeof(FDev));
   if (!f) return NULL;
   f->key_wte = m->wte.data; f->key_blocks = m->blocks;
+  f->gen = next_generation();
   f->vocab = m->vocab; f->dm = m->d_model; f->L = m->n_layers; f->H = m->n_heads; f->KVH = m->n_kv;
   f->hd = m->head_dim; f->dff = m->d_ff; f->max_seq = m->max_seq; f->eps = m->eps;
   f->qd = f->H * f->hd; f->kvd = f->KVH * f->hd; f->nqkv = f->qd + 2 * f->kvd;
@@ -1059,7 +1089,7 @@ void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logi
     if (profiling || getenv("QLLAMA_NO_GRAPH")) {
       rc = enqueue_step_f32(f, kd);
     } else {
-      if (!kd->graph || kd->graph_owner != (const void*)f) {
+      if (!kd->graph || kd->graph_gen != f->gen) {
         if (kd->graph) { qhip_graph_destroy(kd->graph); kd->graph = NULL; }
         void *g = NULL;
         rc = qhip_capture_begin();
@@ -1067,7 +1097,8 @@ void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logi
           const int e = enqueue_step_f32(f, kd);
           rc = qhip_capture_end(&g) || e;
         }
-        if (!rc) { kd->graph = g; kd->graph_owner = f; }
+        if (!rc) { kd->graph = g; kd->graph_gen = f->gen; }
+        else if (g) qhip_graph_destroy(g);
       }
       if (!rc) rc = qhip_graph_launch(kd->graph);
     }
@@ -1127,6 +1158,7 @@ typedef struct {
   unsigned long long *rng;      // device RNG state, then the token (tok)
   int *tok;
   unsigned long long *h;        // pinned: [0] RNG state, [1] token
+  uint64_t gen;                 // new generation whenever the device buffers are reallocated
 } SmpBuf;
 static SmpBuf g_smp;
 
@@ -1144,6 +1176,7 @@ static int smp_reserve(int V) {
   if (!g_smp.row || !g_smp.scratch || !g_smp.rng || !g_smp.h) return 1;
   g_smp.tok = (int*)(g_smp.rng + 1);
   g_smp.V = V;
+  g_smp.gen = next_generation();
   return 0;
 }
 
@@ -1202,15 +1235,16 @@ static int run_sampled_steps(const QDev *d, KVDev *kd, int n, float temperature,
     for (int i = 0; i < n; i++) if (enqueue_sampled(d, kd, temperature, top_k, top_p)) return 1;
     return 0;
   }
-  if (!kd->sgraph || kd->sgraph_owner != (const void*)d || kd->sgraph_scratch != g_smp.scratch ||
+  if (!kd->sgraph || kd->sgraph_gen != d->gen || kd->sgraph_smp_gen != g_smp.gen ||
       kd->sg_t != temperature || kd->sg_k != top_k || kd->sg_p != top_p) {
     if (kd->sgraph) { qhip_graph_destroy(kd->sgraph); kd->sgraph = NULL; }
     if (qhip_capture_begin()) return 1;
     int rc = enqueue_sampled(d, kd, temperature, top_k, top_p);
     void *g = NULL;
-    if (qhip_capture_end(&g) || rc) return 1;
+    rc = qhip_capture_end(&g) || rc;
+    if (rc) { if (g) qhip_graph_destroy(g); return 1; }
     kd->sgraph = g;
-    kd->sgraph_owner = d; kd->sgraph_scratch = g_smp.scratch;
+    kd->sgraph_gen = d->gen; kd->sgraph_smp_gen = g_smp.gen;
     kd->sg_t = temperature; kd->sg_k = top_k; kd->sg_p = top_p;
   }
   for (int i = 0; i < n; i++) if (qhip_graph_launch(kd->sgraph)) return 1;
@@ -1361,4 +1395,90 @@ void *qllama_stream(void) { return qhip_init() ? NULL : qhip_stream(); }
 int qllama_profile(int enable) { profiling = enable ? 1 : 0; return qhip_profile_enable(enable); }
 int qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max) {
   return qhip_profile_read(names, names_len, ms, count, max);
+}
+
+// Op-level decode attention on device-resident data (BASELINE's GQA config):
+// the cache is [n_kv][T][hd] (max_seq = T), position T-1.
+int qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv, int hd,
+                         float rope_base, int mode, int reps, float *o, float *k_row, double *us_per_call) {
+  if (qhip_init()) return 1;
+  if (T <= 0 || n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || hd <= 0 || (hd & 1) ||
+      (mode != QLLAMA_MODE_EXACT && mode != QLLAMA_MODE_FAST)) {
+    fprintf(stderr, "Error: qllama_gqa_decode_ex: bad shape or mode\n");
+    return 1;
+  }
+  if (mode == QLLAMA_MODE_FAST && !qhip_fattn_ok(n_heads, n_kv, hd, T)) {
+    fprintf(stderr, "Error: qllama_gqa_decode_ex: shape not supported by the fast attention\n");
+    return 1;
+  }
+  const int rope = rope_base > 0.0f, qd = n_heads * hd, kvd = n_kv * hd, half = hd / 2;
+  const size_t kvn = (size_t)T * kvd;
+  const size_t sc_bytes = mode == QLLAMA_MODE_FAST ? qhip_fattn_scratch(n_heads, n_kv, hd, T)
+                                                   : qhip_attention_scratch(n_heads, T) * 4;
+  float *dqkv = (float*)qhip_malloc((size_t)(qd + 2 * kvd) * 4), *dk = (float*)qhip_malloc(kvn * 4);
+  float *dv = (float*)qhip_malloc(kvn * 4), *tmp = (float*)qhip_malloc(kvn * 4);
+  float *dout = (float*)qhip_malloc((size_t)qd * 4), *dobm = (float*)qhip_malloc((size_t)qhip_attention_nbm(n_heads, hd) * 4);
+  float *dcos = rope ? (float*)qhip_malloc((size_t)T * half * 4) : NULL;
+  float *dsin = rope ? (float*)qhip_malloc((size_t)T * half * 4) : NULL;
+  void *dsc = qhip_malloc(sc_bytes);
+  int *dpos = (int*)qhip_malloc(256);
+  const int pos = T - 1;
+  int rc = (!dqkv || !dk || !dv || !tmp || !dout || !dobm || !dsc || !dpos || (rope && (!dcos || !dsin))) ? 1 : 0;
+  if (!rc) rc = qhip_h2d(dqkv, q, (size_t)qd * 4) || qhip_h2d(dpos, &pos, 4) || qhip_fill_zero(dsc, sc_bytes);
+  if (!rc && rope) rc = qhip_h2d(dqkv + qd, k + (size_t)pos * kvd, (size_t)kvd * 4) ||
+                        qhip_h2d(dqkv + qd + kvd, v + (size_t)pos * kvd, (size_t)kvd * 4) ||
+                        rope_upload(dcos, dsin, T, hd, rope_base);
+  if (!rc) rc = qhip_h2d(tmp, k, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dk) || qhip_sync() ||
+                qhip_h2d(tmp, v, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dv);
+  const float scale = 1.0f / sqrtf((float)hd);                  // llama.c:532
+#define GQA_LAUNCH()                                                                                            \
+  (mode == QLLAMA_MODE_FAST                                                                                      \
+       ? qhip_fattn(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dcos, dsin, rope, dsc, dout, dobm)          \
+       : (rope ? qhip_attention_rope(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dcos, dsin, (float*)dsc,     \
+                                     dout, dobm)                                                                \
+               : qhip_attention(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, (float*)dsc, dout, dobm)))
+  if (!rc) rc = GQA_LAUNCH() || qhip_sync();
+  if (!rc && reps > 0) {
+    double ms = 0.0;
+    rc = qhip_timer_start();
+    for (int i = 0; i < reps && !rc; i++) rc = GQA_LAUNCH();
+    if (!rc) rc = qhip_timer_stop(&ms);
+    if (!rc && us_per_call) *us_per_call = 1e3 * ms / reps;
+  }
+#undef GQA_LAUNCH
+  if (!rc) rc = qhip_d2h(o, dout, (size_t)qd * 4);
+  if (!rc && k_row)          // row T-1 of every KV head, in the reference's (n_kv*hd) order
+    for (int h = 0; h < n_kv && !rc; h++) rc = qhip_d2h(k_row + (size_t)h * hd, dk + ((size_t)h * T + pos) * hd, (size_t)hd * 4);
+  if (rc) fprintf(stderr, "Error: qllama_gqa_decode_ex: %s\n", qhip_last_error());
+  qhip_free(dqkv); qhip_free(dk); qhip_free(dv); qhip_free(tmp); qhip_free(dout); qhip_free(dobm);
+  qhip_free(dcos); qhip_free(dsin); qhip_free(dsc); qhip_free(dpos);
+  return rc;
+}
+
+// One activation row through the decode GEMV that normalizes its own input
+// (rmsnorm.c:7-21, quantization quant.c:66-78, W8A8 quant.c:79-82): mode 0
+// plain (out: W->cols values), mode 2 SwiGLU over gate columns [0, N) and up
+// columns [N, 2N) of W (out: N = W->cols / 2 values of h, llama.c:583-587).
+// fast selects the fast decode mode's tree-ordered sum of squares.
+int qllama_norm_gemv(const float *x, const float *gamma, float eps, const QTensor *W, int mode, int fast, float *out) {
+  if (qhip_init()) return 1;
+  const int dm = W->rows, cols = W->cols;
+  if (W->layout != QT_LAYOUT_NK || !qhip_gemv_norm_ok(W->kpad, dm) || (mode != 0 && mode != 2) ||
+      (mode == 2 && (cols & 1))) {
+    fprintf(stderr, "Error: qllama_norm_gemv: unsupported shape or mode\n");
+    return 1;
+  }
+  const int N = mode == 2 ? cols / 2 : cols;
+  float *dx = (float*)qhip_malloc((size_t)dm * 4), *dg = (float*)qhip_malloc((size_t)dm * 4);
+  float *dout = (float*)qhip_malloc((size_t)N * 4), *dbm = (float*)qhip_malloc((size_t)qhip_gemv_norm_blocks(N) * 4);
+  int rc = !dx || !dg || !dout || !dbm || qhip_h2d(dx, x, (size_t)dm * 4) || qhip_h2d(dg, gamma, (size_t)dm * 4);
+  if (!rc)
+    rc = mode == 2 ? qhip_gemv_swiglu_norm(QLLAMA_CLS_OTHER, fast, dx, dm, dg, eps, (const int8_t*)W->q, W->scale, N,
+                                           W->kpad, dout, dbm)
+                   : qhip_gemv_plain_norm(QLLAMA_CLS_OTHER, fast, dx, dm, dg, eps, (const int8_t*)W->q, W->scale, N,
+                                          W->kpad, dout, NULL);
+  if (!rc) rc = qhip_d2h(out, dout, (size_t)N * 4);
+  if (rc) fprintf(stderr, "Error: qllama_norm_gemv: %s\n", qhip_last_error());
+  qhip_free(dx); qhip_free(dg); qhip_free(dout); qhip_free(dbm);
+  return rc;
 }

@@ -14,6 +14,8 @@ LIB_PATH = os.path.join(HERE, "libqllama.so")
 
 QT_LAYOUT_NK = 0
 QT_LAYOUT_KN = 1
+MODE_EXACT = 0      # QLLAMA_MODE_EXACT: logits bit-identical to the reference
+MODE_FAST = 1       # QLLAMA_MODE_FAST: split-K attention, tree-ordered norm sums
 
 
 class Tensor(C.Structure):
@@ -80,6 +82,8 @@ def lib():
         L.q_llama_quantize_from.restype = QLlamaModel
         L.q_llama_kv_create.argtypes = [P(QLlamaModel)]
         L.q_llama_kv_create.restype = LlamaKV
+        L.q_llama_kv_create_mode.argtypes = [P(QLlamaModel), C.c_int]
+        L.q_llama_kv_create_mode.restype = LlamaKV
         L.llama_kv_free.argtypes = [P(LlamaKV)]
         L.q_llama_decode_step.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, P(Tensor)]
         L.q_llama_prefill.argtypes = [P(QLlamaModel), P(LlamaKV), P(C.c_int), C.c_int, P(Tensor)]
@@ -113,6 +117,10 @@ def lib():
         L.qllama_device_sync.restype = C.c_int
         L.qllama_test_expf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
         L.qllama_gqa_decode.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 4 + [P(C.c_float)]
+        L.qllama_norm_gemv.argtypes = [P(C.c_float), P(C.c_float), C.c_float, P(QTensor), C.c_int, C.c_int,
+                                       P(C.c_float)]
+        L.qllama_gqa_decode_ex.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 4 + [C.c_float, C.c_int, C.c_int] + \
+            [P(C.c_float), P(C.c_float), P(C.c_double)]
         L.qllama_sync.restype = C.c_int
         L.qllama_stream.restype = C.c_void_p
         L.qllama_profile.argtypes = [C.c_int]
@@ -135,29 +143,37 @@ def host_tensor(a):
 
 
 class Model:
-    """A QLlamaModel plus one LlamaKV, on the GPU."""
+    """A QLlamaModel plus one LlamaKV (decode mode chosen at creation), on the GPU.
+    fork(mode) gives another cache on the same device weights."""
 
-    def __init__(self, m):
+    def __init__(self, m, mode=MODE_EXACT, owner=None):
         self.m = m
-        self.kv = lib().q_llama_kv_create(C.byref(self.m))
+        self.mode = mode
+        self._owner = owner          # the Model that owns the weights, for forks
+        self.kv = lib().q_llama_kv_create_mode(C.byref(self.m), mode)
         self.vocab = m.vocab
         self.logits = np.zeros((1, m.vocab), np.float32)
         self._lt = host_tensor(self.logits)
 
     @classmethod
-    def synth(cls, cfg, rope_base, eps=1e-5, seed=1234, tied=False):
+    def synth(cls, cfg, rope_base, eps=1e-5, seed=1234, tied=False, mode=MODE_EXACT):
         m = QLlamaModel()
         arr = (C.c_int32 * 8)(*cfg)
         if lib().q_llama_model_synth(C.byref(m), arr, rope_base, eps, seed, int(tied)) != 0:
             raise RuntimeError("q_llama_model_synth failed")
-        return cls(m)
+        return cls(m, mode)
 
     @classmethod
-    def load(cls, path):
+    def load(cls, path, mode=MODE_EXACT):
         m = QLlamaModel()
         if lib().q_llama_model_load(os.fsencode(path), C.byref(m)) != 0:
             raise RuntimeError(f"q_llama_model_load failed for {path}")
-        return cls(m)
+        return cls(m, mode)
+
+    def fork(self, mode):
+        """A second cache (q_llama_kv_create_mode) on this model's device weights;
+        close it before the model."""
+        return Model(self.m, mode, owner=self)
 
     @property
     def pos(self):
@@ -201,6 +217,11 @@ class Model:
         return list(out)
 
     def close(self):
+        if self._owner is not None:
+            if self.kv.dev:
+                lib().llama_kv_free(C.byref(self.kv))
+                self.kv.dev = None
+            return
         if self.m.dev:
             lib().llama_kv_free(C.byref(self.kv))
             lib().q_llama_model_free(C.byref(self.m))
@@ -359,6 +380,36 @@ def qacc_columns(qa, qw):
     lib().qacc_columns(qa.ctypes.data_as(C.POINTER(C.c_int8)), qw.ctypes.data_as(C.POINTER(C.c_int8)), K, N,
                        acc.ctypes.data_as(C.POINTER(C.c_int32)))
     return acc
+
+
+def norm_gemv(x, gamma, W, mode=0, fast=False, eps=1e-5):
+    """qllama_norm_gemv: rmsnorm + quantization of the row x inside the decode
+    GEMV against the QWeight W (mode 0 plain, 2 SwiGLU over W's column halves)."""
+    x = np.ascontiguousarray(x, np.float32)
+    g = np.ascontiguousarray(gamma, np.float32)
+    out = np.zeros(W.cols // 2 if mode == 2 else W.cols, np.float32)
+    if lib().qllama_norm_gemv(_f32(x), _f32(g), eps, C.byref(W.t), mode, int(bool(fast)), _f32(out)) != 0:
+        raise RuntimeError("qllama_norm_gemv failed")
+    return out
+
+
+def gqa_decode(q, k, v, n_heads, n_kv, hd, mode=MODE_EXACT, rope_base=0.0, reps=0):
+    """qllama_gqa_decode_ex: decode attention of position T-1 over T cached rows
+    (k, v: (T, n_kv*hd) in the reference's layout).  With rope_base > 0, q and
+    rows T-1 of k and v are unrotated and the device applies RoPE and the cache
+    append.  Returns (o, rotated k row T-1 as cached, microseconds per call or None)."""
+    q = np.ascontiguousarray(q, np.float32).ravel()
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T = k.shape[0]
+    o = np.zeros(n_heads * hd, np.float32)
+    krow = np.zeros(n_kv * hd, np.float32)
+    us = C.c_double(0.0)
+    rc = lib().qllama_gqa_decode_ex(_f32(q), _f32(k), _f32(v), T, n_heads, n_kv, hd, float(rope_base), int(mode),
+                                    int(reps), _f32(o), _f32(krow), C.byref(us))
+    if rc != 0:
+        raise RuntimeError("qllama_gqa_decode_ex failed")
+    return o, krow, (us.value if reps else None)
 
 
 def profile(enable):

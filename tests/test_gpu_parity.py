@@ -298,6 +298,32 @@ def test_gemv_op_level_matches_reference(Q, si):
         W.close()
 
 
+# ---- the decode GEMV's own rmsnorm prologue (rmsnorm.c:7-21 inside k_gemv_dec) --
+@pytest.mark.parametrize("dm", [2048, 4096])
+def test_fused_rmsnorm_gemv_matches_reference(Q, dm):
+    """Every block of the QKV and gate|up decode GEMVs normalizes and quantizes
+    the residual row itself.  On the committed rmsnorm fixtures (rows with
+    non-unit gains) the plain GEMV equals rmsnorm.c's output fed to quant.c's
+    qmatmul bit for bit, and the SwiGLU GEMV equals the oracle's gate and up
+    outputs combined by llama.c:583-587's expression."""
+    xs, g, ys = golden(f"rms_{dm}_x"), golden(f"rms_{dm}_g"), golden(f"rms_{dm}_y")
+    N = 1536
+    w = O.synth(dm * N, 1234, 6000 + dm, 0.02).reshape(dm, N)
+    q, s = O.quantize(w)
+    W = Q.QWeight(w)
+    try:
+        for r in range(xs.shape[0]):
+            out = Q.norm_gemv(xs[r], g, W, mode=0)
+            assert bits_equal(out, O.qmatmul(ys[r:r + 1], q, s)[0]), f"row {r}"
+            h = Q.norm_gemv(xs[r], g, W, mode=2)
+            gu = O.qmatmul(ys[r:r + 1], q, s)[0]
+            gate, up = gu[:N // 2], gu[N // 2:]
+            ref = (gate * (np.float32(1.0) / (np.float32(1.0) + np.exp(-gate)))) * up
+            np.testing.assert_allclose(h, ref, atol=ATOL, rtol=RTOL)
+    finally:
+        W.close()
+
+
 # ---- op-level decode attention (BASELINE config 3) ---------------------------
 @pytest.mark.parametrize("T", [1, 512, 2048, 8192])
 def test_gqa_decode_matches_reference(Q, T):
