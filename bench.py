@@ -317,39 +317,41 @@ def main():
         Q.profile(False)
         return prof
 
-    # exact mode (logits bit-identical to the reference), on the prefilled cache
-    t_exact, pos_first, tok_e = timed_decode(gm, first)
-    prof_exact = kernel_profile(gm, tok_e)
-    # fast mode (split-K attention, tree-ordered norm sums): a second cache on the same weights
+    # exact mode (logits bit-identical to the reference; the headline), on the prefilled cache
+    t_decode, pos_first, tok = timed_decode(gm, first)
+    prof = kernel_profile(gm, tok)
+    # fast mode (split-K attention, tree-ordered norm sums; greedy streams depart
+    # from the reference's, see the design notes): a second cache on the same weights
     gf = gm.fork(Q.MODE_FAST)
     gf.prefill(prompt, want_logits=True)
-    t_decode, pos_fast, tok = timed_decode(gf, int(np.argmax(gf.logits[0])))
+    t_fast, pos_fast, tok_f = timed_decode(gf, int(np.argmax(gf.logits[0])))
     assert pos_fast == pos_first
-    prof = kernel_profile(gf, tok)
+    prof_fast = kernel_profile(gf, tok_f)
     ms_per_step = 1e3 * t_decode / K
     tok_s = K / t_decode
     # context of each timed step: pos + 1 cached rows
     ctx = [pos_first + 1 + i for i in range(K)]
     step_bytes = statistics.mean(decode_bytes(cfg, t) for t in ctx)
     step_frac = step_bytes / (t_decode / K) / (HBM_PEAK_GBS * 1e9)
-    exact_line = {"tok_s": round(K / t_exact, 3), "ms_per_step": round(1e3 * t_exact / K, 4),
-                  "hbm_roofline_frac": round(step_bytes / (t_exact / K) / (HBM_PEAK_GBS * 1e9), 4),
-                  "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof_exact.items())}
-                  if NP else None}
+    fast_line = {"tok_s": round(K / t_fast, 3), "ms_per_step": round(1e3 * t_fast / K, 4),
+                 "hbm_roofline_frac": round(step_bytes / (t_fast / K) / (HBM_PEAK_GBS * 1e9), 4),
+                 "parity": "not bit-exact; greedy stream departs from the reference (tests/test_gpu_fast.py)",
+                 "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof_fast.items())}
+                 if NP else None}
     full = {"fast": full_range(gf), "exact": full_range(gm)} if args.full_range else None
     # sampled decode (sample_token's arithmetic on the device between the steps)
     sampled = None
     if NS:
-        gf.reset(pos_first + K + NP)
+        gm.reset(pos_first + K + NP)
         rng = Q.rng_create(1234)
-        gf.generate(2, 0.8, 40, 0.95, rng)          # allocates the sampler's buffers
+        gm.generate(2, 0.8, 40, 0.95, rng)          # allocates the sampler's buffers
         Q.lib().qllama_device_sync()
         t0 = time.perf_counter()
-        gf.generate(NS, 0.8, 40, 0.95, rng)
+        gm.generate(NS, 0.8, 40, 0.95, rng)
         Q.lib().qllama_device_sync()
         t_s = time.perf_counter() - t0
         sampled = {"tok_s": round(NS / t_s, 3), "steps": NS, "temperature": 0.8, "top_k": 40, "top_p": 0.95,
-                   "ms_per_step": round(1e3 * t_s / NS, 4), "mode": "fast"}
+                   "ms_per_step": round(1e3 * t_s / NS, 4), "mode": "exact"}
     gf.close()
     if args.calib_copy_mib:
         Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
@@ -427,10 +429,10 @@ def main():
         "config": {
             "workload": f"{args.config}-shape int8 LLaMA greedy decode after a {P}-token prefill",
             "cfg": cfg, "rope_base": base, "tied": tied, "prefill_tokens": P,
-            "context_timed": [ctx[0], ctx[-1]], "decode_mode": "fast",
+            "context_timed": [ctx[0], ctx[-1]], "decode_mode": "exact",
         },
         "decode_hbm_roofline_frac": round(step_frac, 4),
-        "decode_exact": exact_line,
+        "decode_fast": fast_line,
         "decode_full_range": full,
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
@@ -441,7 +443,7 @@ def main():
         "model_build_s": round(t_build, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites, fast-mode decode)",
+            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites)",
             "achieved": round(achieved, 1) if achieved else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

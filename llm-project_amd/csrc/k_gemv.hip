@@ -388,7 +388,81 @@ int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const fl
 #undef QG
 }
 
+// Skinny W8A8 product for 2..16 activation rows (qmatmul with a few rows; the
+// batch-8 GEMV of the op-level configuration).  One block of 8 waves per 16
+// output channels; wave w takes the 64-byte K steps w, w + 8, w + 16, ... and
+// forms each with one v_mfma_i32_16x16x64_i8: activation rows as A (rows past M
+// are zero), the 16 weight rows as B.  Fragment layout (as in k_gemm.hip): lane
+// l holds row l % 16 and bytes 16 * (l / 16) .. +15 of the step; result element
+// e of lane l is C[4 * (l / 16) + e][l % 16].  The next batch of steps is in
+// flight while the current one is multiplied.  The waves' int32 tiles are summed
+// in LDS (exact in any order), then out[m][j] = (as[m] * ws[j]) * (float)acc
+// (quant.c:81-82).
+constexpr int kSkWaves = 8, kSkBatch = 4;
+
+__global__ __launch_bounds__(64 * kSkWaves) void k_gemv_mfma(const int8_t *qa, const float *as, int M,
+                                                             const int8_t *W, const float *ws, int N, int kpad,
+                                                             float *out, int ldo) {
+  __shared__ v4i red[kSkWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int fr = lane & 15, kq = lane >> 4;
+  const bool a_ok = fr < M;
+  const int8_t *ap = qa + (size_t)(a_ok ? fr : 0) * kpad + 16 * kq;
+  const int8_t *bp = W + (size_t)min(n0 + fr, N - 1) * kpad + 16 * kq;
+  const int nk = (kpad + 63) / 64;
+  const int ns = wave < nk ? (nk - wave + kSkWaves - 1) / kSkWaves : 0;   // steps of this wave
+  const v4i z = {0, 0, 0, 0};
+  auto load = [&](int i, v4i &a, v4i &b) {
+    const int off = 64 * (wave + kSkWaves * i);
+    const bool in = i < ns && off + 16 * kq < kpad;
+    a = in && a_ok ? *reinterpret_cast<const v4i *>(ap + off) : z;
+    b = in ? __builtin_nontemporal_load(reinterpret_cast<const v4i *>(bp + off)) : z;
+  };
+  v4i acc = z;
+  v4i a0[kSkBatch], b0[kSkBatch], a1[kSkBatch], b1[kSkBatch];
+#pragma unroll
+  for (int u = 0; u < kSkBatch; u++) load(u, a0[u], b0[u]);
+  for (int i0 = 0; i0 < ns; i0 += 2 * kSkBatch) {
+#pragma unroll
+    for (int u = 0; u < kSkBatch; u++) load(i0 + kSkBatch + u, a1[u], b1[u]);
+#pragma unroll
+    for (int u = 0; u < kSkBatch; u++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[u], b0[u], acc, 0, 0, 0);
+    if (i0 + kSkBatch >= ns) break;
+#pragma unroll
+    for (int u = 0; u < kSkBatch; u++) load(i0 + 2 * kSkBatch + u, a0[u], b0[u]);
+#pragma unroll
+    for (int u = 0; u < kSkBatch; u++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[u], b1[u], acc, 0, 0, 0);
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
+    const int l = 16 * (m >> 2) + n, e = m & 3;
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kSkWaves; w++) t += red[w][l][e];
+    if (m < M && n0 + n < N) out[(size_t)m * ldo + n0 + n] = (as[m] * ws[n0 + n]) * (float)t;
+  }
+}
+
 }  // namespace
+
+extern "C" int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws,
+                              int N, int kpad, float *out, int ldo) {
+  if (M < 1 || M > 16 || kpad % 16 || N < 1) return qh::fail_msg("gemv_mfma: needs 1..16 rows and kpad % 16 == 0");
+  QH_LAUNCH(cls, k_gemv_mfma, dim3((N + 15) / 16), dim3(64 * kSkWaves), 0, qa, as, M, W, ws, N, kpad, out, ldo);
+  return 0;
+}
+
+// The W8A8 product of qmatmul for M quantized rows: the decode GEMV for one row,
+// the skinny MFMA kernel up to 16 rows, the MFMA GEMM beyond.
+extern "C" int qhip_qmm_product(const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
+                                int kpad, float *C) {
+  if (M == 1) return qhip_gemv_dec(MODE_PLAIN, QK_OTHER, qa, as, W, ws, N, kpad, C, NULL, NULL, NULL);
+  if (M <= 16) return qhip_gemv_mfma(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
+  return qhip_gemm_i8(0, QK_OTHER, qa, as, W, ws, M, N, kpad, C, N, NULL);
+}
 
 extern "C" int qhip_gemv_blocks(int N, int kpad) {
   switch (kpad) {

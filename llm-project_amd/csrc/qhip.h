@@ -149,6 +149,16 @@ int qhip_gemv_norm_blocks(int N);
 // Quantize v (n values) into qa (kpad, zero padded) and *as from nbm per-block maxima.
 int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa, int kpad, float *as);
 
+// 1..16 activation rows against W [N][kpad] on MFMA (k_gemv.hip):
+// out[m * ldo + j] = (as[m] * ws[j]) * (float)acc[m][j]  (quant.c:81-82).
+int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
+                   int kpad, float *out, int ldo);
+
+// qmatmul's product for M quantized rows (qa [M][kpad], as [M]) into C [M][N]:
+// k_gemv_dec for one row, k_gemv_mfma up to 16, k_gemm_i8 beyond.
+int qhip_qmm_product(const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N, int kpad,
+                     float *C);
+
 // Many-row int8 GEMM on MFMA (k_gemm.hip): out[i][j] for i < M, j < N from
 // activation rows A [M][kpad] and weight rows W [N][kpad] (SwiGLU: [2N][kpad]),
 // with the decode GEMV's epilogues (mode 0 plain + bias, 1 residual, 2 SwiGLU).

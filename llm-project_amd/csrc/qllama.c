@@ -1308,30 +1308,39 @@ void qtensor_quantize(QTensor *t, const float *w) {
   qhip_free(dw);
 }
 
+// qmatmul's device workspace (A, C, the quantized rows and their scales, and an
+// NK copy of a row-major weight), grown to the largest call and kept, so calls
+// after the first of a size allocate nothing.
+static struct { uint8_t *p; size_t bytes; } g_qmm;
+
+static uint8_t *qmm_workspace(size_t bytes) {
+  if (g_qmm.bytes >= bytes) return g_qmm.p;
+  qhip_sync();
+  qhip_free(g_qmm.p);
+  g_qmm.p = (uint8_t*)qhip_malloc(bytes);
+  g_qmm.bytes = g_qmm.p ? bytes : 0;
+  return g_qmm.p;
+}
+
 void qmatmul(const Tensor *A, const QTensor *W, Tensor *C) {
   const int M = A->shape[0], K = W->rows, N = W->cols;
-  const int kp = pad16(K);
+  const int kp = W->layout == QT_LAYOUT_NK ? W->kpad : pad16(K);
   if (qhip_init()) die("qmatmul");
-  float *da = (float*)qhip_malloc((size_t)M * K * 4);
-  float *dc = (float*)qhip_malloc((size_t)M * N * 4);
-  int8_t *qa = (int8_t*)qhip_malloc((size_t)M * kp);
-  float *as = (float*)qhip_malloc((size_t)M * 4);
-  int8_t *wnk = (int8_t*)W->q;
-  int8_t *tmp = NULL;
-  if (!da || !dc || !qa || !as) die("qmatmul");
-  if (W->layout != QT_LAYOUT_NK) {     // row-major device tensor: re-lay it once
-    tmp = (int8_t*)qhip_malloc((size_t)N * kp);
-    if (!tmp || qhip_fill_zero(tmp, (size_t)N * kp) ||
-        qhip_transpose_kn_to_nk((const int8_t*)W->q, K, N, kp, tmp)) die("qmatmul");
-    wnk = tmp;
+  const size_t oc = al256((size_t)M * K * 4), oq = oc + al256((size_t)M * N * 4), os = oq + al256((size_t)M * kp);
+  const size_t ot = os + al256((size_t)M * 4), total = ot + (W->layout != QT_LAYOUT_NK ? al256((size_t)N * kp) : 0);
+  uint8_t *b = qmm_workspace(total);
+  if (!b) die("qmatmul");
+  float *da = (float*)b, *dc = (float*)(b + oc), *as = (float*)(b + os);
+  int8_t *qa = (int8_t*)(b + oq), *wnk = (int8_t*)W->q;
+  if (W->layout != QT_LAYOUT_NK) {     // row-major device tensor: re-lay it
+    wnk = (int8_t*)(b + ot);
+    if (qhip_fill_zero(wnk, (size_t)N * kp) || qhip_transpose_kn_to_nk((const int8_t*)W->q, K, N, kp, wnk))
+      die("qmatmul");
   }
-  if (qhip_h2d(da, A->data, (size_t)M * K * 4) || qhip_fill_zero(qa, (size_t)M * kp) ||
-      qhip_quant_rows(da, M, K, qa, kp, as) ||
-      (M >= 16 ? qhip_gemm_i8(0, 12, qa, as, wnk, W->scale, M, N, kp, dc, N, NULL)    // many rows: MFMA
-               : qhip_gemv(qa, as, M, wnk, W->scale, N, kp, dc, NULL, 0, 12)) ||
+  if (qhip_h2d(da, A->data, (size_t)M * K * 4) || qhip_quant_rows(da, M, K, qa, kp, as) ||
+      qhip_qmm_product(qa, as, M, wnk, W->scale, N, kp, dc) ||
       qhip_d2h_async(C->data, dc, (size_t)M * N * 4) || qhip_sync())
     die("qmatmul");
-  qhip_free(da); qhip_free(dc); qhip_free(qa); qhip_free(as); qhip_free(tmp);
 }
 
 void quantize_int8_percol(const float *w, int rows, int cols, signed char *q, float *scale) {

@@ -272,6 +272,23 @@ def test_qmatmul_many_rows_matches_oracle(Q, M, K, N):
     assert bits_equal(Cg, ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(2, 64, 48), (5, 300, 200), (8, 4096, 4096), (16, 1000, 517), (11, 14336, 96)])
+def test_qmatmul_few_rows_matches_oracle(Q, M, K, N):
+    """2..16 rows go through the skinny MFMA kernel (k_gemv_mfma): bit-identical
+    to quant.c:60-85, including K that is not a multiple of the 64-byte step."""
+    rng = np.random.default_rng(M * 131 + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    A[M - 1] = 0.0                               # an all-zero row: scale 1
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    q, s = O.quantize(w)
+    W = Q.QWeight(w)
+    try:
+        Cg = Q.qmatmul(A, W)
+    finally:
+        W.close()
+    assert bits_equal(Cg, O.qmatmul(A, q, s))
+
+
 def test_qacc_columns_exact(Q):
     rng = np.random.default_rng(3)
     qa = rng.integers(-127, 128, 300).astype(np.int8)
