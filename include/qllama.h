@@ -231,8 +231,31 @@ int q_llama_model_save(const QLlamaModel *m, const char *path);
 // read order (llama.c:603-608).  Returns 0 on success.
 int q_llama_tensor_export(const QTensor *t, signed char *q_host, float *scale_host);
 
+// No counterpart in the reference: an allocation-free qmatmul (quant.c:60-85) for
+// callers that cannot allocate -- code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc.  A (M, K = W->rows) and C (M, W->cols)
+// are f32 row-major DEVICE buffers; W is a device QTensor in QT_LAYOUT_NK.  The
+// quantized activation rows live in a static device array of
+// QLLAMA_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), so M *
+// W->kpad + 4 * M + 256 must fit in it (else the call fails with a message),
+// and K <= 16384.  Results equal qmatmul's bit for bit.  The work is enqueued on
+// qllama_stream() and the call returns without waiting (qllama_sync() waits);
+// it calls no hipMalloc, hipFree or allocating library routine after its first
+// call on a device (which looks up the array's address).  Every call on a GPU
+// shares that GPU's array: calls that overlap on one GPU (concurrent graph
+// replays, other streams) race.  Returns 0 on success.
+#define QLLAMA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int qmatmul_device_noalloc(const float *A, int M, const QTensor *W, float *C);
+
 // Device-side helpers for tests and benchmarks.
 int  qllama_device_count(void);
+// Device buffers for callers that bring their own (qmatmul_device_noalloc's A
+// and C): allocate, free (after the stream drains), and synchronous copies in
+// stream order.
+void *qllama_dev_alloc(size_t bytes);
+void qllama_dev_free(void *p);
+int  qllama_h2d(void *dst, const void *src, size_t bytes);
+int  qllama_d2h(void *dst, const void *src, size_t bytes);
 int  qllama_device_sync(void);
 int  qllama_sync(void);
 void *qllama_stream(void);               // the hipStream_t every launch goes to

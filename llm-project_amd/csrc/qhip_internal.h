@@ -20,6 +20,9 @@ int fail_msg(const char *msg);
 int check_launch(const char *what);
 // When profiling is on: a (start, stop) event pair for one launch of class cls.
 bool prof_events(int cls, hipEvent_t *start, hipEvent_t *stop);
+// While suspended, launches take no timing events (an event is created on first
+// use): the allocation-free entry point suspends it around its launches.
+void prof_suspend(int on);
 }  // namespace qh
 
 // Launch on the library stream and turn a launch error into the function's

@@ -37,6 +37,8 @@ hipEvent_t take_event() {
 }  // namespace
 
 namespace qh {
+thread_local int g_prof_suspended = 0;
+void prof_suspend(int on) { g_prof_suspended = on; }
 hipStream_t stream() { return g_stream; }
 int num_cus() { return g_ncu; }
 
@@ -56,7 +58,7 @@ int check_launch(const char *what) {
 }
 
 bool prof_events(int cls, hipEvent_t *start, hipEvent_t *stop) {
-  if (!g_prof) return false;
+  if (!g_prof || g_prof_suspended) return false;
   hipEvent_t a = take_event(), b = take_event();
   if (!a || !b) {
     if (a) g_event_pool.push_back(a);

@@ -1398,6 +1398,10 @@ int q_llama_tensor_export(const QTensor *t, signed char *q_host, float *scale_ho
 // helpers
 // ---------------------------------------------------------------------------
 int qllama_device_count(void) { return qhip_device_count(); }
+void *qllama_dev_alloc(size_t bytes) { return qhip_init() ? NULL : qhip_malloc(bytes); }
+void qllama_dev_free(void *p) { qhip_sync(); qhip_free(p); }
+int qllama_h2d(void *dst, const void *src, size_t bytes) { return qhip_h2d(dst, src, bytes); }
+int qllama_d2h(void *dst, const void *src, size_t bytes) { return qhip_sync() || qhip_d2h(dst, src, bytes); }
 int qllama_device_sync(void) { return qhip_device_sync(); }
 int qllama_sync(void) { return qhip_sync(); }
 void *qllama_stream(void) { return qhip_init() ? NULL : qhip_stream(); }

@@ -114,6 +114,11 @@ def lib():
         L.q_llama_generate.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, C.c_float, C.c_int, C.c_float, P(Rng),
                                        P(C.c_int)]
         L.qllama_device_count.restype = C.c_int
+        L.qllama_dev_alloc.argtypes = [C.c_size_t]
+        L.qllama_dev_alloc.restype = C.c_void_p
+        L.qllama_dev_free.argtypes = [C.c_void_p]
+        L.qllama_h2d.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        L.qllama_d2h.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         L.qllama_device_sync.restype = C.c_int
         L.qllama_test_expf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
         L.qllama_gqa_decode.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 4 + [P(C.c_float)]
