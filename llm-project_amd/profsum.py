@@ -3,6 +3,8 @@
 
   profsum.py stats DIR
       per-kernel table of DIR/*_kernel_stats.csv (--kernel-trace --stats)
+  profsum.py pmc DIR [DIR ...] [--kernels REGEX]
+      per-kernel average of every counter of --pmc runs (one column per counter)
   profsum.py traffic FETCH_DIR WRITE_DIR --copy-bytes N [--json OUT]
       per-kernel HBM traffic from two --pmc runs (FETCH_SIZE, WRITE_SIZE; KiB
       per dispatch), each scaled so that the library's plain copy kernel
@@ -92,6 +94,27 @@ def traffic(fd, wd, copy_bytes, out_json):
             f.write("\n")
 
 
+def pmc(dirs, kernels):
+    """Per-kernel mean of each counter over its dispatches, across --pmc runs."""
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    order = []
+    for d in dirs:
+        for r in csv.DictReader(open(one(os.path.join(d, "*counter_collection.csv")))):
+            k = short_name(r["Kernel_Name"])
+            if kernels and not re.search(kernels, k):
+                continue
+            if k not in vals:
+                order.append(k)
+            vals[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    names = sorted({c for k in vals for c in vals[k]})
+    print("| kernel | dispatches | " + " | ".join(names) + " |")
+    print("|---|---:|" + "---:|" * len(names))
+    for k in order:
+        n = max(len(v) for v in vals[k].values())
+        cells = [f"{sum(vals[k][c]) / len(vals[k][c]):.4g}" if vals[k][c] else "" for c in names]
+        print(f"| `{k}` | {n} | " + " | ".join(cells) + " |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -103,9 +126,14 @@ def main():
     t.add_argument("write_dir")
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--json")
+    p = sub.add_parser("pmc")
+    p.add_argument("dirs", nargs="+")
+    p.add_argument("--kernels", default=None)
     a = ap.parse_args()
     if a.cmd == "stats":
         stats(a.dir, a.top)
+    elif a.cmd == "pmc":
+        pmc(a.dirs, a.kernels)
     else:
         traffic(a.fetch_dir, a.write_dir, a.copy_bytes, a.json)
 
