@@ -47,7 +47,8 @@ extern "C" {
 #define QUANT_H   // everything quant.h declares is declared here
 
 // tensor.h:10-16 (host tensors; inside a QLlamaModel the data pointer is device memory)
-#ifndef TENSOR_H
+#if !defined(TENSOR_H) && !defined(QL_TENSOR_DEFINED)
+#define QL_TENSOR_DEFINED
 typedef struct {
   float *data;
   float *grad;
@@ -263,6 +264,9 @@ void *qllama_stream(void);               // the hipStream_t every launch goes to
 // profiling was on; returns the number of classes written.
 int  qllama_profile(int enable);
 int  qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max);
+// The device tanhf (the one GPT-2's GELU uses) on the float bit patterns start,
+// start+1, ..., start+count-1, written to host memory.  For parity tests.
+int  qllama_test_tanhf(uint32_t start, uint32_t count, float *out);
 // The device expf (the one attention and SwiGLU use) on the float bit patterns
 // start, start+1, ..., start+count-1, written to host memory.  For parity tests.
 int  qllama_test_expf(uint32_t start, uint32_t count, float *out);

@@ -303,7 +303,7 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
 //     (qdev_seqsum.h), then w_j = e_j * (1 / S) into LDS.
 //  3. o_d = sum_j w_j * V_jd, j in order (llama.c:570-575): wave 0 owns the
 //     chains; waves 1-7 form the product tiles.
-template <int CM>
+template <int CM, bool DIVW>
 __device__ __forceinline__ void pv_block(const float *scores, const float *bmax, const float *vc, int T, int h,
                                          int kvh, int hd, int max_seq, int nch, float *o, float *obm, float *lds,
                                          float *red, qd::SeqScratch &seq, const uint64_t *tab) {
@@ -351,8 +351,12 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const float inv = 1.0f / sum;
 #pragma unroll
   for (int c = 0; c < CM; c += 4)
-    if (j0 + c < wcap)
-      *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
+    if (j0 + c < wcap) {
+      if (DIVW)   // model.c:501: (e_j / sum) * V
+        *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] / sum, e[c + 1] / sum, e[c + 2] / sum, e[c + 3] / sum);
+      else        // llama.c:568-571: e_j * (1 / sum)
+        *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
+    }
   qd::lds_sync();
 
   // 3. the chains
@@ -427,6 +431,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   }
 }
 
+template <bool DIVW>
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, const float *bmax, const float *vc,
                                                         const int *d_pos, int H, int KVH, int hd, int max_seq,
                                                         int nch, float *o, float *obm) {
@@ -438,10 +443,10 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   const int h = head_of_block(blockIdx.x, H, KVH);
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
-  if (T <= kPvThreads * 4) pv_block<4>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else if (T <= kPvThreads * 8) pv_block<8>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else if (T <= kPvThreads * 16) pv_block<16>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else pv_block<32>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  if (T <= kPvThreads * 4) pv_block<4, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else if (T <= kPvThreads * 8) pv_block<8, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else if (T <= kPvThreads * 16) pv_block<16, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  else pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
 }
 
 // ---------------------------------------------------------------------------
@@ -728,7 +733,7 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
   return 0;
 }
 
-size_t g_pv_attr_bytes = 0;   // dynamic LDS the PV kernel is currently allowed
+size_t g_pv_attr_bytes[2] = {0, 0};   // dynamic LDS the PV kernels are currently allowed
 
 size_t pv_lds_bytes(int max_seq) {
   return ((size_t)(max_seq + kTile - 1) / kTile * kTile + 2 * kChains * kTS) * 4;
@@ -737,7 +742,7 @@ size_t pv_lds_bytes(int max_seq) {
 }  // namespace
 
 namespace {
-template <bool ROPE>
+template <bool ROPE, bool DIVW = false>
 int attention(const float *q, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv, int hd, int max_seq,
               float scale, const float *cos_t, const float *sin_t, float *scores, float *o, float *obm) {
   const int nch = (max_seq + kScoreBlock - 1) / kScoreBlock;
@@ -747,11 +752,11 @@ int attention(const float *q, float *kc, float *vc, const int *d_pos, int n_head
     return qh::fail_msg("attention: max_seq too large for the LDS-resident weights");
   if ((long long)max_seq * hd >= (1LL << 27))      // V byte offsets (plus prefetch) stay below 2^30
     return qh::fail_msg("attention: KV head region too large");
-  if (pv_lds > 64 * 1024 && pv_lds > g_pv_attr_bytes) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_pv),
+  if (pv_lds > 64 * 1024 && pv_lds > g_pv_attr_bytes[DIVW]) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_pv<DIVW>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)pv_lds);
     if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_attn_pv)", e);
-    g_pv_attr_bytes = pv_lds;
+    g_pv_attr_bytes[DIVW] = pv_lds;
   }
   const int G = n_heads / n_kv;
   if (G * kScoreBlock > 1024 || G * hd > 512 * 8) return qh::fail_msg("attention: more than 8 query heads per KV head");
@@ -768,8 +773,8 @@ int attention(const float *q, float *kc, float *vc, const int *d_pos, int n_head
                 scale, scores, bmax, nch, cos_t, sin_t);
       break;
   }
-  QH_LAUNCH(QK_ATTN_PV, k_attn_pv, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores, bmax,
-            vc, d_pos, n_heads, n_kv, hd, max_seq, nch, o, obm);
+  QH_LAUNCH(QK_ATTN_PV, k_attn_pv<DIVW>, dim3(n_heads, (hd + kChains - 1) / kChains), dim3(kPvThreads), pv_lds, scores,
+            bmax, vc, d_pos, n_heads, n_kv, hd, max_seq, nch, o, obm);
   return 0;
 }
 }  // namespace
@@ -784,6 +789,14 @@ extern "C" int qhip_attention_rope(const float *qkv, float *kc, float *vc, const
                                    int hd, int max_seq, float scale, const float *cos_t, const float *sin_t,
                                    float *scores, float *o, float *obm) {
   return attention<true>(qkv, kc, vc, d_pos, n_heads, n_kv, hd, max_seq, scale, cos_t, sin_t, scores, o, obm);
+}
+
+// GPT-2's decode attention (model.c:485-504): as qhip_attention (q given, row
+// *d_pos already cached) with the weights formed as e_j / sum.
+extern "C" int qhip_attention_div(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads,
+                                  int n_kv, int hd, int max_seq, float scale, float *scores, float *o) {
+  return attention<false, true>(q, const_cast<float *>(kc), const_cast<float *>(vc), d_pos, n_heads, n_kv, hd, max_seq,
+                                scale, nullptr, nullptr, scores, o, nullptr);
 }
 
 // Number of per-block maxima qhip_attention writes to obm.

@@ -35,7 +35,7 @@ constexpr int kFGroups = kFT / 4;                          // groups of 4 rows p
 constexpr int kFSlots = (kFGroups + kFUnits - 1) / kFUnits;   // groups per producer lane and tile
 constexpr int kFD = 6;                                     // tiles whose W values are in flight
 
-enum { FMODE_PLAIN = 0, FMODE_RESID = 1 };
+enum { FMODE_PLAIN = 0, FMODE_RESID = 1, FMODE_RESID_BIAS = 2, FMODE_GELU_BIAS = 3 };
 
 // W values of tile t for this producer lane: slot g covers rows
 // t*kFT + 4*(u + kFUnits*g) + 0..3 of its column.  The loads go through a buffer
@@ -73,7 +73,9 @@ __device__ __forceinline__ void f_produce(float *B, const float *xs, const float
   }
 }
 
-// out[j] = c[j] (+ bias[j]) or out[j] = out[j] + c[j] (llama.c:319-321, 347, 352)
+// out[j] = c[j] (+ bias[j]) or out[j] = out[j] + c[j] (llama.c:319-321, 347, 352);
+// GPT-2 (model.c:505-514, feedforward.c:23-37): out[j] = out[j] + (c[j] + bias[j])
+// and out[j] = gelu(c[j] + bias[j]) (activation.c:43-50)
 template <int MODE>
 __global__ __launch_bounds__(kFThreads) void k_gemv_f32(const float *x, int K, const float *W, int N, float *out,
                                                        const float *bias) {
@@ -128,6 +130,8 @@ __global__ __launch_bounds__(kFThreads) void k_gemv_f32(const float *x, int K, c
     const int j = j0 + tid;
     if (tid < kFC && j < N) {
       if (MODE == FMODE_RESID) out[j] = out[j] + acc;
+      else if (MODE == FMODE_RESID_BIAS) out[j] = out[j] + (acc + bias[j]);
+      else if (MODE == FMODE_GELU_BIAS) out[j] = qd::gelu_tanh(acc + bias[j]);
       else out[j] = bias ? acc + bias[j] : acc;
     }
   } else {
@@ -189,28 +193,34 @@ __global__ void k_swiglu_f32(const float *gu, int dff, float *h) {
 }
 
 size_t gemv_lds(int K) { return ((size_t)(K + kFT - 1) / kFT * kFT + 2 * kFC * kFS) * 4; }
-size_t g_lds_attr[2] = {0, 0};
+size_t g_lds_attr[4] = {0, 0, 0, 0};
 
 }  // namespace
 
 // Largest K the fp32 GEMV takes (x and two product tiles in LDS).
 extern "C" int qhip_gemv_f32_max_k(void) { return 32768; }
 
-extern "C" int qhip_gemv_f32(int residual, int cls, const float *x, int K, const float *W, int N, float *out,
+extern "C" int qhip_gemv_f32(int mode, int cls, const float *x, int K, const float *W, int N, float *out,
                              const float *bias) {
   if (K <= 0 || N <= 0 || K > qhip_gemv_f32_max_k()) return qh::fail_msg("gemv_f32: bad shape");
+  if (mode < 0 || mode > 3 || (mode >= 2 && !bias)) return qh::fail_msg("gemv_f32: bad mode");
   const size_t lds = gemv_lds(K);
-  const int m = residual ? 1 : 0;
-  const void *fn = residual ? reinterpret_cast<const void *>(k_gemv_f32<FMODE_RESID>)
-                            : reinterpret_cast<const void *>(k_gemv_f32<FMODE_PLAIN>);
-  if (lds > 64 * 1024 && lds > g_lds_attr[m]) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const void *fns[4] = {reinterpret_cast<const void *>(k_gemv_f32<FMODE_PLAIN>),
+                        reinterpret_cast<const void *>(k_gemv_f32<FMODE_RESID>),
+                        reinterpret_cast<const void *>(k_gemv_f32<FMODE_RESID_BIAS>),
+                        reinterpret_cast<const void *>(k_gemv_f32<FMODE_GELU_BIAS>)};
+  if (lds > 64 * 1024 && lds > g_lds_attr[mode]) {
+    hipError_t e = hipFuncSetAttribute(fns[mode], hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_gemv_f32)", e);
-    g_lds_attr[m] = lds;
+    g_lds_attr[mode] = lds;
   }
   const dim3 grid((N + kFC - 1) / kFC);
-  if (residual) QH_LAUNCH(cls, k_gemv_f32<FMODE_RESID>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias);
-  else QH_LAUNCH(cls, k_gemv_f32<FMODE_PLAIN>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias);
+  switch (mode) {
+    case 0: QH_LAUNCH(cls, k_gemv_f32<FMODE_PLAIN>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias); break;
+    case 1: QH_LAUNCH(cls, k_gemv_f32<FMODE_RESID>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias); break;
+    case 2: QH_LAUNCH(cls, k_gemv_f32<FMODE_RESID_BIAS>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias); break;
+    default: QH_LAUNCH(cls, k_gemv_f32<FMODE_GELU_BIAS>, grid, dim3(kFThreads), lds, x, K, W, N, out, bias); break;
+  }
   return 0;
 }
 

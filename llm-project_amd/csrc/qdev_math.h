@@ -66,6 +66,113 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2
   return res;
 }
 
+// ---------------------------------------------------------------------------
+// tanhf with the results of glibc 2.35's, which the reference's GELU calls
+// (activation.c:43-50).  Published method (glibc sysdeps/ieee754/flt-32/
+// s_tanhf.c and s_expm1f.c, from Sun's fdlibm): tanh(x) = 1 - 2 / (expm1(2|x|)
+// + 2) for |x| >= 1, -t / (t + 2) with t = expm1(-2|x|) below, and expm1 by an
+// argument reduction x = k ln2 + r (ln2 split in two floats) and a rational
+// correction of degree 5 in r^2, all in float (glibc's generic float build has
+// no fused multiply-adds).  Checked against the host libm on every float input
+// (tests/test_gpu_gpt.py).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float expm1f_glibc(float x) {
+  const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f;
+  const float o_threshold = 8.8721679688e+01f, ln2_hi = 6.9313812256e-01f, ln2_lo = 9.0580006145e-06f;
+  const float invln2 = 1.4426950216e+00f;
+  const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f, Q4 = 4.0082177293e-06f,
+              Q5 = -2.0109921195e-07f;
+  float y, hi, lo, c = 0.0f, t, e, hxs, hfx, r1;
+  int k;
+  uint32_t hx = __builtin_bit_cast(uint32_t, x);
+  const uint32_t xsb = hx & 0x80000000u;
+  hx &= 0x7fffffffu;
+  if (hx >= 0x4195b844u) {                       // |x| >= 27 ln2
+    if (hx >= 0x42b17218u) {
+      if (hx > 0x7f800000u) return x + x;        // NaN
+      if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;
+      if (x > o_threshold) return huge * huge;
+    }
+    if (xsb != 0) return tiny - one;
+  }
+  if (hx > 0x3eb17218u) {                        // |x| > ln2 / 2: reduce
+    if (hx < 0x3F851592u) {
+      if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+      else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+    } else {
+      k = (int)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+      t = (float)k;
+      hi = x - t * ln2_hi;
+      lo = t * ln2_lo;
+    }
+    x = hi - lo;
+    c = (hi - x) - lo;
+  } else if (hx < 0x33000000u) {                 // |x| < 2^-25
+    t = huge + x;
+    return x - (t - (huge + x));
+  } else {
+    k = 0;
+  }
+  hfx = 0.5f * x;
+  hxs = x * hfx;
+  r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+  t = 3.0f - r1 * hfx;
+  e = hxs * ((r1 - t) / (6.0f - x * t));
+  if (k == 0) return x - (x * e - hxs);
+  e = (x * (e - c) - c);
+  e -= hxs;
+  if (k == -1) return 0.5f * (x - e) - 0.5f;
+  if (k == 1) {
+    if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+    return one + 2.0f * (x - e);
+  }
+  if (k <= -2 || k > 56) {
+    y = one - (e - x);
+    y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
+    return y - one;
+  }
+  if (k < 23) {
+    t = __builtin_bit_cast(float, 0x3f800000u - (0x1000000u >> k));     // 1 - 2^-k
+    y = t - (e - x);
+    y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
+  } else {
+    t = __builtin_bit_cast(float, (uint32_t)(0x7f - k) << 23);          // 2^-k
+    y = x - (e + t);
+    y += one;
+    y = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, y) + ((uint32_t)k << 23));
+  }
+  return y;
+}
+
+__host__ __device__ __forceinline__ float tanhf_glibc(float x) {
+  const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+  float t, z;
+  const uint32_t jx = __builtin_bit_cast(uint32_t, x), ix = jx & 0x7fffffffu;
+  if (ix >= 0x7f800000u) return (int)jx >= 0 ? one / x + one : one / x - one;   // +-inf, NaN
+  if (ix < 0x41b00000u) {                        // |x| < 22
+    if (ix == 0) return x;
+    if (ix < 0x24000000u) return x * (one + x);  // |x| < 2^-55
+    if (ix >= 0x3f800000u) {
+      t = expm1f_glibc(two * fabsf(x));
+      z = one - two / (t + two);
+    } else {
+      t = expm1f_glibc(-two * fabsf(x));
+      z = -t / (t + two);
+    }
+  } else {
+    z = one - tiny;
+  }
+  return (int)jx >= 0 ? z : -z;
+}
+
+// GELU, tanh form (activation.c:43-50): 0.5 x (1 + tanh(k (x + 0.044715 x^3))),
+// with C's left-to-right evaluation of the products.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k = 0.7978845608028654f;
+  const float inner = k * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf_glibc(inner));
+}
+
 // Block barrier for LDS hand-offs: waits for this wave's LDS operations and then
 // for the other waves, leaving global loads in flight (__syncthreads() waits for
 // every outstanding global load too, which would stall any prefetch across it).

@@ -50,6 +50,7 @@ int  qhip_timer_stop(double *ms);
 // per-kernel-class timing with HIP events on the library stream
 int  qhip_profile_enable(int on);
 int  qhip_profile_read(char *names, int names_len, double *ms, long long *count, int max);
+int  qhip_profiling(void);
 
 // ---- generator / weights ------------------------------------------------------
 // Seeded N(0, sigma) matrix of the reference's (rows, cols) shape, quantized per
@@ -194,7 +195,8 @@ int qhip_argmax_row(const float *logits, int V, int *tok, int *d_in, const int *
 // reference's row-major (K, N); qhip_panels_f32_size floats); K <= qhip_gemv_f32_max_k().
 size_t qhip_panels_f32_size(int K, int N);
 int qhip_to_panels_f32(const float *src, int K, int N, float *dst);
-int qhip_gemv_f32(int residual, int cls, const float *x, int K, const float *W, int N, float *out, const float *bias);
+// mode 0: out = c (+ bias); 1: out += c; 2: out = out + (c + bias); 3: out = gelu(c + bias).
+int qhip_gemv_f32(int mode, int cls, const float *x, int K, const float *W, int N, float *out, const float *bias);
 int qhip_gemv_f32_max_k(void);
 int qhip_embed_f32(const float *wte, int dm, const int *d_in, const int *d_state, float *x);
 int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y);
@@ -202,6 +204,16 @@ int qhip_swiglu_f32(const float *gu, int dff, float *h);
 
 // cache rows (T, n_kv*hd) in the reference's layout -> [n_kv][T][hd]
 int qhip_kv_relayout(const float *src, int T, int n_kv, int hd, float *dst);
+
+// GPT-2 (GPTC) decode pieces (k_gpt.hip, k_attn.hip): x = wte[token] + wpe[pos];
+// LayerNorm in the reference's order (layernorm.c:8-38); the new k, v rows of
+// qkv = [q | k | v] into caches [head][max_seq][head_dim]; decode attention with
+// weights e_j / sum (model.c:485-504).
+int qhip_gpt_embed(const float *wte, const float *wpe, int dm, const int *d_in, const int *d_state, float *x);
+int qhip_layernorm_f32(const float *x, int dm, const float *gamma, const float *beta, float eps, float *y);
+int qhip_gpt_kv_append(const float *qkv, int dm, int hd, int max_seq, const int *d_state, float *kc, float *vc);
+int qhip_attention_div(const float *q, const float *kc, const float *vc, const int *d_pos, int n_heads, int n_kv,
+                       int hd, int max_seq, float scale, float *scores, float *o);
 
 // reference-layout column accumulate (matrix.c:354-374) for qacc_columns
 int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc);

@@ -325,3 +325,6 @@ extern "C" int qhip_timer_stop(double *ms) {
   *ms = t;
   return 0;
 }
+
+// 1 while per-kernel event timing is on (callers launch eagerly then).
+extern "C" int qhip_profiling(void) { return g_prof ? 1 : 0; }

@@ -52,6 +52,22 @@ class QLlamaBlock(C.Structure):
                 ("b_v", Tensor)] + [(n, QTensor) for n in ("Wq", "Wk", "Wv", "Wo", "Wgate", "Wup", "Wdown")]
 
 
+class BlockWeights(C.Structure):               # model.h:8-16
+    _fields_ = [(n, Tensor) for n in ("W_q", "W_k", "W_v", "W_o", "b_q", "b_k", "b_v", "b_o", "gamma1", "beta1",
+                                      "gamma2", "beta2", "ff_W1", "ff_b1", "ff_W2", "ff_b2")]
+
+
+class GPT(C.Structure):                        # model.h:19-31
+    _fields_ = [(n, C.c_int) for n in ("vocab_size", "d_model", "n_heads", "n_layers", "d_ff", "max_seq_len")] + \
+               [("wte", Tensor), ("wpe", Tensor), ("blocks", C.POINTER(BlockWeights)), ("ln_f_gamma", Tensor),
+                ("ln_f_beta", Tensor), ("lm_head", Tensor)]
+
+
+class KVCache(C.Structure):                    # model.h:124-129 + the device handle
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "d_model", "n_heads", "max_seq_len", "len")] + \
+               [("K", C.POINTER(Tensor)), ("V", C.POINTER(Tensor)), ("dev", C.c_void_p)]
+
+
 class Rng(C.Structure):
     _fields_ = [("state", C.c_ulonglong)]        # sampler.h:15-17
 
@@ -113,6 +129,14 @@ def lib():
         L.sample_token.argtypes = [P(Tensor), C.c_int, C.c_float, C.c_int, C.c_float, P(Rng)]
         L.q_llama_generate.argtypes = [P(QLlamaModel), P(LlamaKV), C.c_int, C.c_float, C.c_int, C.c_float, P(Rng),
                                        P(C.c_int)]
+        L.gpt_load.argtypes = [C.c_char_p, P(GPT)]
+        L.gpt_save.argtypes = [C.c_char_p, P(GPT)]
+        L.gpt_free.argtypes = [P(GPT)]
+        L.gpt_kvcache_create.argtypes = [P(GPT)]
+        L.gpt_kvcache_create.restype = KVCache
+        L.gpt_kvcache_free.argtypes = [P(KVCache)]
+        L.gpt_decode_step.argtypes = [P(GPT), P(KVCache), C.c_int, P(Tensor)]
+        L.qllama_test_tanhf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
         L.qllama_device_count.restype = C.c_int
         L.qllama_dev_alloc.argtypes = [C.c_size_t]
         L.qllama_dev_alloc.restype = C.c_void_p
@@ -311,6 +335,102 @@ class FModel:
             self.close()
         except Exception:
             pass
+
+
+# ---- GPT-2 (GPTC) path ------------------------------------------------------------
+GPT_BLOCK = ("W_q", "W_k", "W_v", "W_o", "b_q", "b_k", "b_v", "b_o", "gamma1", "beta1", "gamma2", "beta2",
+             "ff_W1", "ff_b1", "ff_W2", "ff_b2")
+
+
+def host_gpt(cfg, tensors):
+    """A reference GPT (host memory, model.h:19-31) over float32 arrays given in
+    the GPTC order (checkpoint.c:17-44) as (name, array) pairs; cfg = (vocab,
+    d_model, n_heads, n_layers, d_ff, max_seq).  The arrays are kept alive by
+    the returned object."""
+    keep = []
+
+    def T(a):
+        a = np.ascontiguousarray(a, np.float32)
+        keep.append(a)
+        t = host_tensor(a)
+        keep.append(t._keep)
+        return t
+
+    m = GPT()
+    (m.vocab_size, m.d_model, m.n_heads, m.n_layers, m.d_ff, m.max_seq_len) = cfg
+    it = iter(tensors)
+    m.wte = T(next(it)[1])
+    m.wpe = T(next(it)[1])
+    blocks = (BlockWeights * cfg[3])()
+    for l in range(cfg[3]):
+        for name in GPT_BLOCK:
+            n, a = next(it)
+            assert n == name, (n, name)
+            setattr(blocks[l], name, T(a))
+    m.blocks = blocks
+    m.ln_f_gamma = T(next(it)[1])
+    m.ln_f_beta = T(next(it)[1])
+    m.lm_head = T(next(it)[1])
+    m._keep = (keep, blocks)
+    return m
+
+
+class GPTDecoder:
+    """gpt_kvcache_create / gpt_decode_step of a host GPT, on the GPU."""
+
+    def __init__(self, host):
+        self.m = host
+        self.kv = lib().gpt_kvcache_create(C.byref(self.m))
+        self.logits = np.zeros((1, host.vocab_size), np.float32)
+        self._lt = host_tensor(self.logits)
+
+    @property
+    def pos(self):
+        return self.kv.len
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def step(self, token):
+        lib().gpt_decode_step(C.byref(self.m), C.byref(self.kv), int(token), C.byref(self._lt))
+        return self.logits[0]
+
+    def close(self):
+        if self.kv.dev:
+            lib().gpt_kvcache_free(C.byref(self.kv))
+            self.kv.dev = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def ctypes_byref(obj):
+    return C.byref(obj)
+
+
+def gpt_load(path):
+    """checkpoint.c gpt_load into a host GPT (free it with gpt_free)."""
+    m = GPT()
+    if lib().gpt_load(os.fsencode(path), C.byref(m)) != 0:
+        raise RuntimeError(f"gpt_load failed for {path}")
+    return m
+
+
+def gpt_tensors(m):
+    """(name, array view) of a host GPT in the GPTC order."""
+    V, dm, ff, S = m.vocab_size, m.d_model, m.d_ff, m.max_seq_len
+    A = lambda t, *shape: np.ctypeslib.as_array(t.data, shape=shape)
+    shapes = {"W_q": (dm, dm), "W_k": (dm, dm), "W_v": (dm, dm), "W_o": (dm, dm), "ff_W1": (dm, ff),
+              "ff_b1": (ff,), "ff_W2": (ff, dm)}
+    out = [("wte", A(m.wte, V, dm)), ("wpe", A(m.wpe, S, dm))]
+    for l in range(m.n_layers):
+        for name in GPT_BLOCK:
+            out.append((name, A(getattr(m.blocks[l], name), *shapes.get(name, (dm,)))))
+    return out + [("ln_f_gamma", A(m.ln_f_gamma, dm)), ("ln_f_beta", A(m.ln_f_beta, dm)),
+                  ("lm_head", A(m.lm_head, dm, V))]
 
 
 # ---- sampler.h API ----------------------------------------------------------

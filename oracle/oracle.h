@@ -99,4 +99,28 @@ void or_f32_decode_step(const OrFModel *m, OrKV *kv, int token, float *logits);
 // Bitwise mismatches of got[i] against the host libm expf at bit pattern start+i.
 long long or_expf_mismatches(uint32_t start, uint32_t count, const float *got);
 
+// GPT-2 (GPTC) fp32 model, reference layout (model.h:8-31): matrices (rows = in,
+// cols = out) f32 row-major; wpe (max_seq, d_model); lm_head (d_model, vocab).
+typedef struct {
+  float *Wq, *Wk, *Wv, *Wo, *bq, *bk, *bv, *bo, *g1, *be1, *g2, *be2, *W1, *bf1, *W2, *bf2;
+} OrGBlock;
+
+typedef struct {
+  int vocab, d_model, n_heads, n_layers, d_ff, max_seq;   // the GPTC config order (checkpoint.c:75-77)
+  float *wte, *wpe;
+  OrGBlock *blocks;
+  float *lnf_g, *lnf_b, *lm_head;
+} OrGPT;
+
+void or_layernorm(const float *x, int rows, int cols, const float *gamma, const float *beta, float eps, float *y);
+void or_gelu(const float *x, size_t n, float *y);
+int  or_gpt_alloc(OrGPT *m, const int32_t cfg[6]);
+int  or_gpt_synth(OrGPT *m, const int32_t cfg[6], uint64_t seed);
+void or_gpt_free(OrGPT *m);
+int  or_gpt_tensors(const OrGPT *m, float **list, size_t *sizes);    // GPTC order (checkpoint.c:17-44)
+uint64_t or_gpt_hash(const OrGPT *m);
+int  or_gkv_create(OrKV *kv, const OrGPT *m);                       // kv_dim = d_model
+void or_gpt_decode_step(const OrGPT *m, OrKV *kv, int token, float *logits);
+long long or_tanhf_mismatches(uint32_t start, uint32_t count, const float *got);
+
 #endif

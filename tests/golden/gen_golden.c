@@ -16,6 +16,10 @@
 //                                  and print its digest
 //   gen_golden <outdir> sample     sample_token draws, and the `llama` command's
 //                                  sampled loop (main.c:658-669) on the tiny model
+//   gen_golden <outdir> gpt <name>  tiny | gpt2s: greedy streams of the GPT-2 KV
+//                                  decode (gpt_decode_step, model.c:457-520)
+//   gen_golden <outdir> gpthash <file>   load a GPTC file with gpt_load and print
+//                                  its digest
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -30,6 +34,8 @@
 #include "rope.h"
 #include "gqa.h"
 #include "sampler.h"
+#include "model.h"
+#include "checkpoint.h"
 #include "synth.h"
 
 static const char *OUT = ".";
@@ -608,6 +614,97 @@ static void fx_cli_f32(FILE *js) {
   free(seq); tensor_free(&logits); llama_kv_free(&kv); llama_model_free(&m);
 }
 
+// ---------------------------------------------------------------------------
+// GPT-2 (GPTC) KV decode: the reference's own model (gpt_create), every weight
+// then overwritten from the generator by its position t in the GPTC order
+// (checkpoint.c:17-44) as tensor id t: matrices, embeddings, biases and
+// LayerNorm betas N(0, 0.02); gammas 1 + N(0, 0.1).
+// ---------------------------------------------------------------------------
+typedef struct { const char *name; int32_t cfg[6]; int prompt, gen; } GCase;   // vocab, dm, heads, layers, ff, seq
+static const GCase GCASES[2] = {
+  {"tiny", {512, 64, 4, 2, 256, 128}, 48, 48},
+  {"gpt2s", {50257, 768, 12, 12, 3072, 1024}, 32, 32},
+};
+
+static int gpt_list(GPT *m, Tensor **t) {
+  int n = 0;
+  t[n++] = &m->wte; t[n++] = &m->wpe;
+  for (int l = 0; l < m->n_layers; l++) {
+    BlockWeights *b = &m->blocks[l];
+    Tensor *blk[16] = {&b->W_q, &b->W_k, &b->W_v, &b->W_o, &b->b_q, &b->b_k, &b->b_v, &b->b_o,
+                       &b->gamma1, &b->beta1, &b->gamma2, &b->beta2, &b->ff_W1, &b->ff_b1, &b->ff_W2, &b->ff_b2};
+    for (int i = 0; i < 16; i++) t[n++] = blk[i];
+  }
+  t[n++] = &m->ln_f_gamma; t[n++] = &m->ln_f_beta; t[n++] = &m->lm_head;
+  return n;
+}
+
+static void build_gpt(GPT *m, const GCase *c, uint64_t seed) {
+  *m = gpt_create(c->cfg[0], c->cfg[1], c->cfg[2], c->cfg[3], c->cfg[4], c->cfg[5]);
+  Tensor **t = malloc(sizeof(Tensor*) * (size_t)(5 + 16 * m->n_layers));
+  const int n = gpt_list(m, t);
+  for (int i = 0; i < n; i++) {
+    const int in_layer = i >= 2 && i < 2 + 16 * m->n_layers, slot = in_layer ? (i - 2) % 16 : -1;
+    const int gamma = (in_layer && (slot == 8 || slot == 10)) || i == n - 3;
+    syn_fill(t[i]->data, t[i]->size, seed, (uint64_t)i, gamma ? 0.1 : 0.02);
+    if (gamma) for (size_t k = 0; k < t[i]->size; k++) t[i]->data[k] = 1.0f + t[i]->data[k];
+  }
+  free(t);
+}
+
+static uint64_t gpt_hash(GPT *m) {
+  Tensor **t = malloc(sizeof(Tensor*) * (size_t)(5 + 16 * m->n_layers));
+  const int n = gpt_list(m, t);
+  uint64_t h = 0;
+  for (int i = 0; i < n; i++) h = h * 31 + syn_hash_f32(t[i]->data, t[i]->size, 0);
+  free(t);
+  return h;
+}
+
+static void run_gpt(const GCase *c) {
+  const uint64_t seed = 1234;
+  GPT m;
+  build_gpt(&m, c, seed);
+  KVCache kv = gpt_kvcache_create(&m);
+  Tensor logits = mat(1, m.vocab_size);
+  const int P = c->prompt, G = c->gen, V = m.vocab_size;
+  int *seq = malloc(sizeof(int) * (size_t)(P + G + 1));
+  uint64_t *lh = malloc(sizeof(uint64_t) * (size_t)(P + G));
+  syn_prompt(seq, P, seed, V);
+  const double t0 = now_s();
+  for (int i = 0; i < P; i++) {
+    gpt_decode_step(&m, &kv, seq[i], &logits);
+    lh[i] = syn_hash_f32(logits.data, (size_t)V, 0);
+  }
+  char nm[128]; long sh[1] = {V < 2048 ? V : 2048};
+  snprintf(nm, sizeof nm, "gpt_%s_logits_prompt_last", c->name);
+  npy_f32(nm, logits.data, 1, sh);
+  int n = P;
+  for (int s = 0; s < G; s++) {
+    const int nxt = sample_argmax(&logits, 0);
+    seq[n++] = nxt;
+    gpt_decode_step(&m, &kv, nxt, &logits);
+    lh[P + s] = syn_hash_f32(logits.data, (size_t)V, 0);
+  }
+  const double t1 = now_s();
+  snprintf(nm, sizeof nm, "gpt_%s_logits_final", c->name);
+  npy_f32(nm, logits.data, 1, sh);
+  char path[1024]; snprintf(path, sizeof path, "%s/gpt_%s.json", OUT, c->name);
+  FILE *js = fopen(path, "w");
+  fprintf(js, "{\n  \"name\": \"%s\", \"seed\": %llu, \"cfg\": [%d,%d,%d,%d,%d,%d],\n", c->name,
+          (unsigned long long)seed, c->cfg[0], c->cfg[1], c->cfg[2], c->cfg[3], c->cfg[4], c->cfg[5]);
+  fprintf(js, "  \"model_hash\": \"%016llx\", \"ref_decode_s\": %.3f,\n  \"prompt\": [",
+          (unsigned long long)gpt_hash(&m), t1 - t0);
+  for (int i = 0; i < P; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"gen\": [");
+  for (int i = P; i < n; i++) fprintf(js, "%s%d", i > P ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"logit_hashes\": [");
+  for (int i = 0; i < P + G; i++) fprintf(js, "%s\"%016llx\"", i ? "," : "", (unsigned long long)lh[i]);
+  fprintf(js, "]\n}\n");
+  fclose(js);
+  free(seq); free(lh); tensor_free(&logits); gpt_kvcache_free(&kv); gpt_free(&m);
+}
+
 int main(int argc, char **argv) {
   if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|sample|e2e <name>\n"); return 2; }
   OUT = argv[1];
@@ -665,6 +762,16 @@ int main(int argc, char **argv) {
     if (llama_model_load(argv[3], &m) != 0) return 1;
     printf("%016llx\n", (unsigned long long)fmodel_hash(&m));
     llama_model_free(&m);
+    return 0;
+  }
+  if (!strcmp(argv[2], "gpt") && argc > 3) {
+    for (int i = 0; i < 2; i++) if (!strcmp(argv[3], GCASES[i].name)) { run_gpt(&GCASES[i]); return 0; }
+  }
+  if (!strcmp(argv[2], "gpthash") && argc > 3) {
+    GPT m;
+    if (gpt_load(argv[3], &m) != 0) return 1;
+    printf("%016llx\n", (unsigned long long)gpt_hash(&m));
+    gpt_free(&m);
     return 0;
   }
   if (!strcmp(argv[2], "e2e") && argc > 3) {

@@ -49,6 +49,17 @@ class OrFModel(C.Structure):
                 ("final_norm", C.POINTER(C.c_float)), ("lm_head", C.POINTER(C.c_float))]
 
 
+class OrGBlock(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in
+                ("Wq", "Wk", "Wv", "Wo", "bq", "bk", "bv", "bo", "g1", "be1", "g2", "be2", "W1", "bf1", "W2", "bf2")]
+
+
+class OrGPT(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("vocab", "d_model", "n_heads", "n_layers", "d_ff", "max_seq")] + \
+               [("wte", C.POINTER(C.c_float)), ("wpe", C.POINTER(C.c_float)), ("blocks", C.POINTER(OrGBlock)),
+                ("lnf_g", C.POINTER(C.c_float)), ("lnf_b", C.POINTER(C.c_float)), ("lm_head", C.POINTER(C.c_float))]
+
+
 class OrKV(C.Structure):
     _fields_ = [("n_layers", C.c_int), ("max_seq", C.c_int), ("kv_dim", C.c_int),
                 ("len", C.c_int), ("k", C.POINTER(C.c_float)), ("v", C.POINTER(C.c_float))]
@@ -103,6 +114,17 @@ def lib():
         L.or_fmodel_free.argtypes = [C.POINTER(OrFModel)]
         L.or_fkv_create.argtypes = [C.POINTER(OrKV), C.POINTER(OrFModel)]
         L.or_f32_decode_step.argtypes = [C.POINTER(OrFModel), C.POINTER(OrKV), C.c_int, fp]
+        L.or_layernorm.argtypes = [fp, C.c_int, C.c_int, fp, fp, C.c_float, fp]
+        L.or_gelu.argtypes = [fp, C.c_size_t, fp]
+        L.or_gpt_synth.argtypes = [C.POINTER(OrGPT), C.POINTER(C.c_int32), C.c_uint64]
+        L.or_gpt_alloc.argtypes = [C.POINTER(OrGPT), C.POINTER(C.c_int32)]
+        L.or_gpt_free.argtypes = [C.POINTER(OrGPT)]
+        L.or_gpt_hash.argtypes = [C.POINTER(OrGPT)]
+        L.or_gpt_hash.restype = C.c_uint64
+        L.or_gkv_create.argtypes = [C.POINTER(OrKV), C.POINTER(OrGPT)]
+        L.or_gpt_decode_step.argtypes = [C.POINTER(OrGPT), C.POINTER(OrKV), C.c_int, fp]
+        L.or_tanhf_mismatches.argtypes = [C.c_uint32, C.c_uint32, fp]
+        L.or_tanhf_mismatches.restype = C.c_longlong
         L.or_rng_create.argtypes = [C.c_uint64]
         L.or_rng_create.restype = C.c_uint64
         L.or_rng_uniform.argtypes = [C.POINTER(C.c_uint64)]
@@ -328,6 +350,90 @@ class FModel:
         if self.m.blocks:
             lib().or_kv_free(C.byref(self.kv))
             lib().or_fmodel_free(C.byref(self.m))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def layernorm(x, g, b, eps=1e-5):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    lib().or_layernorm(fptr(x), rows, cols, fptr(np.ascontiguousarray(g, np.float32)),
+                       fptr(np.ascontiguousarray(b, np.float32)), eps, fptr(y))
+    return y
+
+
+def gelu(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().or_gelu(fptr(x), x.size, fptr(y))
+    return y
+
+
+GPT_BLOCK = ("W_q", "W_k", "W_v", "W_o", "b_q", "b_k", "b_v", "b_o", "gamma1", "beta1", "gamma2", "beta2",
+             "ff_W1", "ff_b1", "ff_W2", "ff_b2")
+_GPT_FIELDS = ("Wq", "Wk", "Wv", "Wo", "bq", "bk", "bv", "bo", "g1", "be1", "g2", "be2", "W1", "bf1", "W2", "bf2")
+
+
+class GPTModel:
+    """Oracle GPT-2 model (model.c:437-520), weights from the generator by GPTC
+    position, or zeros (synth=False) to be filled from caller arrays."""
+
+    def __init__(self, cfg, seed=1234, synth=True):
+        self.cfg = list(cfg)                     # vocab, d_model, n_heads, n_layers, d_ff, max_seq
+        self.m = OrGPT()
+        arr = (C.c_int32 * 6)(*cfg)
+        rc = lib().or_gpt_synth(C.byref(self.m), arr, seed) if synth else lib().or_gpt_alloc(C.byref(self.m), arr)
+        if rc != 0:
+            raise MemoryError("oracle GPT allocation failed")
+        self.kv = OrKV()
+        if lib().or_gkv_create(C.byref(self.kv), C.byref(self.m)) != 0:
+            raise MemoryError("oracle kv allocation failed")
+        self.vocab = cfg[0]
+        self.logits = np.zeros(self.vocab, np.float32)
+
+    def tensors(self):
+        """(name, array view) in the GPTC order (checkpoint.c:17-44), reference shapes."""
+        m = self.m
+        V, dm, ff, S = m.vocab, m.d_model, m.d_ff, m.max_seq
+        A = lambda p, *shape: np.ctypeslib.as_array(p, shape=shape)
+        shapes = {"W_q": (dm, dm), "W_k": (dm, dm), "W_v": (dm, dm), "W_o": (dm, dm), "ff_W1": (dm, ff),
+                  "ff_b1": (ff,), "ff_W2": (ff, dm)}
+        out = [("wte", A(m.wte, V, dm)), ("wpe", A(m.wpe, S, dm))]
+        for l in range(m.n_layers):
+            b = m.blocks[l]
+            for name, fld in zip(GPT_BLOCK, _GPT_FIELDS):
+                out.append((name, A(getattr(b, fld), *shapes.get(name, (dm,)))))
+        return out + [("ln_f_gamma", A(m.lnf_g, dm)), ("ln_f_beta", A(m.lnf_b, dm)), ("lm_head", A(m.lm_head, dm, V))]
+
+    def hash(self):
+        return int(lib().or_gpt_hash(C.byref(self.m)))
+
+    def write_gptc(self, path):
+        """A 'GPTC' v2 checkpoint (checkpoint.c:63-112's byte order): magic, version,
+        6 config ints, then every tensor's f32 values in the GPTC order."""
+        m = self.m
+        with open(path, "wb") as f:
+            f.write(struct.pack("<II", 0x43545047, 2))
+            f.write(struct.pack("<6i", m.vocab, m.d_model, m.n_heads, m.n_layers, m.d_ff, m.max_seq))
+            for _, t in self.tensors():
+                f.write(t.astype("<f4").tobytes())
+
+    def reset(self, length=0):
+        self.kv.len = length
+
+    def step(self, token):
+        lib().or_gpt_decode_step(C.byref(self.m), C.byref(self.kv), token, fptr(self.logits))
+        return self.logits
+
+    def close(self):
+        if self.m.blocks:
+            lib().or_kv_free(C.byref(self.kv))
+            lib().or_gpt_free(C.byref(self.m))
 
     def __del__(self):
         try:

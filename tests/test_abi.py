@@ -12,12 +12,13 @@ import pytest
 import qlib
 
 ROOT = qlib.ROOT
-HEADER = os.path.join(ROOT, "include", "qllama.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("qllama.h", "qgpt.h")]
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"//.*", "", text)
+    text = re.sub(r"(?m)^\s*#.*$", "", text)                 # preprocessor lines
     names = re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{}]*\)\s*;", text)
     return sorted(set(n for n in names if n not in ("sizeof",)))
 
@@ -26,7 +27,8 @@ def test_header_declares_the_reference_api():
     names = declared_functions()
     for ref in ("q_llama_model_load", "q_llama_model_free", "q_llama_quantize_from", "q_llama_kv_create",
                 "llama_kv_free", "q_llama_decode_step", "qtensor_create", "qtensor_free", "qtensor_quantize",
-                "qmatmul", "quantize_int8_percol", "dequantize_int8_percol", "qacc_columns"):
+                "qmatmul", "quantize_int8_percol", "dequantize_int8_percol", "qacc_columns",
+                "gpt_load", "gpt_save", "gpt_free", "gpt_kvcache_create", "gpt_kvcache_free", "gpt_decode_step"):
         assert ref in names
 
 
@@ -51,6 +53,8 @@ def test_struct_layouts_match_header():
     assert C.sizeof(q.QTensor) == 32
     assert q.QLlamaModel.dev.offset == C.sizeof(q.QLlamaModel) - 8
     assert q.LlamaKV.len.offset == 12
+    assert q.KVCache.len.offset == 16 and q.KVCache.dev.offset == C.sizeof(q.KVCache) - 8
+    assert C.sizeof(q.BlockWeights) == 16 * 40
 
 
 def _write(path, header, cfg, fcfg, body=b""):
