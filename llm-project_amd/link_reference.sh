@@ -11,6 +11,10 @@
 #             decode step (llama_kv_create, llama_kv_free, llama_decode_step,
 #             llama.c:275-362) go away: the library serves both paths on the GPU
 #   matrix.c  qacc_columns (matrix.c:370-374) goes away (the library exports it)
+#   model.h   the KVCache typedef and the decode prototypes (model.h:124-136)
+#             become #include "qgpt.h" (KVCache with its device handle)
+#   model.c   gpt_kvcache_create / gpt_kvcache_free / gpt_decode_step
+#             (model.c:437-523) go away: the library serves the GPT-2 decode
 #   quant.c   is not compiled (the library exports its functions)
 # and links -lqllama.  With GPU_SAMPLER=1 in the environment sampler.c is not
 # compiled either: the library's sample_token / sample_argmax / rng_create /
@@ -44,12 +48,20 @@ check llama.c 296 'void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int 
 check llama.c 362 '}'
 check llama.c 447 'static QLlamaBlock q_block_create('
 check matrix.c 370 'void qacc_columns('
+check model.h 124 'typedef struct {'
+check model.h 129 '} KVCache;'
+check model.h 136 'void gpt_decode_step(const GPT *m, KVCache *kv, int token, Tensor *logits);'
+check model.c 437 'KVCache gpt_kvcache_create(const GPT *m) {'
+check model.c 457 'void gpt_decode_step(const GPT *m, KVCache *kv, int token, Tensor *logits) {'
+check model.c 523 '}'
 
 # edits from the bottom up so the earlier line numbers stay valid
 sed -i '108,140d; 94,99c #include "qllama.h"' "$DEST/llama.h"
 sed -i '17d' "$DEST/llama.h"
 sed -i '447,657d; 275,362d' "$DEST/llama.c"
 sed -i '370,374d' "$DEST/matrix.c"
+sed -i '124,136c #include "qgpt.h"' "$DEST/model.h"
+sed -i '437,523d' "$DEST/model.c"
 
 DROP='s/quant\.o//'
 [ "${GPU_SAMPLER:-0}" = 1 ] && DROP='s/quant\.o//; s/sampler\.o//'
