@@ -128,7 +128,9 @@ def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
         tok = int(np.argmax(lg))
     om.close()
     med = statistics.median(times)
+    cpu_model, libc = host_info()
     return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": nthreads, "kind": "port",
+            "cpu_model": cpu_model, "libc": libc,
             "sample": f"{len(times)} decode steps at positions {pos0 + 1}..{pos0 + len(times)} of the same "
                       f"model (weights copied from the GPU, earlier cache rows N(0,1)); median step "
                       f"{med * 1e3:.1f} ms, oracle/liboracle with {nthreads} threads"}
@@ -221,6 +223,157 @@ def main_f32(args, Q, cfg, base, tied, P):
     print(json.dumps(line), flush=True)
 
 
+def host_info():
+    """CPU model and C library of this host (the CPU baseline's context)."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = None
+    return model, libc
+
+
+GEMV_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]   # (M out, K in): BASELINE configs[1]
+
+
+def op_gemv(Q, reps=100):
+    """BASELINE's op-level int8 GEMV: W int8 (K, M) per-channel from the
+    generator's N(0, 0.02) (the parity fixtures' weights), x fp32 N(0, 1) rows,
+    batch 1 and 8, inputs resident in HBM.  Per call: activation quantization +
+    product; the product kernel's own duration gives the roofline."""
+    out = []
+    for si, (M, K) in enumerate(GEMV_SHAPES):
+        W = Q.lib().qtensor_synth(K, M, 1234, 1000 + si, 0.02)
+        try:
+            for B in (1, 8):
+                call, prod, quant = C.c_double(0), C.c_double(0), C.c_double(0)
+                if Q.lib().qllama_bench_qmatmul(C.byref(W), B, reps, C.byref(call), C.byref(prod), C.byref(quant)):
+                    raise RuntimeError("qllama_bench_qmatmul failed")
+                op_bytes = M * K + 4 * M + 4 * B * K + 4 * B * M          # SURVEY 8(d): weights, scales, x, y
+                kern_bytes = M * K + 4 * M + B * K + 4 * B * M            # the product kernel reads int8 rows
+                gbs = kern_bytes / (prod.value * 1e-6) / 1e9
+                out.append({"M": M, "K": K, "batch": B, "kernel": "k_gemv_dec" if B == 1 else "k_gemv_mfma",
+                            "us_per_call": round(call.value, 3), "us_product": round(prod.value, 3),
+                            "us_quant": round(quant.value, 3),
+                            "call_gbs": round(op_bytes / (call.value * 1e-6) / 1e9, 1),
+                            "product_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        finally:
+            Q.lib().qtensor_free(C.byref(W))
+    return out
+
+
+def op_gqa(Q, reps=50):
+    """BASELINE's op-level decode attention: 32 query / 8 KV heads, head_dim 128,
+    RoPE theta 500000 applied on the device to q and the new k row, fp32 cache of
+    N(0, 1) at contexts 1, 512, 2048, 8192; exact and fast modes."""
+    H, KVH, hd = 32, 8, 128
+    rng = np.random.default_rng(11)
+    out = []
+    for T in (1, 512, 2048, 8192):
+        q = rng.standard_normal(H * hd, dtype=np.float32)
+        k = rng.standard_normal((T, KVH * hd), dtype=np.float32)
+        v = rng.standard_normal((T, KVH * hd), dtype=np.float32)
+        for mode, name in ((Q.MODE_EXACT, "exact"), (Q.MODE_FAST, "fast")):
+            _, _, us = Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
+            # kernel time per call: every launch's own events (one warm-up call + reps)
+            Q.profile(True)
+            Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
+            prof = Q.profile_read()
+            Q.profile(False)
+            kern = {c: v_[0] * v_[1] * 1e3 / (reps + 1) for c, v_ in prof.items() if c.startswith("attn")}
+            kus = sum(kern.values())
+            nbytes = 2 * T * KVH * hd * 4
+            out.append({"T": T, "mode": name, "us_per_call": round(us, 3),
+                        "kernel_us": {c: round(x, 3) for c, x in sorted(kern.items())},
+                        "gbs": round(nbytes / (kus * 1e-6) / 1e9, 1) if kus else None,
+                        "frac": round(nbytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if kus else None})
+    return out
+
+
+def small_config(Q, name, steps=64):
+    """Decode (exact and fast modes) and prefill of a smaller BASELINE config."""
+    cfg, base, tied, P = CONFIGS[name]
+    m = Q.Model.synth(cfg, base, seed=1234, tied=tied)
+    f = m.fork(Q.MODE_FAST)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(1234).integers(0, cfg[0], P)]
+        m.prefill(prompt, want_logits=False)
+        m.reset(0)
+        Q.lib().qllama_device_sync()
+        t0 = time.perf_counter()
+        m.prefill(prompt, want_logits=True)
+        Q.lib().qllama_device_sync()
+        t_pf = time.perf_counter() - t0
+        res = {"cfg": cfg, "prefill_tokens": P, "prefill_tok_s": round(P / t_pf, 1)}
+        n = min(steps, cfg[7] - P - 8)
+        for cache, key in ((m, "exact"), (f, "fast")):
+            if cache is f:
+                f.prefill(prompt, want_logits=True)
+            tok = int(np.argmax(cache.logits[0]))
+            out = cache.generate_greedy(tok, 4)
+            Q.lib().qllama_device_sync()
+            pos = cache.pos
+            t0 = time.perf_counter()
+            cache.generate_greedy(out[-1], n)
+            Q.lib().qllama_device_sync()
+            t = time.perf_counter() - t0
+            b = statistics.mean(decode_bytes(cfg, pos + 1 + i) for i in range(n))
+            res[f"decode_{key}_tok_s"] = round(n / t, 1)
+            res[f"decode_{key}_hbm_roofline_frac"] = round(b / (t / n) / (HBM_PEAK_GBS * 1e9), 4)
+        res["decode_context"] = [P + 5, P + 4 + n]
+        return res
+    finally:
+        f.close()
+        m.close()
+
+
+GPT2_SMALL = (50257, 768, 12, 12, 3072, 1024)   # vocab, d_model, heads, layers, d_ff, max_seq
+
+
+def gpt2_decode(Q, prompt=32, steps=32):
+    """GPT-2 (GPTC) KV decode at the GPT-2-small shape, fp32 (gpt_decode_step,
+    host logits as in the reference): numpy N(0, 0.02) weights, gammas 1."""
+    vocab, dm, nh, L, ff, S = GPT2_SMALL
+    rng = np.random.default_rng(5)
+
+    def w(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+    one, zero = np.ones(dm, np.float32), np.zeros(dm, np.float32)
+    t = [("wte", w(vocab, dm)), ("wpe", w(S, dm))]
+    for _ in range(L):
+        t += [("W_q", w(dm, dm)), ("W_k", w(dm, dm)), ("W_v", w(dm, dm)), ("W_o", w(dm, dm)),
+              ("b_q", zero), ("b_k", zero), ("b_v", zero), ("b_o", zero), ("gamma1", one), ("beta1", zero),
+              ("gamma2", one), ("beta2", zero), ("ff_W1", w(dm, ff)), ("ff_b1", np.zeros(ff, np.float32)),
+              ("ff_W2", w(ff, dm)), ("ff_b2", zero)]
+    t += [("ln_f_gamma", one), ("ln_f_beta", zero), ("lm_head", w(dm, vocab))]
+    dec = Q.GPTDecoder(Q.host_gpt(GPT2_SMALL, t))
+    try:
+        ids = rng.integers(0, vocab, prompt)
+        for tok in ids:
+            lg = dec.step(int(tok))
+        tok = int(np.argmax(lg))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tok = int(np.argmax(dec.step(tok)))
+        dt = time.perf_counter() - t0
+    finally:
+        dec.close()
+    wbytes = 4 * (L * (4 * dm * dm + 2 * dm * ff) + dm * vocab)
+    kv = 4 * L * 2 * dm * (prompt + steps // 2)
+    return {"shape": list(GPT2_SMALL), "dtype": "f32", "tok_s": round(steps / dt, 2),
+            "ms_per_step": round(1e3 * dt / steps, 3), "context": [prompt + 1, prompt + steps],
+            "hbm_roofline_frac": round((wbytes + kv) / (dt / steps) / (HBM_PEAK_GBS * 1e9), 4),
+            "note": "gpt_decode_step with host logits each step (as model.c's callers use it)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -243,6 +396,9 @@ def main():
     ap.add_argument("--full-range", action=argparse.BooleanOptionalAction, default=True,
                     help="also decode from the prompt to max_seq in one loop per mode (the config's whole "
                          "decode range)")
+    ap.add_argument("--extras", action=argparse.BooleanOptionalAction, default=True,
+                    help="also measure the op-level GEMV / GQA configs, the 1B and tiny configs, the "
+                         "PCIe-inclusive q_llama_decode_step rate and the GPT-2 decode")
     ap.add_argument("--path", default="int8", choices=["int8", "f32"],
                     help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
     args = ap.parse_args()
@@ -353,6 +509,26 @@ def main():
         sampled = {"tok_s": round(NS / t_s, 3), "steps": NS, "temperature": 0.8, "top_k": 40, "top_p": 0.95,
                    "ms_per_step": round(1e3 * t_s / NS, 4), "mode": "exact"}
     gf.close()
+    # the drop-in q_llama_decode_step: logits copied to the host every token (PCIe),
+    # argmax on the host, as the reference's loop does (main.c:663-668)
+    step_host = None
+    if args.extras and K:
+        gm.reset(pos_first)
+        n = min(K, 32)
+        lg = gm.step(tok)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            lg = gm.step(int(np.argmax(lg)))
+        t_h = time.perf_counter() - t0
+        step_host = {"tok_s": round(n / t_h, 3), "steps": n, "ms_per_step": round(1e3 * t_h / n, 4),
+                     "context": [pos_first + 2, pos_first + 1 + n]}
+    extras = {}
+    if args.extras and args.config == "8b":
+        extras["op_gemv"] = op_gemv(Q)
+        extras["op_gqa"] = op_gqa(Q)
+        extras["config_1b"] = small_config(Q, "1b")
+        extras["config_tiny"] = small_config(Q, "tiny")
+        extras["gpt2_decode"] = gpt2_decode(Q)
     if args.calib_copy_mib:
         Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
         if Q.lib().qllama_test_copy(args.calib_copy_mib << 20) != 0:
@@ -433,6 +609,7 @@ def main():
         },
         "decode_hbm_roofline_frac": round(step_frac, 4),
         "decode_fast": fast_line,
+        "decode_step_host_logits": step_host,
         "decode_full_range": full,
         "decode_bytes_per_token": int(step_bytes),
         "prefill_tok_s": round(P / t_prefill, 2) if P else None,
@@ -455,6 +632,7 @@ def main():
         "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
         "cpu_baseline": cpu,
     }
+    line.update(extras)
     if rank == 0:
         print(json.dumps(line), flush=True)
 

@@ -250,6 +250,13 @@ int qmatmul_device_noalloc(const float *A, int M, const QTensor *W, float *C);
 
 // Device-side helpers for tests and benchmarks.
 int  qllama_device_count(void);
+// A device QTensor (QT_LAYOUT_NK) of the seeded generator's N(0, sigma) (rows,
+// cols) matrix (tensor id tid), quantized per column (quant.c:10-27) on the device.
+QTensor qtensor_synth(int rows, int cols, uint64_t seed, uint64_t tid, double sigma);
+// qmatmul on device-resident data (M rows of N(0, 1) inputs): mean microseconds
+// per call (quantization + product, events around reps calls) and of the product
+// and quantization kernels alone (events on each launch).  Returns 0 on success.
+int  qllama_bench_qmatmul(const QTensor *W, int M, int reps, double *us_call, double *us_product, double *us_quant);
 // Device buffers for callers that bring their own (qmatmul_device_noalloc's A
 // and C): allocate, free (after the stream drains), and synchronous copies in
 // stream order.

@@ -1495,3 +1495,54 @@ int qllama_norm_gemv(const float *x, const float *gamma, float eps, const QTenso
   qhip_free(dx); qhip_free(dg); qhip_free(dout); qhip_free(dbm);
   return rc;
 }
+
+// A device QTensor (NK layout) holding the seeded generator's N(0, sigma) (rows,
+// cols) matrix of tensor id tid, quantized per column (quant.c:10-27): the
+// op-level GEMV configuration's weights, built without a host copy.
+QTensor qtensor_synth(int rows, int cols, uint64_t seed, uint64_t tid, double sigma) {
+  QTensor t = qtensor_create(rows, cols);
+  if (qhip_synth_quant_nk(seed, tid, rows, cols, t.kpad, 0, sigma, (int8_t*)t.q, t.scale) || qhip_sync())
+    die("qtensor_synth");
+  return t;
+}
+
+// Op-level timing of qmatmul on device-resident data: M rows of N(0, 1) inputs
+// (K = W->rows), reps calls after one warm-up.  *us_call: mean time of one call
+// (activation quantization + product, HIP events around the whole sequence);
+// *us_product / *us_quant: mean duration of the product / quantization kernels
+// alone (events bound to each launch).
+int qllama_bench_qmatmul(const QTensor *W, int M, int reps, double *us_call, double *us_product, double *us_quant) {
+  if (qhip_init() || M < 1 || reps < 1 || W->layout != QT_LAYOUT_NK) return 1;
+  const int K = W->rows, N = W->cols, kp = W->kpad;
+  float *da = (float*)qhip_malloc((size_t)M * K * 4), *dc = (float*)qhip_malloc((size_t)M * N * 4);
+  int8_t *qa = (int8_t*)qhip_malloc((size_t)M * kp);
+  float *as = (float*)qhip_malloc((size_t)M * 4);
+  int rc = !da || !dc || !qa || !as || qhip_synth_f32(4321, 77, (size_t)M * K, 1.0, da);
+#define QMM_CALL() (qhip_quant_rows(da, M, K, qa, kp, as) || \
+                    qhip_qmm_product(qa, as, M, (const int8_t*)W->q, W->scale, N, kp, dc))
+  if (!rc) rc = QMM_CALL() || qhip_sync();
+  double ms = 0.0;
+  if (!rc) rc = qhip_timer_start();
+  for (int i = 0; i < reps && !rc; i++) rc = QMM_CALL();
+  if (!rc) rc = qhip_timer_stop(&ms);
+  if (!rc && us_call) *us_call = 1e3 * ms / reps;
+  // the same calls with per-launch events: product (class "other"), quantization ("quant_rows")
+  if (!rc && (us_product || us_quant)) {
+    char names[1024];
+    double cms[32];
+    long long cnt[32];
+    rc = qhip_profile_enable(1);
+    for (int i = 0; i < reps && !rc; i++) rc = QMM_CALL();
+    if (!rc) rc = qhip_sync();
+    const int n = rc ? 0 : qhip_profile_read(names, sizeof names, cms, cnt, 32);
+    qhip_profile_enable(0);
+    char *save = NULL, *tok = strtok_r(names, ",", &save);
+    for (int i = 0; i < n && tok; i++, tok = strtok_r(NULL, ",", &save)) {
+      if (us_product && !strcmp(tok, "other")) *us_product = 1e3 * cms[i];
+      if (us_quant && !strcmp(tok, "quant_rows")) *us_quant = 1e3 * cms[i];
+    }
+  }
+#undef QMM_CALL
+  qhip_free(da); qhip_free(dc); qhip_free(qa); qhip_free(as);
+  return rc;
+}

@@ -137,6 +137,9 @@ def lib():
         L.gpt_kvcache_free.argtypes = [P(KVCache)]
         L.gpt_decode_step.argtypes = [P(GPT), P(KVCache), C.c_int, P(Tensor)]
         L.qllama_test_tanhf.argtypes = [C.c_uint32, C.c_uint32, P(C.c_float)]
+        L.qtensor_synth.argtypes = [C.c_int, C.c_int, C.c_uint64, C.c_uint64, C.c_double]
+        L.qtensor_synth.restype = QTensor
+        L.qllama_bench_qmatmul.argtypes = [P(QTensor), C.c_int, C.c_int] + [P(C.c_double)] * 3
         L.qllama_device_count.restype = C.c_int
         L.qllama_dev_alloc.argtypes = [C.c_size_t]
         L.qllama_dev_alloc.restype = C.c_void_p
