@@ -17,12 +17,14 @@
 // Kernel 2 (k_attn_pv): grid (H, ceil(hd/16)), 512 threads.  All threads form
 //   the head's softmax weights in LDS (each thread a run of consecutive
 //   positions, in registers).  Then lanes 0-15 of wave 0 own 16 output chains
-//   o_d while waves 1-7 stream V tiles of 128 positions, three tiles ahead, and
-//   store the products w_j * V_jd as [d][j] tiles (double-buffered in LDS), so
-//   that the chain lane reads four consecutive positions with one 16-byte LDS
-//   read.  Sixteen chains per block spread a head's V stream over hd/16 CUs:
-//   the rate at which one CU brings in V rows, not the chain, bounded wider
-//   blocks.
+//   o_d while waves 1-7 stream V tiles of 128 positions, five tiles ahead, and
+//   store the products w_j * V_jd as [d][j] tiles (three buffers in LDS, the
+//   producers two tiles ahead of the chains), so that the chain lane reads four
+//   consecutive positions with one 16-byte LDS read and issues the reads of the
+//   next tile before the barrier that ends the current one.  A chain is one
+//   dependent add per position (about 5 clocks with the wave's lanes all
+//   active, which is why lanes 16-63 repeat chain 15); sixteen chains per block
+//   spread a head's V stream over hd/16 CUs.
 #include <hip/hip_runtime.h>
 
 #include "qdev_math.h"
@@ -37,6 +39,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kScoreBlock = 128;        // positions per scores block
 constexpr int kTile = 128;                  // positions per PV tile
 constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
+constexpr int kPBuf = 3;                    // product tiles in LDS
 constexpr int kChains = 16;                 // output dims per PV block (lanes 0-15 of wave 0)
 constexpr int kPvThreads = 512;
 constexpr int kProducers = kPvThreads - 64;
@@ -294,15 +297,107 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
   }
 }
 
+// The chain loop of wave 0 (lane c < kChains owns chain c): for each of the n
+// tiles (buffers 0, 1, 2, 0, ... of 0x2100 bytes, rows of kTS floats), 32
+// 16-byte LDS reads of the lane's row in four groups of eight, each group
+// requested before the previous one is added (s_waitcnt lgkmcnt(8)), the 128
+// dependent adds in position order, and the barrier that ends the tile (not
+// after the last one).  The first group of the next tile is requested before
+// that barrier: the tile has been in LDS since the previous barrier.
+// Written as one asm block because the reads run with exec = lanes 0-15 (one
+// wave's 64-lane 16-byte LDS read costs it about 40 clocks of issue, the
+// 16-lane one about a quarter of that) and the compiler would otherwise copy the
+// conditionally read registers and wait for every read before the adds.  Lanes
+// 16-63 add whatever their registers hold; their sums are never stored.  Every
+// read has landed when the block ends (lgkmcnt(0)), so that no late return
+// writes a register the compiler reuses.
+#define PV_RA(o0, o1, o2, o3, o4, o5, o6, o7)                                                              \
+  "ds_read_b128 v[100:103], %[ad] offset:" #o0 "\n\t"                                                     \
+  "ds_read_b128 v[104:107], %[ad] offset:" #o1 "\n\t"                                                     \
+  "ds_read_b128 v[108:111], %[ad] offset:" #o2 "\n\t"                                                     \
+  "ds_read_b128 v[112:115], %[ad] offset:" #o3 "\n\t"                                                     \
+  "ds_read_b128 v[116:119], %[ad] offset:" #o4 "\n\t"                                                     \
+  "ds_read_b128 v[120:123], %[ad] offset:" #o5 "\n\t"                                                     \
+  "ds_read_b128 v[124:127], %[ad] offset:" #o6 "\n\t"                                                     \
+  "ds_read_b128 v[128:131], %[ad] offset:" #o7 "\n\t"
+#define PV_RB(o0, o1, o2, o3, o4, o5, o6, o7)                                                              \
+  "ds_read_b128 v[132:135], %[ad] offset:" #o0 "\n\t"                                                     \
+  "ds_read_b128 v[136:139], %[ad] offset:" #o1 "\n\t"                                                     \
+  "ds_read_b128 v[140:143], %[ad] offset:" #o2 "\n\t"                                                     \
+  "ds_read_b128 v[144:147], %[ad] offset:" #o3 "\n\t"                                                     \
+  "ds_read_b128 v[148:151], %[ad] offset:" #o4 "\n\t"                                                     \
+  "ds_read_b128 v[152:155], %[ad] offset:" #o5 "\n\t"                                                     \
+  "ds_read_b128 v[156:159], %[ad] offset:" #o6 "\n\t"                                                     \
+  "ds_read_b128 v[160:163], %[ad] offset:" #o7 "\n\t"
+#define PV_X16(reads) "s_mov_b64 %[sx], exec\n\ts_mov_b64 exec, 0xffff\n\t" reads "s_mov_b64 exec, %[sx]\n\t"
+#define PV_A1(r) "v_add_f32 %[acc], %[acc], v" #r "\n\t"
+#define PV_A4(a, b, c, d) PV_A1(a) PV_A1(b) PV_A1(c) PV_A1(d)
+#define PV_ADD_A                                                                                           \
+  PV_A4(100, 101, 102, 103) PV_A4(104, 105, 106, 107) PV_A4(108, 109, 110, 111) PV_A4(112, 113, 114, 115)  \
+  PV_A4(116, 117, 118, 119) PV_A4(120, 121, 122, 123) PV_A4(124, 125, 126, 127) PV_A4(128, 129, 130, 131)
+#define PV_ADD_B                                                                                           \
+  PV_A4(132, 133, 134, 135) PV_A4(136, 137, 138, 139) PV_A4(140, 141, 142, 143) PV_A4(144, 145, 146, 147)  \
+  PV_A4(148, 149, 150, 151) PV_A4(152, 153, 154, 155) PV_A4(156, 157, 158, 159) PV_A4(160, 161, 162, 163)
+
+__device__ __forceinline__ void pv_chain_asm(float &acc, unsigned base, int n) {
+  unsigned ad, bo;
+  uint64_t sx;
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "s_mov_b32 %[bo], 0\n\t"
+      "v_mov_b32 %[ad], %[base]\n\t"
+      PV_X16(PV_RA(0, 16, 32, 48, 64, 80, 96, 112))
+      "1:\n\t"
+      PV_X16(PV_RB(128, 144, 160, 176, 192, 208, 224, 240))
+      "s_waitcnt lgkmcnt(8)\n\t" PV_ADD_A
+      PV_X16(PV_RA(256, 272, 288, 304, 320, 336, 352, 368))
+      "s_waitcnt lgkmcnt(8)\n\t" PV_ADD_B
+      PV_X16(PV_RB(384, 400, 416, 432, 448, 464, 480, 496))
+      "s_waitcnt lgkmcnt(8)\n\t" PV_ADD_A
+      "s_add_u32 %[bo], %[bo], 0x2100\n\t"
+      "s_cmp_eq_u32 %[bo], 0x6300\n\t"
+      "s_cselect_b32 %[bo], 0, %[bo]\n\t"
+      "v_add_u32 %[ad], %[bo], %[base]\n\t"
+      PV_X16(PV_RA(0, 16, 32, 48, 64, 80, 96, 112))
+      "s_waitcnt lgkmcnt(8)\n\t" PV_ADD_B
+      "s_sub_u32 %[n], %[n], 1\n\t"
+      "s_cmp_eq_u32 %[n], 0\n\t"
+      "s_cbranch_scc1 2f\n\t"
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "s_barrier\n\t"
+      "s_branch 1b\n"
+      "2:\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [acc] "+v"(acc), [ad] "=&v"(ad), [bo] "=&s"(bo), [n] "+s"(n), [sx] "=&s"(sx)
+      : [base] "v"(base)
+      : "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112",
+        "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125",
+        "v126", "v127", "v128", "v129", "v130", "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138",
+        "v139", "v140", "v141", "v142", "v143", "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151",
+        "v152", "v153", "v154", "v155", "v156", "v157", "v158", "v159", "v160", "v161", "v162", "v163", "scc",
+        "memory");
+}
+#undef PV_RA
+#undef PV_RB
+#undef PV_X16
+#undef PV_A1
+#undef PV_A4
+#undef PV_ADD_A
+#undef PV_ADD_B
+
 // One PV block with CM softmax terms per thread (512 * CM >= T).
 //  1. Requests the head's block maxima, this thread's CM scores, and the
 //     producers' first three V tiles, in that order, so that each wait leaves
 //     the later requests in flight.
 //  2. Softmax weights (llama.c:557-572): m = max of the block maxima,
-//     e_j = expf(s_j - m) in registers, their sequential sum S exactly
+//     e_j = expf(s_j - m) in registers (all CM terms formed side by side on
+//     every lane, then positions >= T cleared), their sequential sum S exactly
 //     (qdev_seqsum.h), then w_j = e_j * (1 / S) into LDS.
 //  3. o_d = sum_j w_j * V_jd, j in order (llama.c:570-575): wave 0 owns the
-//     chains; waves 1-7 form the product tiles.
+//     chains; waves 1-7 form the product tiles.  Barrier k (k = 0 .. ntile-1,
+//     executed by every wave) certifies that tiles <= k+1 are in LDS and that
+//     the chains are done with tile k-1: tile k sits in buffer k % 3, and the
+//     producers refill buffer (k+2) % 3 = (k-1) % 3 after barrier k.
 template <int CM, bool DIVW>
 __device__ __forceinline__ void pv_block(const float *scores, const float *bmax, const float *vc, int T, int h,
                                          int kvh, int hd, int max_seq, int nch, float *o, float *obm, float *lds,
@@ -310,7 +405,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const int d0 = blockIdx.y * kChains, tid = threadIdx.x;
   const int wcap = (max_seq + kTile - 1) / kTile * kTile;
   float *W = lds;
-  float *P = lds + wcap;                                 // 2 tiles of kChains x kTS
+  float *P = lds + wcap;                                 // kPBuf tiles of kChains x kTS
   const int ntile = (T + kTile - 1) / kTile;
   const float *sh = scores + (size_t)h * max_seq;
 
@@ -344,8 +439,16 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
 
   // 2. softmax weights
   m = block_max<kPvThreads>(m, red);
+  if (__builtin_amdgcn_readfirstlane(j0) < T) {          // waves wholly past T hold zeros only
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = j0 + c < T ? qd::expf_glibc(e[c] - m, tab) : 0.0f;
+    for (int c = 0; c < CM; c++) e[c] = e[c] - m;
+    qd::expf_glibc_n<CM>(e, tab);
+#pragma unroll
+    for (int c = 0; c < CM; c++) e[c] = pv_mask(e[c], j0 + c < T);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CM; c++) e[c] = 0.0f;
+  }
   const float sum =
       qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m, tab); });
   const float inv = 1.0f / sum;
@@ -360,36 +463,15 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   qd::lds_sync();
 
   // 3. the chains
-  if (tid < 64) {                 // lanes past kChains repeat the last chain and store nothing
+  if (tid < 64) {                 // lanes past kChains run garbage chains and store nothing
     const int d = d0 + tid;
     const int crow = tid < kChains ? tid : kChains - 1;
+    const unsigned base = (unsigned)(uintptr_t)(P + crow * kTS);   // LDS byte address of the lane's row
+    static_assert(kChains * kTS * 4 == 0x2100 && kPBuf == 3 && kTile == 128, "pv_chain_asm's constants");
     float acc = 0.0f;
-    for (int t = 0; t < ntile; t++) {
-      lds_barrier();
-      // tile t: four groups of eight 16-byte reads, the next group in flight
-      // while the current one is added
-      const float4 *Pt = reinterpret_cast<const float4 *>(P + (t & 1) * kChains * kTS + crow * kTS);
-      constexpr int GR = 8, NG = kTile / 4 / GR;
-      float4 buf[2][GR];
-#pragma unroll
-      for (int i = 0; i < GR; i++) buf[0][i] = Pt[i];
-#pragma unroll
-      for (int g = 0; g < NG; g++) {
-        if (g + 1 < NG) {
-#pragma unroll
-          for (int i = 0; i < GR; i++) buf[(g + 1) & 1][i] = Pt[(g + 1) * GR + i];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < GR; i++) {
-          acc += buf[g & 1][i].x;
-          acc += buf[g & 1][i].y;
-          acc += buf[g & 1][i].z;
-          acc += buf[g & 1][i].w;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
+    lds_barrier();                                         // barrier 0: tiles 0 and 1
+    int n = ntile;
+    pv_chain_asm(acc, base, n);
     const bool own = tid < kChains && d < hd;
     if (own) o[(size_t)h * hd + d] = acc;
     if (obm) {                 // max |o| of this block, for the activation quantizer
@@ -397,36 +479,27 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
       if (tid == 0) obm[(size_t)h * gridDim.y + blockIdx.y] = mo;
     }
   } else {
-    // tile k is formed from register set k % 3 into LDS buffer k % 2; its V
-    // values are requested three tiles ahead of use
-    float *B0 = P, *B1 = P + kChains * kTS;
+    // tile k is formed from register set k % 3 into LDS buffer k % 3; its V
+    // values are requested five tiles ahead of use (three ahead of forming)
+    float *B0 = P, *B1 = P + kChains * kTS, *B2 = P + 2 * kChains * kTS;
     pv_produce(B0, W, r0, 0, T, cols_full, col_ok, pid);
     pv_load(r0, vrs, vo, 3, ntile, hd);
-    for (int t = 0;; t += 6) {
-      lds_barrier();                                   // consumer takes tile t
-      if (t + 1 >= ntile) break;
-      pv_produce(B1, W, r1, t + 1, T, cols_full, col_ok, pid);
-      pv_load(r1, vrs, vo, t + 4, ntile, hd);
-      lds_barrier();                                   // tile t+1
-      if (t + 2 >= ntile) break;
-      pv_produce(B0, W, r2, t + 2, T, cols_full, col_ok, pid);
-      pv_load(r2, vrs, vo, t + 5, ntile, hd);
-      lds_barrier();                                   // tile t+2
-      if (t + 3 >= ntile) break;
-      pv_produce(B1, W, r0, t + 3, T, cols_full, col_ok, pid);
-      pv_load(r0, vrs, vo, t + 6, ntile, hd);
-      lds_barrier();                                   // tile t+3
-      if (t + 4 >= ntile) break;
-      pv_produce(B0, W, r1, t + 4, T, cols_full, col_ok, pid);
-      pv_load(r1, vrs, vo, t + 7, ntile, hd);
-      lds_barrier();                                   // tile t+4
-      if (t + 5 >= ntile) break;
-      pv_produce(B1, W, r2, t + 5, T, cols_full, col_ok, pid);
-      pv_load(r2, vrs, vo, t + 8, ntile, hd);
-      lds_barrier();                                   // tile t+5
-      if (t + 6 >= ntile) break;
-      pv_produce(B0, W, r0, t + 6, T, cols_full, col_ok, pid);
-      pv_load(r0, vrs, vo, t + 9, ntile, hd);
+    pv_produce(B1, W, r1, 1, T, cols_full, col_ok, pid);   // past the last tile: zeros, never read
+    pv_load(r1, vrs, vo, 4, ntile, hd);
+    lds_barrier();                                         // barrier 0
+    for (int k = 0;; k += 3) {
+      if (k + 1 >= ntile) break;
+      pv_produce(B2, W, r2, k + 2, T, cols_full, col_ok, pid);
+      pv_load(r2, vrs, vo, k + 5, ntile, hd);
+      lds_barrier();                                       // barrier k+1
+      if (k + 2 >= ntile) break;
+      pv_produce(B0, W, r0, k + 3, T, cols_full, col_ok, pid);
+      pv_load(r0, vrs, vo, k + 6, ntile, hd);
+      lds_barrier();                                       // barrier k+2
+      if (k + 3 >= ntile) break;
+      pv_produce(B1, W, r1, k + 4, T, cols_full, col_ok, pid);
+      pv_load(r1, vrs, vo, k + 7, ntile, hd);
+      lds_barrier();                                       // barrier k+3
     }
   }
 }
@@ -491,7 +564,8 @@ __device__ __forceinline__ void pf_softmax_row(float *row, int T, qd::SeqScratch
     for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[i]);
   }
 #pragma unroll
-  for (int c = 0; c < CM; c++) e[c] = qd::expf_glibc(e[c] - m, tab);   // -inf past T: +0
+  for (int c = 0; c < CM; c++) e[c] = e[c] - m;                         // -inf past T: expf gives +0
+  qd::expf_glibc_n<CM>(e, tab);
   const float sum = qd::seq_sum_nonneg<NT, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(row[i] - m, tab); });
   const float inv = 1.0f / sum;
 #pragma unroll
@@ -736,7 +810,7 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
 size_t g_pv_attr_bytes[2] = {0, 0};   // dynamic LDS the PV kernels are currently allowed
 
 size_t pv_lds_bytes(int max_seq) {
-  return ((size_t)(max_seq + kTile - 1) / kTile * kTile + 2 * kChains * kTS) * 4;
+  return ((size_t)(max_seq + kTile - 1) / kTile * kTile + kPBuf * kChains * kTS) * 4;
 }
 
 }  // namespace

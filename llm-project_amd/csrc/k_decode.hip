@@ -265,9 +265,26 @@ int qhip_qacc_kn(const int8_t *qa, const int8_t *qw, int K, int N, int32_t *acc)
 // test entry points
 // ---------------------------------------------------------------------------
 namespace {
+// expf_glibc of inputs start .. start+count-1, eight consecutive inputs per lane
+// also through expf_glibc_n: where the two differ, the lowest bit of the output
+// is flipped, so that the host comparison fails for either form.
 __global__ void k_expf_range(uint32_t start, uint32_t count, float *out) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x)
-    out[i] = qd::expf_glibc(__uint_as_float(start + i));
+  const uint32_t stride = gridDim.x * blockDim.x * 8u;
+  for (uint32_t i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8u; i0 < count; i0 += stride) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = __uint_as_float(start + i0 + u);
+    float a[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) a[u] = v[u];
+    qd::expf_glibc_n<8>(a, qd::kExp2Tab);
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (i0 + u < count) {
+        const uint32_t sc = __float_as_uint(qd::expf_glibc(v[u]));
+        out[i0 + u] = __uint_as_float(sc == __float_as_uint(a[u]) ? sc : sc ^ 1u);
+      }
+  }
 }
 
 // reference cache rows (T, n_kv*hd) -> [n_kv][T][hd]

@@ -48,6 +48,31 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
   return t;
 }
 
+// PRO = 1 inputs of this thread: the maximum of its share of the block maxima
+// vbm (nvbm values) and its NQ chunks of 16 activation values (chunk c =
+// threadIdx.x + 256 * i holds v[16c .. 16c+15], 0 past n).
+template <int KCH, int NQ>
+__device__ __forceinline__ void pro1_load(const float *v, int n, const float *vbm, int nvbm, float (&qx)[NQ][16],
+                                          float &qm) {
+  float mx = 0.0f;
+  for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
+  qm = mx;
+#pragma unroll
+  for (int ci = 0; ci < NQ; ci++) {
+    const int k0 = 16 * (threadIdx.x + 256 * ci);
+    if (k0 + 16 <= n) {
+#pragma unroll
+      for (int e = 0; e < 16; e += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(v + k0 + e);
+        qx[ci][e] = t.x; qx[ci][e + 1] = t.y; qx[ci][e + 2] = t.z; qx[ci][e + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; e++) qx[ci][e] = k0 + e < n ? v[k0 + e] : 0.0f;
+    }
+  }
+}
+
 // KCH = kpad / 1024 chunks of 16 bytes per lane (kpad a multiple of 1024).
 // PRO = 1: the activation arrives unquantized (v, n values, with per-block
 // maxima of |v| in vbm); every block quantizes it itself (quant.c:66-78, the
@@ -56,6 +81,10 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
 // rmsnorm (gain vbm, epsilon eps); every block normalizes and quantizes it
 // itself (the operations of k_rmsnorm_quant) while its first weights are in
 // flight.  PRO = 3: the same with the fast mode's tree-ordered sum of squares.
+// The prologue's inputs are requested before the weights: a wave's loads
+// return in the order they were issued, so waiting for inputs requested after
+// the weights would wait for the weights too, and the prologue would follow the
+// weight stream instead of overlapping it.
 // NS: weight rows (pairs, for SWIGLU) held in registers; rows r+1 .. r+NS-1 are
 // in flight while row r is reduced.
 template <int MODE, int KCH, int R, int PRO, int NS>
@@ -72,26 +101,28 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j0 = (blockIdx.x * 4 + wave) * R;
   float hmax = 0.0f;
+  // the prologue's inputs, then the weights
+  constexpr int CM = PRO >= 2 ? 4 * KCH : 1;         // 256 threads x CM values = kpad
+  float y[CM], gm[CM];
+  if constexpr (PRO >= 2) qd::rmsnorm_load<CM>(v, n, vbm, y, gm);
+  constexpr int NQ = PRO == 1 ? (KCH * 64 + 255) / 256 : 1;   // 16-value chunks per thread
+  float qx[NQ][16], qm = 0.0f;
+  if constexpr (PRO == 1) pro1_load<KCH, NQ>(v, n, vbm, nvbm, qx, qm);
+  __builtin_amdgcn_sched_barrier(0);
   v4i w[NS][KCH], u[NS][KCH];
 #pragma unroll
-  for (int r = 0; r < NS; r++) {                     // weights first: in flight during the prologue
+  for (int r = 0; r < NS; r++) {                     // in flight during the prologue
     if (r < R && j0 + r < N) {
       load_row(w[r], W + (size_t)(j0 + r) * kpad, lane);
       if (MODE == MODE_SWIGLU) load_row(u[r], W + (size_t)(N + j0 + r) * kpad, lane);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   v4i a[KCH];
   float as;
   if constexpr (PRO == 2 || PRO == 3) {
-    constexpr int CM = 4 * KCH;                      // 256 threads x CM values = kpad
-    float y[CM];
-    if constexpr (PRO == 2) {
-      as = qd::rmsnorm_row<256, CM>(v, n, vbm, eps, y, red, seq);
-    } else {
-      float gm[CM];
-      qd::rmsnorm_load<CM>(v, n, vbm, y, gm);
-      as = qd::rmsnorm_apply_fast<256, CM>(n, eps, y, gm, red);
-    }
+    if constexpr (PRO == 2) as = qd::rmsnorm_apply<256, CM>(v, n, eps, y, gm, red, seq);
+    else as = qd::rmsnorm_apply_fast<256, CM>(n, eps, y, gm, red);
     const float inv = 1.0f / as;
 #pragma unroll
     for (int c = 0; c < CM; c += 4)
@@ -100,27 +131,18 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
 #pragma unroll
     for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
   } else if (PRO == 1) {
-    float mx = 0.0f;
-    for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
-    mx = qd::wave_max_f32(mx);
+    float mx = qd::wave_max_f32(qm);
     if (lane == 0) red[wave] = mx;
     qd::lds_sync();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
     const float inv = 1.0f / as;
-    for (int c = threadIdx.x; c < KCH * 64; c += 256) {        // 16 values per chunk
+#pragma unroll
+    for (int ci = 0; ci < NQ; ci++) {                // 16 values per chunk
+      const int c = threadIdx.x + 256 * ci;
+      if (c >= KCH * 64) break;
       const int k0 = 16 * c;
-      float x[16];
-      if (k0 + 16 <= n) {
-#pragma unroll
-        for (int e = 0; e < 16; e += 4) {
-          const float4 t = *reinterpret_cast<const float4 *>(v + k0 + e);
-          x[e] = t.x; x[e + 1] = t.y; x[e + 2] = t.z; x[e + 3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; e++) x[e] = k0 + e < n ? v[k0 + e] : 0.0f;
-      }
+      const float *x = qx[ci];
       v4i pk;
 #pragma unroll
       for (int wd = 0; wd < 4; wd++) {
@@ -350,11 +372,13 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
 // block's prologue runs once: 6 (gate, up) pairs for SwiGLU, 4 rows for QKV.
 constexpr int rows_per_wave(int mode, int pro) { return pro >= 2 ? (mode == MODE_SWIGLU ? 6 : 4) : 2; }
 
-// Weight rows in registers (measured at the 8B shape): two where that keeps
-// every wave resident (the 14336-wide down projection, the QKV GEMV with its
-// prologue), else one.
+// Weight rows in registers (measured at the 8B shape): all of the wave's rows
+// for the GEMVs with a prologue that stay resident with them (QKV: 4, Wo: 2),
+// so that the whole weight stream overlaps the prologue; two for the
+// 14336-wide down projection; else one (the SwiGLU GEMV's 6 row pairs would
+// not stay resident).
 constexpr int weight_slots(int mode, int pro, int kch) {
-  return (pro == 0 && kch == 14) || (pro >= 2 && mode != MODE_SWIGLU) ? 2 : 1;
+  return (pro >= 2 && mode != MODE_SWIGLU) || pro == 1 ? rows_per_wave(mode, pro) : (pro == 0 && kch == 14) ? 2 : 1;
 }
 
 template <int MODE, int PRO>

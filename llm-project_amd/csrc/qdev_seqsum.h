@@ -168,7 +168,15 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   unsigned kp[CM];
   int gh[CM];
   const int gA = seq_grid(fmaxf(P0 * lo, M0)), gB = seq_grid((P0 + loc) * hi);
-  if (__all(gA == gB)) {
+  if (wave * 64 * CM >= n) {
+    // a wave wholly past n holds only +0 terms, and s + 0 is s on any grid: no
+    // step to classify, no hard step, and no boundary to check (gin = -1)
+#pragma unroll
+    for (int c = 0; c < CM; c++) {
+      kp[c] = 0u;
+      gh[c] = 1;
+    }
+  } else if (__all(gA == gB)) {
     // every chunk of the wave is predicted on one grid: only exact ties are hard
 #pragma unroll
     for (int c = 0; c < CM; c++) {
