@@ -70,9 +70,9 @@ typedef struct {
 
 // checkpoint.c:129-174  Read a 'GPTC' v2 checkpoint into a host GPT.
 int gpt_load(const char *path, GPT *out);
-// checkpoint.c:63-112  Write one (same byte order; written in place, not via a temp file).
+// checkpoint.c:62-112  Write one (same byte order; written in place, not via a temp file).
 int gpt_save(const char *path, const GPT *m);
-// model.c (gpt_free): the host model's memory
+// model.c:95-122 (gpt_free): the host model's memory
 void gpt_free(GPT *m);
 // model.c:437-448  A device cache of max_seq_len positions per layer.
 KVCache gpt_kvcache_create(const GPT *m);

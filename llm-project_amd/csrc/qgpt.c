@@ -1,6 +1,6 @@
 // qgpt.c - C11 host side of the GPT-2 (GPTC) KV-cache decode on the GPU: the
 // reference's model.h / checkpoint.h entry points for that path (model.c:437-520,
-// checkpoint.c:63-174) with the same names, argument meaning and errors.
+// checkpoint.c:62-174) with the same names, argument meaning and errors.
 //
 // The model stays the reference's host GPT (fp32 tensors in host memory, as
 // gpt_load fills them).  Each KVCache takes a device copy of the weights when it
