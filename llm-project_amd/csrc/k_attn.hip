@@ -11,9 +11,9 @@
 // (head, d) chains, and between the lanes that form the products w_j * V_jd and
 // the lane that adds them.
 //
-// Kernel 1 (k_attn_scores): grid (H, ceil(max_seq/128)); one thread per (head,
-//   position) computes dot_j and s_j; the block's K rows are copied into LDS
-//   with direct global-to-LDS loads; each block writes its maximum.
+// Kernel 1 (k_attn_scores): grid (n_kv, ceil(max_seq/128)); one thread per
+//   (head, position) computes dot_j and s_j; the block's K rows are copied into
+//   LDS with direct global-to-LDS loads; each block writes its maximum.
 // Kernel 2 (k_attn_pv): grid (H, ceil(hd/16)), 512 threads.  All threads form
 //   the head's softmax weights in LDS (each thread a run of consecutive
 //   positions, in registers).  Then lanes 0-15 of wave 0 own 16 output chains
@@ -36,7 +36,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kScoreBlock = 128;        // positions per scores block
+constexpr int kScoreBlock = 128;        // positions per scores block (two waves per query head)
 constexpr int kTile = 128;                  // positions per PV tile
 constexpr int kTS = kTile + 4;              // LDS row stride of a product tile (conflict-free 16-byte reads)
 constexpr int kPBuf = 3;                    // product tiles in LDS
@@ -147,7 +147,8 @@ __device__ __forceinline__ float score_row_dot(const float *qh, const float *ks,
 
 // One block per (KV head, 128 positions) serves the G = H / n_kv query heads of
 // that group: G x 128 threads, thread (g, t) computes head kvh*G + g at position
-// j0 + t, and the K tile is copied into LDS once for all of them.  With n_kv a
+// j0 + t, and the K tile is copied into LDS once for all of them.  (64-position
+// blocks, twice as many, measured no faster end to end.)  With n_kv a
 // multiple of 8, consecutive KV heads also fall on different XCDs.
 // ROPE: q, k and v of the current position arrive unrotated in qkv (the QKV
 // GEMV's output, H + 2 n_kv heads of hd); every block rotates its G query heads
@@ -222,11 +223,20 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc,
     s = dot * scale;
     scores[(size_t)h * max_seq + j] = s;
   }
-  // per-head block maximum: the head's two waves
+  // per-head block maximum: the head's waves
+  constexpr int WPH = kScoreBlock / 64;                  // waves per query head
   s = qd::wave_max_f32(s);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-  __syncthreads();
-  if (t == 0) bmax[(size_t)h * nch + c] = fmaxf(red[2 * g], red[2 * g + 1]);
+  if (WPH == 1) {
+    if (t == 0) bmax[(size_t)h * nch + c] = s;
+  } else {
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (t == 0) {
+      float mb = red[WPH * g];
+      for (int i = 1; i < WPH; i++) mb = fmaxf(mb, red[WPH * g + i]);
+      bmax[(size_t)h * nch + c] = mb;
+    }
+  }
 }
 
 // Head of PV block x: the query heads of one KV head are given block indices
@@ -833,7 +843,8 @@ int attention(const float *q, float *kc, float *vc, const int *d_pos, int n_head
     g_pv_attr_bytes[DIVW] = pv_lds;
   }
   const int G = n_heads / n_kv;
-  if (G * kScoreBlock > 1024 || G * hd > 512 * 8) return qh::fail_msg("attention: more than 8 query heads per KV head");
+  if (G > 8 || G * kScoreBlock > 1024 || G * hd > 512 * 8)      // qs holds 8 query heads
+    return qh::fail_msg("attention: more than 8 query heads per KV head");
   if (hd > 512 || (hd & 1)) return qh::fail_msg("attention: head_dim must be even and at most 512");
   const dim3 sgrid(n_kv, nch);
   const dim3 sblock(G * kScoreBlock);

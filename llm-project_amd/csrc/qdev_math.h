@@ -66,46 +66,53 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab = kExp2
   return res;
 }
 
-// expf_glibc of N values in place, the same operations stage by stage: all N
-// reductions, then all N table reads, then all N polynomials, so that the
-// values' dependent chains and table reads overlap.  The empty asm marks the
-// main path's result as needed on every lane, so the compiler cannot turn the
-// special-case selects into branches around it (which serialises the values).
+// expf_glibc of N values in place, the same operations stage by stage within
+// batches of up to 8 values: the batch's reductions, then its table reads, then
+// its polynomials, so that the values' dependent chains and table reads overlap
+// (eight at a time: a whole row of 32 would hold 32 doubles of each stage in
+// registers).  The empty asm marks the main path's result as needed on every
+// lane, so the compiler cannot turn the special-case selects into branches
+// around it (which serialises the values).
 template <int N>
 __device__ __forceinline__ void expf_glibc_n(float (&v)[N], const uint64_t *tab) {
+  constexpr int B = N < 8 ? N : 8;
+  static_assert(N % B == 0, "batches of 8");
   const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double Shift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
   const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
   const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  double r[N];
-  uint64_t ki[N], t[N];
 #pragma unroll
-  for (int c = 0; c < N; c++) {
-    const double xd = (double)v[c];
-    double kd = __builtin_fma(InvLn2N, xd, Shift);
-    ki[c] = (uint64_t)__double_as_longlong(kd);
-    kd -= Shift;
-    r[c] = __builtin_fma(InvLn2N, xd, -kd);
-  }
+  for (int b = 0; b < N; b += B) {
+    double r[B];
+    uint64_t ki[B], t[B];
 #pragma unroll
-  for (int c = 0; c < N; c++) t[c] = tab[ki[c] & 31];
+    for (int c = 0; c < B; c++) {
+      const double xd = (double)v[b + c];
+      double kd = __builtin_fma(InvLn2N, xd, Shift);
+      ki[c] = (uint64_t)__double_as_longlong(kd);
+      kd -= Shift;
+      r[c] = __builtin_fma(InvLn2N, xd, -kd);
+    }
 #pragma unroll
-  for (int c = 0; c < N; c++) {
-    const double s = __longlong_as_double((long long)(t[c] + (ki[c] << 47)));
-    const double z = __builtin_fma(C0, r[c], C1);
-    const double r2 = r[c] * r[c];
-    double y = __builtin_fma(C2, r[c], 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    float res = (float)y;
-    asm volatile("" : "+v"(res));
-    const float x = v[c];
-    const uint32_t ux = __float_as_uint(x);
-    res = x < -0x1.9fe368p6f ? 0.0f : res;
-    res = x > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : res;
-    res = ((ux >> 20) & 0x7ffu) >= 0x7f8u && ux != 0xff800000u ? x + x : res;
-    v[c] = res;
+    for (int c = 0; c < B; c++) t[c] = tab[ki[c] & 31];
+#pragma unroll
+    for (int c = 0; c < B; c++) {
+      const double s = __longlong_as_double((long long)(t[c] + (ki[c] << 47)));
+      const double z = __builtin_fma(C0, r[c], C1);
+      const double r2 = r[c] * r[c];
+      double y = __builtin_fma(C2, r[c], 1.0);
+      y = __builtin_fma(z, r2, y);
+      y = y * s;
+      float res = (float)y;
+      asm volatile("" : "+v"(res));
+      const float x = v[b + c];
+      const uint32_t ux = __float_as_uint(x);
+      res = x < -0x1.9fe368p6f ? 0.0f : res;
+      res = x > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : res;
+      res = ((ux >> 20) & 0x7ffu) >= 0x7f8u && ux != 0xff800000u ? x + x : res;
+      v[b + c] = res;
+    }
   }
 }
 
