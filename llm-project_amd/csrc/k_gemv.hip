@@ -48,18 +48,18 @@ __device__ __forceinline__ int dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH])
   return t;
 }
 
-// PRO = 1 inputs of this thread: the maximum of its share of the block maxima
-// vbm (nvbm values) and its NQ chunks of 16 activation values (chunk c =
-// threadIdx.x + 256 * i holds v[16c .. 16c+15], 0 past n).
-template <int KCH, int NQ>
+// PRO = 1 inputs of this thread (one of NTP): the maximum of its share of the
+// block maxima vbm (nvbm values) and its NQ chunks of 16 activation values
+// (chunk c = threadIdx.x + NTP * i holds v[16c .. 16c+15], 0 past n).
+template <int KCH, int NQ, int NTP = 256>
 __device__ __forceinline__ void pro1_load(const float *v, int n, const float *vbm, int nvbm, float (&qx)[NQ][16],
                                           float &qm) {
   float mx = 0.0f;
-  for (int i = threadIdx.x; i < nvbm; i += 256) mx = fmaxf(mx, vbm[i]);
+  for (int i = threadIdx.x; i < nvbm; i += NTP) mx = fmaxf(mx, vbm[i]);
   qm = mx;
 #pragma unroll
   for (int ci = 0; ci < NQ; ci++) {
-    const int k0 = 16 * (threadIdx.x + 256 * ci);
+    const int k0 = 16 * (threadIdx.x + NTP * ci);
     if (k0 + 16 <= n) {
 #pragma unroll
       for (int e = 0; e < 16; e += 4) {
@@ -213,6 +213,204 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
         }
       bm[blockIdx.x] = b;
       bi[blockIdx.x] = i0;
+    }
+  }
+}
+
+// Warp-specialized decode GEMV for the GEMVs with a prologue (PRO 1, 2, 3; the
+// operations of k_gemv_dec's prologues and epilogues, in the same order).  512
+// threads: the first PW waves form the quantized activation and meet at an LDS
+// counter (qd::GroupSync) instead of the block barrier; the RWV waves after them own
+// the output rows, RW consecutive rows (row pairs for SWIGLU) each, request
+// their first NS rows at kernel start and wait on an LDS flag for the
+// activation.  A wave issues its
+// instructions in order and stalls while the memory system holds all it can
+// take, so in k_gemv_dec a wave reaches its prologue only once most of its
+// weight loads are accepted, and every block barrier of the prologue waits for
+// the slowest wave; here the prologue waves issue no weight loads and never
+// wait for a row wave, and the weight stream runs under the whole prologue.
+// The block's one s_barrier, before any wave works, publishes the zeroed
+// counters.  grid: ceil(N / (RWV RW)) blocks; SWIGLU writes one max|h| per block.
+#ifndef QLLAMA_GEMV_WS
+#define QLLAMA_GEMV_WS 1
+#endif
+constexpr bool kUseWs = QLLAMA_GEMV_WS != 0;     // the prologue GEMVs run k_gemv_ws (else k_gemv_dec)
+
+// Prologue waves, row waves and weight slots (rows, or row pairs, in registers
+// per row wave) per mode, measured end to end at the 8B shape (same-box A/B of
+// the decode bench): QKV 8 + 8 waves holding all 3 rows of a row wave; gate|up
+// 4 + 8 waves with 3 row pairs in flight; Wo 4 + 8 waves with 2 rows.  Four
+// waves per SIMD (1024 threads) made the prologue spill; one row wave per SIMD
+// left the stream short of requests.
+#ifndef QLLAMA_WS_PW_PLAIN
+#define QLLAMA_WS_PW_PLAIN 8
+#endif
+#ifndef QLLAMA_WS_RWV_PLAIN
+#define QLLAMA_WS_RWV_PLAIN 8
+#endif
+#ifndef QLLAMA_WS_SLOTS_PLAIN
+#define QLLAMA_WS_SLOTS_PLAIN 12
+#endif
+#ifndef QLLAMA_WS_PW_SWIGLU
+#define QLLAMA_WS_PW_SWIGLU 4
+#endif
+#ifndef QLLAMA_WS_RWV_SWIGLU
+#define QLLAMA_WS_RWV_SWIGLU 8
+#endif
+#ifndef QLLAMA_WS_SLOTS_SWIGLU
+#define QLLAMA_WS_SLOTS_SWIGLU 12
+#endif
+#ifndef QLLAMA_WS_PW_RESID
+#define QLLAMA_WS_PW_RESID 4
+#endif
+#ifndef QLLAMA_WS_RWV_RESID
+#define QLLAMA_WS_RWV_RESID 8
+#endif
+#ifndef QLLAMA_WS_SLOTS_RESID
+#define QLLAMA_WS_SLOTS_RESID 8
+#endif
+constexpr int ws_pro_waves(int mode) {
+  return mode == MODE_PLAIN ? QLLAMA_WS_PW_PLAIN : mode == MODE_SWIGLU ? QLLAMA_WS_PW_SWIGLU : QLLAMA_WS_PW_RESID;
+}
+constexpr int ws_row_waves(int mode) {
+  return mode == MODE_PLAIN ? QLLAMA_WS_RWV_PLAIN : mode == MODE_SWIGLU ? QLLAMA_WS_RWV_SWIGLU : QLLAMA_WS_RWV_RESID;
+}
+// slots x KCH (16-byte chunks per lane and row) is the register budget
+constexpr int ws_slots(int mode, int kch) {
+  const int budget = mode == MODE_PLAIN ? QLLAMA_WS_SLOTS_PLAIN
+                     : mode == MODE_SWIGLU ? QLLAMA_WS_SLOTS_SWIGLU : QLLAMA_WS_SLOTS_RESID;
+  return budget / kch > 0 ? budget / kch : 1;
+}
+
+template <int MODE, int KCH, int PRO, int NS, int PW, int RWV>
+__global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, const float *ws, int N, int kpad, int RW,
+                                                 float *out, const float *bias, float *bm, const float *v, int n,
+                                                 const float *vbm, int nvbm, float eps) {
+  static_assert(PRO >= 1 && PRO <= 3, "prologue GEMVs only");
+  constexpr int NTP = 64 * PW;                         // prologue threads
+  constexpr int CM = PRO >= 2 ? 1024 * KCH / NTP : 4;  // NTP prologue threads x CM values = kpad
+  static_assert(PRO == 1 || (CM % 4 == 0 && CM >= 4), "whole 16-byte words per prologue thread");
+  __shared__ float red[2 * PW];
+  __shared__ float hred[RWV];
+  __shared__ unsigned gctr, ready, done;
+  __shared__ float as_sh;
+  __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
+  __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; }
+  __syncthreads();
+  if (wave < PW) {
+    // ---- the prologue waves ----
+    unsigned epoch = 0u;
+    const qd::GroupSync gs{&gctr, (unsigned)PW, &epoch};
+    float as;
+    if constexpr (PRO >= 2) {
+      float y[CM], gm[CM];
+      qd::rmsnorm_load<CM>(v, n, vbm, y, gm);
+      if constexpr (PRO == 2) as = qd::rmsnorm_apply<NTP, CM>(v, n, eps, y, gm, red, seq, gs);
+      else as = qd::rmsnorm_apply_fast<NTP, CM>(n, eps, y, gm, red, gs);
+      const float inv = 1.0f / as;
+#pragma unroll
+      for (int c = 0; c < CM; c += 4)
+        *reinterpret_cast<uint32_t *>(qsh + threadIdx.x * CM + c) = qd::quant_word(y, c, inv);
+    } else {
+      constexpr int NQ = (KCH * 64 + NTP - 1) / NTP;   // 16-value chunks per thread
+      float qx[NQ][16], qm = 0.0f;
+      pro1_load<KCH, NQ, NTP>(v, n, vbm, nvbm, qx, qm);
+      float mx = qd::wave_max_f32(qm);
+      if (lane == 0) red[wave] = mx;
+      gs();
+      mx = red[0];
+#pragma unroll
+      for (int i = 1; i < PW; i++) mx = fmaxf(mx, red[i]);
+      as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
+      const float inv = 1.0f / as;
+#pragma unroll
+      for (int ci = 0; ci < NQ; ci++) {
+        const int c = threadIdx.x + NTP * ci;
+        if (c >= KCH * 64) break;
+        const int k0 = 16 * c;
+        v4i pk;
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int k = k0 + 4 * wd + e;
+            const int q = k < n ? qd::quant_i8(qx[ci][4 * wd + e], inv) : 0;
+            word |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
+          }
+          pk[wd] = (int)word;
+        }
+        *reinterpret_cast<v4i *>(qsh + k0) = pk;
+      }
+    }
+    if (threadIdx.x == 0) as_sh = as;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's bytes (and as) have landed
+    if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return;
+  }
+  // ---- the row waves ----
+  const int rw = wave - PW;
+  const int j0 = (blockIdx.x * RWV + rw) * RW;
+  v4i w[NS][KCH], u[NS][KCH];
+#pragma unroll
+  for (int sl = 0; sl < NS; sl++) {
+    if (sl < RW && j0 + sl < N) {
+      load_row(w[sl], W + (size_t)(j0 + sl) * kpad, lane);
+      if (MODE == MODE_SWIGLU) load_row(u[sl], W + (size_t)(N + j0 + sl) * kpad, lane);
+    }
+  }
+  while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW)
+    __builtin_amdgcn_s_sleep(1);
+  asm volatile("" ::: "memory");
+  v4i a[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+  const float as = as_sh;
+  float hmax = 0.0f;
+  for (int r0 = 0; r0 < RW; r0 += NS) {
+#pragma unroll
+    for (int sl = 0; sl < NS; sl++) {
+      const int r = r0 + sl, j = j0 + r;
+      if (r < RW && j < N) {
+        const int accw = dot_row(w[sl], a);
+        int accu = 0;
+        if (MODE == MODE_SWIGLU) accu = dot_row(u[sl], a);
+        if (r + NS < RW && j + NS < N) {             // the slot takes row r + NS
+          load_row(w[sl], W + (size_t)(j + NS) * kpad, lane);
+          if (MODE == MODE_SWIGLU) load_row(u[sl], W + (size_t)(N + j + NS) * kpad, lane);
+        }
+        const int sw = qd::wave_sum_i32(accw);
+        if (MODE == MODE_SWIGLU) {
+          const int su = qd::wave_sum_i32(accu);
+          const float g = (as * ws[j]) * (float)sw;
+          const float up = (as * ws[N + j]) * (float)su;
+          const float sg = 1.0f / (1.0f + qd::expf_glibc(-g));
+          const float h = (g * sg) * up;
+          hmax = fmaxf(hmax, fabsf(h));
+          if (lane == 0) out[j] = h;
+        } else {
+          const float c = (as * ws[j]) * (float)sw;
+          if (lane == 0) {
+            if (MODE == MODE_RESID) out[j] = out[j] + c;
+            else out[j] = bias ? c + bias[j] : c;
+          }
+        }
+      }
+    }
+  }
+  if (MODE == MODE_SWIGLU) {       // the block's max |h|: the last row wave to finish writes it
+    if (lane == 0) hred[rw] = hmax;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    unsigned old = 0u;
+    if (lane == 0) old = __hip_atomic_fetch_add(&done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = (unsigned)__builtin_amdgcn_readfirstlane((int)old);
+    if (old == RWV - 1u && lane == 0) {
+      float mb = hred[0];
+#pragma unroll
+      for (int i = 1; i < RWV; i++) mb = fmaxf(mb, hred[i]);
+      bm[blockIdx.x] = mb;
     }
   }
 }
@@ -412,6 +610,37 @@ int launch(int cls, const int8_t *qa, const float *as, const int8_t *W, const fl
 #undef QG
 }
 
+// Rows per row wave and blocks of k_gemv_ws with RWV row waves: one block per
+// CU where the rows allow (N rows, or row pairs for SWIGLU).
+static inline void ws_shape(int N, int rwv, int &rw, int &blocks) {
+  const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256;
+  int nb = (N + rwv - 1) / rwv;
+  if (nb > cus) nb = cus;
+  rw = (N + rwv * nb - 1) / (rwv * nb);
+  blocks = (N + rwv * rw - 1) / (rwv * rw);
+}
+
+template <int MODE, int PRO>
+int launch_ws(int cls, const int8_t *W, const float *ws, int N, int kpad, float *out, const float *bias, float *bm,
+              const float *v, int n, const float *vbm, int nvbm, float eps) {
+  constexpr int PW = ws_pro_waves(MODE), RWV = ws_row_waves(MODE);
+  int rw, blocks;
+  ws_shape(N, RWV, rw, blocks);
+#define QW(KCH)                                                                                               \
+  QH_LAUNCH(cls, (k_gemv_ws<MODE, KCH, PRO, ws_slots(MODE, KCH), PW, RWV>), dim3(blocks), dim3(64 * (PW + RWV)), \
+            0, W, ws, N, kpad, rw, out, bias, bm, v, n, vbm, nvbm, eps)
+  switch (kpad) {
+    case 2048: QW(2); return 0;
+    case 4096: QW(4); return 0;
+    case 8192: QW(8); return 0;
+    case 14336:
+      if constexpr (PRO == 1) { QW(14); return 0; }
+      return qh::fail_msg("gemv: fused rmsnorm needs kpad 2048/4096/8192");
+    default: return qh::fail_msg("gemv: fused prologue needs kpad 2048/4096/8192/14336");
+  }
+#undef QW
+}
+
 // Skinny W8A8 product for 2..16 activation rows (qmatmul with a few rows; the
 // batch-8 GEMV of the op-level configuration).  One block of 8 waves per 16
 // output channels; wave w takes the 64-byte K steps w, w + 8, w + 16, ... and
@@ -512,6 +741,7 @@ extern "C" int qhip_gemv_dec(int mode, int cls, const int8_t *qa, const float *a
 extern "C" int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vbm, int nvbm, const int8_t *W,
                                  const float *ws, int N, int kpad, float *out) {
   if (kpad % 16 || n > kpad) return qh::fail_msg("gemv_resid_q: bad shape");
+  if (kUseWs) return launch_ws<MODE_RESID, 1>(cls, W, ws, N, kpad, out, NULL, NULL, v, n, vbm, nvbm, 0.0f);
   return launch<MODE_RESID, 1>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, NULL, NULL, v, n, vbm, nvbm, 0.0f);
 }
 
@@ -520,6 +750,10 @@ extern "C" int qhip_gemv_resid_q(int cls, const float *v, int n, const float *vb
 extern "C" int qhip_gemv_swiglu_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps,
                                      const int8_t *W, const float *ws, int N, int kpad, float *out, float *bm) {
   if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_swiglu_norm: unsupported shape");
+  if (kUseWs) {
+    if (fast) return launch_ws<MODE_SWIGLU, 3>(cls, W, ws, N, kpad, out, NULL, bm, x, dm, gamma, 0, eps);
+    return launch_ws<MODE_SWIGLU, 2>(cls, W, ws, N, kpad, out, NULL, bm, x, dm, gamma, 0, eps);
+  }
   if (fast) return launch<MODE_SWIGLU, 3>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, bm, NULL, x, dm, gamma, 0, eps);
   return launch<MODE_SWIGLU, 2>(cls, NULL, NULL, W, ws, N, kpad, out, NULL, bm, NULL, x, dm, gamma, 0, eps);
 }
@@ -531,6 +765,11 @@ extern "C" int qhip_gemv_norm_ok(int kpad, int dm) {
 
 // Number of per-block maxima qhip_gemv_swiglu_norm writes.
 extern "C" int qhip_gemv_norm_blocks(int N) {
+  if (kUseWs) {
+    int rw, blocks;
+    ws_shape(N, ws_row_waves(MODE_SWIGLU), rw, blocks);
+    return blocks;
+  }
   constexpr int per_block = 4 * rows_per_wave(MODE_SWIGLU, 2);
   return (N + per_block - 1) / per_block;
 }
@@ -540,6 +779,10 @@ extern "C" int qhip_gemv_norm_blocks(int N) {
 extern "C" int qhip_gemv_plain_norm(int cls, int fast, const float *x, int dm, const float *gamma, float eps,
                                     const int8_t *W, const float *ws, int N, int kpad, float *out, const float *bias) {
   if (!qhip_gemv_norm_ok(kpad, dm)) return qh::fail_msg("gemv_plain_norm: unsupported shape");
+  if (kUseWs) {
+    if (fast) return launch_ws<MODE_PLAIN, 3>(cls, W, ws, N, kpad, out, bias, NULL, x, dm, gamma, 0, eps);
+    return launch_ws<MODE_PLAIN, 2>(cls, W, ws, N, kpad, out, bias, NULL, x, dm, gamma, 0, eps);
+  }
   if (fast) return launch<MODE_PLAIN, 3>(cls, NULL, NULL, W, ws, N, kpad, out, bias, NULL, NULL, x, dm, gamma, 0, eps);
   return launch<MODE_PLAIN, 2>(cls, NULL, NULL, W, ws, N, kpad, out, bias, NULL, NULL, x, dm, gamma, 0, eps);
 }

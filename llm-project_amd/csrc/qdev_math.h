@@ -229,6 +229,32 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // The memory clobber keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// The meeting points of a block-wide routine (the exact sums, rmsnorm): every
+// wave of the block at s_barrier ...
+struct BlockSync {
+  __device__ __forceinline__ void operator()() const { lds_sync(); }
+};
+
+// ... or only the first `waves` waves, at an LDS counter, so that the block's
+// other waves (loading weights, say) are not waited for.  ctr is zeroed and
+// published (one block barrier) before its first use; epoch is the calling
+// wave's running target.  Every wave of the group calls it the same number of
+// times.  A wave's LDS writes have landed before its increment, and LDS
+// requests are served in order, so once a wave sees the count reach the target
+// it sees every group member's earlier writes.
+struct GroupSync {
+  unsigned *ctr;
+  unsigned waves;
+  unsigned *epoch;
+  __device__ __forceinline__ void operator()() const {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const unsigned target = (*epoch += waves);
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
+  }
+};
+
 // Copies the table into LDS (dst: 32 entries); the caller synchronizes.
 __device__ __forceinline__ void exp_table_to_lds(uint64_t *dst) {
   if (threadIdx.x < 32) dst[threadIdx.x] = kExp2Tab[threadIdx.x];

@@ -45,15 +45,17 @@ __device__ __forceinline__ void rmsnorm_load(const float *xr, int n, const float
 }
 
 // Normalizes the loaded y[] in place (0 past n) and returns the quantization
-// scale of the whole row.  red holds NT/64 floats.  All threads must call it.
-template <int NT, int CM>
+// scale of the whole row.  red holds NT/64 floats.  All NT threads must call it;
+// sync as for seq_sum_nonneg.
+template <int NT, int CM, typename Sync = BlockSync>
 __device__ __forceinline__ float rmsnorm_apply(const float *xr, int n, float eps, float (&y)[CM],
-                                               const float (&gm)[CM], float *red, SeqScratch &seq) {
+                                               const float (&gm)[CM], float *red, SeqScratch &seq,
+                                               const Sync &sync = Sync()) {
   const int j0 = threadIdx.x * CM;
   float sq[CM];
 #pragma unroll
   for (int c = 0; c < CM; c++) sq[c] = y[c] * y[c];
-  float ms = seq_sum_nonneg<NT, CM>(sq, n, seq, [&](int i) { return xr[i] * xr[i]; });   // rmsnorm.c:15
+  float ms = seq_sum_nonneg<NT, CM>(sq, n, seq, [&](int i) { return xr[i] * xr[i]; }, nullptr, sync);   // rmsnorm.c:15
   ms *= 1.0f / (float)n;
   const float r = 1.0f / sqrtf(ms + eps);
   float mx = 0.0f;
@@ -64,7 +66,7 @@ __device__ __forceinline__ float rmsnorm_apply(const float *xr, int n, float eps
   }
   mx = wave_max_f32(mx);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  lds_sync();
+  sync();
   mx = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
@@ -74,17 +76,17 @@ __device__ __forceinline__ float rmsnorm_apply(const float *xr, int n, float eps
 // The fast decode mode's form of rmsnorm_apply: the sum of squares is a fixed-
 // shape tree (per-thread partial sums, then the wave, then the waves in order),
 // so it is deterministic but not the reference's sequential order; everything
-// after it is the same.  red holds 2 * NT/64 floats.
-template <int NT, int CM>
+// after it is the same.  red holds 2 * NT/64 floats; sync as for rmsnorm_apply.
+template <int NT, int CM, typename Sync = BlockSync>
 __device__ __forceinline__ float rmsnorm_apply_fast(int n, float eps, float (&y)[CM], const float (&gm)[CM],
-                                                    float *red) {
+                                                    float *red, const Sync &sync = Sync()) {
   const int j0 = threadIdx.x * CM;
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < CM; c++) ss = __builtin_fmaf(y[c], y[c], ss);      // y is 0 past n
   ss = wave_sum_f32(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  lds_sync();
+  sync();
   ss = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; w++) ss += red[w];
@@ -98,7 +100,7 @@ __device__ __forceinline__ float rmsnorm_apply_fast(int n, float eps, float (&y)
   }
   mx = wave_max_f32(mx);
   if ((threadIdx.x & 63) == 0) red[NT / 64 + (threadIdx.x >> 6)] = mx;
-  lds_sync();
+  sync();
   mx = red[NT / 64];
 #pragma unroll
   for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[NT / 64 + w]);

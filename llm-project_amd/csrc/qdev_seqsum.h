@@ -120,15 +120,19 @@ __device__ float seq_serial(int n, Term term) {
 }
 
 // The sequential float32 sum of n terms, every one finite and >= 0.  Thread t
-// of the NT-thread block (NT = blockDim.x, a multiple of 64, at most 1024) holds
-// terms t*CM .. t*CM+CM-1 in a[], zero past n; n <= NT*CM.  term(i) returns term
-// i again, for the rare fallback.  All threads must call it; all get the result.
-// Three block barriers (LDS only: global loads in flight stay in flight); S may be
-// used again by the next call without another.
+// of the NT participating threads (threads 0 .. NT-1 of the block, NT a multiple
+// of 64, at most 1024) holds terms t*CM .. t*CM+CM-1 in a[], zero past n;
+// n <= NT*CM.  term(i) returns term i again, for the rare fallback.  All NT
+// threads must call it; all get the result.  Three meetings, through sync: the
+// block barrier by default (then NT = blockDim.x), or GroupSync over the first
+// NT/64 waves, which leaves the block's other waves running (LDS only: global
+// loads in flight stay in flight).  S may be used again by the next call
+// without another.
 // info (optional, written by one thread): number of hard steps, 1 if the
 // fallback ran.
-template <int NT, int CM, typename Term>
-__device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term term, int *info = nullptr) {
+template <int NT, int CM, typename Term, typename Sync = BlockSync>
+__device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term term, int *info = nullptr,
+                                const Sync &sync = Sync()) {
   static_assert(NT % 64 == 0 && NT / 64 <= kSeqMaxWaves, "block size");
   static_assert(CM >= 1 && CM <= 32, "terms per thread");
   constexpr int NW = NT / 64;
@@ -151,7 +155,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   const float mex = seq_wave_scan_max(__uint_as_float(seq_shr1(__float_as_uint(cmx))));   // exclusive
   if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = fmaxf(mex, cmx); }
   if (tid == 0) S.bad = 0;
-  lds_sync();
+  sync();
   float P0 = xin - loc, M0 = mex;
 #pragma unroll
   for (int w = 0; w < NW - 1; w++)
@@ -231,7 +235,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   }
   if (lane == 63) { S.wk[wave] = kin; S.wh[wave] = hin; S.wg[wave] = gout; }
   if (lane == 0) S.wgi[wave] = gin;
-  lds_sync();
+  sync();
 
   // 4. wave 0: the waves' offsets, the boundary checks between waves, and the
   // walk with the proof of every run.  The hard steps are taken 64 at a time:
@@ -319,7 +323,7 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
       if (info) { info[0] = htot; info[1] = !ok; }
     }
   }
-  lds_sync();
+  sync();
   return S.result;
 }
 
