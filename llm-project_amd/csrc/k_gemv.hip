@@ -269,16 +269,20 @@ constexpr bool kUseWs = QLLAMA_GEMV_WS != 0;     // the prologue GEMVs run k_gem
 #ifndef QLLAMA_WS_SLOTS_RESID
 #define QLLAMA_WS_SLOTS_RESID 8
 #endif
-constexpr int ws_pro_waves(int mode) {
-  return mode == MODE_PLAIN ? QLLAMA_WS_PW_PLAIN : mode == MODE_SWIGLU ? QLLAMA_WS_PW_SWIGLU : QLLAMA_WS_PW_RESID;
+constexpr int ws_pro_waves(int mode, int kch) {
+  return mode == MODE_PLAIN ? QLLAMA_WS_PW_PLAIN
+         : mode == MODE_SWIGLU ? QLLAMA_WS_PW_SWIGLU
+         : QLLAMA_WS_PW_RESID;
 }
-constexpr int ws_row_waves(int mode) {
-  return mode == MODE_PLAIN ? QLLAMA_WS_RWV_PLAIN : mode == MODE_SWIGLU ? QLLAMA_WS_RWV_SWIGLU : QLLAMA_WS_RWV_RESID;
+constexpr int ws_row_waves(int mode, int kch) {
+  return mode == MODE_PLAIN ? QLLAMA_WS_RWV_PLAIN
+         : mode == MODE_SWIGLU ? QLLAMA_WS_RWV_SWIGLU
+         : kch > 8 ? 4 : QLLAMA_WS_RWV_RESID;      // long rows: two rows in flight need the registers of 2 waves/SIMD
 }
 // slots x KCH (16-byte chunks per lane and row) is the register budget
 constexpr int ws_slots(int mode, int kch) {
   const int budget = mode == MODE_PLAIN ? QLLAMA_WS_SLOTS_PLAIN
-                     : mode == MODE_SWIGLU ? QLLAMA_WS_SLOTS_SWIGLU : QLLAMA_WS_SLOTS_RESID;
+                     : mode == MODE_SWIGLU ? QLLAMA_WS_SLOTS_SWIGLU : kch > 8 ? 2 * kch : QLLAMA_WS_SLOTS_RESID;
   return budget / kch > 0 ? budget / kch : 1;
 }
 
@@ -364,9 +368,29 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW)
     __builtin_amdgcn_s_sleep(1);
   asm volatile("" ::: "memory");
-  v4i a[KCH];
+  // the activation in registers, or (long rows) read from LDS at each row
+  constexpr bool A_LDS = KCH > 8;
+  v4i a[A_LDS ? 1 : KCH];
+  if constexpr (!A_LDS) {
 #pragma unroll
-  for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+    for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+  }
+  auto dot = [&](const v4i (&wr)[KCH]) {
+    if constexpr (A_LDS) {
+      int t = 0;
+#pragma unroll
+      for (int i = 0; i < KCH; i++) {
+        const v4i al = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+        t = __builtin_amdgcn_sdot4(al.x, wr[i].x, t, false);
+        t = __builtin_amdgcn_sdot4(al.y, wr[i].y, t, false);
+        t = __builtin_amdgcn_sdot4(al.z, wr[i].z, t, false);
+        t = __builtin_amdgcn_sdot4(al.w, wr[i].w, t, false);
+      }
+      return t;
+    } else {
+      return dot_row(wr, reinterpret_cast<const v4i (&)[KCH]>(a));
+    }
+  };
   const float as = as_sh;
   float hmax = 0.0f;
   for (int r0 = 0; r0 < RW; r0 += NS) {
@@ -374,9 +398,9 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
     for (int sl = 0; sl < NS; sl++) {
       const int r = r0 + sl, j = j0 + r;
       if (r < RW && j < N) {
-        const int accw = dot_row(w[sl], a);
+        const int accw = dot(w[sl]);
         int accu = 0;
-        if (MODE == MODE_SWIGLU) accu = dot_row(u[sl], a);
+        if (MODE == MODE_SWIGLU) accu = dot(u[sl]);
         if (r + NS < RW && j + NS < N) {             // the slot takes row r + NS
           load_row(w[sl], W + (size_t)(j + NS) * kpad, lane);
           if (MODE == MODE_SWIGLU) load_row(u[sl], W + (size_t)(N + j + NS) * kpad, lane);
@@ -623,12 +647,12 @@ static inline void ws_shape(int N, int rwv, int &rw, int &blocks) {
 template <int MODE, int PRO>
 int launch_ws(int cls, const int8_t *W, const float *ws, int N, int kpad, float *out, const float *bias, float *bm,
               const float *v, int n, const float *vbm, int nvbm, float eps) {
-  constexpr int PW = ws_pro_waves(MODE), RWV = ws_row_waves(MODE);
   int rw, blocks;
-  ws_shape(N, RWV, rw, blocks);
-#define QW(KCH)                                                                                               \
-  QH_LAUNCH(cls, (k_gemv_ws<MODE, KCH, PRO, ws_slots(MODE, KCH), PW, RWV>), dim3(blocks), dim3(64 * (PW + RWV)), \
-            0, W, ws, N, kpad, rw, out, bias, bm, v, n, vbm, nvbm, eps)
+#define QW(KCH)                                                                                                     \
+  ws_shape(N, ws_row_waves(MODE, KCH), rw, blocks);                                                                  \
+  QH_LAUNCH(cls, (k_gemv_ws<MODE, KCH, PRO, ws_slots(MODE, KCH), ws_pro_waves(MODE, KCH), ws_row_waves(MODE, KCH)>), \
+            dim3(blocks), dim3(64 * (ws_pro_waves(MODE, KCH) + ws_row_waves(MODE, KCH))), 0, W, ws, N, kpad, rw, out,   \
+            bias, bm, v, n, vbm, nvbm, eps)
   switch (kpad) {
     case 2048: QW(2); return 0;
     case 4096: QW(4); return 0;
@@ -767,7 +791,7 @@ extern "C" int qhip_gemv_norm_ok(int kpad, int dm) {
 extern "C" int qhip_gemv_norm_blocks(int N) {
   if (kUseWs) {
     int rw, blocks;
-    ws_shape(N, ws_row_waves(MODE_SWIGLU), rw, blocks);
+    ws_shape(N, ws_row_waves(MODE_SWIGLU, 4), rw, blocks);
     return blocks;
   }
   constexpr int per_block = 4 * rows_per_wave(MODE_SWIGLU, 2);

@@ -682,9 +682,11 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
       rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
       rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
     }
-    // h is quantized by its own kernel: quantizing the d_ff values inside every
-    // down block (qhip_gemv_resid_q) measured 2.5% slower end to end, because a
-    // wave's prologue cannot start before all of its weight loads are issued
+    // h is quantized by its own kernel: quantizing the d_ff values inside the
+    // down GEMV (qhip_gemv_resid_q) measured slower end to end, 2.5% with every
+    // wave quantizing and 3.6% with prologue waves beside four row waves per CU
+    // (at 14336 bytes a row, two rows in flight need the registers of two waves
+    // per SIMD, too few requests for the stream)
     rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, nbh, d->qa, d->kp_ff, d->as);
     rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
   }
