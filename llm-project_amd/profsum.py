@@ -30,6 +30,10 @@ GEMV_SITES = {
     "k_gemv_dec<2, 4, 6, 2, 1>": "gemv_gate_up",
     "k_gemv_dec<1, 14, 2, 0, 2>": "gemv_down",
     "k_gemv_dec<3, 4, 2, 0, 1>": "gemv_head",
+    # warp-specialized prologue GEMVs (k_gemv_ws<MODE, KCH, PRO, NS, PW, RWV>)
+    "k_gemv_ws<0, 4, 2, 3, 8, 8>": "gemv_qkv",
+    "k_gemv_ws<1, 4, 1, 2, 4, 8>": "gemv_o",
+    "k_gemv_ws<2, 4, 2, 3, 4, 8>": "gemv_gate_up",
 }
 
 
