@@ -9,9 +9,11 @@
 // multiple of u = 2^(e-23), so s + a_i rounds to s + u * rne(a_i / u): the step
 // adds an integer number of u that depends on a_i alone (unless a_i / u ends in
 // exactly .5, where the tie goes to the even neighbour and depends on s).  Sums
-// of integers do not depend on their order.  Grids are named by g = max(E, 1),
-// E the biased exponent field, so that 0, the subnormals and [2^-126, 2^-125)
-// share g = 1 and unit 2^-149; the unit of grid g is 2^(g-150).
+// of integers do not depend on their order.  Grids are named by g = E, the
+// biased exponent field; the unit of grid g >= 1 is 2^(g-150).  Grid 0 (zero and
+// the subnormals) takes the unit 2^-150, half their spacing: every float there
+// is a multiple of it and sums that stay below 2^-126 are exact, so its steps
+// add exact integer multiples as well.
 //
 // Method (one block; thread t holds terms [t*CM, t*CM + CM) in registers):
 //   1. P, a float block scan of the chunk totals, predicts every partial sum.
@@ -48,12 +50,14 @@ constexpr int kSeqMaxWaves = 16;           // blocks of up to 1024 threads
 
 struct SeqScratch {
   float wf[kSeqMaxWaves];        // per wave: predicted total of its terms
-  float wm[kSeqMaxWaves];        //           largest term
+  unsigned wm[kSeqMaxWaves];     //           bits of the largest term
   unsigned wk[kSeqMaxWaves];     //           total of its k (mod 2^32)
   int wh[kSeqMaxWaves];          //           hard steps
   int wg[kSeqMaxWaves];          //           grid of the run continuing past its last step
   int wgi[kSeqMaxWaves];         //           grid of its first step if that step is easy, else -1
   int4 hs[kSeqMaxHard];          // hard steps by wave: k prefix within the wave, index, term bits, grid after it
+  float2 walk[72];               // one batch of the walk: run total, hard term (+8 read ahead)
+  float wst[64];                 //                         partial sum the run starts from
   int bad;
   float result;
 };
@@ -83,9 +87,10 @@ __device__ __forceinline__ float seq_wave_scan(float x) {
   return x;
 }
 
-__device__ __forceinline__ float seq_wave_scan_max(float x) {     // x >= 0
+// Inclusive scan of the maximum, on the bits of floats >= 0 (ordered as the values).
+__device__ __forceinline__ unsigned seq_wave_scan_umax(unsigned x) {
 #pragma unroll
-  for (int k = 0; k < 6; k++) x = fmaxf(x, __uint_as_float(seq_dpp_u(__float_as_uint(x), k)));
+  for (int k = 0; k < 6; k++) x = max(x, seq_dpp_u(x, k));
   return x;
 }
 
@@ -108,8 +113,10 @@ __device__ __forceinline__ unsigned seq_row_scan(unsigned x) {
   return x;
 }
 
-// grid of a float p >= 0 (see above)
-__device__ __forceinline__ int seq_grid(float p) { return max((int)(__float_as_uint(p) >> 23), 1); }
+// grid of a float p >= 0 (see above), and of the larger of p and the float
+// whose bits are lb (both >= 0: their bits are ordered as their values)
+__device__ __forceinline__ int seq_grid(float p) { return (int)(__float_as_uint(p) >> 23); }
+__device__ __forceinline__ int seq_grid_max(float p, unsigned lb) { return (int)(max(__float_as_uint(p), lb) >> 23); }
 
 // The plain loop over term(0..n), for the fallback and as the definition.
 template <typename Term>
@@ -141,25 +148,29 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
 
   // 1. predicted partial sum at the start of this thread's chunk (any order will
   // do) and the largest term before it
-  float loc, cmx = 0.0f;
+  // (largest terms are kept as bits: for floats >= 0 the integer maximum is the
+  // float maximum)
+  float loc;
+  unsigned cmx = 0u;
   {
     float q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < CM; c++) {
       q[c & 3] += a[c];
-      cmx = fmaxf(cmx, a[c]);
+      cmx = max(cmx, __float_as_uint(a[c]));
     }
     loc = (q[0] + q[1]) + (q[2] + q[3]);
   }
   const float xin = seq_wave_scan(loc);
-  const float mex = seq_wave_scan_max(__uint_as_float(seq_shr1(__float_as_uint(cmx))));   // exclusive
-  if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = fmaxf(mex, cmx); }
+  const unsigned mex = seq_wave_scan_umax(seq_shr1(cmx));   // exclusive
+  if (lane == 63) { S.wf[wave] = xin; S.wm[wave] = max(mex, cmx); }
   if (tid == 0) S.bad = 0;
   sync();
-  float P0 = xin - loc, M0 = mex;
+  float P0 = xin - loc;
+  unsigned M0 = mex;
 #pragma unroll
   for (int w = 0; w < NW - 1; w++)
-    if (w < wave) { P0 += S.wf[w]; M0 = fmaxf(M0, S.wm[w]); }
+    if (w < wave) { P0 += S.wf[w]; M0 = max(M0, S.wm[w]); }
 
   // 2. classify; rho: 16 standard deviations of the rounding error a sequential sum
   // of i terms accumulates (each below half a unit in the last place), plus the
@@ -168,23 +179,24 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   const float rho = 0x1p-20f * __builtin_amdgcn_sqrtf((float)((tid + 1) * CM + 2)) + 0x1p-17f;
   const float lo = 1.0f - rho, hi = 1.0f + rho;
   unsigned ks = 0, hardmask = 0;
-  int nh = 0, gin = -1, gout = 1;
+  int nh = 0, gin = -1, gout = 0;
   unsigned kp[CM];
   int gh[CM];
-  const int gA = seq_grid(fmaxf(P0 * lo, M0)), gB = seq_grid((P0 + loc) * hi);
+  const int gA = seq_grid_max(P0 * lo, M0), gB = seq_grid((P0 + loc) * hi);
   if (wave * 64 * CM >= n) {
     // a wave wholly past n holds only +0 terms, and s + 0 is s on any grid: no
     // step to classify, no hard step, and no boundary to check (gin = -1)
 #pragma unroll
     for (int c = 0; c < CM; c++) {
       kp[c] = 0u;
-      gh[c] = 1;
+      gh[c] = 0;
     }
   } else if (__all(gA == gB)) {
     // every chunk of the wave is predicted on one grid: only exact ties are hard
+    // (a term of the chunk is below the grid's binade top, so t < 2^24)
 #pragma unroll
     for (int c = 0; c < CM; c++) {
-      const float t = fminf(ldexpf(a[c], 150 - gA), 0x1p30f);
+      const float t = ldexpf(a[c], 150 - gA);
       const bool tie = __builtin_amdgcn_fractf(t) == 0.5f;
       kp[c] = ks;
       ks += tie ? 0u : (unsigned)__builtin_rintf(t);
@@ -195,22 +207,27 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
     gin = (hardmask & 1u) ? -1 : gA;
     gout = gA;
   } else {
-    float P = P0, L = M0;
+    // (an easy step's term is below its grid's binade top, so t < 2^24; a hard
+    // step's t, possibly huge, is not used)
+    float P = P0;
+    unsigned L = M0;
+    int g0 = seq_grid_max(P * lo, L);
 #pragma unroll
     for (int c = 0; c < CM; c++) {
       const float Pn = P + a[c];
-      const int g0 = seq_grid(fmaxf(P * lo, L));
-      L = fmaxf(L, a[c]);
+      L = max(L, __float_as_uint(a[c]));
       const int g1 = seq_grid(Pn * hi);
-      const float t = fminf(ldexpf(a[c], 150 - g0), 0x1p30f);
+      const float t = ldexpf(a[c], 150 - g0);
       const bool easy = (g0 == g1) && (__builtin_amdgcn_fractf(t) != 0.5f);
       kp[c] = ks;
       ks += easy ? (unsigned)__builtin_rintf(t) : 0u;
       nh += easy ? 0 : 1;
       hardmask |= easy ? 0u : (1u << c);
       if (c == 0) gin = easy ? g0 : -1;
-      gh[c] = seq_grid(fmaxf(Pn * lo, L));               // grid after this step, if it is hard
-      gout = easy ? g0 : gh[c];                          // grid of the run continuing past this step
+      const int gn = seq_grid_max(Pn * lo, L);           // the next step's grid: the grid after a hard step
+      gh[c] = gn;
+      gout = easy ? g0 : gn;                             // grid of the run continuing past this step
+      g0 = gn;
       P = Pn;
     }
   }
@@ -241,78 +258,80 @@ __device__ float seq_sum_nonneg(const float (&a)[CM], int n, SeqScratch &S, Term
   // walk with the proof of every run.  The hard steps are taken 64 at a time:
   // lane i prepares run m = base + i (the run before hard step m; run htot is
   // the tail) and its exact total, the serial part adds only run totals and
-  // hard terms (lane i records the partial sum its run starts from), and the
-  // runs are then proven in parallel.
+  // hard terms, and the runs are then proven in parallel.
   if (wave == 0) {
     const unsigned wk_l = lane < NW ? S.wk[lane] : 0u;
     const int wh_l = lane < NW ? S.wh[lane] : 0;
-    const int wg_prev = lane >= 1 && lane < NW ? S.wg[lane - 1] : 1;
+    const int wg_prev = lane >= 1 && lane < NW ? S.wg[lane - 1] : 0;
     const int wgi_l = lane < NW ? S.wgi[lane] : -1;
     const unsigned koff_l = seq_row_scan(wk_l) - wk_l;            // lanes 0..NW-1
-    const int hoff_l = (int)(seq_row_scan((unsigned)wh_l) - (unsigned)wh_l);
+    const int hend_l = (int)seq_row_scan((unsigned)wh_l);        // end of the wave's hard steps
+    const int hoff_l = hend_l - wh_l;
     const unsigned ktot = (unsigned)__builtin_amdgcn_readlane((int)(koff_l + wk_l), NW - 1);
-    const int htot = __builtin_amdgcn_readlane(hoff_l + wh_l, NW - 1);
+    const int htot = __builtin_amdgcn_readlane(hend_l, NW - 1);
     bool ok = S.bad == 0 && !__any(lane < NW && (wh_l > HCAP || (wgi_l >= 0 && wgi_l != wg_prev)));
-    int hoff_s[NW], wh_s[NW];
-    unsigned koff_s[NW];
+    int hend_s[NW];
 #pragma unroll
-    for (int v = 0; v < NW; v++) {
-      hoff_s[v] = __builtin_amdgcn_readlane(hoff_l, v);
-      wh_s[v] = __builtin_amdgcn_readlane(wh_l, v);
-      koff_s[v] = (unsigned)__builtin_amdgcn_readlane((int)koff_l, v);
-    }
+    for (int v = 0; v < NW; v++) hend_s[v] = __builtin_amdgcn_readlane(hend_l, v);
     float s = 0.0f;
+    int cx = 0, cy = -1, cw = 0;    // the record before the batch's first run: k prefix, index, grid after
     for (int base = 0; ok && base <= htot; base += 64) {
       const int m = base + lane;
-      // the waves holding this lane's hard step (or the tail) and the one before it
-      int rc = m, rp = m - 1;
-      unsigned kc = 0, kpv = 0;
+      // the wave holding hard step m is the number of waves whose hard steps end
+      // at or before m (NW for the tail); its offsets come from its lane
+      int v = 0;
 #pragma unroll
-      for (int v = 0; v < NW; v++) {
-        const bool sc = wh_s[v] > 0 && m >= hoff_s[v], sp = wh_s[v] > 0 && m - 1 >= hoff_s[v];
-        rc = sc ? v * HCAP + m - hoff_s[v] : rc;
-        kc = sc ? koff_s[v] : kc;
-        rp = sp ? v * HCAP + m - 1 - hoff_s[v] : rp;
-        kpv = sp ? koff_s[v] : kpv;
-      }
-      int4 cur = make_int4((int)ktot, NT * CM, 0, 1), prv = make_int4(0, -1, 0, 1);
+      for (int u = 0; u < NW; u++) v += hend_s[u] <= m ? 1 : 0;
+      const int src = 4 * min(v, NW - 1);
+      const int hoff_v = __builtin_amdgcn_ds_bpermute(src, hoff_l);
+      const unsigned koff_v = (unsigned)__builtin_amdgcn_ds_bpermute(src, (int)koff_l);
+      int4 cur = make_int4((int)ktot, NT * CM, 0, 0);                // the tail
       if (m < htot) {
-        cur = S.hs[rc];
-        cur.x = (int)((unsigned)cur.x + kc);
+        cur = S.hs[v * HCAP + m - hoff_v];
+        cur.x = (int)((unsigned)cur.x + koff_v);
       }
-      if (m > 0 && m <= htot) {
-        prv = S.hs[rp];
-        prv.x = (int)((unsigned)prv.x + kpv);
-      }
-      const unsigned K = (unsigned)cur.x - (unsigned)prv.x;
-      const int gp = prv.w;
-      const bool live = m <= htot && cur.y > prv.y + 1;   // run m has steps
+      // the record before run m is lane m-1's (lane 0: the carry, DPP wave_shr:1)
+      const int px = __builtin_amdgcn_update_dpp(cx, cur.x, 0x138, 0xf, 0xf, false);
+      const int py = __builtin_amdgcn_update_dpp(cy, cur.y, 0x138, 0xf, 0xf, false);
+      const int gp = __builtin_amdgcn_update_dpp(cw, cur.w, 0x138, 0xf, 0xf, false);
+      cx = __builtin_amdgcn_readlane(cur.x, 63);
+      cy = __builtin_amdgcn_readlane(cur.y, 63);
+      cw = __builtin_amdgcn_readlane(cur.w, 63);
+      const unsigned K = (unsigned)cur.x - (unsigned)px;
+      const bool live = m <= htot && cur.y > py + 1;     // run m has steps
       const float T = live ? ldexpf((float)K, gp - 150) : 0.0f;   // 0 past the tail: adds nothing
       const float ah = __int_as_float(cur.z);                     // 0 from the tail on
-      const int cnt = min(64, htot + 1 - base);
-      // Batches of 8 steps with constant lane indices; steps past cnt add +0.
-      // The partial sum before each step is shifted into a lane register (lane
-      // 0 takes it, every other lane takes its neighbour's), so after c steps
-      // lane j holds the sum before step c-1-j.
-      int sh = 0, c = 0;
-#pragma unroll
-      for (int b = 0; b < 8; b++) {
-        if (8 * b >= cnt) break;
-        float Ti[8], ai[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          Ti[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(T), 8 * b + u));
-          ai[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ah), 8 * b + u));
+      // The serial part: lane 0 alone (exec holds one lane, so its LDS reads,
+      // adds and writes cost the least) adds the pairs in order, 8 at a time
+      // with the next 8 in flight, and records the partial sum each run starts
+      // from.  Pairs past the tail are (+0, +0) and leave s unchanged; the reads
+      // ahead past them stay inside walk[] and are not used.  A wave's LDS
+      // operations complete in order, so lane 0 reads what the wave has just
+      // written, and the wave reads back what lane 0 has written.
+      S.walk[lane] = make_float2(T, ah);
+      asm volatile("" ::: "memory");                      // keep the reads below the writes
+      if (lane == 0) {
+        const int cnt = min(64, htot + 1 - base);
+        const float4 *wp = reinterpret_cast<const float4 *>(S.walk);
+        float4 q0 = wp[0], q1 = wp[1], q2 = wp[2], q3 = wp[3];
+        for (int c = 0; c < cnt; c += 8) {
+          const float4 n0 = wp[(c >> 1) + 4], n1 = wp[(c >> 1) + 5], n2 = wp[(c >> 1) + 6], n3 = wp[(c >> 1) + 7];
+          float4 r0, r1;
+          r0.x = s; s = s + q0.x; s = s + q0.y;
+          r0.y = s; s = s + q0.z; s = s + q0.w;
+          r0.z = s; s = s + q1.x; s = s + q1.y;
+          r0.w = s; s = s + q1.z; s = s + q1.w;
+          r1.x = s; s = s + q2.x; s = s + q2.y;
+          r1.y = s; s = s + q2.z; s = s + q2.w;
+          r1.z = s; s = s + q3.x; s = s + q3.y;
+          r1.w = s; s = s + q3.z; s = s + q3.w;
+          *reinterpret_cast<float4 *>(&S.wst[c]) = r0;
+          *reinterpret_cast<float4 *>(&S.wst[c + 4]) = r1;
+          q0 = n0; q1 = n1; q2 = n2; q3 = n3;
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-          sh = __builtin_amdgcn_update_dpp(__float_as_int(s), sh, 0x138, 0xf, 0xf, false);   // wave_shr:1
-          s = s + Ti[u];
-          s = s + ai[u];
-        }
-        c += 8;
       }
-      const float st = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * ((c - 1 - lane) & 63), sh));
+      asm volatile("" ::: "memory");
+      const float st = S.wst[lane];                       // read only where live
       const float top = __uint_as_float((unsigned)(gp + 1) << 23);
       const bool bad = live && !(K <= (1u << 23) && seq_grid(st) == gp && T <= top - st);
       ok = ok && !__any(bad);
