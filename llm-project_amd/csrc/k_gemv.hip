@@ -143,18 +143,10 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
       if (c >= KCH * 64) break;
       const int k0 = 16 * c;
       const float *x = qx[ci];
-      v4i pk;
+      v4i pk;                                          // values past n were loaded as 0 and give 0
 #pragma unroll
-      for (int wd = 0; wd < 4; wd++) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int k = k0 + 4 * wd + e;
-          const int q = k < n ? qd::quant_i8(x[4 * wd + e], inv) : 0;
-          word |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
-        }
-        pk[wd] = (int)word;
-      }
+      for (int wd = 0; wd < 4; wd++)
+        pk[wd] = (int)qd::quant_i8x4(x[4 * wd], x[4 * wd + 1], x[4 * wd + 2], x[4 * wd + 3], inv);
       *reinterpret_cast<v4i *>(qsh + k0) = pk;
     }
     qd::lds_sync();
@@ -296,12 +288,12 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   static_assert(PRO == 1 || (CM % 4 == 0 && CM >= 4), "whole 16-byte words per prologue thread");
   __shared__ float red[2 * PW];
   __shared__ float hred[RWV];
-  __shared__ unsigned gctr, ready, done;
+  __shared__ unsigned gctr, ready, done, issued;
   __shared__ float as_sh;
   __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
   __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; }
+  if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; issued = 0u; }
   __syncthreads();
   if (wave < PW) {
     // ---- the prologue waves ----
@@ -311,6 +303,10 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
     if constexpr (PRO >= 2) {
       float y[CM], gm[CM];
       qd::rmsnorm_load<CM>(v, n, vbm, y, gm);
+      if constexpr (PRO == 2) {                          // inputs requested: the row waves may start
+        __builtin_amdgcn_sched_barrier(0);
+        if (lane == 0) __hip_atomic_fetch_add(&issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       if constexpr (PRO == 2) as = qd::rmsnorm_apply<NTP, CM>(v, n, eps, y, gm, red, seq, gs);
       else as = qd::rmsnorm_apply_fast<NTP, CM>(n, eps, y, gm, red, gs);
       const float inv = 1.0f / as;
@@ -334,18 +330,10 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
         const int c = threadIdx.x + NTP * ci;
         if (c >= KCH * 64) break;
         const int k0 = 16 * c;
-        v4i pk;
+        v4i pk;                                        // values past n were loaded as 0 and give 0
 #pragma unroll
-        for (int wd = 0; wd < 4; wd++) {
-          uint32_t word = 0;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int k = k0 + 4 * wd + e;
-            const int q = k < n ? qd::quant_i8(qx[ci][4 * wd + e], inv) : 0;
-            word |= (uint32_t)(uint8_t)(int8_t)q << (8 * e);
-          }
-          pk[wd] = (int)word;
-        }
+        for (int wd = 0; wd < 4; wd++)
+          pk[wd] = (int)qd::quant_i8x4(qx[ci][4 * wd], qx[ci][4 * wd + 1], qx[ci][4 * wd + 2], qx[ci][4 * wd + 3], inv);
         *reinterpret_cast<v4i *>(qsh + k0) = pk;
       }
     }
@@ -357,6 +345,13 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   // ---- the row waves ----
   const int rw = wave - PW;
   const int j0 = (blockIdx.x * RWV + rw) * RW;
+  if constexpr (PRO == 2) {
+    // the exact rmsnorm's inputs are requested before any weight, so that they
+    // do not queue behind the weight stream (its long prologue is the kernel's
+    // critical path; the shorter ones gain nothing from the wait)
+    while (__hip_atomic_load(&issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW)
+      __builtin_amdgcn_s_sleep(1);
+  }
   v4i w[NS][KCH], u[NS][KCH];
 #pragma unroll
   for (int sl = 0; sl < NS; sl++) {
@@ -577,15 +572,8 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
   const float inv = 1.0f / as;
-  if (k0 < kpad) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int q = k0 + r < n ? qd::quant_i8(x[r], inv) : 0;
-      packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * r);
-    }
-    *reinterpret_cast<uint32_t *>(qa + k0) = packed;
-  }
+  if (k0 < kpad)                                       // values past n were loaded as 0 and give 0
+    *reinterpret_cast<uint32_t *>(qa + k0) = qd::quant_i8x4(x[0], x[1], x[2], x[3], inv);
   if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
 }
 

@@ -364,13 +364,26 @@ __device__ __forceinline__ float gen_value(uint64_t key, uint64_t i, double sigm
 }
 
 // int8 quantization of one value with the reference's rounding (quant.c:74-77):
-// lrintf is round-half-even in the default mode, then clamp to +-127.
+// lrintf is round-half-even in the default mode, then clamp to +-127; NaN gives 0
+// ((int)lrintf(NaN) is the low half of LONG_MIN on x86-64).  v_cvt_i32_f32 turns
+// NaN into 0 and saturates values out of the int range, so clamping the integer
+// after it is clamping the float before it.
 __device__ __forceinline__ int quant_i8(float v, float inv) {
-  float r = __builtin_rintf(v * inv);
-  if (r != r) return 0;   // (int)lrintf(NaN): LONG_MIN on x86-64, whose low 32 bits are 0
-  r = r > 127.0f ? 127.0f : r;
-  r = r < -127.0f ? -127.0f : r;
-  return (int)r;
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(__builtin_rintf(v * inv)));
+  return min(max(q, -127), 127);
+}
+
+// The low bytes of four quantized values, little-endian in one word (v_perm_b32:
+// selector bytes 0-3 pick the second operand's bytes, 4-7 the first's, 12 gives 0).
+__device__ __forceinline__ uint32_t pack_i8x4(int q0, int q1, int q2, int q3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+__device__ __forceinline__ uint32_t quant_i8x4(float a, float b, float c, float d, float inv) {
+  return pack_i8x4(quant_i8(a, inv), quant_i8(b, inv), quant_i8(c, inv), quant_i8(d, inv));
 }
 
 // ---------------------------------------------------------------------------

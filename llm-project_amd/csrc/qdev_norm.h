@@ -119,10 +119,7 @@ __device__ __forceinline__ float rmsnorm_row(const float *xr, int n, const float
 // The quantized bytes of y[c .. c+3] (quant.c:71-78), packed little-endian.
 template <int CM>
 __device__ __forceinline__ uint32_t quant_word(const float (&y)[CM], int c, float inv) {
-  uint32_t w = 0;
-#pragma unroll
-  for (int e = 0; e < 4; e++) w |= (uint32_t)(uint8_t)(int8_t)quant_i8(y[c + e], inv) << (8 * e);
-  return w;
+  return quant_i8x4(y[c], y[c + 1], y[c + 2], y[c + 3], inv);
 }
 
 }  // namespace qd
