@@ -349,8 +349,8 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
     // the exact rmsnorm's inputs are requested before any weight, so that they
     // do not queue behind the weight stream (its long prologue is the kernel's
     // critical path; the shorter ones gain nothing from the wait)
-    while (__hip_atomic_load(&issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW)
-      __builtin_amdgcn_s_sleep(1);
+    while (__hip_atomic_load(&issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW) {
+    }
   }
   v4i w[NS][KCH], u[NS][KCH];
 #pragma unroll
@@ -360,8 +360,8 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
       if (MODE == MODE_SWIGLU) load_row(u[sl], W + (size_t)(N + j0 + sl) * kpad, lane);
     }
   }
-  while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW)
-    __builtin_amdgcn_s_sleep(1);
+  while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW) {
+  }
   asm volatile("" ::: "memory");
   // the activation in registers, or (long rows) read from LDS at each row
   constexpr bool A_LDS = KCH > 8;

@@ -241,7 +241,8 @@ struct BlockSync {
 // wave's running target.  Every wave of the group calls it the same number of
 // times.  A wave's LDS writes have landed before its increment, and LDS
 // requests are served in order, so once a wave sees the count reach the target
-// it sees every group member's earlier writes.
+// it sees every group member's earlier writes.  The wait polls the counter
+// without sleeping between reads (sleeping added latency to every meeting).
 struct GroupSync {
   unsigned *ctr;
   unsigned waves;
@@ -250,7 +251,8 @@ struct GroupSync {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const unsigned target = (*epoch += waves);
     if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    }
     asm volatile("" ::: "memory");
   }
 };
