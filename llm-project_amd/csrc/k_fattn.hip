@@ -85,11 +85,16 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
   return __builtin_fmaf(a.w, b.w, __builtin_fmaf(a.z, b.z, __builtin_fmaf(a.y, b.y, a.x * b.x)));
 }
 
+// Heads of a group padded to whole 16-byte words, so that one row's weights
+// for every head come with one or two LDS reads.
+template <int G>
+constexpr int fa_gp() { return (G + 3) / 4 * 4; }
+
 template <int G, int HD>
 struct FaLds {
   float qs[G * HD];                    // the group's (rotated) queries
   float kcur[HD], vcur[HD];            // the current position's k (rotated) and v
-  float sc[G * kFaMaxChunk];           // scores, then e_j, by head
+  float sc[(kFaMaxChunk + 32) * fa_gp<G>()];   // scores, then e_j, [row][head] (0 past the chunk)
   float ro[kFaWaves * G * HD];         // per-wave partial o
   float sm[G], sl[G];                  // chunk max and sum by head
 };
@@ -195,7 +200,19 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn(const float *qkv, float *k
 #pragma unroll
   for (int g = 0; g < G; g++) qf[g] = cok ? *reinterpret_cast<const float4 *>(&S.qs[g * HD + 4 * c]) : f4_zero();
 
-  // 1. scores
+  // 1. scores (the current row, which reads as 0 from the cache, is formed
+  // after the loop from LDS by every lane group and stored by its owner)
+  constexpr int GP = fa_gp<G>();
+  auto store_scores = [&](const float4 &k, int r) {
+    float d[GP];
+#pragma unroll
+    for (int g = 0; g < GP; g++) d[g] = g < G ? group_sum<LPR>(dot4(qf[g], k)) * scale : 0.0f;
+    if (c == 0 && r < n) {
+#pragma unroll
+      for (int g = 0; g < GP; g += 4)
+        *reinterpret_cast<float4 *>(&S.sc[r * GP + g]) = make_float4(d[g], d[g + 1], d[g + 2], d[g + 3]);
+    }
+  };
   for (int b0 = 0; b0 < nround; b0 += kFaBatch) {
     if (b0) {
 #pragma unroll
@@ -204,28 +221,26 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn(const float *qkv, float *k
 #pragma unroll
     for (int b = 0; b < kFaBatch; b++) {
       if (b0 + b >= nround) break;
-      float4 k = kr[b];
-      if (ROPE && holds_pos && row_pos(b0 + b) == pos && cok) k = *reinterpret_cast<const float4 *>(&S.kcur[4 * c]);
-      const int r = (b0 + b) * RPR + rlane;
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        const float dot = group_sum<LPR>(dot4(qf[g], k));
-        if (c == 0 && r < n) S.sc[g * kFaMaxChunk + r] = dot * scale;
-      }
+      store_scores(kr[b], (b0 + b) * RPR + rlane);
     }
   }
+  // row n-1 is the last row of its lane group (rows go round-robin over the groups)
+  const bool owns_pos = ROPE && holds_pos && rlane == (n - 1) % RPR;
+  if (ROPE && holds_pos)
+    store_scores(cok ? *reinterpret_cast<const float4 *>(&S.kcur[4 * c]) : f4_zero(), owns_pos ? n - 1 : n);
   qd::lds_sync();
 
-  // 2. chunk softmax by head: m, e_j (in place), l
+  // 2. chunk softmax by head: m, e_j (in place), l; rows n .. nround*RPR-1,
+  // which the PV loop reads, are set to 0
+  const int nz = nround * RPR;
   for (int g = wave; g < G; g += kFaWaves) {
-    float *sg = S.sc + g * kFaMaxChunk;
     float m = -INFINITY;
-    for (int r = lane; r < n; r += 64) m = fmaxf(m, sg[r]);
+    for (int r = lane; r < n; r += 64) m = fmaxf(m, S.sc[r * GP + g]);
     m = qd::wave_max_f32(m);
     float l = 0.0f;
-    for (int r = lane; r < n; r += 64) {
-      const float e = qd::expf_glibc(sg[r] - m);
-      sg[r] = e;
+    for (int r = lane; r < nz; r += 64) {
+      const float e = r < n ? qd::expf_glibc(S.sc[r * GP + g] - m) : 0.0f;
+      S.sc[r * GP + g] = e;
       l += e;
     }
     l = qd::wave_sum_f32(l);
@@ -245,13 +260,21 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn(const float *qkv, float *k
 #pragma unroll
     for (int b = 0; b < kFaBatch; b++) {
       if (b0 + b >= nround) break;
-      float4 v = vr[b];
-      if (ROPE && holds_pos && row_pos(b0 + b) == pos && cok) v = *reinterpret_cast<const float4 *>(&S.vcur[4 * c]);
-      const int r = (b0 + b) * RPR + rlane;
-      const bool ok = r < n;
+      const int r = (b0 + b) * RPR + rlane;             // rows past n have e = 0 and v = 0
+      float w[GP];
 #pragma unroll
-      for (int g = 0; g < G; g++) acc[g] = fma4(ok ? S.sc[g * kFaMaxChunk + r] : 0.0f, v, acc[g]);
+      for (int g = 0; g < GP; g += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(&S.sc[r * GP + g]);
+        w[g] = t.x; w[g + 1] = t.y; w[g + 2] = t.z; w[g + 3] = t.w;
+      }
+#pragma unroll
+      for (int g = 0; g < G; g++) acc[g] = fma4(w[g], vr[b], acc[g]);
     }
+  }
+  if (owns_pos) {       // the current row (read as 0 above) is its lane group's last row
+    const float4 v = cok ? *reinterpret_cast<const float4 *>(&S.vcur[4 * c]) : f4_zero();
+#pragma unroll
+    for (int g = 0; g < G; g++) acc[g] = fma4(S.sc[(n - 1) * GP + g], v, acc[g]);
   }
   // rows of one wave instruction, then the waves (fixed order)
 #pragma unroll
@@ -301,12 +324,18 @@ __global__ __launch_bounds__(merge_threads<HD>()) void k_fattn_merge(const float
   const int T = *d_pos + 1, nact = (T + chunk - 1) / chunk;
   const float *pm = part, *pl = part + (size_t)KVH * nsmax * G, *po = part + (size_t)2 * KVH * nsmax * G;
   const size_t base = (size_t)kvh * nsmax;
-  // requests first: the first chunks' o for this thread's dim, then the maxima
-  constexpr int U = 8;
+  // requests first: the o of up to 64 chunks for this thread's dim (every load of
+  // a batch in flight at once), then the maxima
+  constexpr int U = 64;
+  // (through a buffer resource over the head's nact chunk slots: an offset past
+  // them reads 0 without memory traffic, so no load needs a branch)
   float ov[U];
-  const float *src = po + base * G * HD + (size_t)g * HD + (dim_ok ? tid : 0);
+  const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(po + base * G * HD + (size_t)g * HD), (short)0, nact * G * HD * 4, 0x00020000);
+  const int vo = (dim_ok ? tid : 0) * 4, ostep = G * HD * 4;
+  auto oload = [&](int c) { return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ors, vo + c * ostep, 0, 0)); };
 #pragma unroll
-  for (int u = 0; u < U; u++) ov[u] = u < nact ? src[(size_t)u * G * HD] : 0.0f;
+  for (int u = 0; u < U; u++) ov[u] = oload(u);
   float M = -INFINITY;
   for (int s = tid; s < nact; s += NT) M = fmaxf(M, pm[(base + s) * G + g]);
   M = qd::wave_max_f32(M);
@@ -332,7 +361,7 @@ __global__ __launch_bounds__(merge_threads<HD>()) void k_fattn_merge(const float
   for (int u = 0; u < U; u++) if (u < nact) a = __builtin_fmaf(wm[u], ov[u], a);
   for (int s0 = U; s0 < nact; s0 += U) {
 #pragma unroll
-    for (int u = 0; u < U; u++) ov[u] = s0 + u < nact ? src[(size_t)(s0 + u) * G * HD] : 0.0f;
+    for (int u = 0; u < U; u++) ov[u] = oload(s0 + u);
 #pragma unroll
     for (int u = 0; u < U; u++) if (s0 + u < nact) a = __builtin_fmaf(wm[s0 + u], ov[u], a);
   }
