@@ -597,7 +597,7 @@ __global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int 
   __shared__ uint64_t tab[32];
   qd::exp_table_to_lds(tab);
   __syncthreads();                                   // publishes the exp table
-  const int r = blockIdx.x, h = blockIdx.y;
+  const int h = blockIdx.x, r = R - 1 - blockIdx.y;   // the longest rows are dispatched first
   const int T = p0 + r + 1;
   float *row = w + ((size_t)h * R + r) * Tp;
   if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, seq, red, tab);
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(512) void k_pf_pv(const float *w, const float *vc, 
   static_assert(HD == 128 || HD <= 64, "two dims per lane at 128, one below");
   constexpr int DPL = HD == 128 ? 2 : 1;
   const int G = H / KVH;
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPvRows;
+  const int kvh = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPvRows;   // longest blocks first
   const int g = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int h = kvh * G + g;
   const int rend = min(R, r0 + kPvRows);
@@ -809,9 +809,9 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
   const int Tmax = p0 + R;
   const dim3 sgrid(KVH, (R + kPsRows - 1) / kPsRows, (Tmax + kPsKeys - 1) / kPsKeys);
   QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
-  if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(R, H), dim3(64), 0, w, R, p0, Tp);
-  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(R, H), dim3(256), 0, w, R, p0, Tp);
-  else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(R, H), dim3(512), 0, w, R, p0, Tp);
+  if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(H, R), dim3(64), 0, w, R, p0, Tp);
+  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(H, R), dim3(256), 0, w, R, p0, Tp);
+  else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(H, R), dim3(512), 0, w, R, p0, Tp);
   const dim3 pgrid(KVH, (R + kPvRows - 1) / kPvRows);
   QH_LAUNCH(QK_PF_ATTN, k_pf_pv<HD>, pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
   return 0;
