@@ -192,10 +192,12 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
 // Staged layout of the pipelined kernel: 64-byte rows, 16-byte chunk c of row r
 // at slot c ^ swz32(r).  The fragment reads of v_mfma_i32_32x32x32_i8 take one
-// chunk of 32 consecutive rows per half-wave; with the XOR of row bits (1^3,
-// 2^4) the lanes the LDS serves together hit distinct banks (measured: the
-// bits-1,2 swizzle of the register-staged kernel leaves 2-way conflicts here).
-__device__ __forceinline__ int swz32(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | ((((r >> 2) ^ (r >> 4)) & 1) << 1); }
+// chunk of 32 consecutive rows per half-wave.  XOR with row bits 2-3 makes those
+// 16-byte reads conflict-free on gfx950 (measured with SQ_LDS_BANK_CONFLICT on
+// this access pattern: bits 2-3 or 3-4, or 80-byte rows, 0 conflict cycles;
+// bits 1-2, or bits 1^3 and 2^4, half of the LDS cycles; bits 0-1 or none,
+// three quarters).  The staging writes fill whole 1 KiB runs and never conflict.
+__device__ __forceinline__ int swz32(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int stage_off32(int r, int c) { return r * BK + ((c ^ swz32(r)) << 4); }
 
 template <int N>
