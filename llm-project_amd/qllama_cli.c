@@ -24,24 +24,37 @@
 
 #include "qllama.h"
 
-// main.c:561-572
-static int parse_ids(char *line, int *seq, int vocab, int max_seq) {
-  char *p = line;
-  if ((unsigned char)p[0] == 0xEF && (unsigned char)p[1] == 0xBB && (unsigned char)p[2] == 0xBF) p += 3;
-  int n = 0;
-  for (char *t = strtok(p, " \t\r\n"); t && n < max_seq; t = strtok(NULL, " \t\r\n")) {
-    int id = atoi(t);
-    if (id < 0 || id >= vocab) { fprintf(stderr, "skip out-of-range id %d (vocab %d)\n", id, vocab); continue; }
-    seq[n++] = id;
+// One stdin line into token ids, with the protocol of main.c:561-572: a
+// leading UTF-8 byte order mark is ignored; fields are separated by spaces,
+// tabs, CR and LF and each is read as atoi reads it; an id outside [0, vocab)
+// is reported on stderr and dropped; once max_seq ids are kept, the rest of the
+// line is not looked at.
+static int read_prompt(char *line, int *ids, int vocab, int max_seq) {
+  static const char sep[] = " \t\r\n";
+  char *cur = line;
+  if ((unsigned char)cur[0] == 0xEF && (unsigned char)cur[1] == 0xBB && (unsigned char)cur[2] == 0xBF) cur += 3;
+  int kept = 0;
+  while (kept < max_seq) {
+    cur += strspn(cur, sep);
+    if (!*cur) break;
+    const size_t len = strcspn(cur, sep);
+    const char end = cur[len];
+    cur[len] = '\0';
+    const int id = atoi(cur);
+    cur[len] = end;
+    cur += len;
+    if (id >= 0 && id < vocab) ids[kept++] = id;
+    else fprintf(stderr, "skip out-of-range id %d (vocab %d)\n", id, vocab);
   }
-  return n;
+  return kept;
 }
 
-// main.c:574-579
-static void print_gen(const int *seq, int n) {
-  printf("gen:");
-  for (int i = 0; i < n; i++) printf(" %d", seq[i]);
-  printf("\n");
+// The line that ends each prompt's output (main.c:574-579): "gen:" and every id
+// of the sequence, each after one space.
+static void emit_gen(const int *ids, int count) {
+  fputs("gen:", stdout);
+  for (int i = 0; i < count; i++) printf(" %d", ids[i]);
+  putchar('\n');
   fflush(stdout);
 }
 
@@ -141,7 +154,7 @@ static int run_llama_f32(const char *path, int n_new) {
   int *seq = (int*)malloc((size_t)m.max_seq * sizeof(int));
   if (!seq) { fprintf(stderr, "Error: out of memory\n"); return 1; }
   while (fgets(line, sizeof(line), stdin)) {
-    int n = parse_ids(line, seq, m.vocab, m.max_seq);
+    int n = read_prompt(line, seq, m.vocab, m.max_seq);
     if (n == 0) continue;
     kv.len = 0;
     for (int i = 0; i < n; i++) llama_decode_step(&m, &kv, seq[i], &logits);
@@ -152,7 +165,7 @@ static int run_llama_f32(const char *path, int n_new) {
       fflush(stdout);
       llama_decode_step(&m, &kv, nxt, &logits);
     }
-    print_gen(seq, n);
+    emit_gen(seq, n);
   }
   free(seq);
   free_tensor(&logits);
@@ -203,7 +216,7 @@ static int run_llama(int argc, char **argv) {
   if (!seq) { fprintf(stderr, "Error: out of memory\n"); return 1; }
   int rc = 0;
   while (!rc && fgets(line, sizeof(line), stdin)) {
-    int n = parse_ids(line, seq, m.vocab, m.max_seq);
+    int n = read_prompt(line, seq, m.vocab, m.max_seq);
     if (n == 0) continue;
     kv.len = 0;
     if (q_llama_prefill(&m, &kv, seq, n, NULL) != 0) { rc = 1; break; }
@@ -214,7 +227,7 @@ static int run_llama(int argc, char **argv) {
       printf("t %d\n", nxt);
       fflush(stdout);
     }
-    if (!rc) print_gen(seq, n);
+    if (!rc) emit_gen(seq, n);
   }
   if (rc) fprintf(stderr, "Error: generation failed on the GPU\n");
   free(seq);
