@@ -37,6 +37,8 @@ CONFIGS = {
 METRIC = "decode tok/s + % HBM roofline, 8B-shape int8 LLaMA (1 GPU); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
 INT8_MFMA_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+F32_MFMA_TFLOPS = 157.3           # MI355X published fp32 peak
+F32_VALU_TFLOPS = 39.3            # 256 CUs x 64 lanes x 2.4 GHz, one unpacked fp32 op per lane
 # HBM bytes per GEMV dispatch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs
 # (scaled by a plain copy of known size), written by llm-project_amd/profsum.py
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "k_gemv_dec_traffic_8b.json")
@@ -196,6 +198,21 @@ def main_f32(args, Q, cfg, base, tied, P):
             tok = int(np.argmax(m.step(tok)))
         prof = Q.profile_read()
         Q.profile(False)
+    fwd = None
+    FR = args.forward_rows
+    if FR:
+        # llama_model_forward (llama.c:167-186): FR rows through the batched
+        # GEMMs and prefill attention, host logits (FR, vocab) as in the reference
+        fids = [int(t) for t in np.random.default_rng(7).integers(0, cfg[0], FR)]
+        m.forward(fids)                                  # first call: buffers, kernel loads
+        t0 = time.perf_counter()
+        m.forward(fids)
+        t_fwd = time.perf_counter() - t0
+        Q.profile(True)
+        m.forward(fids)
+        fprof = Q.profile_read()
+        Q.profile(False)
+        fwd = f32_forward_line(cfg, FR, t_fwd, fprof)
     m.close()
     vocab, dm, L, H, KVH, hd, ff, _ = cfg
     qd, kvd = H * hd, KVH * hd
@@ -219,8 +236,30 @@ def main_f32(args, Q, cfg, base, tied, P):
                      "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None},
         "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
         "host_model_s": round(t_host, 2), "upload_s": round(t_up, 3),
+        "forward": fwd,
     }
     print(json.dumps(line), flush=True)
+
+
+def f32_forward_line(cfg, rows, t_s, prof):
+    """The batched fp32 forward's rate and its GEMMs against the VALU bound: each
+    multiply-add is a separate v_mul_f32 and v_add_f32 (the reference rounds every
+    product before its add), so the ceiling is the unpacked, unfused fp32 lane rate."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    macs = rows * (L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab)
+    ms = {k: v[0] * v[1] for k, v in prof.items()}
+    gemm_ms = ms.get("pf_gemm", 0.0)
+    tf = 2 * macs / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None
+    return {"rows": rows, "tok_s": round(rows / t_s, 1), "ms": round(1e3 * t_s, 3),
+            "note": "llama_model_forward, host logits (rows, vocab) copied back inside the timed call",
+            "kernel_ms": {k: round(v, 3) for k, v in sorted(ms.items())},
+            "gemm": {"bound": "valu", "achieved": round(tf, 2) if tf else None,
+                     "peak": F32_VALU_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / F32_VALU_TFLOPS, 4) if tf else None,
+                     "peak_note": "unpacked fp32 v_mul + v_add, 256 CUs x 64 lanes x 2.4 GHz (the product "
+                                  "is rounded before its add, as in matrix.c:188, so no FMA or packed math); "
+                                  f"the published fp32 matrix peak is {F32_MFMA_TFLOPS} TFLOP/s"}}
 
 
 def host_info():
@@ -399,6 +438,8 @@ def main():
     ap.add_argument("--extras", action=argparse.BooleanOptionalAction, default=True,
                     help="also measure the op-level GEMV / GQA configs, the 1B and tiny configs, the "
                          "PCIe-inclusive q_llama_decode_step rate and the GPT-2 decode")
+    ap.add_argument("--forward-rows", type=int, default=512,
+                    help="f32 path: also time llama_model_forward over this many rows (0: skip)")
     ap.add_argument("--path", default="int8", choices=["int8", "f32"],
                     help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
     args = ap.parse_args()

@@ -158,7 +158,11 @@ LlamaKV llama_kv_create(const LlamaModel *m);
 void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logits);
 // llama.c:167-186  Logits (seq_len, vocab) of every position of ids (host tensor),
 // on the GPU.  Row i equals the reference's batched forward bit for bit (which
-// equals its decode step at position i); seq_len <= max_seq.
+// equals its decode step at position i).  Batched over all rows for head_dim 48,
+// 64 or 128 with at most 8 query heads per KV head, seq_len <= 16384 (max_seq
+// does not bound it); other head layouts replay decode steps, seq_len <= max_seq.
+// Uses the model's device copy if a cache holds one, else uploads one for the
+// call.  Ids outside [0, vocab) abort with a message.
 void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits);
 
 // sampler.h:12-31.  Inside the reference's build this takes the place of

@@ -170,11 +170,20 @@ __global__ void k_embed_f32(const float *wte, int dm, const int *d_in, const int
   x[j] = wte[(size_t)d_in[d_state[0]] * dm + j];
 }
 
-// y = rmsnorm(x) (rmsnorm.c:7-21), one block
+// Row r of x = wte[ids[r]] (llama.c:172-174)
+__global__ void k_embed_f32_rows(const float *wte, int dm, const int *ids, float *x) {
+  const int j = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+  if (j >= dm) return;
+  x[(size_t)r * dm + j] = wte[(size_t)ids[r] * dm + j];
+}
+
+// y = rmsnorm(x) (rmsnorm.c:7-21), one block per row of dm floats
 template <int NT, int CM>
 __global__ __launch_bounds__(NT) void k_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y) {
   __shared__ float red[NT / 64];
   __shared__ qd::SeqScratch seq;
+  x += (size_t)blockIdx.x * dm;
+  y += (size_t)blockIdx.x * dm;
   float v[CM];
   (void)qd::rmsnorm_row<NT, CM>(x, dm, gamma, eps, v, red, seq);
   const int j0 = threadIdx.x * CM;
@@ -183,13 +192,117 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_f32(const float *x, int dm, cons
     if (j0 + c < dm) y[j0 + c] = v[c];
 }
 
-// h = SiLU(g) * u = (g * (1 / (1 + expf(-g)))) * u over gu = [g | u] (swiglu.c:7-10, 36-39)
+// h = SiLU(g) * u = (g * (1 / (1 + expf(-g)))) * u over gu = [g | u] (swiglu.c:7-10, 36-39),
+// row blockIdx.y of gu [rows][2 dff] into h [rows][dff]
 __global__ void k_swiglu_f32(const float *gu, int dff, float *h) {
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= dff) return;
+  gu += (size_t)blockIdx.y * 2 * dff;
+  h += (size_t)blockIdx.y * dff;
   const float z = gu[j];
   const float s = 1.0f / (1.0f + qd::expf_glibc(-z));
   h[j] = (z * s) * gu[dff + j];
+}
+
+// ---------------------------------------------------------------------------
+// Many-row f32 matmul (matrix.c:178-190 over M rows): the GEMMs of the batched
+// forward.  Every output element is one serial chain in k order, the
+// reference's, with each product rounded before its add.  A 64 x 64 block tile
+// gives each of 256 threads 4 rows x 4 columns, 16 independent chains; K is
+// staged kKT rows at a time through LDS (A transposed to [k][row], W from the
+// block's four panels as [k][column]), and the next stage's global loads are in
+// flight while the current one is summed.  A chain takes exactly K terms: a
+// padded 0 * w term would turn a -0 sum into +0.
+// ---------------------------------------------------------------------------
+constexpr int kMT = 64;           // rows per block tile
+constexpr int kNT = 4 * kFC;      // columns per block tile: four panels
+constexpr int kKT = 32;           // k rows per LDS stage
+constexpr int kAS = kMT + 4;      // LDS stride of a k row of A
+constexpr int kWS = kNT + 4;      // LDS stride of a k row of W
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemm_f32(const float *A, int M, int K, const float *W, int N, float *out,
+                                                  const float *bias) {
+  __shared__ __align__(16) float As[kKT * kAS];
+  __shared__ __align__(16) float Ws[kKT * kWS];
+  const int tid = threadIdx.x;
+  const int i0 = blockIdx.y * kMT, j0 = blockIdx.x * kNT;
+  const int np = (N + kFC - 1) / kFC;
+  const bool vec = (K & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;   // whole aligned float4s
+  // staging of A: thread -> row ar, k offsets ak .. ak+7 of the stage
+  const int ar = tid >> 2, ak = (tid & 3) * 8;
+  const bool arow = i0 + ar < M;
+  const float *Ar = A + (size_t)(arow ? i0 + ar : 0) * K;
+  // staging of W: float4 f = tid + 256 g is panel f / 128, k row (f % 128) / 4, column quad f % 4
+  float av[8];
+  float4 wv[2];
+  auto gload = [&](int k0) {
+    if (vec) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int k = k0 + ak + 4 * h;
+        const float4 v = arow && k < K ? *reinterpret_cast<const float4 *>(Ar + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        av[4 * h] = v.x; av[4 * h + 1] = v.y; av[4 * h + 2] = v.z; av[4 * h + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) av[e] = arow && k0 + ak + e < K ? Ar[k0 + ak + e] : 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const int f = tid + 256 * g, p = blockIdx.x * 4 + (f >> 7), k = k0 + ((f & 127) >> 2);
+      wv[g] = p < np && k < K ? *reinterpret_cast<const float4 *>(W + ((size_t)p * K + k) * kFC + (f & 3) * 4)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  const int ty = tid >> 4, tx = tid & 15;
+  float acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[r][c] = 0.0f;
+  gload(0);
+  for (int k0 = 0; k0 < K; k0 += kKT) {
+    __syncthreads();                              // the previous stage is summed
+#pragma unroll
+    for (int e = 0; e < 8; e++) As[(ak + e) * kAS + ar] = av[e];
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const int f = tid + 256 * g;
+      *reinterpret_cast<float4 *>(&Ws[((f & 127) >> 2) * kWS + (f >> 7) * kFC + (f & 3) * 4]) = wv[g];
+    }
+    __syncthreads();
+    if (k0 + kKT < K) gload(k0 + kKT);
+    const int kn = min(kKT, K - k0);
+    auto step = [&](int kk) {
+      const float4 a = *reinterpret_cast<const float4 *>(&As[kk * kAS + ty * 4]);
+      const float4 w = *reinterpret_cast<const float4 *>(&Ws[kk * kWS + tx * 4]);
+      const float ar4[4] = {a.x, a.y, a.z, a.w}, wr4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[r][c] = acc[r][c] + ar4[r] * wr4[c];
+    };
+    if (kn == kKT) {
+#pragma unroll 8
+      for (int kk = 0; kk < kKT; kk++) step(kk);
+    } else {
+      for (int kk = 0; kk < kn; kk++) step(kk);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int i = i0 + ty * 4 + r;
+    if (i >= M) continue;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int j = j0 + tx * 4 + c;
+      if (j >= N) continue;
+      float *o = out + (size_t)i * N + j;
+      if (MODE == FMODE_RESID) *o = *o + acc[r][c];
+      else *o = bias ? acc[r][c] + bias[j] : acc[r][c];
+    }
+  }
 }
 
 size_t gemv_lds(int K) { return ((size_t)(K + kFT - 1) / kFT * kFT + 2 * kFC * kFS) * 4; }
@@ -238,17 +351,40 @@ extern "C" int qhip_embed_f32(const float *wte, int dm, const int *d_in, const i
   return 0;
 }
 
-extern "C" int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y) {
-  if (dm <= 256 * 4) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 4>), dim3(1), dim3(256), 0, x, dm, gamma, eps, y);
-  else if (dm <= 256 * 8) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 8>), dim3(1), dim3(256), 0, x, dm, gamma, eps, y);
-  else if (dm <= 256 * 16) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 16>), dim3(1), dim3(256), 0, x, dm, gamma, eps, y);
-  else if (dm <= 256 * 32) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 32>), dim3(1), dim3(256), 0, x, dm, gamma, eps, y);
-  else if (dm <= 1024 * 16) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<1024, 16>), dim3(1), dim3(1024), 0, x, dm, gamma, eps, y);
+extern "C" int qhip_rmsnorm_f32_rows(const float *x, int R, int dm, const float *gamma, float eps, float *y) {
+  const dim3 g(R);
+  if (R <= 0) return qh::fail_msg("rmsnorm_f32: no rows");
+  if (dm <= 256 * 4) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 4>), g, dim3(256), 0, x, dm, gamma, eps, y);
+  else if (dm <= 256 * 8) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 8>), g, dim3(256), 0, x, dm, gamma, eps, y);
+  else if (dm <= 256 * 16) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 16>), g, dim3(256), 0, x, dm, gamma, eps, y);
+  else if (dm <= 256 * 32) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<256, 32>), g, dim3(256), 0, x, dm, gamma, eps, y);
+  else if (dm <= 1024 * 16) QH_LAUNCH(QK_RMSNORM, (k_rmsnorm_f32<1024, 16>), g, dim3(1024), 0, x, dm, gamma, eps, y);
   else return qh::fail_msg("rmsnorm_f32: d_model above 16384");
   return 0;
 }
 
-extern "C" int qhip_swiglu_f32(const float *gu, int dff, float *h) {
-  QH_LAUNCH(QK_SWIGLU, k_swiglu_f32, dim3((dff + 255) / 256), dim3(256), 0, gu, dff, h);
+extern "C" int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y) {
+  return qhip_rmsnorm_f32_rows(x, 1, dm, gamma, eps, y);
+}
+
+extern "C" int qhip_swiglu_f32_rows(const float *gu, int R, int dff, float *h) {
+  QH_LAUNCH(QK_SWIGLU, k_swiglu_f32, dim3((dff + 255) / 256, R), dim3(256), 0, gu, dff, h);
+  return 0;
+}
+
+extern "C" int qhip_swiglu_f32(const float *gu, int dff, float *h) { return qhip_swiglu_f32_rows(gu, 1, dff, h); }
+
+extern "C" int qhip_embed_f32_rows(const float *wte, int dm, const int *ids, int R, float *x) {
+  QH_LAUNCH(QK_EMBED, k_embed_f32_rows, dim3((dm + 255) / 256, R), dim3(256), 0, wte, dm, ids, x);
+  return 0;
+}
+
+extern "C" int qhip_gemm_f32(int mode, int cls, const float *A, int M, int K, const float *W, int N, float *out,
+                             const float *bias) {
+  if (M <= 0 || K <= 0 || N <= 0 || M > 65535 * kMT) return qh::fail_msg("gemm_f32: bad shape");
+  const dim3 grid((N + kNT - 1) / kNT, (M + kMT - 1) / kMT);
+  if (mode == 0) QH_LAUNCH(cls, k_gemm_f32<FMODE_PLAIN>, grid, dim3(256), 0, A, M, K, W, N, out, bias);
+  else if (mode == 1) QH_LAUNCH(cls, k_gemm_f32<FMODE_RESID>, grid, dim3(256), 0, A, M, K, W, N, out, bias);
+  else return qh::fail_msg("gemm_f32: bad mode");
   return 0;
 }

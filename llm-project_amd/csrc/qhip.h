@@ -201,6 +201,15 @@ int qhip_gemv_f32_max_k(void);
 int qhip_embed_f32(const float *wte, int dm, const int *d_in, const int *d_state, float *x);
 int qhip_rmsnorm_f32(const float *x, int dm, const float *gamma, float eps, float *y);
 int qhip_swiglu_f32(const float *gu, int dff, float *h);
+// The batched fp32 forward (llama.c:167-186) over R rows: x [R][dm] = wte[ids];
+// rmsnorm of each row; h [R][dff] from gu [R][2 dff]; and out (M, N) = c (+ bias)
+// (mode 0) or out += c (mode 1) with c = A (M, K) times W (K, N) in the panel
+// layout, every c[i][j] summed in k order as the GEMV does.
+int qhip_embed_f32_rows(const float *wte, int dm, const int *ids, int R, float *x);
+int qhip_rmsnorm_f32_rows(const float *x, int R, int dm, const float *gamma, float eps, float *y);
+int qhip_swiglu_f32_rows(const float *gu, int R, int dff, float *h);
+int qhip_gemm_f32(int mode, int cls, const float *A, int M, int K, const float *W, int N, float *out,
+                  const float *bias);
 
 // cache rows (T, n_kv*hd) in the reference's layout -> [n_kv][T][hd]
 int qhip_kv_relayout(const float *src, int T, int n_kv, int hd, float *dst);

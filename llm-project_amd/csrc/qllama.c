@@ -1111,17 +1111,78 @@ void llama_decode_step(const LlamaModel *m, LlamaKV *kv, int token, Tensor *logi
   kv->len += 1;
 }
 
-// llama.c:167-186: logits (seq_len, vocab) for every position of ids.  Row i of
-// the reference's batched forward is bit-identical to the decode step of ids[i]
-// at position i after ids[0..i-1] (the reference's own check, selftest.c:1144-1178,
-// and the fixtures), so each row is computed by the device decode step on a
-// cache of its own; positions are limited to max_seq.
-void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits) {
-  if (!m || !ids || !logits || !logits->data || seq_len <= 0 || seq_len > m->max_seq) {
-    fprintf(stderr, "Error: llama_model_forward: needs 1 <= seq_len <= max_seq (%d) and a (seq_len, vocab) tensor\n",
-            m ? m->max_seq : 0);
-    abort();
+// ---------------------------------------------------------------------------
+// llama.c:167-186: logits (seq_len, vocab) for every position of ids, batched.
+// Row i of the reference's forward is bit-identical to its decode step of ids[i]
+// at position i after ids[0..i-1] (selftest.c:1144-1178 checks this, and so do
+// the fixtures), and the device pieces keep that: the GEMMs sum each element in
+// k order as the decode GEMV does, and the attention and RoPE are the int8
+// prefill's, which equal the decode step's.  The forward runs layer by layer
+// over all rows, a layer's rows in passes of at most FWD_ROWS; each pass appends
+// its keys and values to the layer's cache (stride seq_len) before its attention
+// reads them, so every row sees all earlier rows, and one cache serves every
+// layer.  Head layouts the prefill attention does not take replay decode steps
+// on a cache of their own (then seq_len <= max_seq).
+// ---------------------------------------------------------------------------
+#define FWD_ROWS 2048        // rows per pass through a layer
+#define FWD_MAX_ROWS 16384   // the prefill attention's largest cache stride
+#define FWD_CLS 14           // profiling class of the forward's GEMMs (QK_PF_GEMM)
+
+static int fwd_supported(const FDev *f) {
+  const int G = f->H / f->KVH;
+  return (f->hd == 128 || f->hd == 64 || f->hd == 48) && G >= 1 && G <= 8 && G * f->hd <= 1024;
+}
+
+static int fwd_run(const FDev *f, float rope_base, const int *ids, int n, float *logits) {
+  const int R = n < FWD_ROWS ? n : FWD_ROWS, half = f->hd / 2, own_rope = n > f->max_seq;
+  const size_t dm = (size_t)f->dm, V = (size_t)f->vocab, per = (size_t)f->KVH * n * f->hd;
+  size_t off = 0;
+#define FTAKE(nf) (off += al256((size_t)(nf) * 4), off - al256((size_t)(nf) * 4))
+  const size_t o_ids = FTAKE(n), o_x = FTAKE((size_t)n * dm), o_xn = FTAKE(R * dm), o_qkv = FTAKE((size_t)R * f->nqkv);
+  const size_t o_q = FTAKE((size_t)R * f->qd), o_o = FTAKE((size_t)R * f->qd), o_gu = FTAKE((size_t)R * 2 * f->dff);
+  const size_t o_h = FTAKE((size_t)R * f->dff), o_lg = FTAKE(R * V), o_kc = FTAKE(per), o_vc = FTAKE(per);
+  const size_t o_ws = FTAKE(qhip_pf_attention_scratch(R, f->H, n));
+  const size_t o_cos = FTAKE(own_rope ? (size_t)n * half : 1), o_sin = FTAKE(own_rope ? (size_t)n * half : 1);
+#undef FTAKE
+  uint8_t *b = (uint8_t*)qhip_malloc(off);
+  if (!b) return 1;
+  int *d_ids = (int*)(b + o_ids);
+  float *X = (float*)(b + o_x), *xn = (float*)(b + o_xn), *qkv = (float*)(b + o_qkv), *q = (float*)(b + o_q);
+  float *o = (float*)(b + o_o), *gu = (float*)(b + o_gu), *h = (float*)(b + o_h), *lg = (float*)(b + o_lg);
+  float *kc = (float*)(b + o_kc), *vc = (float*)(b + o_vc), *ws = (float*)(b + o_ws);
+  const float *cs = f->rope_cos, *sn = f->rope_sin;
+  int rc = qhip_h2d(d_ids, ids, (size_t)n * sizeof(int));
+  if (!rc && own_rope) {        // positions past max_seq: tables of n rows (rope.c:58-61)
+    rc = rope_upload((float*)(b + o_cos), (float*)(b + o_sin), n, f->hd, rope_base);
+    cs = (const float*)(b + o_cos); sn = (const float*)(b + o_sin);
   }
+  if (!rc) rc = qhip_embed_f32_rows(f->wte, f->dm, d_ids, n, X);
+  for (int l = 0; l < f->L && !rc; l++)
+    for (int c0 = 0; c0 < n && !rc; c0 += R) {
+      const int r = n - c0 < R ? n - c0 : R;
+      float *Xc = X + (size_t)c0 * dm;
+      rc |= qhip_rmsnorm_f32_rows(Xc, r, f->dm, f->g_attn[l], f->eps, xn);
+      rc |= qhip_gemm_f32(0, FWD_CLS, xn, r, f->dm, f->wqkv[l], f->nqkv, qkv, f->bqkv[l]);
+      rc |= qhip_pf_rope_append(qkv, r, f->H, f->KVH, f->hd, cs, sn, c0, q, kc, vc, n);
+      rc |= qhip_pf_attention(q, kc, vc, r, c0, f->H, f->KVH, f->hd, n, f->attn_scale, ws, o);
+      rc |= qhip_gemm_f32(1, FWD_CLS, o, r, f->qd, f->wo[l], f->dm, Xc, NULL);
+      rc |= qhip_rmsnorm_f32_rows(Xc, r, f->dm, f->g_ffn[l], f->eps, xn);
+      rc |= qhip_gemm_f32(0, FWD_CLS, xn, r, f->dm, f->wgu[l], 2 * f->dff, gu, NULL);
+      rc |= qhip_swiglu_f32_rows(gu, r, f->dff, h);
+      rc |= qhip_gemm_f32(1, FWD_CLS, h, r, f->dff, f->wd[l], f->dm, Xc, NULL);
+    }
+  for (int c0 = 0; c0 < n && !rc; c0 += R) {   // final norm and head (llama.c:182-183)
+    const int r = n - c0 < R ? n - c0 : R;
+    rc |= qhip_rmsnorm_f32_rows(X + (size_t)c0 * dm, r, f->dm, f->g_final, f->eps, xn);
+    rc |= qhip_gemm_f32(0, FWD_CLS, xn, r, f->dm, f->head, f->vocab, lg, NULL);
+    rc = rc || qhip_d2h_async(logits + (size_t)c0 * V, lg, (size_t)r * V * 4) || qhip_sync();
+  }
+  if (qhip_sync()) rc = 1;
+  qhip_free(b);
+  return rc;
+}
+
+static void fwd_steps(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits) {
   LlamaKV kv = llama_kv_create(m);
   int shape[2] = {1, m->vocab};
   for (int i = 0; i < seq_len; i++) {
@@ -1131,6 +1192,34 @@ void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tenso
     llama_decode_step(m, &kv, ids[i], &row);
   }
   llama_kv_free(&kv);
+}
+
+void llama_model_forward(const LlamaModel *m, const int *ids, int seq_len, Tensor *logits) {
+  if (!m || !ids || !logits || !logits->data || seq_len <= 0) {
+    fprintf(stderr, "Error: llama_model_forward: needs seq_len >= 1, ids and a (seq_len, vocab) tensor\n");
+    abort();
+  }
+  for (int i = 0; i < seq_len; i++)
+    if (ids[i] < 0 || ids[i] >= m->vocab) {
+      fprintf(stderr, "Error: llama_model_forward: token %d at %d out of range\n", ids[i], i);
+      abort();
+    }
+  FDev *f = fdev_find(m);
+  if (!f) f = fdev_upload(m);
+  if (!f) abort();
+  f->refs++;                          // held for the call (a cache freed meanwhile keeps it)
+  // QLLAMA_FORWARD_STEPS=1: replay decode steps instead (same results)
+  const int batched = fwd_supported(f) && !getenv("QLLAMA_FORWARD_STEPS");
+  if (batched && seq_len <= FWD_MAX_ROWS) {
+    if (fwd_run(f, m->rope_base, ids, seq_len, logits->data)) die("llama_model_forward");
+  } else if (seq_len <= m->max_seq) {
+    fwd_steps(m, ids, seq_len, logits);
+  } else {
+    fprintf(stderr, "Error: llama_model_forward: seq_len %d is above %d for this model\n", seq_len,
+            batched ? FWD_MAX_ROWS : m->max_seq);
+    abort();
+  }
+  fdev_release(f);
 }
 
 // ---------------------------------------------------------------------------

@@ -149,18 +149,87 @@ def test_f32_forward_matches_reference(Q, name):
         ref.close()
 
 
+def perturb(ref, seed):
+    """Nonzero q/k/v biases and norm gains other than 1 (llama.c:319-321, rmsnorm.c:18)."""
+    rng = np.random.default_rng(seed)
+    for name, t in ref.tensors():
+        if name in ("b_q", "b_k", "b_v"):
+            t[:] = rng.standard_normal(t.shape).astype(np.float32) * np.float32(0.1)
+        if name in ("attn_norm", "ffn_norm", "final_norm"):
+            t[:] = (1.0 + rng.standard_normal(t.shape) * 0.2).astype(np.float32)
+
+
+def test_f32_forward_two_passes_match_oracle(Q):
+    """The batched forward over 2100 rows, so each layer takes two passes (2048 +
+    52 rows) and the second pass attends to the first's cache rows; biases, norm
+    gains and an FFN width of 250 (not a multiple of 4: the GEMM's scalar loads).
+    Every row bit for bit against the oracle's decode step at that position."""
+    cfg = [700, 128, 2, 4, 2, 64, 250, 2112]
+    n = 2100
+    ref = O.FModel(cfg, 10000.0, seed=41)
+    try:
+        perturb(ref, 9)
+        ids = [int(t) for t in np.random.default_rng(3).integers(0, cfg[0], n)]
+        g = gpu_model(Q, ref, cfg, 10000.0)
+        try:
+            log("forward of 2100 rows")
+            L = g.forward(ids)
+        finally:
+            g.close()
+        for i, t in enumerate(ids):
+            r = ref.step(t)
+            assert np.array_equal(bits(L[i]), bits(r)), i
+    finally:
+        ref.close()
+
+
+def test_f32_forward_past_max_seq_matches_oracle(Q):
+    """seq_len above the model's max_seq (the reference's forward has no such
+    bound, llama.c:167-186): positions 16 .. 39 take RoPE tables made for the
+    call.  Rows against the oracle's decode steps on the same weights with room
+    for 64 positions."""
+    cfg16 = [500, 192, 2, 6, 2, 48, 320, 16]
+    cfg64 = cfg16[:7] + [64]
+    ref = O.FModel(cfg64, 10000.0, seed=17)
+    try:
+        ids = [int(t) for t in np.random.default_rng(4).integers(0, 500, 40)]
+        g = gpu_model(Q, ref, cfg16, 10000.0)
+        try:
+            L = g.forward(ids)
+        finally:
+            g.close()
+        for i, t in enumerate(ids):
+            assert np.array_equal(bits(L[i]), bits(ref.step(t))), i
+    finally:
+        ref.close()
+
+
+def test_f32_forward_batched_equals_steps(Q, monkeypatch):
+    """The batched forward and the decode-step replay (QLLAMA_FORWARD_STEPS=1)
+    give the same bits on the mid fixture's model."""
+    meta = golden_json("e2e_f32_mid")
+    ref = O.FModel(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    try:
+        g = gpu_model(Q, ref, meta["cfg"], meta["rope_base"])
+        try:
+            ids = list(meta["prompt"]) * 3
+            a = g.forward(ids)
+            monkeypatch.setenv("QLLAMA_FORWARD_STEPS", "1")
+            b = g.forward(ids)
+            assert np.array_equal(bits(a), bits(b))
+        finally:
+            g.close()
+    finally:
+        ref.close()
+
+
 def test_f32_nonzero_biases_and_gains_match_oracle(Q):
     """Biases (Qwen-style checkpoints, llama.c:319-321) and norm gains other than 1
     (rmsnorm.c:18) through the fp32 step, bit for bit against the oracle."""
     cfg = [3000, 256, 2, 8, 2, 32, 512, 64]
     ref = O.FModel(cfg, 10000.0, seed=31)
     try:
-        rng = np.random.default_rng(5)
-        for name, t in ref.tensors():
-            if name in ("b_q", "b_k", "b_v"):
-                t[:] = rng.standard_normal(t.shape).astype(np.float32) * np.float32(0.1)
-            if name in ("attn_norm", "ffn_norm", "final_norm"):
-                t[:] = (1.0 + rng.standard_normal(t.shape) * 0.2).astype(np.float32)
+        perturb(ref, 5)
         g = gpu_model(Q, ref, cfg, 10000.0)
         try:
             for t in [3, 17, 2999, 0, 42, 7]:
