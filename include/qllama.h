@@ -294,6 +294,15 @@ int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, in
 // one warm-up (HIP events on the library stream); *us_per_call receives the mean.
 int  qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv, int hd,
                           float rope_base, int mode, int reps, float *o, float *k_row, double *us_per_call);
+// Causal prompt attention (llama.c:554-576 for rows p0 .. p0+R-1) on the device:
+// q (R, n_heads*hd) already rotated, k and v (p0+R, n_kv*hd) in the reference's
+// cache layout, o (R, n_heads*hd); all host memory.  mode QLLAMA_MODE_EXACT is
+// q_llama_prefill's exact path (every row equal to its decode step);
+// QLLAMA_MODE_FAST is the fast mode's fp32 MFMA attention (head_dim 64 or 128).
+// reps > 0 times that many launches after one warm-up; *us_per_call receives the
+// mean.  For op-level parity and the bench.
+int  qllama_pf_attention_ex(const float *q, const float *k, const float *v, int R, int p0, int n_heads, int n_kv,
+                            int hd, int mode, int reps, float *o, double *us_per_call);
 // One activation row through the decode GEMV that normalizes its own input:
 // rmsnorm (rmsnorm.c:7-21) + activation quantization (quant.c:66-78) formed in
 // every block, then the W8A8 product (quant.c:79-82).  mode 0: out = W->cols

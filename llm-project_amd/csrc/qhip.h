@@ -175,6 +175,11 @@ int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, 
 int qhip_pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads, int n_kv,
                       int hd, int max_seq, float scale, float *ws, float *o);
 size_t qhip_pf_attention_scratch(int R, int n_heads, int max_seq);
+// The fast mode's prompt attention (k_pfa.hip): the same causal attention with
+// fp32 MFMA and an online softmax (not bit-exact); head_dim 64 or 128, G <= 8.
+int qhip_pf_attention_fast_ok(int n_heads, int n_kv, int hd);
+int qhip_pf_attention_fast(const float *q, const float *kc, const float *vc, int R, int p0, int n_heads, int n_kv,
+                           int hd, int max_seq, float scale, float *o);
 
 // Token sampling on the device (k_sample.hip).  qhip_sample: temperature > 0,
 // top-k, top-p over one row of V logits (sampler.c:54-143) with the xorshift64

@@ -815,6 +815,7 @@ static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
   int st[2] = {pos + n - 1, pos + n};
   if (qhip_h2d(d->d_in + pos, ids, (size_t)n * sizeof(int)) || qhip_h2d(d->d_state, st, sizeof st)) return 1;
   const size_t per = (size_t)d->max_seq * d->kvd;
+  const int fast_attn = kd->mode == QLLAMA_MODE_FAST && qhip_pf_attention_fast_ok(d->H, d->KVH, d->hd);
   int rc = 0;
   for (int c0 = 0; c0 < n && !rc; c0 += rows) {
     const int R = n - c0 < rows ? n - c0 : rows, p0 = pos + c0;
@@ -826,8 +827,11 @@ static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
                          d->bqkv[l]);
       rc |= qhip_pf_rope_append(d->pf_qkv, R, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, p0, d->pf_q, kc, vc,
                                 d->max_seq);
-      rc |= qhip_pf_attention(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_attn,
-                              d->pf_o);
+      if (fast_attn)      // fast cache: MFMA attention, a tolerance path like the fast decode
+        rc |= qhip_pf_attention_fast(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_o);
+      else
+        rc |= qhip_pf_attention(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_attn,
+                                d->pf_o);
       rc |= qhip_quant_rows(d->pf_o, R, d->qd, d->pf_qa, d->kp_qd, d->pf_as);
       rc |= qhip_gemm_i8(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm, NULL);
       rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_ffn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
@@ -1566,6 +1570,47 @@ int qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, 
 // plain (out: W->cols values), mode 2 SwiGLU over gate columns [0, N) and up
 // columns [N, 2N) of W (out: N = W->cols / 2 values of h, llama.c:583-587).
 // fast selects the fast decode mode's tree-ordered sum of squares.
+int qllama_pf_attention_ex(const float *q, const float *k, const float *v, int R, int p0, int n_heads, int n_kv,
+                           int hd, int mode, int reps, float *o, double *us_per_call) {
+  if (qhip_init()) return 1;
+  const int T = p0 + R;
+  if (!q || !k || !v || !o || R <= 0 || p0 < 0 || n_kv <= 0 || n_heads <= 0 || n_heads % n_kv || hd <= 0 ||
+      (mode != QLLAMA_MODE_EXACT && mode != QLLAMA_MODE_FAST) || T > 16384) {
+    fprintf(stderr, "Error: qllama_pf_attention_ex: bad shape or mode\n");
+    return 1;
+  }
+  const int G = n_heads / n_kv;
+  if (mode == QLLAMA_MODE_FAST ? !qhip_pf_attention_fast_ok(n_heads, n_kv, hd)
+                               : !((hd == 128 || hd == 64 || hd == 48) && G <= 8 && G * hd <= 1024)) {
+    fprintf(stderr, "Error: qllama_pf_attention_ex: shape not supported in this mode\n");
+    return 1;
+  }
+  const size_t qn = (size_t)R * n_heads * hd, kvn = (size_t)T * n_kv * hd;
+  const size_t ws_n = mode == QLLAMA_MODE_FAST ? 1 : qhip_pf_attention_scratch(R, n_heads, T);
+  float *dq = (float*)qhip_malloc(qn * 4), *dk = (float*)qhip_malloc(kvn * 4), *dv = (float*)qhip_malloc(kvn * 4);
+  float *tmp = (float*)qhip_malloc(kvn * 4), *dout = (float*)qhip_malloc(qn * 4), *ws = (float*)qhip_malloc(ws_n * 4);
+  int rc = (!dq || !dk || !dv || !tmp || !dout || !ws) ? 1 : 0;
+  if (!rc) rc = qhip_h2d(dq, q, qn * 4) || qhip_h2d(tmp, k, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dk) ||
+                qhip_sync() || qhip_h2d(tmp, v, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dv);
+  const float scale = 1.0f / sqrtf((float)hd);                  // llama.c:532
+#define PFA_LAUNCH()                                                                                       \
+  (mode == QLLAMA_MODE_FAST ? qhip_pf_attention_fast(dq, dk, dv, R, p0, n_heads, n_kv, hd, T, scale, dout)  \
+                            : qhip_pf_attention(dq, dk, dv, R, p0, n_heads, n_kv, hd, T, scale, ws, dout))
+  if (!rc) rc = PFA_LAUNCH() || qhip_sync();
+  if (!rc && reps > 0) {
+    double ms = 0.0;
+    rc = qhip_timer_start();
+    for (int i = 0; i < reps && !rc; i++) rc = PFA_LAUNCH();
+    if (!rc) rc = qhip_timer_stop(&ms);
+    if (!rc && us_per_call) *us_per_call = 1e3 * ms / reps;
+  }
+#undef PFA_LAUNCH
+  if (!rc) rc = qhip_d2h(o, dout, qn * 4);
+  if (rc) fprintf(stderr, "Error: qllama_pf_attention_ex: %s\n", qhip_last_error());
+  qhip_free(dq); qhip_free(dk); qhip_free(dv); qhip_free(tmp); qhip_free(dout); qhip_free(ws);
+  return rc;
+}
+
 int qllama_norm_gemv(const float *x, const float *gamma, float eps, const QTensor *W, int mode, int fast, float *out) {
   if (qhip_init()) return 1;
   const int dm = W->rows, cols = W->cols;

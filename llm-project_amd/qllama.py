@@ -153,6 +153,7 @@ def lib():
                                        P(C.c_float)]
         L.qllama_gqa_decode_ex.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 4 + [C.c_float, C.c_int, C.c_int] + \
             [P(C.c_float), P(C.c_float), P(C.c_double)]
+        L.qllama_pf_attention_ex.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 7 + [P(C.c_float), P(C.c_double)]
         L.qllama_sync.restype = C.c_int
         L.qllama_stream.restype = C.c_void_p
         L.qllama_profile.argtypes = [C.c_int]
@@ -538,6 +539,24 @@ def gqa_decode(q, k, v, n_heads, n_kv, hd, mode=MODE_EXACT, rope_base=0.0, reps=
     if rc != 0:
         raise RuntimeError("qllama_gqa_decode_ex failed")
     return o, krow, (us.value if reps else None)
+
+
+def pf_attention(q, k, v, n_heads, n_kv, hd, p0=0, mode=MODE_EXACT, reps=0):
+    """qllama_pf_attention_ex: causal attention of the R rows of q (rotated, at
+    positions p0 .. p0+R-1) over the p0+R rows of k, v (reference layout).
+    Returns (o of shape (R, n_heads*hd), microseconds per call or None)."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    R = q.shape[0]
+    assert k.shape[0] == p0 + R and v.shape == k.shape
+    o = np.zeros((R, n_heads * hd), np.float32)
+    us = C.c_double(0.0)
+    rc = lib().qllama_pf_attention_ex(_f32(q), _f32(k), _f32(v), R, p0, n_heads, n_kv, hd, int(mode), int(reps),
+                                      _f32(o), C.byref(us))
+    if rc != 0:
+        raise RuntimeError("qllama_pf_attention_ex failed")
+    return o, (us.value if reps else None)
 
 
 def profile(enable):

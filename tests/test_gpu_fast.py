@@ -120,6 +120,45 @@ def test_fast_attention_groupings_match_oracle(Q, shape):
     np.testing.assert_allclose(o, ref, atol=ATOL, rtol=RTOL)
 
 
+# ---- prompt attention of the fast mode (fp32 MFMA, k_pfa.hip) --------------------
+@pytest.mark.parametrize("shape", [(32, 8, 128), (16, 4, 64), (8, 8, 64), (16, 2, 128), (12, 4, 64)])
+def test_fast_prompt_attention_close_to_exact(Q, shape):
+    """Causal attention of 200 prompt rows at positions 37 .. 236 (partial row
+    and key tiles, every grouping G = 1, 3, 4, 8): the fast mode's MFMA kernel
+    against the exact path within the north star's tolerance; the exact path's
+    rows against the decode attention of the same row, bit for bit."""
+    H, KVH, hd = shape
+    R, p0 = 200, 37
+    rng = np.random.default_rng(hd + 7 * H + KVH)
+    q = rng.standard_normal((R, H * hd)).astype(np.float32)
+    k = rng.standard_normal((p0 + R, KVH * hd)).astype(np.float32)
+    v = rng.standard_normal((p0 + R, KVH * hd)).astype(np.float32)
+    ex, _ = Q.pf_attention(q, k, v, H, KVH, hd, p0=p0, mode=Q.MODE_EXACT)
+    fa, _ = Q.pf_attention(q, k, v, H, KVH, hd, p0=p0, mode=Q.MODE_FAST)
+    np.testing.assert_allclose(fa, ex, atol=ATOL, rtol=RTOL)
+    err = float(np.max(np.abs(fa - ex)))
+    log(f"{shape}: max |fast - exact| = {err:.3g}")
+    assert err < 1e-4
+    for r in (0, 1, 63, R - 1):
+        T = p0 + r + 1
+        o, _, _ = Q.gqa_decode(q[r], k[:T], v[:T], H, KVH, hd, mode=Q.MODE_EXACT)
+        assert bits_equal(ex[r], o), r
+
+
+def test_fast_prompt_attention_long_prompt(Q):
+    """The 8B shape's 2048-row prompt (64 row blocks, the longest with 64 key
+    tiles): fast against exact within tolerance."""
+    H, KVH, hd, R = 32, 8, 128, 2048
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((R, H * hd)).astype(np.float32)
+    k = rng.standard_normal((R, KVH * hd)).astype(np.float32)
+    v = rng.standard_normal((R, KVH * hd)).astype(np.float32)
+    ex, _ = Q.pf_attention(q, k, v, H, KVH, hd, mode=Q.MODE_EXACT)
+    fa, _ = Q.pf_attention(q, k, v, H, KVH, hd, mode=Q.MODE_FAST)
+    np.testing.assert_allclose(fa, ex, atol=ATOL, rtol=RTOL)
+    log(f"2048 rows: max |fast - exact| = {float(np.max(np.abs(fa - ex))):.3g}")
+
+
 @pytest.mark.parametrize("dm", [2048, 4096])
 def test_fast_rmsnorm_gemv_close_to_exact(Q, dm):
     """The fast mode's tree-ordered sum of squares inside the GEMV: outputs equal
@@ -208,11 +247,13 @@ def test_fast_e2e_8b_bounded(Q):
     _fast_vs_reference(Q, "8b")
 
 
-@pytest.mark.parametrize("name", ["1b", "8b"])
-def test_fast_cache_prefill_is_exact(Q, name):
-    """The bench's sequence: prompt ingestion (the exact batched prefill, whatever
-    the cache's mode) into a fast cache gives the reference's logits bit for bit
-    and its first token; fast greedy decoding then continues on the device."""
+@pytest.mark.parametrize("name", ["tiny", "1b", "8b"])
+def test_fast_cache_prefill_bounded(Q, name):
+    """The bench's sequence on a fast cache: prompt ingestion (the batched
+    prefill with the fast mode's MFMA attention where head_dim is 64 or 128; the
+    exact attention at head_dim 48) then fast greedy decoding on the device.  The
+    prompt's last logits stay correlated with the reference's (the bound of the
+    fast decode tests; bit for bit at the tiny shape, whose prefill is exact)."""
     if not have_golden(f"e2e_{name}.json"):
         pytest.skip(f"{name} fixture not generated")
     meta = golden_json(f"e2e_{name}")
@@ -220,9 +261,13 @@ def test_fast_cache_prefill_is_exact(Q, name):
     try:
         lg = m.prefill(meta["prompt"]).copy()
         ref = golden(f"e2e_{name}_logits_prompt_last")          # the fixture keeps the first logits
-        assert bits_equal(lg[:ref.size], ref)
+        corr = float(np.corrcoef(lg[:ref.size], ref)[0, 1])
+        log(f"{name}: fast-cache prefill, max |d| {float(np.max(np.abs(lg[:ref.size] - ref))):.3g}, "
+            f"correlation {corr:.5f}, first token {int(np.argmax(lg))} (reference {meta['gen'][0]})")
+        if meta["cfg"][5] == 48:
+            assert bits_equal(lg[:ref.size], ref)
+        assert corr >= MIN_CORR
         first = int(np.argmax(lg))
-        assert first == meta["gen"][0]
         out = m.generate_greedy(first, 32)
         assert len(out) == 32 and all(0 <= t < meta["cfg"][0] for t in out)
         assert m.pos == len(meta["prompt"]) + 32
