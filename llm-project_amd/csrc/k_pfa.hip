@@ -13,7 +13,14 @@
 //   O^T += V^T . P^T  (hd x 32 rows), whose B operand is each lane's own
 //   probabilities: the MFMA's K slots are matched to the keys a lane holds.
 // q is pre-scaled by scale * log2(e), so p = exp2(s - m) (v_exp_f32).  At the
-// end o = O / l.  Blocks of later rows see more keys; they are dispatched first.
+// end o = O / l.
+//
+// Later rows see more keys.  With pairing (G <= 4), block i serves row blocks i
+// and nrb-1-i with 2G waves (the second set on the SIMDs of the first), so
+// every block and every SIMD does nrb+1 tiles of MFMA work; the staged tiles
+// serve both sets, the first set idling at the barriers once its rows have
+// seen all their keys.  Without pairing (G > 4: 2G waves would not hold their
+// registers) blocks of later rows are dispatched first.
 #include <hip/hip_runtime.h>
 
 #include "qhip.h"
@@ -28,20 +35,33 @@ constexpr int kKeys = 32;    // keys per tile (the MFMA's rows of S^T)
 
 template <int HD>
 __global__ __launch_bounds__(512) void k_pf_fa(const float *q, const float *kc, const float *vc, int R, int p0, int H,
-                                               int KVH, int max_seq, float qscale, float *o) {
+                                               int KVH, int max_seq, float qscale, float *o, int pair) {
   constexpr int QK = HD / 8;       // groups of 8 dims: lane half hf holds dims 8m + 4hf .. +3 of its row
   constexpr int NB = HD / 32;      // 32-dim blocks of the output
   constexpr int KS = HD + 4;       // LDS row stride of the K tile (conflict-free 16-byte reads)
   constexpr int VS = kKeys + 4;    // LDS row stride of the transposed V tile
   __shared__ __attribute__((aligned(16))) float Ks[kKeys * KS];
   __shared__ __attribute__((aligned(16))) float Vt[HD * VS];
-  const int G = H / KVH;
-  const int kvh = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kRows;
+  const int G = H / KVH, nrb = (R + kRows - 1) / kRows;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
-  const int h = kvh * G + wave;
+  const int kvh = blockIdx.x;
+  int rb, rb_last;                                 // this wave's row block, the block's longest
+  bool active = true;
+  if (pair) {
+    const int i = blockIdx.y, j = nrb - 1 - i, second = wave >= G;
+    rb = second ? j : i;
+    rb_last = j;
+    active = !second || j != i;                    // an odd middle block has one set
+  } else {
+    rb = rb_last = gridDim.y - 1 - blockIdx.y;
+  }
+  const int r0 = rb * kRows;
+  const int h = kvh * G + wave % G;
   const int rl = min(r0 + lr, R - 1);              // this lane's query row (rows past R are not stored)
   const int pos = p0 + rl;
-  const int kend = p0 + min(r0 + kRows, R);        // keys 0 .. kend-1 are seen by some row of the block
+  const int kmine = p0 + min(r0 + kRows, R);       // keys 0 .. kmine-1 are seen by some row of the set
+  const int kend = p0 + min(rb_last * kRows + kRows, R);   // ... and kend-1 by some row of the block
+  const int nmine = (kmine + kKeys - 1) / kKeys;
 
   float qf[QK][4];
   {
@@ -74,6 +94,10 @@ __global__ __launch_bounds__(512) void k_pf_fa(const float *q, const float *kc, 
       Vt[(d4 + 3) * VS + key] = vv.w;
     }
     __syncthreads();
+    if (!active || t >= nmine) {                   // this set's rows have seen all their keys
+      __syncthreads();
+      continue;
+    }
 
     // S^T[key][row]: A = K (lane: key lr, K slot hf), B = q (lane: row lr, K slot hf);
     // instruction (m, c) takes dim 8m + 4hf + c in both operands
@@ -125,7 +149,7 @@ __global__ __launch_bounds__(512) void k_pf_fa(const float *q, const float *kc, 
   }
 
   const float inv = 1.0f / (lrun + __shfl_xor(lrun, 32));
-  if (r0 + lr < R) {
+  if (active && r0 + lr < R) {
     // element e of block b is dim 32b + 8(e/4) + 4hf + e%4 of this lane's row
     float *orow = o + (size_t)(r0 + lr) * H * HD + (size_t)h * HD + 4 * hf;
 #pragma unroll
@@ -150,12 +174,12 @@ extern "C" int qhip_pf_attention_fast(const float *q, const float *kc, const flo
                                       int n_kv, int hd, int max_seq, float scale, float *o) {
   if (!qhip_pf_attention_fast_ok(n_heads, n_kv, hd)) return qh::fail_msg("pf_attention_fast: unsupported shape");
   if (R <= 0 || p0 < 0 || p0 + R > max_seq) return qh::fail_msg("pf_attention_fast: positions out of range");
-  const int G = n_heads / n_kv;
-  const dim3 grid(n_kv, (R + kRows - 1) / kRows), block(64 * G);
+  const int G = n_heads / n_kv, nrb = (R + kRows - 1) / kRows, pair = G <= 4 && nrb > 1;
+  const dim3 grid(n_kv, pair ? (nrb + 1) / 2 : nrb), block(64 * G * (pair ? 2 : 1));
   const float qscale = scale * 1.4426950408889634f;     // log2(e): p = exp2(s * log2(e) - m)
   if (hd == 128)
-    QH_LAUNCH(QK_PF_ATTN, k_pf_fa<128>, grid, block, 0, q, kc, vc, R, p0, n_heads, n_kv, max_seq, qscale, o);
+    QH_LAUNCH(QK_PF_ATTN, k_pf_fa<128>, grid, block, 0, q, kc, vc, R, p0, n_heads, n_kv, max_seq, qscale, o, pair);
   else
-    QH_LAUNCH(QK_PF_ATTN, k_pf_fa<64>, grid, block, 0, q, kc, vc, R, p0, n_heads, n_kv, max_seq, qscale, o);
+    QH_LAUNCH(QK_PF_ATTN, k_pf_fa<64>, grid, block, 0, q, kc, vc, R, p0, n_heads, n_kv, max_seq, qscale, o, pair);
   return 0;
 }
