@@ -102,7 +102,11 @@ const char *qhip_last_error(void) { return g_err; }
 void *qhip_malloc(size_t bytes) {
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
-  if (e != hipSuccess) { fail("hipMalloc", e); return nullptr; }
+  if (e != hipSuccess) {
+    fail("hipMalloc", e);
+    (void)hipGetLastError();     // a refused allocation must not fail the next launch's check
+    return nullptr;
+  }
   return p;
 }
 
@@ -111,7 +115,11 @@ void qhip_free(void *p) { if (p) (void)hipFree(p); }
 void *qhip_host_alloc(size_t bytes) {
   void *p = nullptr;
   hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
-  if (e != hipSuccess) { fail("hipHostMalloc", e); return nullptr; }
+  if (e != hipSuccess) {
+    fail("hipHostMalloc", e);
+    (void)hipGetLastError();
+    return nullptr;
+  }
   return p;
 }
 

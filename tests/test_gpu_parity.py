@@ -223,6 +223,25 @@ def test_decode_rejects_position_past_max_seq(Q):
     assert r.returncode != 0 and "exceeds max_seq" in r.stderr
 
 
+def test_refused_device_allocation_is_an_error_not_a_crash(Q, capfd):
+    """A model larger than the GPU's memory (about 440 GB of int8 weights): the
+    device allocation is refused, q_llama_model_synth prints an error and
+    returns nonzero (as the reference's loaders do on failure), and the library
+    stays usable: a small model built afterwards decodes bit-exactly."""
+    big = [128256, 16384, 200, 128, 16, 128, 32768, 64]
+    with pytest.raises(RuntimeError):
+        Q.Model.synth(big, 10000.0)
+    assert "device allocation" in capfd.readouterr().err
+    meta = golden_json("e2e_tiny")
+    m = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"])
+    try:
+        for i, t in enumerate(meta["prompt"][:4]):
+            lg = m.step(t)
+            assert O.hash_f32(lg) == int(meta["logit_hashes"][i], 16), i
+    finally:
+        m.close()
+
+
 # ---- quant.h API ------------------------------------------------------------
 @pytest.mark.parametrize("case", ["a", "b"])
 def test_quantize_int8_percol_matches_reference(Q, case):
