@@ -23,32 +23,51 @@ __global__ void k_gpt_embed(const float *wte, const float *wpe, int dm, const in
 
 // layernorm.c:8-38 for one row, one block of NT threads (thread t holds
 // elements [t*CM, t*CM + CM)):
-//   mean = (sum_j x_j, in order) / cols       -- a serial chain (signed terms)
+//   mean = (sum_j x_j, in order) / cols       -- a serial chain (signed terms), one lane
 //   var  = (sum_j (x_j - mean)^2, in order) / cols   -- exact parallel sum (qdev_seqsum.h)
 //   y_j  = ((x_j - mean) * (1 / sqrtf(var + eps))) * gamma_j + beta_j
 template <int NT, int CM>
 __global__ __launch_bounds__(NT) void k_layernorm_f32(const float *x, int dm, const float *gamma, const float *beta,
                                                       float eps, float *y) {
-  __shared__ float xs[NT * CM];
+  __shared__ __attribute__((aligned(16))) float xs[NT * CM];
   __shared__ qd::SeqScratch seq;
   __shared__ float mean_s;
   const int j0 = threadIdx.x * CM;
-  float v[CM];
+  float v[CM], ga[CM], be[CM];
 #pragma unroll
   for (int c = 0; c < CM; c++) {
     v[c] = j0 + c < dm ? x[j0 + c] : 0.0f;
-    xs[j0 + c] = v[c];                                  // +0 past dm: adds nothing to the chain
+    ga[c] = j0 + c < dm ? gamma[j0 + c] : 0.0f;       // requested now, used at the end
+    be[c] = j0 + c < dm ? beta[j0 + c] : 0.0f;
   }
+#pragma unroll
+  for (int c = 0; c < CM; c++) xs[j0 + c] = v[c];
   qd::lds_sync();
   if (threadIdx.x == 0) {
+    // the chain over exactly dm terms, 16 at a time from LDS with the next 16
+    // requested before the current ones are added (the reads land while the
+    // adds run); a tail of dm % 16 terms one by one
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    const int n16 = dm / 16;
     float s = 0.0f;
-    for (int j = 0; j < dm; j += 8) {                   // eight loads in flight ahead of the adds
-      float t[8];
+    float4 a[4], b[4];
 #pragma unroll
-      for (int u = 0; u < 8; u++) t[u] = j + u < dm ? xs[j + u] : 0.0f;
+    for (int u = 0; u < 4; u++) a[u] = n16 > 0 ? x4[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < n16; i++) {
+      const int nx = i + 1 < n16 ? i + 1 : i;
 #pragma unroll
-      for (int u = 0; u < 8; u++) s += t[u];
+      for (int u = 0; u < 4; u++) b[u] = x4[4 * nx + u];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        s += a[u].x;
+        s += a[u].y;
+        s += a[u].z;
+        s += a[u].w;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) a[u] = b[u];
     }
+    for (int j = 16 * n16; j < dm; j++) s += xs[j];
     mean_s = s / (float)dm;
   }
   qd::lds_sync();
@@ -69,7 +88,7 @@ __global__ __launch_bounds__(NT) void k_layernorm_f32(const float *x, int dm, co
   for (int c = 0; c < CM; c++) {
     if (j0 + c < dm) {
       const float t = (v[c] - mean) * inv_std;
-      y[j0 + c] = t * gamma[j0 + c] + beta[j0 + c];
+      y[j0 + c] = t * ga[c] + be[c];
     }
   }
 }
