@@ -1,7 +1,7 @@
-// qdev_chain.h - the serial add chain of a product-tile pipeline, shared by the
-// decode PV kernel (k_attn.hip) and the fp32 GEMV (k_gemv_f32.hip).
+// qdev_chain.h - the serial add chain of a product-tile pipeline (the decode PV
+// kernel's, k_attn.hip).
 //
-// Layout both kernels use: three LDS buffers of kChainBufBytes, each 16 rows
+// Layout: three LDS buffers of kChainBufBytes, each 16 rows
 // (one per chain) of 128 products plus 4 floats of padding; tile k sits in
 // buffer k % 3.  The chain lane of row c adds its 128 products of a tile in
 // order, and an s_barrier separates consecutive tiles: with the producers'
