@@ -156,31 +156,32 @@ __global__ void k_pf_embed(const int8_t *wte, const float *s, int dm, const int 
 }
 
 // Prompt rows: RoPE at position p0 + r (rope.c:48-68) with cos/sin from the host
-// tables; blocks [0, H) rotate query heads into q_out row r, [H, H+KVH) rotate
-// key heads into the cache at p0 + r, [H+KVH, H+2KVH) copy value heads there.
-__global__ void k_pf_rope_append(const float *qkv, int H, int KVH, int hd, const float *cos_t, const float *sin_t,
-                                 int p0, float *q_out, float *kc, float *vc, int max_seq) {
-  const int r = blockIdx.y, pos = p0 + r;
+// tables; query heads rotate into q_out row r, key heads into the cache at
+// p0 + r, and value heads are copied there.  One block per row: the threads
+// take the (k, k + hd/2) pairs of the H + KVH rotated heads, then the value
+// elements.
+__global__ __launch_bounds__(256) void k_pf_rope_append(const float *qkv, int H, int KVH, int hd,
+                                                        const float *cos_t, const float *sin_t, int p0, float *q_out,
+                                                        float *kc, float *vc, int max_seq) {
+  const int r = blockIdx.x, pos = p0 + r;
   const int half = hd >> 1;
-  const int b = blockIdx.x;
   const int nqkv = (H + 2 * KVH) * hd;
   const float *row = qkv + (size_t)r * nqkv;
   const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
-  if (b < H + KVH) {
-    const bool isq = b < H;
+  const int nrot = (H + KVH) * half;
+  for (int i = threadIdx.x; i < nrot; i += blockDim.x) {
+    const int b = i / half, k = i % half;
     const float *xh = row + (size_t)b * hd;
-    float *dst = isq ? q_out + (size_t)r * H * hd + (size_t)b * hd : kc + ((size_t)(b - H) * max_seq + pos) * hd;
-    for (int k = threadIdx.x; k < half; k += blockDim.x) {
-      const float c = ct[k], s = st[k];
-      const float x1 = xh[k], x2 = xh[k + half];
-      dst[k] = x1 * c - x2 * s;
-      dst[k + half] = x2 * c + x1 * s;
-    }
-  } else {
-    const int h = b - H - KVH;
-    const float *vh = row + (size_t)(H + KVH) * hd + (size_t)h * hd;
-    float *dst = vc + ((size_t)h * max_seq + pos) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = vh[d];
+    float *dst = b < H ? q_out + (size_t)r * H * hd + (size_t)b * hd : kc + ((size_t)(b - H) * max_seq + pos) * hd;
+    const float c = ct[k], s = st[k];
+    const float x1 = xh[k], x2 = xh[k + half];
+    dst[k] = x1 * c - x2 * s;
+    dst[k + half] = x2 * c + x1 * s;
+  }
+  const float *vrow = row + (size_t)(H + KVH) * hd;
+  for (int i = threadIdx.x; i < KVH * hd; i += blockDim.x) {
+    const int h = i / hd, d = i % hd;
+    vc[((size_t)h * max_seq + pos) * hd + d] = vrow[i];
   }
 }
 
@@ -249,8 +250,8 @@ int qhip_pf_embed(const int8_t *wte, const float *wte_s, int dm, const int *ids,
 
 int qhip_pf_rope_append(const float *qkv, int R, int n_heads, int n_kv, int hd, const float *cos_t,
                         const float *sin_t, int p0, float *q_out, float *kc, float *vc, int max_seq) {
-  QH_LAUNCH(QK_PF_OTHER, k_pf_rope_append, dim3(n_heads + 2 * n_kv, R), dim3(128), 0, qkv, n_heads, n_kv, hd, cos_t,
-            sin_t, p0, q_out, kc, vc, max_seq);
+  QH_LAUNCH(QK_PF_OTHER, k_pf_rope_append, dim3(R), dim3(256), 0, qkv, n_heads, n_kv, hd, cos_t, sin_t, p0, q_out,
+            kc, vc, max_seq);
   return 0;
 }
 
