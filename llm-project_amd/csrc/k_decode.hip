@@ -31,11 +31,16 @@ __device__ __forceinline__ float block_max(float m, float *red) {
 
 // Write row `row` of qa (int8, kpad wide, zero padded) from values v[0..n) held
 // in LDS, given the row's max |v| (quant.c:66-78).
+// Four codes per thread and store (kpad is a multiple of 16).
 __device__ __forceinline__ void quantize_row_lds(const float *v, int n, int kpad, float mx, int8_t *qa_row,
                                                  float *as_out) {
   const float as = (mx > 0.0f) ? mx / 127.0f : 1.0f;
   const float inv = 1.0f / as;
-  for (int k = threadIdx.x; k < kpad; k += blockDim.x) qa_row[k] = (int8_t)(k < n ? qd::quant_i8(v[k], inv) : 0);
+  for (int k = 4 * threadIdx.x; k < kpad; k += 4 * blockDim.x) {
+    const float a = k < n ? v[k] : 0.0f, b = k + 1 < n ? v[k + 1] : 0.0f;
+    const float c = k + 2 < n ? v[k + 2] : 0.0f, d = k + 3 < n ? v[k + 3] : 0.0f;
+    *reinterpret_cast<uint32_t *>(qa_row + k) = qd::quant_i8x4(a, b, c, d, inv);
+  }
   if (threadIdx.x == 0) *as_out = as;
 }
 
@@ -73,10 +78,20 @@ __global__ __launch_bounds__(1024) void k_quant_rows(const float *vin, int n, in
   const int row = blockIdx.x;
   const float *vr = vin + (size_t)row * n;
   float mx = 0.0f;
-  for (int j = threadIdx.x; j < n; j += blockDim.x) {
-    const float a = vr[j];
-    lds[j] = a;
-    mx = fmaxf(mx, fabsf(a));
+  if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(vr) & 15) == 0) {   // whole aligned 16-byte words
+    const float4 *v4 = reinterpret_cast<const float4 *>(vr);
+    float4 *l4 = reinterpret_cast<float4 *>(lds);
+    for (int j = threadIdx.x; j < n / 4; j += blockDim.x) {
+      const float4 a = v4[j];
+      l4[j] = a;
+      mx = fmaxf(fmaxf(mx, fmaxf(fabsf(a.x), fabsf(a.y))), fmaxf(fabsf(a.z), fabsf(a.w)));
+    }
+  } else {
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+      const float a = vr[j];
+      lds[j] = a;
+      mx = fmaxf(mx, fabsf(a));
+    }
   }
   mx = block_max(mx, red);
   __syncthreads();
@@ -222,12 +237,14 @@ int qhip_rmsnorm_quant(const float *x, int rows, int dm, const float *gamma, flo
 
 int qhip_quant_rows(const float *v, int rows, int n, int8_t *qa, int kpad, float *as) {
   if (n > 32768) return qh::fail_msg("quant_rows: row above 32768");
+  if (kpad % 16 || kpad < n) return qh::fail_msg("quant_rows: bad row padding");
   QH_LAUNCH(QK_QUANT, k_quant_rows, dim3(rows), dim3(1024), (size_t)n * 4, v, n, qa, kpad, as);
   return 0;
 }
 
 int qhip_swiglu_quant(const float *gu, int rows, int dff, int8_t *qa, int kpad, float *as) {
   if (dff > 32768) return qh::fail_msg("swiglu_quant: d_ff above 32768");
+  if (kpad % 16 || kpad < dff) return qh::fail_msg("swiglu_quant: bad row padding");
   QH_LAUNCH(QK_SWIGLU, k_swiglu_quant, dim3(rows), dim3(1024), (size_t)dff * 4, gu, dff, qa, kpad, as);
   return 0;
 }
