@@ -305,10 +305,12 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn(const float *qkv, float *k
 
 }
 
-// Merge of the chunks of one query head (block h, one thread per dim, in whole
-// waves): M = max_c m_c, w_c = expf(m_c - M), o = (sum_c w_c o_c) * (1 / sum_c
-// w_c l_c), c in order; obm[h] = max_d |o_d| (the Wo GEMV's activation
-// quantizer reads these).
+// Merge of the chunks of one query head (one thread per dim, in whole waves):
+// M = max_c m_c, w_c = expf(m_c - M), o = (sum_c w_c o_c) * (1 / sum_c w_c l_c),
+// c in order; obm[h] = max_d |o_d| (the Wo GEMV's activation quantizer reads
+// these).  Block b serves KV head b % KVH, like the chunk blocks (x % KVH), so
+// with KVH a multiple of 8 it runs on the XCD whose L2 holds that head's
+// partials.
 template <int HD>
 constexpr int merge_threads() { return (HD + 63) / 64 * 64; }
 
@@ -317,15 +319,17 @@ __global__ __launch_bounds__(merge_threads<HD>()) void k_fattn_merge(const float
                                                                      int G, int chunk, int nsmax, float *o,
                                                                      float *obm) {
   constexpr int NT = merge_threads<HD>(), NW = NT / 64;
+  constexpr int SPT = (kFaMaxSplits + NT - 1) / NT;     // chunk slots a thread may hold
   __shared__ float wm[kFaMaxSplits];
   __shared__ float red[3][NW];
-  const int h = blockIdx.x, kvh = h / G, g = h % G, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.x % KVH, g = blockIdx.x / KVH, h = kvh * G + g;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool dim_ok = tid < HD;
   const int T = *d_pos + 1, nact = (T + chunk - 1) / chunk;
   const float *pm = part, *pl = part + (size_t)KVH * nsmax * G, *po = part + (size_t)2 * KVH * nsmax * G;
   const size_t base = (size_t)kvh * nsmax;
-  // requests first: the o of up to 64 chunks for this thread's dim (every load of
-  // a batch in flight at once), then the maxima
+  // every request first: the o of up to 64 chunks for this thread's dim, and the
+  // m and l of the thread's chunks s = tid, tid + NT, ...
   constexpr int U = 64;
   // (through a buffer resource over the head's nact chunk slots: an offset past
   // them reads 0 without memory traffic, so no load needs a branch)
@@ -336,8 +340,16 @@ __global__ __launch_bounds__(merge_threads<HD>()) void k_fattn_merge(const float
   auto oload = [&](int c) { return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ors, vo + c * ostep, 0, 0)); };
 #pragma unroll
   for (int u = 0; u < U; u++) ov[u] = oload(u);
+  float mv[SPT], lv[SPT];
+#pragma unroll
+  for (int u = 0; u < SPT; u++) {
+    const int s = tid + u * NT;
+    mv[u] = s < nact ? pm[(base + s) * G + g] : -INFINITY;
+    lv[u] = s < nact ? pl[(base + s) * G + g] : 0.0f;
+  }
   float M = -INFINITY;
-  for (int s = tid; s < nact; s += NT) M = fmaxf(M, pm[(base + s) * G + g]);
+#pragma unroll
+  for (int u = 0; u < SPT; u++) M = fmaxf(M, mv[u]);
   M = qd::wave_max_f32(M);
   if (lane == 0) red[0][wave] = M;
   __syncthreads();
@@ -345,10 +357,14 @@ __global__ __launch_bounds__(merge_threads<HD>()) void k_fattn_merge(const float
 #pragma unroll
   for (int w = 1; w < NW; w++) M = fmaxf(M, red[0][w]);
   float L = 0.0f;
-  for (int s = tid; s < nact; s += NT) {
-    const float w = qd::expf_glibc(pm[(base + s) * G + g] - M);
-    wm[s] = w;
-    L = __builtin_fmaf(w, pl[(base + s) * G + g], L);
+#pragma unroll
+  for (int u = 0; u < SPT; u++) {
+    const int s = tid + u * NT;
+    if (s < nact) {
+      const float w = qd::expf_glibc(mv[u] - M);
+      wm[s] = w;
+      L = __builtin_fmaf(w, lv[u], L);
+    }
   }
   L = qd::wave_sum_f32(L);
   if (lane == 0) red[1][wave] = L;
