@@ -215,10 +215,16 @@ __device__ __forceinline__ void block_sync_lds() {
 // Block tile TM x TN, waves WM x WN, each wave (TM/WM) x (TN/WN) from 32 x 32
 // v_mfma_i32_32x32x32_i8 blocks: RB row blocks x 2 column blocks (SWIGLU: the
 // wave's 32 gate columns and the matching 32 up columns).
-template <int MODE, int TM, int TN, int WM, int WN, int NSTAGE>
+//
+// Split K (PART): block b of the grid takes tile b % bps and the K steps
+// [split * nks, split * nks + nks) of split b / bps, and stores its int32 partial
+// sums to part[split][M][N] (SWIGLU: [split][M][2N], up columns at N + j) for
+// k_gemm_split_epi.
+template <int MODE, int TM, int TN, int WM, int WN, int NSTAGE, bool PART = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, const float *as, const int8_t *W,
                                                               const float *ws, int M, int N, int kpad, float *out,
-                                                              int ldo, const float *bias, int mt_count, int nt_count) {
+                                                              int ldo, const float *bias, int mt_count, int nt_count,
+                                                              int bps, int nks, int *part) {
   static_assert(NSTAGE == 3 || NSTAGE == 4, "pipeline depth");
   constexpr int NWAVE = WM * WN, RB = TM / WM / 32;
   static_assert(TN == 64 * WN, "two 32-column blocks per wave");
@@ -230,8 +236,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
   __shared__ __attribute__((aligned(16))) int8_t sA0[TM * BK], sA1[TM * BK], sA2[TM * BK], sA3[NSTAGE > 3 ? TM * BK : 16];
   __shared__ __attribute__((aligned(16))) int8_t sB0[TN * BK], sB1[TN * BK], sB2[TN * BK], sB3[NSTAGE > 3 ? TN * BK : 16];
   int mtile, ntile;
-  gemm_tile(blockIdx.x, mt_count, mtile, ntile);
+  const int split = PART ? (int)blockIdx.x / bps : 0;
+  gemm_tile(PART ? (int)blockIdx.x % bps : (int)blockIdx.x, mt_count, mtile, ntile);
   if (ntile >= nt_count) return;                                   // uniform for the block
+  const int kt0 = split * nks;                                     // first K step of this block
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
   for (int i = 0; i < LA; i++) {
     const int slot = (wave * LA + i) * 64 + lane, row = slot >> 2;
     const int c = (slot & 3) ^ swz32(row);
-    ga[i] = A + (size_t)min(m0 + row, M - 1) * kpad + c * 16;
+    ga[i] = A + (size_t)min(m0 + row, M - 1) * kpad + c * 16 + (size_t)kt0 * BK;
   }
 #pragma unroll
   for (int i = 0; i < LB; i++) {
@@ -255,9 +263,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
     int wrow;
     if (MODE == GM_SWIGLU) wrow = row < TN / 2 ? min(n0 + row, N - 1) : N + min(n0 + row - TN / 2, N - 1);
     else wrow = min(n0 + row, N - 1);
-    gb[i] = W + (size_t)wrow * kpad + c * 16;
+    gb[i] = W + (size_t)wrow * kpad + c * 16 + (size_t)kt0 * BK;
   }
-  const int nk = kpad / BK;
+  const int nk = PART ? min(nks, kpad / BK - kt0) : kpad / BK;
   auto bufA = [&](auto st) -> int8_t * {
     if constexpr (decltype(st)::value == 0) return sA0;
     else if constexpr (decltype(st)::value == 1) return sA1;
@@ -353,6 +361,33 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
     if (NSTAGE > 3 && kt + 3 < nk) step(std::integral_constant<int, (NSTAGE > 3 ? 3 : 0)>(), kt + 3);
   }
 
+  if constexpr (PART) {                // int32 partial sums of this split
+    const int ldp = MODE == GM_SWIGLU ? 2 * N : N;
+    int *pp = part + (size_t)split * M * ldp;
+#pragma unroll
+    for (int a = 0; a < RB; a++) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int i = m0 + wm * (TM / WM) + a * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (i >= M) continue;
+        if (MODE == GM_SWIGLU) {
+          const int j = n0 + wn * 32 + (lane & 31);
+          if (j < N) {
+            pp[(size_t)i * ldp + j] = acc[a][0][e];
+            pp[(size_t)i * ldp + N + j] = acc[a][1][e];
+          }
+        } else {
+#pragma unroll
+          for (int b = 0; b < 2; b++) {
+            const int j = n0 + wn * 64 + b * 32 + (lane & 31);
+            if (j < N) pp[(size_t)i * ldp + j] = acc[a][b][e];
+          }
+        }
+      }
+    }
+    return;
+  }
+
   // epilogue (the decode GEMV's operations and order)
 #pragma unroll
   for (int a = 0; a < RB; a++) {
@@ -385,14 +420,66 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
   }
 }
 
+// Split-K epilogue: acc = the sum of the S int32 partials (exact in any order:
+// every partial sum of the products is bounded like the whole, |acc| <= 127^2 K),
+// then the fused epilogue's operations on it.  Grid (ceil(N / 256), M).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemm_split_epi(const int *part, int S, const float *as, const float *ws,
+                                                        int M, int N, float *out, int ldo, const float *bias) {
+  const int j = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y;
+  if (j >= N) return;
+  const int ldp = MODE == GM_SWIGLU ? 2 * N : N;
+  const size_t plane = (size_t)M * ldp;
+  const int *pp = part + (size_t)i * ldp + j;
+  int acc = 0, accu = 0;
+  for (int s = 0; s < S; s++) {
+    acc += pp[s * plane];
+    if (MODE == GM_SWIGLU) accu += pp[s * plane + N];
+  }
+  const float asi = as[i];
+  if (MODE == GM_SWIGLU) {
+    const float g = (asi * ws[j]) * (float)acc;
+    const float up = (asi * ws[N + j]) * (float)accu;
+    const float sg = 1.0f / (1.0f + qd::expf_glibc(-g));
+    out[(size_t)i * ldo + j] = (g * sg) * up;
+  } else {
+    const float c = (asi * ws[j]) * (float)acc;
+    float *o = out + (size_t)i * ldo + j;
+    if (MODE == GM_RESID) *o = *o + c;
+    else *o = bias ? c + bias[j] : c;
+  }
+}
+
+// Tiles that leave CUs idle (a short prompt, a narrow output) split K when the
+// caller lends a workspace: S splits of at least 8 K steps, so that tiles x S
+// reach one block per CU, with S partial planes of M x N int32 in the workspace.
 template <int MODE, int TM, int TN, int WM, int WN, int NS>
 int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N, int kpad, float *out,
-                int ldo, const float *bias, int cls) {
+                int ldo, const float *bias, int cls, int *work, size_t work_bytes) {
   const int nout = MODE == GM_SWIGLU ? TN / 2 : TN;
   const int mt = (M + TM - 1) / TM, nt = (N + nout - 1) / nout;
   const int blocks = 8 * mt * ((nt + 7) / 8);
-  QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS>), dim3(blocks), dim3(64 * WM * WN), 0, A, as, W, ws, M, N,
-            kpad, out, ldo, bias, mt, nt);
+  const int nkt = kpad / BK;
+  int S = 1;
+  if (work) {
+    const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256, active = mt * nt;
+    if (active < cus) {
+      S = min((cus + active - 1) / active, nkt / 8);
+      const size_t plane = (size_t)M * (MODE == GM_SWIGLU ? 2 * N : N) * 4;
+      while (S > 1 && (size_t)S * plane > work_bytes) S--;
+    }
+  }
+  if (S < 2) {
+    QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS>), dim3(blocks), dim3(64 * WM * WN), 0, A, as, W, ws, M,
+              N, kpad, out, ldo, bias, mt, nt, blocks, nkt, static_cast<int *>(nullptr));
+    return 0;
+  }
+  const int nks = (nkt + S - 1) / S;
+  S = (nkt + nks - 1) / nks;                                       // every split has steps
+  QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS, true>), dim3(blocks * S), dim3(64 * WM * WN), 0, A, as, W,
+            ws, M, N, kpad, out, ldo, bias, mt, nt, blocks, nks, work);
+  QH_LAUNCH(cls, k_gemm_split_epi<MODE>, dim3((N + 255) / 256, M), dim3(256), 0, work, S, as, ws, M, N, out, ldo,
+            bias);
   return 0;
 }
 
@@ -401,12 +488,13 @@ int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *
 // K not a multiple of 64 takes the register-staged kernel.
 template <int MODE>
 int launch(const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N, int kpad, float *out,
-           int ldo, const float *bias, int cls) {
+           int ldo, const float *bias, int cls, int *work, size_t work_bytes) {
   if (kpad % BK == 0) {
     if (MODE == GM_SWIGLU || (MODE == GM_RESID && kpad >= 8192))
-      return launch_pipe<MODE, 256, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
-    if (MODE == GM_RESID) return launch_pipe<MODE, 128, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
-    return launch_pipe<MODE, 128, 128, 4, 2, 4>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
+      return launch_pipe<MODE, 256, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
+    if (MODE == GM_RESID)
+      return launch_pipe<MODE, 128, 128, 4, 2, 3>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
+    return launch_pipe<MODE, 128, 128, 4, 2, 4>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
   }
   const int nout = MODE == GM_SWIGLU ? BN / 2 : BN;
   const int mt = (M + BM - 1) / BM, nt = (N + nout - 1) / nout;
@@ -417,13 +505,19 @@ int launch(const int8_t *A, const float *as, const int8_t *W, const float *ws, i
 
 }  // namespace
 
-extern "C" int qhip_gemm_i8(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws,
-                            int M, int N, int kpad, float *out, int ldo, const float *bias) {
+extern "C" int qhip_gemm_i8_ws(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws,
+                               int M, int N, int kpad, float *out, int ldo, const float *bias, int *work,
+                               size_t work_bytes) {
   if (M <= 0 || N <= 0 || kpad <= 0 || kpad % 16) return qh::fail_msg("gemm_i8: bad shape");
   switch (mode) {
-    case GM_PLAIN: return launch<GM_PLAIN>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
-    case GM_RESID: return launch<GM_RESID>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
-    case GM_SWIGLU: return launch<GM_SWIGLU>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls);
+    case GM_PLAIN: return launch<GM_PLAIN>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
+    case GM_RESID: return launch<GM_RESID>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
+    case GM_SWIGLU: return launch<GM_SWIGLU>(A, as, W, ws, M, N, kpad, out, ldo, bias, cls, work, work_bytes);
     default: return qh::fail_msg("gemm_i8: bad mode");
   }
+}
+
+extern "C" int qhip_gemm_i8(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws,
+                            int M, int N, int kpad, float *out, int ldo, const float *bias) {
+  return qhip_gemm_i8_ws(mode, cls, A, as, W, ws, M, N, kpad, out, ldo, bias, nullptr, 0);
 }

@@ -165,6 +165,11 @@ int qhip_qmm_product(const int8_t *qa, const float *as, int M, const int8_t *W, 
 // with the decode GEMV's epilogues (mode 0 plain + bias, 1 residual, 2 SwiGLU).
 int qhip_gemm_i8(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N,
                  int kpad, float *out, int ldo, const float *bias);
+// As qhip_gemm_i8, splitting K over more blocks when the tiles leave CUs idle and
+// work (work_bytes of device memory, int32 partial sums) is lent; the results
+// are the same bits (the int32 sums are exact in any order).
+int qhip_gemm_i8_ws(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws, int M,
+                    int N, int kpad, float *out, int ldo, const float *bias, int *work, size_t work_bytes);
 
 // Prompt ingestion over R rows at positions p0 .. p0+R-1 (k_decode.hip, k_attn.hip).
 int qhip_pf_embed(const int8_t *wte, const float *wte_s, int dm, const int *ids, int R, float *x);

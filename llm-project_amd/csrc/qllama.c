@@ -59,6 +59,7 @@ typedef struct {
   int pf_rows;
   float *pf_x, *pf_qkv, *pf_q, *pf_o, *pf_h, *pf_as, *pf_attn;
   int8_t *pf_qa;
+  int *pf_work;      // split-K partial sums of the prompt GEMMs (PF_WORK_BYTES)
 } QDev;
 
 typedef struct {
@@ -122,9 +123,10 @@ static QTensor dev_qt(int8_t *q, float *s, int rows, int cols, int layout) {
 
 static void pf_free(QDev *d) {
   qhip_free(d->pf_x); qhip_free(d->pf_qkv); qhip_free(d->pf_q); qhip_free(d->pf_o);
-  qhip_free(d->pf_h); qhip_free(d->pf_as); qhip_free(d->pf_attn); qhip_free(d->pf_qa);
+  qhip_free(d->pf_h); qhip_free(d->pf_as); qhip_free(d->pf_attn); qhip_free(d->pf_qa); qhip_free(d->pf_work);
   d->pf_x = d->pf_qkv = d->pf_q = d->pf_o = d->pf_h = d->pf_as = d->pf_attn = NULL;
   d->pf_qa = NULL;
+  d->pf_work = NULL;
   d->pf_rows = 0;
 }
 
@@ -780,6 +782,7 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
 #define PF_MIN_ROWS 16      // shorter prompts replay the decode graph
 #define PF_CLS_GEMM 14      // profiling class of the prefill GEMMs (QK_PF_GEMM)
 #define PF_MAX_ROWS 2048    // rows per pass through the layers
+#define PF_WORK_BYTES ((size_t)64 << 20)   // split-K partial sums (a few planes of rows x outputs)
 
 static int pf_supported(const QDev *d) {
   const int G = d->H / d->KVH;
@@ -799,7 +802,9 @@ static int pf_alloc(QDev *d, int rows) {
   d->pf_as = (float*)qhip_malloc(R * 4);
   d->pf_attn = (float*)qhip_malloc(qhip_pf_attention_scratch(rows, d->H, d->max_seq) * 4);
   d->pf_qa = (int8_t*)qhip_malloc(R * d->kp_max);
-  if (!d->pf_x || !d->pf_qkv || !d->pf_q || !d->pf_o || !d->pf_h || !d->pf_as || !d->pf_attn || !d->pf_qa) {
+  d->pf_work = (int*)qhip_malloc(PF_WORK_BYTES);
+  if (!d->pf_x || !d->pf_qkv || !d->pf_q || !d->pf_o || !d->pf_h || !d->pf_as || !d->pf_attn || !d->pf_qa ||
+      !d->pf_work) {
     pf_free(d);
     return 1;
   }
@@ -823,8 +828,8 @@ static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
     for (int l = 0; l < d->L && !rc; l++) {
       float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
       rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_attn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
-      rc |= qhip_gemm_i8(0, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wqkv[l], d->sqkv[l], R, d->nqkv, d->kp_dm, d->pf_qkv, d->nqkv,
-                         d->bqkv[l]);
+      rc |= qhip_gemm_i8_ws(0, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wqkv[l], d->sqkv[l], R, d->nqkv, d->kp_dm, d->pf_qkv,
+                            d->nqkv, d->bqkv[l], d->pf_work, PF_WORK_BYTES);
       rc |= qhip_pf_rope_append(d->pf_qkv, R, d->H, d->KVH, d->hd, d->rope_cos, d->rope_sin, p0, d->pf_q, kc, vc,
                                 d->max_seq);
       if (fast_attn)      // fast cache: MFMA attention, a tolerance path like the fast decode
@@ -833,11 +838,14 @@ static int pf_run(QDev *d, const KVDev *kd, int pos, const int *ids, int n) {
         rc |= qhip_pf_attention(d->pf_q, kc, vc, R, p0, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->pf_attn,
                                 d->pf_o);
       rc |= qhip_quant_rows(d->pf_o, R, d->qd, d->pf_qa, d->kp_qd, d->pf_as);
-      rc |= qhip_gemm_i8(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm, NULL);
+      rc |= qhip_gemm_i8_ws(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wo[l], d->so[l], R, d->dm, d->kp_qd, d->pf_x, d->dm,
+                            NULL, d->pf_work, PF_WORK_BYTES);
       rc |= qhip_rmsnorm_quant(d->pf_x, R, d->dm, d->g_ffn[l], d->eps, d->pf_qa, d->kp_dm, d->pf_as);
-      rc |= qhip_gemm_i8(2, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wgu[l], d->sgu[l], R, d->dff, d->kp_dm, d->pf_h, d->dff, NULL);
+      rc |= qhip_gemm_i8_ws(2, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wgu[l], d->sgu[l], R, d->dff, d->kp_dm, d->pf_h, d->dff,
+                            NULL, d->pf_work, PF_WORK_BYTES);
       rc |= qhip_quant_rows(d->pf_h, R, d->dff, d->pf_qa, d->kp_ff, d->pf_as);
-      rc |= qhip_gemm_i8(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wd[l], d->sd[l], R, d->dm, d->kp_ff, d->pf_x, d->dm, NULL);
+      rc |= qhip_gemm_i8_ws(1, PF_CLS_GEMM, d->pf_qa, d->pf_as, d->wd[l], d->sd[l], R, d->dm, d->kp_ff, d->pf_x, d->dm,
+                            NULL, d->pf_work, PF_WORK_BYTES);
     }
     if (!rc && c0 + R == n) {       // last row: final norm, head, argmax (llama.c:592-593, sampler.c:36-49)
       const float *xl = d->pf_x + (size_t)(R - 1) * d->dm;
