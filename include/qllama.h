@@ -320,6 +320,12 @@ int  qllama_test_seqsum(const float *a, int n, float *out, int *info);
 // fresh buffers, on the library's stream: the known-size reference that
 // scales the HBM traffic counters of a profiler run.
 int  qllama_test_copy(size_t bytes);
+// One int8 GEMM of the prompt path (mode 0 plain + bias, 1 residual add, 2
+// SwiGLU over W's 2N rows; quant.c:60-85 over M rows) from host operands, run
+// whole and with K split over extra blocks; both results (out_plain, out_split:
+// residual inputs on entry) and the split count used.  For parity tests.
+int  qllama_test_gemm_split(int mode, const int8_t *A, const float *as, const int8_t *W, const float *ws, int M,
+                            int N, int kpad, const float *bias, float *out_plain, float *out_split, int *splits);
 
 #ifdef __cplusplus
 }

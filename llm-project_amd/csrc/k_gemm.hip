@@ -453,6 +453,8 @@ __global__ __launch_bounds__(256) void k_gemm_split_epi(const int *part, int S, 
 // Tiles that leave CUs idle (a short prompt, a narrow output) split K when the
 // caller lends a workspace: S splits of at least 8 K steps, so that tiles x S
 // reach one block per CU, with S partial planes of M x N int32 in the workspace.
+int g_last_splits = 1;                 // K splits of the last pipelined launch (for the split test)
+
 template <int MODE, int TM, int TN, int WM, int WN, int NS>
 int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *ws, int M, int N, int kpad, float *out,
                 int ldo, const float *bias, int cls, int *work, size_t work_bytes) {
@@ -469,6 +471,7 @@ int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *
       while (S > 1 && (size_t)S * plane > work_bytes) S--;
     }
   }
+  g_last_splits = S < 2 ? 1 : S;
   if (S < 2) {
     QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS>), dim3(blocks), dim3(64 * WM * WN), 0, A, as, W, ws, M,
               N, kpad, out, ldo, bias, mt, nt, blocks, nkt, static_cast<int *>(nullptr));
@@ -476,6 +479,7 @@ int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *
   }
   const int nks = (nkt + S - 1) / S;
   S = (nkt + nks - 1) / nks;                                       // every split has steps
+  g_last_splits = S;
   QH_LAUNCH(cls, (k_gemm_i8_pipe<MODE, TM, TN, WM, WN, NS, true>), dim3(blocks * S), dim3(64 * WM * WN), 0, A, as, W,
             ws, M, N, kpad, out, ldo, bias, mt, nt, blocks, nks, work);
   QH_LAUNCH(cls, k_gemm_split_epi<MODE>, dim3((N + 255) / 256, M), dim3(256), 0, work, S, as, ws, M, N, out, ldo,
@@ -520,4 +524,34 @@ extern "C" int qhip_gemm_i8_ws(int mode, int cls, const int8_t *A, const float *
 extern "C" int qhip_gemm_i8(int mode, int cls, const int8_t *A, const float *as, const int8_t *W, const float *ws,
                             int M, int N, int kpad, float *out, int ldo, const float *bias) {
   return qhip_gemm_i8_ws(mode, cls, A, as, W, ws, M, N, kpad, out, ldo, bias, nullptr, 0);
+}
+
+// Test entry: one GEMM (mode 0 plain + bias, 1 residual, 2 SwiGLU) from host
+// operands, run whole and with a 64 MB split-K workspace; out_plain and
+// out_split hold the residual's initial values on entry (mode 1) and the two
+// results on return; *splits = the K splits the second run used.
+extern "C" int qllama_test_gemm_split(int mode, const int8_t *A, const float *as, const int8_t *W, const float *ws,
+                                      int M, int N, int kpad, const float *bias, float *out_plain, float *out_split,
+                                      int *splits) {
+  if (qhip_init()) return 1;
+  if (mode < 0 || mode > 2 || M <= 0 || N <= 0 || kpad <= 0 || kpad % 16) return qh::fail_msg("test_gemm_split: bad shape");
+  const size_t wrows = mode == GM_SWIGLU ? 2 * (size_t)N : (size_t)N, nout = (size_t)M * N;
+  const size_t work_bytes = (size_t)64 << 20;
+  int8_t *dA = (int8_t *)qhip_malloc((size_t)M * kpad), *dW = (int8_t *)qhip_malloc(wrows * kpad);
+  float *das = (float *)qhip_malloc((size_t)M * 4), *dws = (float *)qhip_malloc(wrows * 4);
+  float *db = bias ? (float *)qhip_malloc((size_t)N * 4) : nullptr;
+  float *o1 = (float *)qhip_malloc(nout * 4), *o2 = (float *)qhip_malloc(nout * 4);
+  int *work = (int *)qhip_malloc(work_bytes);
+  int rc = (!dA || !dW || !das || !dws || (bias && !db) || !o1 || !o2 || !work) ? 1 : 0;
+  if (!rc)
+    rc = qhip_h2d(dA, A, (size_t)M * kpad) || qhip_h2d(dW, W, wrows * kpad) || qhip_h2d(das, as, (size_t)M * 4) ||
+         qhip_h2d(dws, ws, wrows * 4) || (bias && qhip_h2d(db, bias, (size_t)N * 4)) ||
+         qhip_h2d(o1, out_plain, nout * 4) || qhip_h2d(o2, out_split, nout * 4);
+  if (!rc) rc = qhip_gemm_i8(mode, QK_OTHER, dA, das, dW, dws, M, N, kpad, o1, N, db);
+  if (!rc) rc = qhip_gemm_i8_ws(mode, QK_OTHER, dA, das, dW, dws, M, N, kpad, o2, N, db, work, work_bytes);
+  if (!rc) *splits = g_last_splits;
+  if (!rc) rc = qhip_device_sync() || qhip_d2h(out_plain, o1, nout * 4) || qhip_d2h(out_split, o2, nout * 4);
+  qhip_free(dA); qhip_free(dW); qhip_free(das); qhip_free(dws); qhip_free(db); qhip_free(o1); qhip_free(o2);
+  qhip_free(work);
+  return rc;
 }

@@ -411,3 +411,41 @@ def test_e2e_1b_matches_reference(Q):
 
 def test_e2e_8b_matches_reference(Q):
     _big_e2e(Q, "8b")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,M,N,kpad,bias", [
+    (0, 40, 200, 1024, True),      # plain + bias (QKV-like), 2 tiles
+    (1, 100, 96, 2048, False),     # residual add
+    (2, 64, 150, 1024, False),     # SwiGLU over 2N weight rows
+    (1, 300, 64, 8192, False),     # long K: 256-row tiles, 16 splits
+    (2, 17, 700, 4096, False),
+])
+def test_split_k_gemm_same_bits(Q, mode, M, N, kpad, bias):
+    """The prompt GEMM with K split over extra blocks (int32 partial sums, then
+    the epilogue) gives the unsplit GEMM's bits; for the plain and residual
+    epilogues both equal the float32 restatement of quant.c:60-85's scaling
+    over the exact integer sums."""
+    import ctypes as C
+    rng = np.random.default_rng(7000 + 31 * mode + M)
+    wrows = 2 * N if mode == 2 else N
+    A = rng.integers(-127, 128, (M, kpad), dtype=np.int8)
+    W = rng.integers(-127, 128, (wrows, kpad), dtype=np.int8)
+    a_s = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    w_s = rng.uniform(1e-4, 1e-2, wrows).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    init = rng.standard_normal((M, N)).astype(np.float32)
+    o1, o2, splits = init.copy(), init.copy(), C.c_int(0)
+    f = Q.lib().qllama_test_gemm_split
+    f.restype = C.c_int
+    f.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                  C.c_void_p, C.c_void_p, C.POINTER(C.c_int)]
+    p = lambda x: None if x is None else x.ctypes.data_as(C.c_void_p)
+    assert f(mode, p(A), p(a_s), p(W), p(w_s), M, N, kpad, p(b), p(o1), p(o2), C.byref(splits)) == 0
+    assert splits.value >= 2, "the shape was meant to split K"
+    assert o1.tobytes() == o2.tobytes()
+    if mode != 2:
+        acc = A.astype(np.int64) @ W.astype(np.int64).T
+        c = (a_s[:, None] * w_s[None, :]) * acc.astype(np.float32)
+        want = init + c if mode == 1 else (c + b if bias else c)
+        assert np.array_equal(o1.view(np.uint32), want.astype(np.float32).view(np.uint32))
