@@ -295,7 +295,7 @@ def op_gemv(Q, reps=100):
                 call, prod, quant = C.c_double(0), C.c_double(0), C.c_double(0)
                 if Q.lib().qllama_bench_qmatmul(C.byref(W), B, reps, C.byref(call), C.byref(prod), C.byref(quant)):
                     raise RuntimeError("qllama_bench_qmatmul failed")
-                op_bytes = M * K + 4 * M + 4 * B * K + 4 * B * M          # weights, scales, x, y
+                op_bytes = M * K + 4 * M + 4 * B * K + 4 * B * M          # algorithmic bytes: weights, scales, x, y
                 kern_bytes = M * K + 4 * M + B * K + 4 * B * M            # the product kernel reads int8 rows
                 gbs = kern_bytes / (prod.value * 1e-6) / 1e9
                 out.append({"M": M, "K": K, "batch": B, "kernel": "k_gemv_dec" if B == 1 else "k_gemv_mfma",
