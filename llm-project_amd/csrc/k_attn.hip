@@ -452,7 +452,10 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 // (the same sums in the same order).  Scratch w[h][r][Tp] holds the scores and
 // then, in place, the softmax weights.
 // ---------------------------------------------------------------------------
-constexpr int kPvRows = 8;            // query rows per PV block
+constexpr int kPvRows = 8;            // query rows per PV block (half for short prompts)
+#ifndef QLLAMA_PF_SMALL_ROWS
+#define QLLAMA_PF_SMALL_ROWS 1024     // prompts of at most this many rows per pass take the half blocks
+#endif
 constexpr size_t kPfScratchBytes = (size_t)1 << 30;   // score scratch per attention pass (bounds the rows of a pass)
 
 // Softmax weights of one (head, row) (llama.c:557-572): NT threads, thread t
@@ -551,13 +554,13 @@ __device__ __forceinline__ void pf_pv_vload(const float *Vh, int HD, int k0, int
 
 // The adds of one group: every key seen by every row (MASK false) or masked
 // per (row, key) at the causal diagonal.
-template <bool MASK, int DPL>
-__device__ __forceinline__ void pf_pv_group(float (&acc)[kPvRows][DPL], const float (&v)[kPvKeys][DPL],
-                                          const f8v (&wv)[kPvRows], int k0, int rlast0) {
+template <bool MASK, int DPL, int PR>
+__device__ __forceinline__ void pf_pv_group(float (&acc)[PR][DPL], const float (&v)[kPvKeys][DPL],
+                                          const f8v (&wv)[PR], int k0, int rlast0) {
 #pragma unroll
   for (int u = 0; u < kPvKeys; u++) {
 #pragma unroll
-    for (int c = 0; c < kPvRows; c++) {
+    for (int c = 0; c < PR; c++) {
       const float wk = wv[c][u];
 #pragma unroll
       for (int e = 0; e < DPL; e++) {
@@ -568,42 +571,42 @@ __device__ __forceinline__ void pf_pv_group(float (&acc)[kPvRows][DPL], const fl
   }
 }
 
-template <int HD>
+template <int HD, int PR>
 __global__ __launch_bounds__(512) void k_pf_pv(const float *w, const float *vc, int R, int p0, int H, int KVH,
                                                int max_seq, int Tp, float *o) {
   static_assert(HD == 128 || HD <= 64, "two dims per lane at 128, one below");
   constexpr int DPL = HD == 128 ? 2 : 1;
   const int G = H / KVH;
-  const int kvh = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kPvRows;   // longest blocks first
+  const int kvh = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * PR;   // longest blocks first
   const int g = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int h = kvh * G + g;
-  const int rend = min(R, r0 + kPvRows);
+  const int rend = min(R, r0 + PR);
   const int kend = p0 + rend;                                        // keys 0 .. kend-1 are used
   const int rlast0 = p0 + r0;                                        // last key row r0 sees
   const int dfirst = DPL * lane;
   const bool lane_ok = dfirst < HD;
   const float *Vh = vc + (size_t)kvh * max_seq * HD + (lane_ok ? dfirst : 0);
-  cfloat_t *wr[kPvRows];
+  cfloat_t *wr[PR];
 #pragma unroll
-  for (int c = 0; c < kPvRows; c++) wr[c] = (cfloat_t *)(w + ((size_t)h * R + min(r0 + c, R - 1)) * Tp);
+  for (int c = 0; c < PR; c++) wr[c] = (cfloat_t *)(w + ((size_t)h * R + min(r0 + c, R - 1)) * Tp);
   const int klast = (kend - 1) / kPvKeys * kPvKeys;                  // group starts are clamped to it
 
-  float acc[kPvRows][DPL];
+  float acc[PR][DPL];
 #pragma unroll
-  for (int c = 0; c < kPvRows; c++)
+  for (int c = 0; c < PR; c++)
 #pragma unroll
     for (int e = 0; e < DPL; e++) acc[c][e] = 0.0f;
   // three V register sets in rotation: group k in set k % 3, requested two
   // groups before it is added
   float v0[kPvKeys][DPL], v1[kPvKeys][DPL], v2[kPvKeys][DPL];
-  f8v wv[kPvRows];
+  f8v wv[PR];
   pf_pv_vload<DPL>(Vh, HD, 0, kend, v0);
   pf_pv_vload<DPL>(Vh, HD, min(kPvKeys, klast), kend, v1);
   auto run = [&](int k, const float (&v)[kPvKeys][DPL]) {
 #pragma unroll
-    for (int c = 0; c < kPvRows; c++) wv[c] = *(cf8v_t *)(wr[c] + k);
-    if (k + kPvKeys <= rlast0 + 1) pf_pv_group<false, DPL>(acc, v, wv, k, rlast0);
-    else pf_pv_group<true, DPL>(acc, v, wv, k, rlast0);
+    for (int c = 0; c < PR; c++) wv[c] = *(cf8v_t *)(wr[c] + k);
+    if (k + kPvKeys <= rlast0 + 1) pf_pv_group<false, DPL, PR>(acc, v, wv, k, rlast0);
+    else pf_pv_group<true, DPL, PR>(acc, v, wv, k, rlast0);
   };
   for (int k0 = 0; k0 < kend; k0 += 3 * kPvKeys) {
     pf_pv_vload<DPL>(Vh, HD, min(k0 + 2 * kPvKeys, klast), kend, v2);
@@ -617,7 +620,7 @@ __global__ __launch_bounds__(512) void k_pf_pv(const float *w, const float *vc, 
   }
   if (lane_ok) {
 #pragma unroll
-    for (int c = 0; c < kPvRows; c++)
+    for (int c = 0; c < PR; c++)
       if (r0 + c < R) {
         float *orow = o + (size_t)(r0 + c) * H * HD + (size_t)h * HD + dfirst;
         if constexpr (DPL == 2) *reinterpret_cast<float2 *>(orow) = make_float2(acc[c][0], acc[c][1]);
@@ -675,13 +678,13 @@ __device__ __forceinline__ void ps_chunks(cfloat_t *const (&qp)[kPsPairs], const
   ps_chunk<HD, 0>(qp, k, acc, qa, qb);
 }
 
-template <int HD>
+template <int HD, int RB>
 __global__ __launch_bounds__(kPsKeys) void k_pf_scores(const float *q, const float *kc, int R, int p0, int H,
                                                          int KVH, int max_seq, float scale, float *w, int Tp) {
   static_assert(HD % kPsDims == 0, "whole scalar loads of q");
-  const int kvh = blockIdx.x, r0 = blockIdx.y * kPsRows, j0 = blockIdx.z * kPsKeys;
+  const int kvh = blockIdx.x, r0 = blockIdx.y * RB, j0 = blockIdx.z * kPsKeys;
   const int G = H / KVH;
-  const int rend = min(R, r0 + kPsRows);
+  const int rend = min(R, r0 + RB);
   const int jvis = p0 + rend - 1;                                    // last key any row here sees
   const int jw = j0 + 64 * __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (jw > jvis) return;                                             // uniform for the wave
@@ -695,13 +698,13 @@ __global__ __launch_bounds__(kPsKeys) void k_pf_scores(const float *q, const flo
       k[4 * i] = t.x; k[4 * i + 1] = t.y; k[4 * i + 2] = t.z; k[4 * i + 3] = t.w;
     }
   }
-  const int npair = G * kPsRows;
+  const int npair = G * RB;
 #pragma unroll 1
   for (int c0 = 0; c0 < npair; c0 += kPsPairs) {
     cfloat_t *qp[kPsPairs];
 #pragma unroll
     for (int u = 0; u < kPsPairs; u++) {
-      const int pair = c0 + u, g = pair / kPsRows, r = min(r0 + pair % kPsRows, R - 1);
+      const int pair = c0 + u, g = pair / RB, r = min(r0 + pair % RB, R - 1);
       qp[u] = (cfloat_t *)(q + (size_t)r * H * HD + (size_t)(kvh * G + g) * HD);
     }
     float acc[kPsPairs];
@@ -710,7 +713,7 @@ __global__ __launch_bounds__(kPsKeys) void k_pf_scores(const float *q, const flo
     ps_chunks<HD, 0>(qp, k, acc);
 #pragma unroll
     for (int u = 0; u < kPsPairs; u++) {
-      const int pair = c0 + u, g = pair / kPsRows, r = r0 + pair % kPsRows;
+      const int pair = c0 + u, g = pair / RB, r = r0 + pair % RB;
       if (r < R && j <= p0 + r) w[((size_t)(kvh * G + g) * R + r) * Tp + j] = acc[u] * scale;
     }
   }
@@ -721,13 +724,19 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
                  float scale, float *w, float *o) {
   const int G = H / KVH, Tp = (max_seq + 7) & ~7;          // rows of whole 32-byte words
   const int Tmax = p0 + R;
-  const dim3 sgrid(KVH, (R + kPsRows - 1) / kPsRows, (Tmax + kPsKeys - 1) / kPsKeys);
-  QH_LAUNCH(QK_PF_ATTN, k_pf_scores<HD>, sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
+  // short prompts: half the rows per block, twice the waves (the per-row sums
+  // do not depend on how rows are grouped into blocks)
+  const bool small = R <= QLLAMA_PF_SMALL_ROWS;
+  const int rbs = small ? kPsRows / 2 : kPsRows, rbp = small ? kPvRows / 2 : kPvRows;
+  const dim3 sgrid(KVH, (R + rbs - 1) / rbs, (Tmax + kPsKeys - 1) / kPsKeys);
+  if (small) QH_LAUNCH(QK_PF_ATTN, (k_pf_scores<HD, kPsRows / 2>), sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
+  else QH_LAUNCH(QK_PF_ATTN, (k_pf_scores<HD, kPsRows>), sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
   if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(H, R), dim3(64), 0, w, R, p0, Tp);
   else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(H, R), dim3(256), 0, w, R, p0, Tp);
   else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(H, R), dim3(512), 0, w, R, p0, Tp);
-  const dim3 pgrid(KVH, (R + kPvRows - 1) / kPvRows);
-  QH_LAUNCH(QK_PF_ATTN, k_pf_pv<HD>, pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
+  const dim3 pgrid(KVH, (R + rbp - 1) / rbp);
+  if (small) QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, kPvRows / 2>), pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
+  else QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, kPvRows>), pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
   return 0;
 }
 
