@@ -420,6 +420,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8_pipe(const int8_t *A, 
   }
 }
 
+constexpr int kMaxSplits = 16;         // K splits of one GEMM at most
+
 // Split-K epilogue: acc = the sum of the S int32 partials (exact in any order:
 // every partial sum of the products is bounded like the whole, |acc| <= 127^2 K),
 // then the fused epilogue's operations on it.  Grid (ceil(N / 256), M).
@@ -431,10 +433,18 @@ __global__ __launch_bounds__(256) void k_gemm_split_epi(const int *part, int S, 
   const int ldp = MODE == GM_SWIGLU ? 2 * N : N;
   const size_t plane = (size_t)M * ldp;
   const int *pp = part + (size_t)i * ldp + j;
+  // every partial requested before the first add (S <= kMaxSplits)
+  int pv[kMaxSplits], pu[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++) {
+    pv[s] = s < S ? pp[s * plane] : 0;
+    pu[s] = MODE == GM_SWIGLU && s < S ? pp[s * plane + N] : 0;
+  }
   int acc = 0, accu = 0;
-  for (int s = 0; s < S; s++) {
-    acc += pp[s * plane];
-    if (MODE == GM_SWIGLU) accu += pp[s * plane + N];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++) {
+    acc += pv[s];
+    accu += pu[s];
   }
   const float asi = as[i];
   if (MODE == GM_SWIGLU) {
@@ -466,7 +476,7 @@ int launch_pipe(const int8_t *A, const float *as, const int8_t *W, const float *
   if (work) {
     const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256, active = mt * nt;
     if (active < cus) {
-      S = min((cus + active - 1) / active, nkt / 8);
+      S = min(min((cus + active - 1) / active, nkt / 8), kMaxSplits);
       const size_t plane = (size_t)M * (MODE == GM_SWIGLU ? 2 * N : N) * 4;
       while (S > 1 && (size_t)S * plane > work_bytes) S--;
     }
