@@ -343,7 +343,7 @@ def small_config(Q, name, steps=64):
     f = m.fork(Q.MODE_FAST)
     try:
         prompt = [int(t) for t in np.random.default_rng(1234).integers(0, cfg[0], P)]
-        m.prefill(prompt, want_logits=False)
+        m.prefill(prompt, want_logits=True)
         m.reset(0)
         Q.lib().qllama_device_sync()
         t0 = time.perf_counter()
@@ -464,9 +464,10 @@ def main():
     t_build = time.perf_counter() - t0
     prompt = [int(t) for t in np.random.default_rng(1234).integers(0, cfg[0], P)]
 
-    # prefill (timed separately, after one untimed ingestion that allocates its buffers)
+    # prefill (timed separately, after one untimed ingestion of the same call: it
+    # allocates the buffers and loads every kernel the call uses, logits path included)
     if P:
-        gm.prefill(prompt, want_logits=False)
+        gm.prefill(prompt, want_logits=True)
         gm.reset(0)
     Q.lib().qllama_device_sync()
     t0 = time.perf_counter()
@@ -524,7 +525,7 @@ def main():
     gf = gm.fork(Q.MODE_FAST)
     t_prefill_fast = None
     if P:
-        gf.prefill(prompt, want_logits=False)
+        gf.prefill(prompt, want_logits=True)
         gf.reset(0)
         Q.lib().qllama_device_sync()
         t0 = time.perf_counter()
