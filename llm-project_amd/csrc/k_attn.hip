@@ -32,6 +32,9 @@
 #include "qdev_seqsum.h"
 #include "qhip.h"
 #include "qhip_internal.h"
+#include "qdev_tl.h"
+
+QTL_DEFINE(attn)
 
 namespace {
 
@@ -169,6 +172,8 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc,
   const int G = H / KVH;
   const int pos = *d_pos, T = pos + 1;
   if (c * kScoreBlock >= T) return;                      // uniform for the block
+  if (threadIdx.x < 64) QTL_MARK(0, 0);
+  QTL_ID(0);
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x / kScoreBlock), t = threadIdx.x % kScoreBlock;
   const int h = kvh * G + g;
   const int j0 = c * kScoreBlock, j = j0 + t;
@@ -205,6 +210,7 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc,
     for (int d = threadIdx.x; d < G * hd; d += blockDim.x) qs[d] = q[(size_t)kvh * G * hd + d];
   }
   __syncthreads();                                       // q, the current k row, the K tile copies (vmcnt)
+  if (threadIdx.x < 64) QTL_MARK(0, 1);
   if (HD && ROPE && last) {                              // the current row into its (skewed) place in the tile
     constexpr int CPR = (HD ? HD : 128) / 4;
     const int rr = pos - j0;
@@ -238,6 +244,7 @@ __global__ __launch_bounds__(1024) void k_attn_scores(const float *q, float *kc,
       bmax[(size_t)h * nch + c] = mb;
     }
   }
+  QTL_MAX(0, 4);
 }
 
 // Head of PV block x: the query heads of one KV head are given block indices
@@ -363,6 +370,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
 
   // 2. softmax weights
   m = block_max<kPvThreads>(m, red);
+  if (tid < 64) QTL_MARK(1, 1);
   if (__builtin_amdgcn_readfirstlane(j0) < T) {          // waves wholly past T hold zeros only
 #pragma unroll
     for (int c = 0; c < CM; c++) e[c] = e[c] - m;
@@ -376,6 +384,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const float sum =
       qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m, tab); });
   const float inv = 1.0f / sum;
+  if (tid < 64) QTL_MARK(1, 2);
 #pragma unroll
   for (int c = 0; c < CM; c += 4)
     if (j0 + c < wcap) {
@@ -385,6 +394,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
         *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
     }
   qd::lds_sync();
+  if (tid < 64) QTL_MARK(1, 3);
 
   // 3. the chains
   if (tid < 64) {                 // lanes past kChains run garbage chains and store nothing
@@ -394,8 +404,11 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
     static_assert(kChains * kTS * 4 == qd::kChainBufBytes && kPBuf == 3 && kTile == 128, "chain_tiles_asm's layout");
     float acc = 0.0f;
     lds_barrier();                                         // barrier 0: tiles 0 and 1
+    QTL_CYC(2, 0);
     int n = ntile;
     qd::chain_tiles_asm(acc, base, n);
+    QTL_CYC(2, 1);
+    QTL_MARK(1, 5);
     const bool own = tid < kChains && d < hd;
     if (own) o[(size_t)h * hd + d] = acc;
     if (obm) {                 // max |o| of this block, for the activation quantizer
@@ -426,6 +439,7 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
       lds_barrier();                                       // barrier k+3
     }
   }
+  QTL_MAX(1, 4);
 }
 
 template <bool DIVW>
@@ -436,6 +450,8 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   __shared__ float red[kPvThreads / 64];
   __shared__ qd::SeqScratch seq;
   __shared__ uint64_t tab[32];
+  if (threadIdx.x < 64) QTL_MARK(1, 0);
+  QTL_ID(1);
   qd::exp_table_to_lds(tab);                             // published by the block max's barrier
   const int h = head_of_block(blockIdx.x, H, KVH);
   const int T = *d_pos + 1;

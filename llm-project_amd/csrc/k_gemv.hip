@@ -21,6 +21,9 @@
 #include "qdev_norm.h"
 #include "qhip.h"
 #include "qhip_internal.h"
+#include "qdev_tl.h"
+
+QTL_DEFINE(gemv)
 
 namespace {
 
@@ -99,6 +102,8 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
   float best = -INFINITY;
   int besti = 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave == 0) QTL_MARK(3 + MODE, 0);
+  QTL_ID(3 + MODE);
   const int j0 = (blockIdx.x * 4 + wave) * R;
   float hmax = 0.0f;
   // the prologue's inputs, then the weights
@@ -207,6 +212,7 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t *qa, const float 
       bi[blockIdx.x] = i0;
     }
   }
+  QTL_MAX(3 + MODE, 4);
 }
 
 // Warp-specialized decode GEMV for the GEMVs with a prologue (PRO 1, 2, 3; the
@@ -293,6 +299,8 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
   __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave == 0) QTL_MARK(MODE, 0);
+  QTL_ID(MODE);
   if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; issued = 0u; }
   __syncthreads();
   if (wave < PW) {
@@ -338,6 +346,7 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
       }
     }
     if (threadIdx.x == 0) as_sh = as;
+    if (wave == 0) QTL_MARK(MODE, 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's bytes (and as) have landed
     if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return;
@@ -363,6 +372,7 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW) {
   }
   asm volatile("" ::: "memory");
+  if (rw == 0) QTL_MARK(MODE, 2);
   // the activation in registers, or (long rows) read from LDS at each row
   constexpr bool A_LDS = KCH > 8;
   v4i a[A_LDS ? 1 : KCH];
@@ -416,9 +426,11 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
             else out[j] = bias ? c + bias[j] : c;
           }
         }
+        if (rw == 0 && r == 0) QTL_MARK(MODE, 3);
       }
     }
   }
+  QTL_MAX(MODE, 4);
   if (MODE == MODE_SWIGLU) {       // the block's max |h|: the last row wave to finish writes it
     if (lane == 0) hred[rw] = hmax;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -560,6 +572,8 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float *bv, const in
 __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *qa,
                                                       int kpad, float *as_out) {
   __shared__ float red[4];
+  if (threadIdx.x < 64) QTL_MARK(7, 0);
+  QTL_ID(7);
   const int k0 = blockIdx.x * 1024 + threadIdx.x * 4;
   float x[4];
 #pragma unroll
@@ -575,6 +589,7 @@ __global__ __launch_bounds__(256) void k_quant_blocks(const float *v, int n, con
   if (k0 < kpad)                                       // values past n were loaded as 0 and give 0
     *reinterpret_cast<uint32_t *>(qa + k0) = qd::quant_i8x4(x[0], x[1], x[2], x[3], inv);
   if (blockIdx.x == 0 && threadIdx.x == 0) *as_out = as;
+  QTL_MAX(7, 4);
 }
 
 // Output channels per wave.  The GEMVs that normalize their own input take
