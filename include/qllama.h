@@ -271,6 +271,11 @@ int  qllama_d2h(void *dst, const void *src, size_t bytes);
 int  qllama_device_sync(void);
 int  qllama_sync(void);
 void *qllama_stream(void);               // the hipStream_t every launch goes to
+// 1 when the model's exact decode steps run the attention half of each layer
+// (QKV GEMV, RoPE, cache append, scores, softmax, PV) as one launch, 0 when
+// they run it as separate kernels (shapes the one launch does not serve, or
+// QLLAMA_NO_ATTN_LAYER=1 in the environment when the model was made).
+int  qllama_attn_layer_active(const QLlamaModel *m);
 // Average duration (ms) of each kernel class over the decode steps run while
 // profiling was on; returns the number of classes written.
 int  qllama_profile(int enable);

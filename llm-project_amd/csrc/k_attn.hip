@@ -29,6 +29,7 @@
 
 #include "qdev_chain.h"
 #include "qdev_math.h"
+#include "qdev_norm.h"
 #include "qdev_seqsum.h"
 #include "qhip.h"
 #include "qhip_internal.h"
@@ -283,8 +284,11 @@ __device__ __forceinline__ float pv_mask(float p, bool keep) {
   return __uint_as_float(__float_as_uint(p) & (keep ? 0xffffffffu : 0u));
 }
 
+// vpos >= 0: the value of V at position vpos is vpatch (for this lane's column)
+// instead of what the load returned (the row the same launch has just appended).
 __device__ __forceinline__ void pv_produce(float *B, const float *W, const float (&v)[kGSlots][4], int t, int T,
-                                           bool cols_full, bool col_ok, int pid) {
+                                           bool cols_full, bool col_ok, int pid, int vpos = -1,
+                                           float vpatch = 0.0f) {
   const int u = pid / kChains, dd = pid % kChains;
   const bool full = cols_full && (t + 1) * kTile <= T;
   float4 w[kGSlots];
@@ -299,11 +303,18 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
     const int grp = u + kUnits * g;
     if (kUnits * (g + 1) <= kGroups || grp < kGroups) {
       const int jb = t * kTile + 4 * grp;
+      float v0 = v[g][0], v1 = v[g][1], v2 = v[g][2], v3 = v[g][3];
+      if (vpos >= jb && vpos < jb + 4) {
+        v0 = vpos == jb ? vpatch : v0;
+        v1 = vpos == jb + 1 ? vpatch : v1;
+        v2 = vpos == jb + 2 ? vpatch : v2;
+        v3 = vpos == jb + 3 ? vpatch : v3;
+      }
       float4 p;
-      p.x = w[g].x * v[g][0];
-      p.y = w[g].y * v[g][1];
-      p.z = w[g].z * v[g][2];
-      p.w = w[g].w * v[g][3];
+      p.x = w[g].x * v0;
+      p.y = w[g].y * v1;
+      p.z = w[g].z * v2;
+      p.w = w[g].w * v3;
       if (!full) {
         p.x = pv_mask(p.x, col_ok && jb + 0 < T);
         p.y = pv_mask(p.y, col_ok && jb + 1 < T);
@@ -315,6 +326,30 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
   }
 }
 
+
+// The V stream of one PV block's producer lanes (waves 1-7): the buffer
+// resource over its KV head's rows, each lane's slot offsets, and the first
+// three tiles, requested by pv_v_start.  A caller that starts it early
+// (k_attn_layer) hands it to pv_block, which otherwise starts it itself.
+struct PvV {
+  __amdgpu_buffer_rsrc_t rs;
+  int vo[kGSlots];
+  float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
+};
+
+__device__ __forceinline__ void pv_v_start(PvV &v, const float *vc, int kvh, int hd, int max_seq, int d0, int ntile) {
+  const int tid = threadIdx.x, pid = tid - 64;
+  const float *Vh = vc + (size_t)kvh * max_seq * hd;
+  v.rs = __builtin_amdgcn_make_buffer_rsrc((void *)Vh, (short)0, max_seq * hd * 4, 0x00020000);
+#pragma unroll
+  for (int g = 0; g < kGSlots; g++) {
+    const int grp = pid / kChains + kUnits * g;
+    v.vo[g] = tid >= 64 && grp < kGroups ? (4 * grp * hd + d0 + pid % kChains) * 4 : 0x40000000;   // else: no traffic
+  }
+  pv_load(v.r0, v.rs, v.vo, 0, ntile, hd);
+  pv_load(v.r1, v.rs, v.vo, 1, ntile, hd);
+  pv_load(v.r2, v.rs, v.vo, 2, ntile, hd);
+}
 
 // One PV block with CM softmax terms per thread (512 * CM >= T).
 //  1. Requests the head's block maxima, this thread's CM scores, and the
@@ -329,11 +364,17 @@ __device__ __forceinline__ void pv_produce(float *B, const float *W, const float
 //     executed by every wave) certifies that tiles <= k+1 are in LDS and that
 //     the chains are done with tile k-1: tile k sits in buffer k % 3, and the
 //     producers refill buffer (k+2) % 3 = (k-1) % 3 after barrier k.
-template <int CM, bool DIVW>
+// XCH: the scores and block maxima were written by other blocks of the same
+// launch on this XCD (k_attn_layer): they are read past the L1, the maxima
+// are at bmax[h * nch + i] for i < nbm, and V's row T-1 (appended by the same
+// launch) comes from vrow instead of the cache.
+// PRE: the caller has started the V stream (pre, from pv_v_start).
+template <int CM, bool DIVW, bool XCH = false, bool PRE = false>
 __device__ __forceinline__ void pv_block(const float *scores, const float *bmax, const float *vc, int T, int h,
                                          int kvh, int hd, int max_seq, int nch, float *o, float *obm, float *lds,
-                                         float *red, qd::SeqScratch &seq, const uint64_t *tab) {
-  const int d0 = blockIdx.y * kChains, tid = threadIdx.x;
+                                         float *red, qd::SeqScratch &seq, const uint64_t *tab, int slice,
+                                         int nslice, int nbm = 0, const float *vrow = nullptr, PvV *pre = nullptr) {
+  const int d0 = slice * kChains, tid = threadIdx.x;
   const int wcap = (max_seq + kTile - 1) / kTile * kTile;
   float *W = lds;
   float *P = lds + wcap;                                 // kPBuf tiles of kChains x kTS
@@ -341,32 +382,29 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const float *sh = scores + (size_t)h * max_seq;
 
   // 1. requests (block maxima: at most 128 <= 512 per head)
-  const int nc = (T + kScoreBlock - 1) / kScoreBlock;
-  float m = tid < nc ? bmax[(size_t)h * nch + tid] : -INFINITY;
+  const int nc = XCH ? nbm : (T + kScoreBlock - 1) / kScoreBlock;
+  float m = -INFINITY;
+  if (tid < nc)
+    m = XCH ? __hip_atomic_load(bmax + (size_t)h * nch + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+            : bmax[(size_t)h * nch + tid];
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void *)sh, (short)0, max_seq * 4, 0x00020000);
   const int j0 = tid * CM;
   float e[CM];
 #pragma unroll
   for (int c = 0; c < CM; c += 4) {       // positions past max_seq read as 0; past T they are masked below
-    const v4i q = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(srs, (j0 + c) * 4, 0, 0));
+    const v4i q = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
     e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
     e[c + 2] = __int_as_float(q.z); e[c + 3] = __int_as_float(q.w);
   }
   const int pid = tid - 64;
-  const float *Vh = vc + (size_t)kvh * max_seq * hd;
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void *)Vh, (short)0, max_seq * hd * 4, 0x00020000);
+  PvV own;
+  PvV &V = PRE ? *pre : own;
+  if constexpr (!PRE) pv_v_start(own, vc, kvh, hd, max_seq, d0, ntile);
   const bool cols_full = d0 + kChains <= hd, col_ok = d0 + pid % kChains < hd;
-  int vo[kGSlots];
-#pragma unroll
-  for (int g = 0; g < kGSlots; g++) {
-    const int grp = pid / kChains + kUnits * g;
-    vo[g] = tid >= 64 && grp < kGroups ? (4 * grp * hd + d0 + pid % kChains) * 4 : 0x40000000;   // else: no traffic
-  }
-  float r0[kGSlots][4], r1[kGSlots][4], r2[kGSlots][4];
-  pv_load(r0, vrs, vo, 0, ntile, hd);
-  pv_load(r1, vrs, vo, 1, ntile, hd);
-  pv_load(r2, vrs, vo, 2, ntile, hd);
+  const int vpos = XCH ? T - 1 : -1;
+  const float vpatch = XCH && tid >= 64 && col_ok
+                           ? __hip_atomic_load(vrow + d0 + pid % kChains, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.0f;
 
   // 2. softmax weights
   m = block_max<kPvThreads>(m, red);
@@ -381,8 +419,10 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
 #pragma unroll
     for (int c = 0; c < CM; c++) e[c] = 0.0f;
   }
-  const float sum =
-      qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) { return qd::expf_glibc(sh[i] - m, tab); });
+  const float sum = qd::seq_sum_nonneg<kPvThreads, CM>(e, T, seq, [&](int i) {
+    const float si = XCH ? __hip_atomic_load(sh + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : sh[i];
+    return qd::expf_glibc(si - m, tab);
+  });
   const float inv = 1.0f / sum;
   if (tid < 64) QTL_MARK(1, 2);
 #pragma unroll
@@ -413,29 +453,29 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
     if (own) o[(size_t)h * hd + d] = acc;
     if (obm) {                 // max |o| of this block, for the activation quantizer
       const float mo = qd::wave_max_f32(own ? fabsf(acc) : 0.0f);
-      if (tid == 0) obm[(size_t)h * gridDim.y + blockIdx.y] = mo;
+      if (tid == 0) obm[(size_t)h * nslice + slice] = mo;
     }
   } else {
     // tile k is formed from register set k % 3 into LDS buffer k % 3; its V
     // values are requested five tiles ahead of use (three ahead of forming)
     float *B0 = P, *B1 = P + kChains * kTS, *B2 = P + 2 * kChains * kTS;
-    pv_produce(B0, W, r0, 0, T, cols_full, col_ok, pid);
-    pv_load(r0, vrs, vo, 3, ntile, hd);
-    pv_produce(B1, W, r1, 1, T, cols_full, col_ok, pid);   // past the last tile: zeros, never read
-    pv_load(r1, vrs, vo, 4, ntile, hd);
+    pv_produce(B0, W, V.r0, 0, T, cols_full, col_ok, pid, vpos, vpatch);
+    pv_load(V.r0, V.rs, V.vo, 3, ntile, hd);
+    pv_produce(B1, W, V.r1, 1, T, cols_full, col_ok, pid, vpos, vpatch);   // past the last tile: zeros, never read
+    pv_load(V.r1, V.rs, V.vo, 4, ntile, hd);
     lds_barrier();                                         // barrier 0
     for (int k = 0;; k += 3) {
       if (k + 1 >= ntile) break;
-      pv_produce(B2, W, r2, k + 2, T, cols_full, col_ok, pid);
-      pv_load(r2, vrs, vo, k + 5, ntile, hd);
+      pv_produce(B2, W, V.r2, k + 2, T, cols_full, col_ok, pid, vpos, vpatch);
+      pv_load(V.r2, V.rs, V.vo, k + 5, ntile, hd);
       lds_barrier();                                       // barrier k+1
       if (k + 2 >= ntile) break;
-      pv_produce(B0, W, r0, k + 3, T, cols_full, col_ok, pid);
-      pv_load(r0, vrs, vo, k + 6, ntile, hd);
+      pv_produce(B0, W, V.r0, k + 3, T, cols_full, col_ok, pid, vpos, vpatch);
+      pv_load(V.r0, V.rs, V.vo, k + 6, ntile, hd);
       lds_barrier();                                       // barrier k+2
       if (k + 3 >= ntile) break;
-      pv_produce(B1, W, r1, k + 4, T, cols_full, col_ok, pid);
-      pv_load(r1, vrs, vo, k + 7, ntile, hd);
+      pv_produce(B1, W, V.r1, k + 4, T, cols_full, col_ok, pid, vpos, vpatch);
+      pv_load(V.r1, V.rs, V.vo, k + 7, ntile, hd);
       lds_barrier();                                       // barrier k+3
     }
   }
@@ -456,10 +496,305 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   const int h = head_of_block(blockIdx.x, H, KVH);
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
-  if (T <= kPvThreads * 4) pv_block<4, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else if (T <= kPvThreads * 8) pv_block<8, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else if (T <= kPvThreads * 16) pv_block<16, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
-  else pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab);
+  if (T <= kPvThreads * 4) pv_block<4, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+  else if (T <= kPvThreads * 8) pv_block<8, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+  else if (T <= kPvThreads * 16) pv_block<16, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+  else pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+}
+
+// ---------------------------------------------------------------------------
+// The attention half of a decode layer in one launch (exact mode):
+//   Q  the QKV GEMV with its exact rmsnorm prologue (rmsnorm.c:7-21,
+//      quant.c:60-85, llama.c:541-548), for the rows of one KV head's query,
+//      key and value heads;
+//   S  RoPE (rope.c:48-68), the cache append (llama.c:551-552) and the scores
+//      s_j = (q . K_j) * scale of 1/32 of the positions (llama.c:557-563);
+//   P  the softmax and o = sum_j w_j V_j (llama.c:564-575), as k_attn_pv.
+// Grid: 32 blocks per KV head, n_kv = 8.  Workgroups are dealt to the eight
+// XCDs round-robin, continuing from where the previous launches left off:
+// block b runs on XCD (s + b) % 8 for a start s that changes from launch to
+// launch.  A block therefore serves the KV head of the XCD it runs on (read
+// from the hardware), with rank b / 8 among that XCD's 32 blocks, so a KV
+// head's blocks share one XCD and its L2 whatever s is (the host probes once
+// that a launch covers every XCD 32 times).  Between the phases the head's 32 blocks meet at a
+// counter (ly_meet) instead of a kernel boundary, and what one block hands to
+// another (the QKV outputs, the scores, the block maxima) goes through that
+// shared L2: plain stores, which the write-through L1 passes on to the L2 before
+// the store counter drains, and device-scope loads, which skip the L1 (whose
+// lines could predate the store).  Every block must be resident at once: the host launches the
+// kernel only where there are 32 * n_kv CUs for its one block per CU.  A
+// meeting that waits too long (a block not resident, or an XCD given other
+// than 32 blocks), sets an error flag, which the host reports as an error; the
+// block goes on, so the kernel always ends.
+// ---------------------------------------------------------------------------
+constexpr int kLyNB = 32;                   // blocks per KV head
+constexpr int kLyThreads = 512;
+constexpr int kLyWaves = kLyThreads / 64;
+constexpr int kLyPW = 4;                    // phase Q: prologue waves (rmsnorm, quantization of x) ...
+constexpr int kLyRW = kLyWaves - kLyPW;     // ... and row waves
+constexpr int kLyRowsPerWave = 6;           // QKV rows of a row wave: (G + 2) * hd / (32 * 4) at most
+constexpr int kLyKRows = 128;               // K rows of a block in LDS: at most 32 * 128 positions
+constexpr unsigned kLySpin = 1u << 18;      // polls before a meeting gives up (~0.1 s; a meeting takes ~1 us)
+static_assert(kLyThreads == kPvThreads, "phase P is the PV block");
+
+__device__ __forceinline__ float ly_ld(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The blocks of one KV head meet: every wave's stores have completed, one
+// thread counts the block in (the counter only grows, by kLyNB per launch) and
+// waits until all of this launch's blocks have arrived.
+__device__ __forceinline__ void ly_meet(unsigned *ctr, unsigned *err, int tk = -1) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (tk >= 0) QTL_MARK(tk, 5);
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned target = old - old % kLyNB + kLyNB;
+    for (unsigned n = 0;; n++) {
+      const unsigned c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((int)(c - target) >= 0) break;
+      if (n == kLySpin) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
+// Row of the QKV matrix ([q heads | k heads | v heads] x head_dim rows) that is
+// local row l of KV head kvh's rows [q of its G heads | k | v].
+__device__ __forceinline__ int ly_row(int kvh, int l, int G, int H, int KVH, int hd) {
+  if (l < G * hd) return kvh * G * hd + l;
+  l -= G * hd;
+  if (l < hd) return H * hd + kvh * hd + l;
+  return H * hd + KVH * hd + kvh * hd + (l - hd);
+}
+
+template <int KCH>
+__device__ __forceinline__ void ly_load_row(v4i (&w)[KCH], const int8_t *row, int lane) {
+  const v4i *p = reinterpret_cast<const v4i *>(row);
+#pragma unroll
+  for (int i = 0; i < KCH; i++) w[i] = __builtin_nontemporal_load(&p[lane + 64 * i]);
+}
+
+template <int KCH>
+__device__ __forceinline__ int ly_dot_row(const v4i (&w)[KCH], const v4i (&a)[KCH]) {
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < KCH; i++) {
+    t = __builtin_amdgcn_sdot4(a[i].x, w[i].x, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].y, w[i].y, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].z, w[i].z, t, false);
+    t = __builtin_amdgcn_sdot4(a[i].w, w[i].w, t, false);
+  }
+  return t;
+}
+
+// K rows j0 .. j0+nr-1 (nr <= kLyKRows) into LDS, laid out as score_copy_rows
+// lays them out (row rr's 16-byte chunk c at slot (c + rr mod 8) mod CPR), so
+// score_row_dot reads them; rows past nr repeat the last one (the same lines:
+// no extra HBM traffic).
+template <int HD>
+__device__ __forceinline__ void ly_copy_k(const float *Kh, int j0, int nr, float *ks) {
+  constexpr int CPR = HD / 4;                 // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;               // rows per wave instruction
+  constexpr int NI = kLyKRows / RPI / kLyRW;  // copies per row wave: a fixed count, so that the compiler
+                                              // can wait for earlier loads without waiting for these
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) - kLyPW;
+  const int sub = lane / CPR, slot = lane % CPR;
+  const int last = nr > 0 ? j0 + nr - 1 : 0;      // a block without positions copies row 0 (never read)
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int kk = wv + kLyRW * i;
+    const int rr = kk * RPI + sub;
+    const int c = (slot - (rr & 7)) & (CPR - 1);
+    const int j = min(j0 + rr, last);
+    __builtin_amdgcn_global_load_lds((const void *)(Kh + (size_t)j * HD + 4 * c), (lds_void_ptr)(ks + kk * 64 * 4),
+                                     16, 0, 0);
+  }
+}
+
+template <int HD, int KCH>
+__global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const float *gain, float eps, int dm,
+                                                           const int8_t *W, const float *ws, const float *bias,
+                                                           int kpad, float *kc, float *vc, const int *d_pos, int H,
+                                                           int KVH, int max_seq, float scale, const float *cos_t,
+                                                           const float *sin_t, float *scores, float *bmax,
+                                                           float *qx, unsigned *sync, float *o, float *obm) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];   // the K rows, then the PV weights and tiles
+  __shared__ __attribute__((aligned(16))) float qs[4 * HD];
+  __shared__ __attribute__((aligned(16))) float kcur[HD];
+  __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
+  __shared__ float red[2 * (kLyThreads / 64)];
+  __shared__ qd::SeqScratch seq;
+  __shared__ uint64_t tab[32];
+  __shared__ unsigned ly_gctr, ly_issued, ly_ready;
+  __shared__ float ly_as;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const int kvh = (int)(xcc & 7u), r = blockIdx.x / 8;        // the KV head of this XCD; rank on it
+  const int G = H / KVH;
+  const int nrow = (G + 2) * HD, RB = nrow / kLyNB;           // the KV head's QKV rows; per block
+  const int T = *d_pos + 1, pos = T - 1;
+  const int PB = (T + kLyNB - 1) / kLyNB;                     // score positions per block
+  const int j0 = r * PB, j1 = min(T, j0 + PB), nr = max(0, j1 - j0);
+  float *Kh = kc + (size_t)kvh * max_seq * HD;
+  float *xq = qx + (size_t)kvh * nrow;                         // this launch's q (G heads), k, v of the KV head
+  unsigned *err = sync + 2 * 64 * KVH;
+  if (wave == 0) QTL_MARK(3, 0);
+  QTL_ID(3);
+  const uint64_t tabv = tid < 32 ? qd::kExp2Tab[tid] : 0;      // to LDS after the prologue: a store
+                                                              // now would wait for the load at once
+  if (tid == 0) {
+    ly_gctr = 0u; ly_issued = 0u; ly_ready = 0u;
+    if (xcc > 7u) __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();                                             // the counters
+
+  // ---- Q: the KV head's QKV rows (k_gemv_ws PRO = 2's operations and order) ----
+  // Waves 0-3 normalize and quantize x into LDS, meeting at an LDS counter;
+  // waves 4-7 request their weight rows and this block's K rows of phase S as
+  // soon as the prologue's inputs are requested, then wait on an LDS flag.  At
+  // the end the producer waves (1-7) request phase P's first V tiles, which the
+  // meeting after this phase lets land.
+  const int NS = (HD + kChains - 1) / kChains;
+  const bool pv = r < G * NS;                                   // this block has a phase P
+  const int ph = kvh * G + r / NS, pslice = r % NS;
+  PvV vpre;
+  if (wave < kLyPW) {
+    constexpr int NTP = 64 * kLyPW, CMQ = KCH * 1024 / NTP;    // kpad = NTP * CMQ
+    unsigned epoch = 0u;
+    const qd::GroupSync gs{&ly_gctr, (unsigned)kLyPW, &epoch};
+    float y[CMQ], gm[CMQ];
+    qd::rmsnorm_load<CMQ>(x, dm, gain, y, gm);
+    __builtin_amdgcn_sched_barrier(0);
+    if (lane == 0) __hip_atomic_fetch_add(&ly_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const float as = qd::rmsnorm_apply<NTP, CMQ>(x, dm, eps, y, gm, red, seq, gs);
+    const float inv = 1.0f / as;
+#pragma unroll
+    for (int c = 0; c < CMQ; c += 4) *reinterpret_cast<uint32_t *>(qsh + tid * CMQ + c) = qd::quant_word(y, c, inv);
+    if (tid == 0) ly_as = as;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");        // this wave's bytes (and as) have landed
+    if (lane == 0) __hip_atomic_fetch_add(&ly_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (wave == 0) QTL_MARK(3, 1);
+  } else {
+    const int rw = wave - kLyPW;
+    while (__hip_atomic_load(&ly_issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kLyPW) {
+    }
+    v4i w[kLyRowsPerWave][KCH];
+    float wsc[kLyRowsPerWave], wb[kLyRowsPerWave];
+#pragma unroll
+    for (int s = 0; s < kLyRowsPerWave; s++) {
+      const int l = min(rw + kLyRW * s, RB - 1);                // rows past RB repeat the last (not used)
+      const int j = ly_row(kvh, r * RB + l, G, H, KVH, HD);
+      ly_load_row<KCH>(w[s], W + (size_t)j * kpad, lane);
+      wsc[s] = ws[j];
+      wb[s] = bias ? bias[j] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);                          // the K copies after every weight and scale
+    ly_copy_k<HD>(Kh, j0, nr, lds);                             // phase S's K rows, straight into LDS
+    __builtin_amdgcn_sched_barrier(0);
+    while (__hip_atomic_load(&ly_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kLyPW) {
+    }
+    asm volatile("" ::: "memory");
+    const float as = ly_as;
+    v4i a[KCH];
+#pragma unroll
+    for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
+#pragma unroll
+    for (int s = 0; s < kLyRowsPerWave; s++) {
+      const int l = rw + kLyRW * s;
+      const int acc = qd::wave_sum_i32(ly_dot_row<KCH>(w[s], a));
+      if (rw == 0 && s == 0) QTL_MARK(3, 2);
+      if (l < RB) {
+        const float c = (as * wsc[s]) * (float)acc;
+        if (lane == 0) xq[r * RB + l] = bias ? c + wb[s] : c;
+      }
+    }
+    if (rw == 0) QTL_MARK(3, 3);
+  }
+  if (pv) pv_v_start(vpre, vc, kvh, HD, max_seq, pslice * kChains, (T + kTile - 1) / kTile);
+  if (tid < 32) tab[tid] = tabv;                               // published by the meeting
+  ly_meet(sync + (0 * KVH + kvh) * 64, err, 3);                  // also: this block's K rows are in LDS
+  if (wave == 0) QTL_MARK(3, 4);
+
+  // ---- S: RoPE, the cache append, the scores of positions j0 .. j1-1 ----
+  if (wave == 0) QTL_MARK(0, 0);
+  constexpr int half = HD / 2;
+  const bool holds = j0 <= pos && pos < j1;
+  {
+    const float *ct = cos_t + (size_t)pos * half, *st = sin_t + (size_t)pos * half;
+    for (int i = tid; i < G * half; i += kLyThreads) {
+      const int gg = i / half, k = i % half;
+      const float cs = ct[k], sn = st[k];
+      const float x1 = ly_ld(xq + gg * HD + k), x2 = ly_ld(xq + gg * HD + k + half);
+      qs[gg * HD + k] = x1 * cs - x2 * sn;
+      qs[gg * HD + k + half] = x2 * cs + x1 * sn;
+    }
+    if (holds) {
+      float *kdst = Kh + (size_t)pos * HD, *vdst = vc + ((size_t)kvh * max_seq + pos) * HD;
+      for (int k = tid; k < half; k += kLyThreads) {
+        const float cs = ct[k], sn = st[k];
+        const float x1 = ly_ld(xq + G * HD + k), x2 = ly_ld(xq + G * HD + k + half);
+        const float y1 = x1 * cs - x2 * sn, y2 = x2 * cs + x1 * sn;
+        kcur[k] = y1;
+        kcur[k + half] = y2;
+        kdst[k] = y1;
+        kdst[k + half] = y2;
+      }
+      for (int d = tid; d < HD; d += kLyThreads) vdst[d] = ly_ld(xq + (G + 1) * HD + d);
+    }
+  }
+  __syncthreads();
+  if (holds) {                                                 // the current row into its place in the tile
+    constexpr int CPR = HD / 4;
+    const int rr = pos - j0;
+    for (int d = tid; d < HD; d += kLyThreads) lds[rr * HD + 4 * (((d >> 2) + (rr & 7)) & (CPR - 1)) + (d & 3)] = kcur[d];
+    __syncthreads();
+  }
+  if (wave == 0) QTL_MARK(0, 1);
+  {
+    const int g = __builtin_amdgcn_readfirstlane(tid / kScoreBlock), t = tid % kScoreBlock;
+    float s = -INFINITY;
+    if (g < G && t < nr) {
+      s = score_row_dot<HD>(qs + g * HD, lds, t) * scale;
+      scores[(size_t)(kvh * G + g) * max_seq + j0 + t] = s;
+    }
+    s = qd::wave_max_f32(s);                                   // two waves per query head
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    if (tid < G) bmax[(size_t)(kvh * G + tid) * kLyNB + r] = fmaxf(red[2 * tid], red[2 * tid + 1]);
+  }
+  QTL_MAX(0, 4);
+  ly_meet(sync + (1 * KVH + kvh) * 64, err);
+
+  // ---- P: softmax weights and the chains of 16 output dims of one query head ----
+  if (pv) {
+    if (wave == 0) QTL_MARK(1, 0);
+    QTL_ID(1);
+    const int nbm = (T + PB - 1) / PB;                         // blocks that had positions
+    const float *vrow = xq + (G + 1) * HD;
+    if (T <= kPvThreads * 4)
+      pv_block<4, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
+                                     pslice, NS, nbm, vrow, &vpre);
+    else
+      pv_block<8, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
+                                     pslice, NS, nbm, vrow, &vpre);
+  }
+}
+
+// The XCC (XCD) each of n blocks ran on.
+__global__ void k_xcc_probe(unsigned *out) {
+  if (threadIdx.x == 0) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    out[blockIdx.x] = v & 0xfu;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -813,6 +1148,94 @@ extern "C" int qhip_attention_rope(const float *qkv, float *kc, float *vc, const
                                    int hd, int max_seq, float scale, const float *cos_t, const float *sin_t,
                                    float *scores, float *o, float *obm) {
   return attention<true>(qkv, kc, vc, d_pos, n_heads, n_kv, hd, max_seq, scale, cos_t, sin_t, scores, o, obm);
+}
+
+// ---- the attention half of a decode layer in one launch (k_attn_layer) ----
+namespace {
+int g_ly_probe = -1;          // -1: not probed yet; 1: 32 * 8 blocks land on XCD (block % 8)
+size_t g_ly_attr[2] = {0, 0};
+constexpr size_t kLyLds = 96 * 1024;   // dynamic LDS: the K rows (64 KB) or the PV weights and tiles; with
+                                       // the static arrays more than half of a CU's LDS: one block per CU
+}  // namespace
+
+// Whether a launch of 32 * 8 blocks puts block b on XCD (s + b) % 8 for one
+// start s, so that every XCD runs 32 blocks with distinct ranks b / 8 (what
+// k_attn_layer assumes).  Probed once, with one small launch; call outside
+// graph capture.
+extern "C" int qhip_attn_layer_probe(void) {
+  if (g_ly_probe >= 0) return g_ly_probe;
+  g_ly_probe = 0;
+  constexpr int n = kLyNB * 8;
+  if (qh::num_cus() < n) return 0;
+  unsigned *d = nullptr, h[n];
+  if (hipMalloc(&d, n * sizeof(unsigned)) != hipSuccess) { (void)hipGetLastError(); return 0; }
+  hipLaunchKernelGGL(k_xcc_probe, dim3(n), dim3(64), 0, qh::stream(), d);
+  bool ok = hipGetLastError() == hipSuccess &&
+            hipMemcpyAsync(h, d, sizeof h, hipMemcpyDeviceToHost, qh::stream()) == hipSuccess &&
+            hipStreamSynchronize(qh::stream()) == hipSuccess;
+  (void)hipFree(d);
+  for (int b = 0; ok && b < n; b++) ok = h[b] < 8u && (h[b] + 8u - (unsigned)(b % 8)) % 8u == (h[0] + 8u) % 8u;
+  g_ly_probe = ok ? 1 : 0;
+  return g_ly_probe;
+}
+
+// Shapes k_attn_layer serves: 8 KV heads (one per XCD), at most 4 query heads
+// per KV head, head_dim 128, kpad 2048 or 4096, max_seq <= 4096, and a device
+// with the 256 CUs its blocks need at once.
+extern "C" int qhip_attn_layer_ok(int n_heads, int n_kv, int hd, int kpad, int max_seq) {
+  if (n_kv != 8 || n_heads % n_kv || hd != 128 || (kpad != 2048 && kpad != 4096)) return 0;
+  const int G = n_heads / n_kv;
+  if (G < 1 || G > 4 || (G + 2) * hd % kLyNB || (G + 2) * hd / kLyNB > kLyRW * kLyRowsPerWave) return 0;
+  if (G * ((hd + kChains - 1) / kChains) > kLyNB || max_seq > kLyNB * kLyKRows) return 0;
+  if (pv_lds_bytes(max_seq) > kLyLds || (size_t)kLyKRows * hd * 4 > kLyLds) return 0;
+  return qh::num_cus() >= kLyNB * n_kv && qhip_attn_layer_probe() == 1;
+}
+
+// Scratch of k_attn_layer: floats (the exchanged QKV outputs and block maxima),
+// and 32-bit words of meeting counters and error flag, zero before first use.
+extern "C" size_t qhip_attn_layer_scratch(int n_heads, int n_kv, int hd) {
+  return (size_t)n_kv * (n_heads / n_kv + 2) * hd + (size_t)n_heads * kLyNB;
+}
+extern "C" size_t qhip_attn_layer_sync_words(int n_kv) { return (size_t)2 * 64 * n_kv + 64; }
+
+extern "C" int qhip_attn_layer(const float *x, const float *gain, float eps, int dm, const int8_t *W,
+                               const float *ws, const float *bias, int kpad, float *kc, float *vc, const int *d_pos,
+                               int n_heads, int n_kv, int hd, int max_seq, float scale, const float *cos_t,
+                               const float *sin_t, float *scores, float *scratch, unsigned *sync, float *o,
+                               float *obm) {
+  if (!qhip_attn_layer_ok(n_heads, n_kv, hd, kpad, max_seq) || dm > kpad || dm + 15 < kpad)
+    return qh::fail_msg("attn_layer: unsupported shape");
+  const int G = n_heads / n_kv;
+  float *qx = scratch, *bmax = scratch + (size_t)n_kv * (G + 2) * hd;
+  const int kch = kpad / 1024;
+  const void *fn = kch == 4 ? reinterpret_cast<const void *>(k_attn_layer<128, 4>)
+                            : reinterpret_cast<const void *>(k_attn_layer<128, 2>);
+  if (g_ly_attr[kch == 4] < kLyLds) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLyLds);
+    if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_attn_layer)", e);
+    g_ly_attr[kch == 4] = kLyLds;
+  }
+  if (kch == 4)
+    QH_LAUNCH(QK_ATTN, (k_attn_layer<128, 4>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
+              bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
+              obm);
+  else
+    QH_LAUNCH(QK_ATTN, (k_attn_layer<128, 2>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
+              bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
+              obm);
+  return 0;
+}
+
+// The k_attn_layer error flag since the sync words were zeroed: 0 none, 1 a
+// meeting timed out (blocks not resident at once, or an XCD given other than
+// 32 blocks), 2 an XCC id past 7, -1 the flag could not be read (synchronizes
+// the stream).
+extern "C" int qhip_attn_layer_failed(const unsigned *sync, int n_kv) {
+  unsigned e = 0;
+  if (hipMemcpyAsync(&e, sync + 2 * 64 * n_kv, sizeof e, hipMemcpyDeviceToHost, qh::stream()) != hipSuccess ||
+      hipStreamSynchronize(qh::stream()) != hipSuccess)
+    return -1;
+  return (int)e;
 }
 
 // GPT-2's decode attention (model.c:485-504): as qhip_attention (q given, row

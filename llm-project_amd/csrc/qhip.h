@@ -111,6 +111,23 @@ int qhip_attention_rope(const float *qkv, float *kc, float *vc, const int *d_pos
                         int max_seq, float scale, const float *cos_t, const float *sin_t, float *scores, float *o,
                         float *obm);
 int qhip_attention_nbm(int n_heads, int hd);
+// The attention half of a decode layer in one launch (exact mode): the QKV GEMV
+// with its rmsnorm prologue (as qhip_gemv_plain_norm), RoPE, the cache append,
+// the scores, the softmax and PV (as qhip_attention_rope), one KV head per XCD.
+// qhip_attn_layer_ok tells whether a shape (and the device) is served;
+// scratch holds qhip_attn_layer_scratch floats, sync qhip_attn_layer_sync_words
+// words that are zero before the first launch and then left to the kernel.
+// obm receives qhip_attention_nbm maxima.  qhip_attn_layer_failed reports a
+// launch whose blocks could not all meet (it synchronizes the stream).
+int    qhip_attn_layer_probe(void);
+int    qhip_attn_layer_ok(int n_heads, int n_kv, int hd, int kpad, int max_seq);
+size_t qhip_attn_layer_scratch(int n_heads, int n_kv, int hd);
+size_t qhip_attn_layer_sync_words(int n_kv);
+int    qhip_attn_layer(const float *x, const float *gain, float eps, int dm, const int8_t *W, const float *ws,
+                       const float *bias, int kpad, float *kc, float *vc, const int *d_pos, int n_heads, int n_kv,
+                       int hd, int max_seq, float scale, const float *cos_t, const float *sin_t, float *scores,
+                       float *scratch, unsigned *sync, float *o, float *obm);
+int    qhip_attn_layer_failed(const unsigned *sync, int n_kv);
 // The fast decode mode's attention (k_fattn.hip): split-K over positions with an
 // online-softmax merge, same inputs and outputs as qhip_attention_rope (rope = 1)
 // or qhip_attention (rope = 0, q pre-rotated and row pos already cached); obm

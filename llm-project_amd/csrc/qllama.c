@@ -60,6 +60,10 @@ typedef struct {
   float *pf_x, *pf_qkv, *pf_q, *pf_o, *pf_h, *pf_as, *pf_attn;
   int8_t *pf_qa;
   int *pf_work;      // split-K partial sums of the prompt GEMMs (PF_WORK_BYTES)
+  // the attention half of a decode layer in one launch (qhip_attn_layer), where served
+  int ly_ok;
+  float *ly_scratch;
+  unsigned *ly_sync;
 } QDev;
 
 typedef struct {
@@ -233,6 +237,8 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
   size_t o_state = TAKE(64);
   size_t o_in = TAKE((size_t)(d->max_seq + 1) * 4);
   size_t o_out = TAKE((size_t)(d->max_seq + 1) * 4);
+  size_t o_ly = TAKE(qhip_attn_layer_scratch(d->H, d->KVH, d->hd) * 4);
+  size_t o_lys = TAKE(qhip_attn_layer_sync_words(d->KVH) * 4);
 #undef TAKE
   d->blob = (uint8_t*)qhip_malloc(off);
   d->h_stage = (int*)qhip_host_alloc((size_t)(d->max_seq + 2) * sizeof(int));
@@ -262,8 +268,12 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
   d->obm = (float*)(b + o_obm); d->hbm = (float*)(b + o_hbm);
   d->amax_v = (float*)(b + o_amv); d->amax_i = (int*)(b + o_ami); d->qa = (int8_t*)(b + o_qa);
   d->d_state = (int*)(b + o_state); d->d_in = (int*)(b + o_in); d->d_out = (int*)(b + o_out);
+  d->ly_scratch = (float*)(b + o_ly); d->ly_sync = (unsigned*)(b + o_lys);
+  // QLLAMA_NO_ATTN_LAYER=1 keeps the separate QKV, scores and PV kernels (same results)
+  d->ly_ok = !getenv("QLLAMA_NO_ATTN_LAYER") && qhip_gemv_norm_ok(d->kp_dm, d->dm) &&
+             qhip_attn_layer_ok(d->H, d->KVH, d->hd, d->kp_dm, d->max_seq);
   if (qhip_fill_zero(d->qa, (size_t)d->kp_max) || qhip_fill_zero(d->d_in, (size_t)(d->max_seq + 1) * 4) ||
-      qhip_fill_zero(d->d_state, 64)) {
+      qhip_fill_zero(d->d_state, 64) || qhip_fill_zero(d->ly_sync, qhip_attn_layer_sync_words(d->KVH) * 4)) {
     qdev_free(d);
     return 1;
   }
@@ -656,19 +666,24 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
   const int fuse_o = qhip_gemv_fused_ok(d->kp_qd), fuse_gu = qhip_gemv_norm_ok(d->kp_dm, d->dm);
   const int nbh = fuse_gu ? qhip_gemv_norm_blocks(d->dff) : qhip_gemv_blocks(d->dff, d->kp_dm);
   int rc = qhip_embed(d->wte, d->wte_s, d->dm, d->d_in, d->d_state, d->x);
+  const int ly = !fast && d->ly_ok;
   for (int l = 0; l < d->L && !rc; l++) {
     float *kc = kd->kbase + (size_t)l * per, *vc = kd->vbase + (size_t)l * per;
-    if (fuse_gu) {       // rmsnorm inside the QKV GEMV
+    if (ly) {            // QKV GEMV, RoPE, cache append, scores, softmax and PV in one launch
+      rc |= qhip_attn_layer(d->x, d->g_attn[l], d->eps, d->dm, d->wqkv[l], d->sqkv[l], d->bqkv[l], d->kp_dm, kc, vc,
+                            dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos, d->rope_sin, d->scores,
+                            d->ly_scratch, d->ly_sync, d->o, d->obm);
+    } else if (fuse_gu) {       // rmsnorm inside the QKV GEMV
       rc |= qhip_gemv_plain_norm(2, fast, d->x, d->dm, d->g_attn[l], d->eps, d->wqkv[l], d->sqkv[l], d->nqkv,
                                  d->kp_dm, d->qkv, d->bqkv[l]);
     } else {
       rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_attn[l], d->eps, d->qa, d->kp_dm, d->as);
       rc |= qhip_gemv_dec(0, 2, d->qa, d->as, d->wqkv[l], d->sqkv[l], d->nqkv, d->kp_dm, d->qkv, d->bqkv[l], NULL, NULL);
     }
-    if (fa)
+    if (!ly && fa)
       rc |= qhip_fattn(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos, d->rope_sin,
                        1, kd->fa_scratch, d->o, d->obm);
-    else
+    else if (!ly)
       rc |= qhip_attention_rope(d->qkv, kc, vc, dpos, d->H, d->KVH, d->hd, d->max_seq, d->attn_scale, d->rope_cos,
                                 d->rope_sin, d->scores, d->o, d->obm);
     if (fuse_o) {        // o quantized inside the Wo GEMV
@@ -701,6 +716,18 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
 }
 
 static int profiling = 0;
+
+// After a synchronization: a k_attn_layer launch whose blocks could not all be
+// resident at once has set its flag (its results are not to be used).
+static int layer_check(const QDev *d, const char *who) {
+  if (!d->ly_ok) return 0;
+  const int e = qhip_attn_layer_failed(d->ly_sync, d->KVH);
+  if (!e) return 0;
+  fprintf(stderr, "Error: %s: the fused attention launch %s (QLLAMA_NO_ATTN_LAYER=1 selects the separate "
+          "kernels)\n", who, e == 1 ? "timed out waiting for blocks (not resident at once, or not 32 per XCD)"
+                            : e == 2 ? "ran on more than eight XCDs" : "state could not be read");
+  return 1;
+}
 
 // Run `n` steps: a graph replay each, or eager launches while profiling.
 static int run_steps(const QDev *d, KVDev *kd, int n) {
@@ -766,7 +793,8 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
   const QDev *d = (const QDev*)m->dev;
   KVDev *kd = (KVDev*)kv->dev;
   if (stage_inputs(d, kv->len, &token, 1) || run_steps(d, kd, 1) ||
-      qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4) || qhip_sync())
+      qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4) || qhip_sync() ||
+      layer_check(d, "q_llama_decode_step"))
     die("q_llama_decode_step");
   kv->len += 1;
 }
@@ -872,7 +900,7 @@ int q_llama_prefill(const QLlamaModel *m, LlamaKV *kv, const int *ids, int n, Te
     if (stage_inputs(d, kv->len, ids, n) || run_steps(d, kd, n)) return 1;
   }
   if (logits && qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4)) return 1;
-  if (qhip_sync()) return 1;
+  if (qhip_sync() || layer_check(d, "q_llama_prefill")) return 1;
   kv->len += n;
   return 0;
 }
@@ -885,7 +913,7 @@ int q_llama_generate_greedy(const QLlamaModel *m, LlamaKV *kv, int token, int n_
   const int pos = kv->len;
   if (stage_inputs(d, pos, &token, 1) || run_steps(d, kd, n_steps)) return 1;
   if (out && qhip_d2h_async(d->h_stage, d->d_out + pos, (size_t)n_steps * sizeof(int))) return 1;
-  if (qhip_sync()) return 1;
+  if (qhip_sync() || layer_check(d, "q_llama_generate_greedy")) return 1;
   if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
   kv->len += n_steps;
   return 0;
@@ -1376,7 +1404,7 @@ int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float tempe
   if (run_sampled_steps(d, kd, n_steps, temperature, top_k, top_p)) return 1;
   if (qhip_d2h_async(g_smp.h, g_smp.rng, 8)) return 1;
   if (out && qhip_d2h_async(d->h_stage, d->d_out + pos - 1, (size_t)n_steps * sizeof(int))) return 1;
-  if (qhip_sync()) return 1;
+  if (qhip_sync() || layer_check(d, "q_llama_generate")) return 1;
   if (out) memcpy(out, d->h_stage, (size_t)n_steps * sizeof(int));
   rng->state = g_smp.h[0];
   kv->len += n_steps;
@@ -1509,6 +1537,10 @@ int qllama_h2d(void *dst, const void *src, size_t bytes) { return qhip_h2d(dst, 
 int qllama_d2h(void *dst, const void *src, size_t bytes) { return qhip_sync() || qhip_d2h(dst, src, bytes); }
 int qllama_device_sync(void) { return qhip_device_sync(); }
 int qllama_sync(void) { return qhip_sync(); }
+
+// 1 when the model's exact decode steps run the attention half of each layer in
+// one launch (qhip_attn_layer), 0 when they run the separate kernels.
+int qllama_attn_layer_active(const QLlamaModel *m) { return m && m->dev && ((const QDev*)m->dev)->ly_ok; }
 void *qllama_stream(void) { return qhip_init() ? NULL : qhip_stream(); }
 int qllama_profile(int enable) { profiling = enable ? 1 : 0; return qhip_profile_enable(enable); }
 int qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max) {

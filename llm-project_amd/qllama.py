@@ -155,6 +155,8 @@ def lib():
             [P(C.c_float), P(C.c_float), P(C.c_double)]
         L.qllama_pf_attention_ex.argtypes = [P(C.c_float)] * 3 + [C.c_int] * 7 + [P(C.c_float), P(C.c_double)]
         L.qllama_sync.restype = C.c_int
+        L.qllama_attn_layer_active.argtypes = [P(QLlamaModel)]
+        L.qllama_attn_layer_active.restype = C.c_int
         L.qllama_stream.restype = C.c_void_p
         L.qllama_profile.argtypes = [C.c_int]
         L.qllama_profile_read.argtypes = [C.c_char_p, C.c_int, P(C.c_double), P(C.c_longlong), C.c_int]
@@ -217,6 +219,11 @@ class Model:
 
     def hash(self):
         return int(lib().q_llama_model_hash(C.byref(self.m)))
+
+    def attn_layer_active(self):
+        """Whether the exact decode steps run each layer's attention half
+        (QKV, RoPE, cache append, scores, softmax, PV) as one launch."""
+        return bool(lib().qllama_attn_layer_active(C.byref(self.m)))
 
     def step(self, token):
         lib().q_llama_decode_step(C.byref(self.m), C.byref(self.kv), int(token), C.byref(self._lt))

@@ -44,8 +44,10 @@ CONFIGS = {
 # (unit, kernel id) -> name, in the order the layer runs them; events per kernel
 LAYER = [
     (("gemv", 0), "gemv_qkv (k_gemv_ws, rmsnorm prologue)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
-    (("attn", 0), "attn_scores (k_attn_scores)", {1: "K tile + q in LDS"}),
-    (("attn", 1), "attn_pv (k_attn_pv)", {1: "block maxima", 2: "exact sum", 3: "weights in LDS", 5: "chains end"}),
+    (("attn", 3), "attn_layer Q phase (QKV rows of one KV head)",
+     {1: "prologue done", 2: "first row (weights in)", 3: "rows stored", 5: "at the meeting"}),
+    (("attn", 0), "attn_scores (k_attn_scores; S phase of k_attn_layer)", {1: "K tile + q in LDS"}),
+    (("attn", 1), "attn_pv (k_attn_pv; P phase of k_attn_layer)", {1: "block maxima", 2: "exact sum", 3: "weights in LDS", 5: "chains end"}),
     (("gemv", 1), "gemv_o (k_gemv_ws, quantizes o)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("gemv", 2), "gemv_gate_up (k_gemv_ws, rmsnorm prologue)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("gemv", 7), "quant_h (k_quant_blocks)", {}),
@@ -127,9 +129,23 @@ def main():
     prompt = [int(t) for t in np.random.default_rng(1234).integers(0, cfg[0], P)]
     m.prefill(prompt, want_logits=True)
     tok = int(np.argmax(m.logits[0]))
-    m.generate_greedy(tok, a.steps)
+    failed = None
+    try:
+        m.generate_greedy(tok, a.steps)
+    except RuntimeError as e:       # the stamps still tell where the blocks ran
+        failed = str(e)
     L.qllama_device_sync()
     bufs = {u: read(L, u) for u in ("gemv", "attn")}
+    ly = bufs["attn"][3]
+    ran = ly[:, 0] > 0
+    if ran.any():
+        nb = int(ran.sum())
+        xcc = (ly[:nb, 7] >> 16) & 0xF
+        off = [int(b) for b in range(nb) if int(xcc[b]) != b % 8]
+        print(f"k_attn_layer: {nb} blocks; {len(off)} not on XCD block % 8"
+              + (f" (block: XCD {', '.join(f'{b}: {int(xcc[b])}' for b in off[:24])})" if off else ""))
+    if failed:
+        sys.exit(f"timeline: {failed}")
     ctx = P + a.steps
     layer = summarize(bufs, LAYER)
     # the PV chain rate: shader-clock cycles (kernel id 2) and wall time (kernel id 1)

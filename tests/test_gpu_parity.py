@@ -4,6 +4,8 @@ the north-star tolerance (max-abs 1e-3, relative 1e-4) -- and reported when they
 are bit-exact, which is what this implementation aims for."""
 import sys
 
+import os
+
 import numpy as np
 import pytest
 
@@ -128,15 +130,30 @@ def test_prefill_in_pieces_equals_whole_prompt(Q):
         m.close()
 
 
-def _big_prefill(Q, name):
+def _synth_layer_path(Q, meta, fused):
+    """The fixture's model, with the attention half of each decode layer as one
+    launch (fused) or as separate kernels (QLLAMA_NO_ATTN_LAYER at creation)."""
+    if fused:
+        return Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    os.environ["QLLAMA_NO_ATTN_LAYER"] = "1"
+    try:
+        return Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    finally:
+        del os.environ["QLLAMA_NO_ATTN_LAYER"]
+
+
+def _big_prefill(Q, name, fused=True):
     """The whole prompt through the batched (MFMA) prefill, then device greedy
     decoding: last prompt logits, the token stream and the final logits equal
     the reference's."""
     if not have_golden(f"e2e_{name}.json") or not have_golden(f"e2e_{name}_logits_prompt_last.npy"):
         pytest.skip(f"{name} fixture not generated")
     meta = golden_json(f"e2e_{name}")
-    m = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
+    m = _synth_layer_path(Q, meta, fused)
     try:
+        log(f"{name}: attention half of each decode layer in one launch: {m.attn_layer_active()}")
+        if name == "8b":      # the shape the one-launch path serves
+            assert m.attn_layer_active() == fused
         log(f"{name}: batched prefill of {len(meta['prompt'])} tokens")
         lg = m.prefill(meta["prompt"]).copy()
         ref = golden(f"e2e_{name}_logits_prompt_last")
@@ -159,8 +176,9 @@ def test_e2e_1b_batched_prefill_matches_reference(Q):
     _big_prefill(Q, "1b")
 
 
-def test_e2e_8b_batched_prefill_matches_reference(Q):
-    _big_prefill(Q, "8b")
+@pytest.mark.parametrize("path", ["one_launch", "separate"])
+def test_e2e_8b_batched_prefill_matches_reference(Q, path):
+    _big_prefill(Q, "8b", fused=path == "one_launch")
 
 
 # Batched prefill over head groupings G = H/KVH, head sizes and cache lengths
@@ -393,6 +411,9 @@ def _big_e2e(Q, name):
     m = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
     try:
         assert m.hash() == int(meta["model_hash"], 16)
+        log(f"{name}: attention half of each decode layer in one launch: {m.attn_layer_active()}")
+        if name == "8b":
+            assert m.attn_layer_active()
         log(f"{name}: weights match; decoding {len(meta['argmax'])} steps")
         gen, exact = _run_steps(m, meta)
         final = m.logits[0].copy()
