@@ -527,6 +527,9 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
 // than 32 blocks), sets an error flag, which the host reports as an error; the
 // block goes on, so the kernel always ends.
 // ---------------------------------------------------------------------------
+#ifndef QLLAMA_LY_L2_COUNTER
+#define QLLAMA_LY_L2_COUNTER 1
+#endif
 constexpr int kLyNB = 32;                   // blocks per KV head
 constexpr int kLyThreads = 512;
 constexpr int kLyWaves = kLyThreads / 64;
@@ -549,7 +552,12 @@ __device__ __forceinline__ void ly_meet(unsigned *ctr, unsigned *err, int tk = -
   __syncthreads();
   if (threadIdx.x == 0) {
     if (tk >= 0) QTL_MARK(tk, 5);
+#if QLLAMA_LY_L2_COUNTER
+    // every block of the meeting runs on this XCD: its L2 performs the add
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#else
     const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
     const unsigned target = old - old % kLyNB + kLyNB;
     for (unsigned n = 0;; n++) {
       const unsigned c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -674,6 +682,9 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     qd::rmsnorm_load<CMQ>(x, dm, gain, y, gm);
     __builtin_amdgcn_sched_barrier(0);
     if (lane == 0) __hip_atomic_fetch_add(&ly_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#if QLLAMA_TIMELINE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");            // (stamped builds only) x has arrived
+    if (wave == 0) QTL_MARK(3, 6);
     const float as = qd::rmsnorm_apply<NTP, CMQ>(x, dm, eps, y, gm, red, seq, gs);
     const float inv = 1.0f / as;
 #pragma unroll
@@ -718,6 +729,7 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     }
     if (rw == 0) QTL_MARK(3, 3);
   }
+#endif
   if (pv) pv_v_start(vpre, vc, kvh, HD, max_seq, pslice * kChains, (T + kTile - 1) / kTile);
   if (tid < 32) tab[tid] = tabv;                               // published by the meeting
   ly_meet(sync + (0 * KVH + kvh) * 64, err, 3);                  // also: this block's K rows are in LDS

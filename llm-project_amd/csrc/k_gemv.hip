@@ -267,15 +267,23 @@ constexpr bool kUseWs = QLLAMA_GEMV_WS != 0;     // the prologue GEMVs run k_gem
 #ifndef QLLAMA_WS_SLOTS_RESID
 #define QLLAMA_WS_SLOTS_RESID 8
 #endif
+#ifndef QLLAMA_WS_RWV_LONG
+#define QLLAMA_WS_RWV_LONG 6
+#endif
+#ifndef QLLAMA_WS_PW_LONG
+#define QLLAMA_WS_PW_LONG 2
+#endif
 constexpr int ws_pro_waves(int mode, int kch) {
   return mode == MODE_PLAIN ? QLLAMA_WS_PW_PLAIN
          : mode == MODE_SWIGLU ? QLLAMA_WS_PW_SWIGLU
-         : QLLAMA_WS_PW_RESID;
+         : kch > 8 ? QLLAMA_WS_PW_LONG : QLLAMA_WS_PW_RESID;
 }
 constexpr int ws_row_waves(int mode, int kch) {
+  // long rows (the down projection's 14336 bytes): 2 prologue and 6 row waves
+  // holding two rows each (eight waves: 256 registers a wave)
   return mode == MODE_PLAIN ? QLLAMA_WS_RWV_PLAIN
          : mode == MODE_SWIGLU ? QLLAMA_WS_RWV_SWIGLU
-         : kch > 8 ? 4 : QLLAMA_WS_RWV_RESID;      // long rows: two rows in flight need the registers of 2 waves/SIMD
+         : kch > 8 ? QLLAMA_WS_RWV_LONG : QLLAMA_WS_RWV_RESID;
 }
 // slots x KCH (16-byte chunks per lane and row) is the register budget
 constexpr int ws_slots(int mode, int kch) {
@@ -299,8 +307,9 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
   __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (wave == 0) QTL_MARK(MODE, 0);
-  QTL_ID(MODE);
+  constexpr int TK = MODE == MODE_RESID && KCH > 8 ? 5 : MODE;   // timeline id: the down projection apart
+  if (wave == 0) QTL_MARK(TK, 0);
+  QTL_ID(TK);
   if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; issued = 0u; }
   __syncthreads();
   if (wave < PW) {
@@ -325,6 +334,10 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
       constexpr int NQ = (KCH * 64 + NTP - 1) / NTP;   // 16-value chunks per thread
       float qx[NQ][16], qm = 0.0f;
       pro1_load<KCH, NQ, NTP>(v, n, vbm, nvbm, qx, qm);
+      if constexpr (KCH > 8) {                           // inputs requested: the row waves may start
+        __builtin_amdgcn_sched_barrier(0);
+        if (lane == 0) __hip_atomic_fetch_add(&issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       float mx = qd::wave_max_f32(qm);
       if (lane == 0) red[wave] = mx;
       gs();
@@ -346,7 +359,7 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
       }
     }
     if (threadIdx.x == 0) as_sh = as;
-    if (wave == 0) QTL_MARK(MODE, 1);
+    if (wave == 0) QTL_MARK(TK, 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's bytes (and as) have landed
     if (lane == 0) __hip_atomic_fetch_add(&ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return;
@@ -354,10 +367,14 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   // ---- the row waves ----
   const int rw = wave - PW;
   const int j0 = (blockIdx.x * RWV + rw) * RW;
-  if constexpr (PRO == 2) {
-    // the exact rmsnorm's inputs are requested before any weight, so that they
-    // do not queue behind the weight stream (its long prologue is the kernel's
-    // critical path; the shorter ones gain nothing from the wait)
+#ifndef QLLAMA_WS_LONG_WAIT
+#define QLLAMA_WS_LONG_WAIT 1
+#endif
+  if constexpr (PRO == 2 || (KCH > 8 && QLLAMA_WS_LONG_WAIT)) {
+    // the prologue's inputs are requested before any weight, so that they do
+    // not queue behind the weight stream: for the exact rmsnorm (its long
+    // prologue is the kernel's critical path) and for long rows (57 KB of
+    // activations per block); the short quantization prologues gain nothing
     while (__hip_atomic_load(&issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW) {
     }
   }
@@ -372,7 +389,7 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   while (__hip_atomic_load(&ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)PW) {
   }
   asm volatile("" ::: "memory");
-  if (rw == 0) QTL_MARK(MODE, 2);
+  if (rw == 0) QTL_MARK(TK, 2);
   // the activation in registers, or (long rows) read from LDS at each row
   constexpr bool A_LDS = KCH > 8;
   v4i a[A_LDS ? 1 : KCH];
@@ -426,11 +443,11 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
             else out[j] = bias ? c + bias[j] : c;
           }
         }
-        if (rw == 0 && r == 0) QTL_MARK(MODE, 3);
+        if (rw == 0 && r == 0) QTL_MARK(TK, 3);
       }
     }
   }
-  QTL_MAX(MODE, 4);
+  QTL_MAX(TK, 4);
   if (MODE == MODE_SWIGLU) {       // the block's max |h|: the last row wave to finish writes it
     if (lane == 0) hred[rw] = hmax;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");

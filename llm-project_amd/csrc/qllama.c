@@ -700,10 +700,10 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
       rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
     }
     // h is quantized by its own kernel: quantizing the d_ff values inside the
-    // down GEMV (qhip_gemv_resid_q) measured slower end to end, 2.5% with every
-    // wave quantizing and 3.6% with prologue waves beside four row waves per CU
-    // (at 14336 bytes a row, two rows in flight need the registers of two waves
-    // per SIMD, too few requests for the stream)
+    // down GEMV (qhip_gemv_resid_q: prologue waves beside row waves holding the
+    // 14336-byte rows) measured 0.4-3.6% slower end to end at the 8B shape in
+    // every wave layout tried; the prologue's 57 KB of h per block and the fewer
+    // rows in flight cost more than the kernel boundary it saves
     rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, nbh, d->qa, d->kp_ff, d->as);
     rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
   }

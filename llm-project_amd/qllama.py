@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqllama.so")
+# QLLAMA_LIB selects another build of the same library (a variant for an A/B run)
+LIB_PATH = os.environ.get("QLLAMA_LIB") or os.path.join(HERE, "libqllama.so")
 
 QT_LAYOUT_NK = 0
 QT_LAYOUT_KN = 1

@@ -45,13 +45,14 @@ CONFIGS = {
 LAYER = [
     (("gemv", 0), "gemv_qkv (k_gemv_ws, rmsnorm prologue)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("attn", 3), "attn_layer Q phase (QKV rows of one KV head)",
-     {1: "prologue done", 2: "first row (weights in)", 3: "rows stored", 5: "at the meeting"}),
+     {6: "x arrived", 1: "prologue done", 2: "first row (weights in)", 3: "rows stored", 5: "at the meeting"}),
     (("attn", 0), "attn_scores (k_attn_scores; S phase of k_attn_layer)", {1: "K tile + q in LDS"}),
     (("attn", 1), "attn_pv (k_attn_pv; P phase of k_attn_layer)", {1: "block maxima", 2: "exact sum", 3: "weights in LDS", 5: "chains end"}),
     (("gemv", 1), "gemv_o (k_gemv_ws, quantizes o)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("gemv", 2), "gemv_gate_up (k_gemv_ws, rmsnorm prologue)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("gemv", 7), "quant_h (k_quant_blocks)", {}),
     (("gemv", 4), "gemv_down (k_gemv_dec)", {}),
+    (("gemv", 5), "gemv_down (k_gemv_ws, quantizes h)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
 ]
 
 
