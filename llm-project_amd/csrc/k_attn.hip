@@ -685,6 +685,7 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
 #if QLLAMA_TIMELINE
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");            // (stamped builds only) x has arrived
     if (wave == 0) QTL_MARK(3, 6);
+#endif
     const float as = qd::rmsnorm_apply<NTP, CMQ>(x, dm, eps, y, gm, red, seq, gs);
     const float inv = 1.0f / as;
 #pragma unroll
@@ -729,7 +730,6 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     }
     if (rw == 0) QTL_MARK(3, 3);
   }
-#endif
   if (pv) pv_v_start(vpre, vc, kvh, HD, max_seq, pslice * kChains, (T + kTile - 1) / kTile);
   if (tid < 32) tab[tid] = tabv;                               // published by the meeting
   ly_meet(sync + (0 * KVH + kvh) * 64, err, 3);                  // also: this block's K rows are in LDS
