@@ -70,7 +70,8 @@ typedef struct {
 
 // checkpoint.c:129-174  Read a 'GPTC' v2 checkpoint into a host GPT.
 int gpt_load(const char *path, GPT *out);
-// checkpoint.c:62-112  Write one (same byte order; written in place, not via a temp file).
+// checkpoint.c:62-112  Write one (same byte order), through path.tmp renamed
+// over path only once complete: a failed save leaves an existing file intact.
 int gpt_save(const char *path, const GPT *m);
 // model.c:95-122 (gpt_free): the host model's memory
 void gpt_free(GPT *m);

@@ -200,10 +200,15 @@ int q_llama_generate(const QLlamaModel *m, LlamaKV *kv, int n_steps, float tempe
 // Decode modes of a KV cache, chosen when it is created.
 #define QLLAMA_MODE_EXACT 0  // every float sum in the reference's order: logits bit-identical to llama.c:528-600
 #define QLLAMA_MODE_FAST  1  // split-K attention with an online-softmax merge and tree-ordered rmsnorm sums;
-                             // the integer GEMV arithmetic is unchanged (greedy streams equal, logits within
-                             // max-abs 1e-3 / relative 1e-4 of the reference on the committed fixtures)
+                             // the integer GEMV arithmetic is unchanged.  NOT the reference's arithmetic:
+                             // a reordered sum moves an activation by an ulp, which can flip an int8 code
+                             // of the per-row quantizer, and from there the greedy stream departs (measured
+                             // on the 1B and 8B fixtures: 194 of 256 and 289 of 512 tokens equal, logits
+                             // outside max-abs 1e-3 / relative 1e-4 from the first step)
 // q_llama_kv_create (llama.c:513-526) with a decode mode; every entry point that
-// takes the cache then decodes in that mode (prompt ingestion stays exact).
+// takes the cache then decodes in that mode.  Prompt ingestion on a fast cache
+// runs the batched prefill with fp32 MFMA prompt attention (an online softmax,
+// not the reference's order) at head_dim 64 and 128; its GEMMs stay exact.
 LlamaKV q_llama_kv_create_mode(const QLlamaModel *m, int mode);
 
 // Prompt ingestion: n tokens at positions kv->len .. kv->len+n-1.  Same result

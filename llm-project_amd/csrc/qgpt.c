@@ -147,9 +147,29 @@ int gpt_load(const char *path, GPT *out) {
   return 0;
 }
 
+// Moves the finished temporary file over dst (checkpoint.c:56-60: where rename
+// cannot replace an existing file, remove it first).
+static int replace_file(const char *tmp, const char *dst) {
+  if (rename(tmp, dst) == 0) return 0;
+  remove(dst);
+  return rename(tmp, dst);
+}
+
+// checkpoint.c:62-103: the bytes go to path.tmp, which is flushed, closed and
+// only then renamed over path, so a failed or interrupted save leaves an
+// existing checkpoint at path untouched.
 int gpt_save(const char *path, const GPT *m) {
-  FILE *f = fopen(path, "wb");
-  if (!f) { fprintf(stderr, "Error: cannot open '%s' for writing\n", path); return 1; }
+  const size_t pl = strlen(path);
+  char *tmp = (char*)malloc(pl + 5);
+  if (!tmp) { fprintf(stderr, "Error: out of memory saving '%s'\n", path); return 1; }
+  memcpy(tmp, path, pl);
+  memcpy(tmp + pl, ".tmp", 5);
+  FILE *f = fopen(tmp, "wb");
+  if (!f) {
+    fprintf(stderr, "Error: cannot open '%s' for writing\n", tmp);
+    free(tmp);
+    return 1;
+  }
   const uint32_t header[2] = {GPTC_MAGIC, GPTC_VERSION};
   const int32_t cfg[6] = {m->vocab_size, m->d_model, m->n_heads, m->n_layers, m->d_ff, m->max_seq_len};
   int ok = fwrite(header, sizeof(uint32_t), 2, f) == 2 && fwrite(cfg, sizeof(int32_t), 6, f) == 6;
@@ -158,8 +178,16 @@ int gpt_save(const char *path, const GPT *m) {
   const int n = ok ? gpt_list(m, list) : 0;
   for (int i = 0; i < n && ok; i++) ok = fwrite(list[i]->data, sizeof(float), list[i]->size, f) == list[i]->size;
   free(list);
-  if (fclose(f) != 0) ok = 0;
-  if (!ok) { fprintf(stderr, "Error: failed while writing '%s'\n", path); return 1; }
+  if (fflush(f) != 0) ok = 0;
+  if (fclose(f) != 0) ok = 0;          // deferred write errors (a full disk) surface here
+  if (ok) ok = replace_file(tmp, path) == 0;
+  if (!ok) {
+    remove(tmp);
+    fprintf(stderr, "Error: failed while writing '%s'\n", path);
+    free(tmp);
+    return 1;
+  }
+  free(tmp);
   return 0;
 }
 

@@ -206,6 +206,14 @@ class Model:
             raise RuntimeError(f"q_llama_model_load failed for {path}")
         return cls(m, mode)
 
+    @classmethod
+    def quantize_from(cls, cfg, rope_base, eps, tensors, mode=MODE_EXACT):
+        """q_llama_quantize_from (llama.c:490-511) of a host fp32 LlamaModel given
+        as (name, array) pairs in the canonical LLMA order (llama.c:198-219)."""
+        host = host_model(cfg, rope_base, eps, tensors)
+        m = lib().q_llama_quantize_from(C.byref(host))
+        return cls(m, mode)
+
     def fork(self, mode):
         """A second cache (q_llama_kv_create_mode) on this model's device weights;
         close it before the model."""

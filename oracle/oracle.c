@@ -454,6 +454,34 @@ int or_model_synth(OrModel *m, const int32_t cfg[8], float rope_base, float eps,
   return 0;
 }
 
+// llama.c:490-511 (q_llama_quantize_from): the int8 model of an fp32 model:
+// every matrix quantized per column (quant.c:10-27), norms and biases copied.
+int or_model_quantize_from(OrModel *m, const OrFModel *f) {
+  const int32_t cfg[8] = {f->vocab, f->d_model, f->n_layers, f->n_heads, f->n_kv, f->head_dim, f->d_ff, f->max_seq};
+  if (or_model_alloc(m, cfg, f->rope_base, f->eps)) return 1;
+  const int dm = m->d_model, qd = m->n_heads * m->head_dim, kvd = m->n_kv * m->head_dim;
+  or_quantize_int8_percol(f->wte, m->vocab, dm, m->wte.q, m->wte.scale);
+  for (int l = 0; l < m->n_layers; l++) {
+    const OrFBlock *a = &f->blocks[l];
+    OrBlock *b = &m->blocks[l];
+    memcpy(b->attn_norm, a->attn_norm, (size_t)dm * sizeof(float));
+    memcpy(b->ffn_norm, a->ffn_norm, (size_t)dm * sizeof(float));
+    memcpy(b->b_q, a->b_q, (size_t)qd * sizeof(float));
+    memcpy(b->b_k, a->b_k, (size_t)kvd * sizeof(float));
+    memcpy(b->b_v, a->b_v, (size_t)kvd * sizeof(float));
+    or_quantize_int8_percol(a->Wq, dm, qd, b->Wq.q, b->Wq.scale);
+    or_quantize_int8_percol(a->Wk, dm, kvd, b->Wk.q, b->Wk.scale);
+    or_quantize_int8_percol(a->Wv, dm, kvd, b->Wv.q, b->Wv.scale);
+    or_quantize_int8_percol(a->Wo, qd, dm, b->Wo.q, b->Wo.scale);
+    or_quantize_int8_percol(a->Wgate, dm, m->d_ff, b->Wgate.q, b->Wgate.scale);
+    or_quantize_int8_percol(a->Wup, dm, m->d_ff, b->Wup.q, b->Wup.scale);
+    or_quantize_int8_percol(a->Wdown, m->d_ff, dm, b->Wdown.q, b->Wdown.scale);
+  }
+  memcpy(m->final_norm, f->final_norm, (size_t)dm * sizeof(float));
+  or_quantize_int8_percol(f->lm_head, dm, m->vocab, m->lm_head.q, m->lm_head.scale);
+  return 0;
+}
+
 static uint64_t qt_hash(const OrQT *t, uint64_t salt) {
   return syn_hash_i8(t->q, (size_t)t->rows * t->cols, salt) * 3 +
          syn_hash_f32(t->scale, (size_t)t->cols, salt ^ 0x5CA1E5ULL);

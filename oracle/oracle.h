@@ -95,6 +95,8 @@ int  or_fmodel_synth(OrFModel *m, const int32_t cfg[8], float rope_base, float e
 void or_fmodel_free(OrFModel *m);
 int  or_fkv_create(OrKV *kv, const OrFModel *m);
 void or_f32_decode_step(const OrFModel *m, OrKV *kv, int token, float *logits);
+// llama.c:490-511: the int8 model of an fp32 model (allocates m).
+int  or_model_quantize_from(OrModel *m, const OrFModel *f);
 
 // Bitwise mismatches of got[i] against the host libm expf at bit pattern start+i.
 long long or_expf_mismatches(uint32_t start, uint32_t count, const float *got);

@@ -20,6 +20,9 @@
 //                                  decode (gpt_decode_step, model.c:457-520)
 //   gen_golden <outdir> gpthash <file>   load a GPTC file with gpt_load and print
 //                                  its digest
+//   gen_golden <outdir> qfrom      q_llama_quantize_from of two fp32 models (one at
+//                                  selftest [21]'s shape, one with gains and
+//                                  biases), and their decode steps
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -705,6 +708,84 @@ static void run_gpt(const GCase *c) {
   free(seq); free(lh); tensor_free(&logits); gpt_kvcache_free(&kv); gpt_free(&m);
 }
 
+// ---------------------------------------------------------------------------
+// q_llama_quantize_from (llama.c:490-511): an fp32 model from the generator
+// quantized by the reference, then its decode steps.  Tensor ids: the fp32
+// path's (build_fmodel), plus gains 1 + N(0, g) and biases N(0, b) at ids
+// 1000 + 8 l + {0 attn_norm, 1 b_q, 2 b_k, 3 b_v, 4 ffn_norm} and 999 for the
+// final norm; lm_head's column 5 is zeroed (an all-zero column: scale 1).
+// ---------------------------------------------------------------------------
+typedef struct { const char *name; int32_t cfg[8]; float gsig, bsig; int n_ids; int ids[8]; } QFCase;
+static const QFCase QFCASES[2] = {
+  // selftest [21]'s model shape and token ids (selftest.c:1215-1250)
+  {"selftest21", {32, 8, 2, 4, 2, 2, 16, 64}, 0.0f, 0.0f, 6, {3, 7, 1, 9, 2, 5}},
+  // gains and biases away from 1 and 0, head size 16, three query heads per KV head
+  {"biased", {300, 96, 2, 6, 2, 16, 160, 48}, 0.1f, 0.1f, 8, {11, 290, 7, 3, 150, 42, 99, 0}},
+};
+
+static void qf_fill(Tensor *t, uint64_t tid, double sig, float base) {
+  syn_fill(t->data, t->size, 21, tid, sig > 0 ? sig : 0.0);
+  for (size_t i = 0; i < t->size; i++) t->data[i] = sig > 0 ? base + t->data[i] : base;
+}
+
+static void run_qfrom(const QFCase *c) {
+  const int32_t *g = c->cfg;
+  LlamaModel f = llama_model_create(g[0], g[1], g[2], g[3], g[4], g[5], g[6], g[7], 10000.0f, 1e-5f);
+  const int L = g[2];
+  syn_fill(f.wte.data, f.wte.size, 21, 0, 1.0);
+  for (int l = 0; l < L; l++) {
+    LlamaBlock *b = &f.blocks[l];
+    const uint64_t t0 = 1 + 12 * (uint64_t)l, u = 1000 + 8 * (uint64_t)l;
+    syn_fill(b->Wq.data, b->Wq.size, 21, t0 + 1, 0.3);
+    syn_fill(b->Wk.data, b->Wk.size, 21, t0 + 2, 0.3);
+    syn_fill(b->Wv.data, b->Wv.size, 21, t0 + 3, 0.3);
+    syn_fill(b->Wo.data, b->Wo.size, 21, t0 + 7, 0.3);
+    syn_fill(b->Wgate.data, b->Wgate.size, 21, t0 + 9, 0.3);
+    syn_fill(b->Wup.data, b->Wup.size, 21, t0 + 10, 0.3);
+    syn_fill(b->Wdown.data, b->Wdown.size, 21, t0 + 11, 0.3);
+    qf_fill(&b->attn_norm, u + 0, c->gsig, 1.0f);
+    qf_fill(&b->b_q, u + 1, c->bsig, 0.0f);
+    qf_fill(&b->b_k, u + 2, c->bsig, 0.0f);
+    qf_fill(&b->b_v, u + 3, c->bsig, 0.0f);
+    qf_fill(&b->ffn_norm, u + 4, c->gsig, 1.0f);
+  }
+  qf_fill(&f.final_norm, 999, c->gsig, 1.0f);
+  syn_fill(f.lm_head.data, f.lm_head.size, 21, 2 + 12 * (uint64_t)L, 0.3);
+  for (int k = 0; k < g[1]; k++) f.lm_head.data[(size_t)k * g[0] + 5] = 0.0f;
+
+  QLlamaModel m = q_llama_quantize_from(&f);
+  LlamaKV kv = q_llama_kv_create(&m);
+  Tensor logits = mat(1, m.vocab);
+  const int G = 12, S = c->n_ids + G;
+  float *all = malloc(sizeof(float) * (size_t)S * m.vocab);
+  int seq[32], n = 0;
+  for (int i = 0; i < c->n_ids; i++) {
+    seq[n] = c->ids[i];
+    q_llama_decode_step(&m, &kv, seq[n], &logits);
+    memcpy(all + (size_t)n++ * m.vocab, logits.data, sizeof(float) * m.vocab);
+  }
+  for (int s = 0; s < G; s++) {
+    seq[n] = sample_argmax(&logits, 0);
+    q_llama_decode_step(&m, &kv, seq[n], &logits);
+    memcpy(all + (size_t)n++ * m.vocab, logits.data, sizeof(float) * m.vocab);
+  }
+  char nm[128]; long sv[2] = {S, m.vocab};
+  snprintf(nm, sizeof nm, "qfrom_%s_logits", c->name);
+  npy_f32(nm, all, 2, sv);
+  char path[1024]; snprintf(path, sizeof path, "%s/qfrom_%s.json", OUT, c->name);
+  FILE *js = fopen(path, "w");
+  fprintf(js, "{\n  \"name\": \"%s\", \"seed\": 21, \"cfg\": [%d,%d,%d,%d,%d,%d,%d,%d],\n", c->name, g[0], g[1],
+          g[2], g[3], g[4], g[5], g[6], g[7]);
+  fprintf(js, "  \"rope_base\": 10000.0, \"eps\": 1e-5, \"gain_sigma\": %.2f, \"bias_sigma\": %.2f,\n", c->gsig,
+          c->bsig);
+  fprintf(js, "  \"fp32_hash\": \"%016llx\", \"model_hash\": \"%016llx\",\n  \"tokens\": [",
+          (unsigned long long)fmodel_hash(&f), (unsigned long long)model_hash(&m));
+  for (int i = 0; i < S; i++) fprintf(js, "%s%d", i ? "," : "", seq[i]);
+  fprintf(js, "],\n  \"n_prompt\": %d\n}\n", c->n_ids);
+  fclose(js);
+  free(all); tensor_free(&logits); llama_kv_free(&kv); q_llama_model_free(&m); llama_model_free(&f);
+}
+
 int main(int argc, char **argv) {
   if (argc < 3) { fprintf(stderr, "usage: gen_golden <outdir> ops|gqa8192|sample|e2e <name>\n"); return 2; }
   OUT = argv[1];
@@ -772,6 +853,10 @@ int main(int argc, char **argv) {
     if (gpt_load(argv[3], &m) != 0) return 1;
     printf("%016llx\n", (unsigned long long)gpt_hash(&m));
     gpt_free(&m);
+    return 0;
+  }
+  if (!strcmp(argv[2], "qfrom")) {
+    for (int i = 0; i < 2; i++) run_qfrom(&QFCASES[i]);
     return 0;
   }
   if (!strcmp(argv[2], "e2e") && argc > 3) {

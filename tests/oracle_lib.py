@@ -99,6 +99,7 @@ def lib():
         L.or_model_synth.argtypes = [C.POINTER(OrModel), C.POINTER(C.c_int32), C.c_float, C.c_float,
                                      C.c_uint64, C.c_int]
         L.or_model_alloc.argtypes = [C.POINTER(OrModel), C.POINTER(C.c_int32), C.c_float, C.c_float]
+        L.or_model_quantize_from.argtypes = [C.POINTER(OrModel), C.POINTER(OrFModel)]
         L.or_model_free.argtypes = [C.POINTER(OrModel)]
         L.or_model_hash.argtypes = [C.POINTER(OrModel)]
         L.or_model_hash.restype = C.c_uint64
@@ -171,6 +172,50 @@ def prompt(n, seed, vocab):
     ids = (C.c_int * n)()
     lib().syn_prompt(ids, n, seed, vocab)
     return list(ids)
+
+
+def qfrom_tensors(cfg, gain_sigma, bias_sigma, seed=21):
+    """The fp32 model of the quantize_from fixtures (tests/golden/gen_golden.c
+    run_qfrom), as (name, array) pairs in the canonical LLMA order
+    (llama.c:198-219): generator weights N(0, 0.3), embeddings N(0, 1), gains
+    1 + N(0, g) and biases N(0, b) (1 and 0 when the sigma is 0), lm_head's
+    column 5 zero."""
+    V, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+
+    def fill(shape, tid, sigma, base=0.0):
+        n = int(np.prod(shape))
+        if sigma <= 0:
+            return np.full(shape, base, np.float32)
+        # the fixture generator keeps sigma as a float32 (0.1f) and widens it
+        return (np.float32(base) + synth(n, seed, tid, float(np.float32(sigma)))).reshape(shape).astype(np.float32)
+
+    out = [("wte", synth(V * dm, seed, 0, 1.0).reshape(V, dm))]
+    for l in range(L):
+        t0, u = 1 + 12 * l, 1000 + 8 * l
+        out += [("attn_norm", fill((dm,), u, gain_sigma, 1.0)),
+                ("Wq", synth(dm * qd, seed, t0 + 1, 0.3).reshape(dm, qd)),
+                ("Wk", synth(dm * kvd, seed, t0 + 2, 0.3).reshape(dm, kvd)),
+                ("Wv", synth(dm * kvd, seed, t0 + 3, 0.3).reshape(dm, kvd)),
+                ("b_q", fill((qd,), u + 1, bias_sigma)), ("b_k", fill((kvd,), u + 2, bias_sigma)),
+                ("b_v", fill((kvd,), u + 3, bias_sigma)),
+                ("Wo", synth(qd * dm, seed, t0 + 7, 0.3).reshape(qd, dm)),
+                ("ffn_norm", fill((dm,), u + 4, gain_sigma, 1.0)),
+                ("Wgate", synth(dm * ff, seed, t0 + 9, 0.3).reshape(dm, ff)),
+                ("Wup", synth(dm * ff, seed, t0 + 10, 0.3).reshape(dm, ff)),
+                ("Wdown", synth(ff * dm, seed, t0 + 11, 0.3).reshape(ff, dm))]
+    head = synth(dm * V, seed, 2 + 12 * L, 0.3).reshape(dm, V)
+    head[:, 5] = 0.0
+    return out + [("final_norm", fill((dm,), 999, gain_sigma, 1.0)), ("lm_head", head)]
+
+
+def tensors_hash(tensors):
+    """The fixtures' fp32 digest: h = h*31 + hash of each tensor, canonical order."""
+    h = 0
+    for i, (_, t) in enumerate(tensors):
+        d = hash_f32(t)
+        h = d if i == 0 else (h * 31 + d) & 0xFFFFFFFFFFFFFFFF
+    return h
 
 
 def hash_f32(a):
@@ -492,6 +537,42 @@ class Model:
             raise MemoryError("oracle kv allocation failed")
         self.vocab = cfg[0]
         self.logits = np.zeros(self.vocab, np.float32)
+
+    @classmethod
+    def quantize_from(cls, cfg, rope_base, eps, tensors):
+        """llama.c:490-511 on an fp32 model given as (name, array) pairs in the
+        canonical LLMA order (llama.c:198-219): the oracle's int8 model."""
+        self = cls.__new__(cls)
+        keep = []
+
+        def P(a):
+            a = np.ascontiguousarray(a, np.float32)
+            keep.append(a)
+            return fptr(a)
+
+        f = OrFModel()
+        (f.vocab, f.d_model, f.n_layers, f.n_heads, f.n_kv, f.head_dim, f.d_ff, f.max_seq) = cfg
+        f.rope_base, f.eps = rope_base, eps
+        it = iter(tensors)
+        f.wte = P(next(it)[1])
+        blocks = (OrFBlock * cfg[2])()
+        for l in range(cfg[2]):
+            for name in ("attn_norm", "Wq", "Wk", "Wv", "b_q", "b_k", "b_v", "Wo", "ffn_norm", "Wgate", "Wup", "Wdown"):
+                n, a = next(it)
+                assert n == name, (n, name)
+                setattr(blocks[l], name, P(a))
+        f.blocks = blocks
+        f.final_norm = P(next(it)[1])
+        f.lm_head = P(next(it)[1])
+        self.m = OrModel()
+        if lib().or_model_quantize_from(C.byref(self.m), C.byref(f)) != 0:
+            raise MemoryError("oracle model allocation failed")
+        self.kv = OrKV()
+        if lib().or_kv_create(C.byref(self.kv), C.byref(self.m)) != 0:
+            raise MemoryError("oracle kv allocation failed")
+        self.vocab = cfg[0]
+        self.logits = np.zeros(self.vocab, np.float32)
+        return self
 
     def hash(self):
         return int(lib().or_model_hash(C.byref(self.m)))

@@ -116,6 +116,38 @@ def test_library_gpt_load_and_save(tmp_path):
         assert r.returncode != 0 and msg in r.stderr, (msg, r.stderr)
 
 
+def test_library_gpt_save_replaces_only_when_complete(tmp_path):
+    """checkpoint.c:62-103: gpt_save writes path.tmp and renames it over path,
+    so a save that fails leaves an existing checkpoint byte for byte as it was,
+    and a good save replaces it and leaves no temporary file."""
+    Q = qlib.load()
+    meta = golden_json("gpt_tiny")
+    om = O.GPTModel(meta["cfg"], seed=meta["seed"])
+    src = tmp_path / "tiny.gptc"
+    om.write_gptc(str(src))
+    m = Q.gpt_load(str(src))
+    try:
+        target = tmp_path / "ckpt.gptc"
+        old = b"an existing checkpoint" * 100
+        target.write_bytes(old)
+        (tmp_path / "ckpt.gptc.tmp").mkdir()           # the temporary file cannot be created
+        r = subprocess.run(
+            ["python3", "-c",
+             f"import sys, ctypes; sys.path.insert(0, {os.path.join(ROOT, 'tests')!r}); import qlib; "
+             f"q = qlib.load(); m = q.gpt_load({str(src)!r}); "
+             f"sys.exit(q.lib().gpt_save({str(target).encode()!r}, ctypes.byref(m)))"],
+            capture_output=True, text=True, timeout=120)
+        assert r.returncode != 0 and "cannot open" in r.stderr, r.stderr
+        assert target.read_bytes() == old
+        (tmp_path / "ckpt.gptc.tmp").rmdir()
+        assert Q.lib().gpt_save(os.fsencode(str(target)), C_ref(m)) == 0
+        assert target.read_bytes() == src.read_bytes()
+        assert not (tmp_path / "ckpt.gptc.tmp").exists()
+    finally:
+        Q.lib().gpt_free(C_ref(m))
+        om.close()
+
+
 def C_ref(m):
     import ctypes
     return ctypes.byref(m)

@@ -21,6 +21,8 @@ from conftest import golden, golden_json, have_golden
 
 pytestmark = pytest.mark.gpu
 ATOL, RTOL = 1e-3, 1e-4
+FAST_MEDIAN_MAX_ABS = {"tiny": 3e-5, "1b": 1.0, "8b": 2.7}
+FAST_PREFILL_MAX_ABS = {"tiny": 0.0, "1b": 0.6, "8b": 1.4}   # 2.5x the measured 0.237 and 0.538
 
 
 def log(msg):
@@ -207,6 +209,7 @@ def _fast_vs_reference(Q, name):
     ex = Q.Model.synth(meta["cfg"], meta["rope_base"], seed=meta["seed"], tied=bool(meta["tied"]))
     fa = ex.fork(Q.MODE_FAST)
     max_abs, worst, first_tol, first_div, exact_ok, agree, min_corr = 0.0, -1, None, None, 0, 0, 1.0
+    step_max = []
     try:
         assert ex.hash() == int(meta["model_hash"], 16)
         for i in range(n):
@@ -215,6 +218,7 @@ def _fast_vs_reference(Q, name):
             exact_ok += O.hash_f32(a) == hashes[i]
             d = np.abs(b - a)
             m = float(d.max())
+            step_max.append(m)
             if m > max_abs:
                 max_abs, worst = m, i
             if first_tol is None and not np.all(d <= ATOL + RTOL * np.abs(a)):
@@ -231,8 +235,16 @@ def _fast_vs_reference(Q, name):
     log(f"{name}: {exact_ok}/{n} exact steps hash-equal to the reference; fast mode: first step outside "
         f"atol/rtol {first_tol}, max |d| {max_abs:.3g} (step {worst}), min logit correlation {min_corr:.4f}, "
         f"greedy token equal on {agree}/{len(toks) - P} steps (first difference after step {first_div})")
+    med = float(np.median(step_max))
+    log(f"{name}: median per-step max |d| {med:.3g}")
     assert exact_ok == n
     assert min_corr >= MIN_CORR, f"fast-mode logits decorrelated from the reference ({min_corr:.4f})"
+    # bounds on the departure itself, about 2.5x the medians measured when the
+    # fast mode was characterized (tiny 1.2e-5, 1B 0.41, 8B 1.07): a systematic
+    # error of the fast kernels would exceed them long before the correlation drops
+    assert med <= FAST_MEDIAN_MAX_ABS[name], f"median per-step max |d| {med:.3g}"
+    if name == "tiny":           # its first steps stay inside the north star's tolerance
+        assert first_tol is None or first_tol >= 8, f"first step outside atol/rtol: {first_tol}"
 
 
 def test_fast_e2e_tiny_bounded(Q):
@@ -267,6 +279,7 @@ def test_fast_cache_prefill_bounded(Q, name):
         if meta["cfg"][5] == 48:
             assert bits_equal(lg[:ref.size], ref)
         assert corr >= MIN_CORR
+        assert float(np.max(np.abs(lg[:ref.size] - ref))) <= FAST_PREFILL_MAX_ABS[name]
         first = int(np.argmax(lg))
         out = m.generate_greedy(first, 32)
         assert len(out) == 32 and all(0 <= t < meta["cfg"][0] for t in out)

@@ -441,6 +441,8 @@ def test_e2e_8b_matches_reference(Q):
     (2, 64, 150, 1024, False),     # SwiGLU over 2N weight rows
     (1, 300, 64, 8192, False),     # long K: 256-row tiles, 16 splits
     (2, 17, 700, 4096, False),
+    (0, 24, 6144, 4096, True),     # the 8B QKV at a short prompt: a last split shorter than the others
+    (1, 20, 1024, 14336, False),   # K = 14336 (the down projection's), 224 K steps
 ])
 def test_split_k_gemm_same_bits(Q, mode, M, N, kpad, bias):
     """The prompt GEMM with K split over extra blocks (int32 partial sums, then
@@ -464,6 +466,10 @@ def test_split_k_gemm_same_bits(Q, mode, M, N, kpad, bias):
     p = lambda x: None if x is None else x.ctypes.data_as(C.c_void_p)
     assert f(mode, p(A), p(a_s), p(W), p(w_s), M, N, kpad, p(b), p(o1), p(o2), C.byref(splits)) == 0
     assert splits.value >= 2, "the shape was meant to split K"
+    nkt = (kpad + 63) // 64
+    log(f"split K: {splits.value} splits of {nkt} K steps (last split shorter: {nkt % splits.value != 0})")
+    if (mode, M, N, kpad) == (0, 24, 6144, 4096):
+        assert nkt % splits.value != 0, "this case was meant to have a shorter last split"
     assert o1.tobytes() == o2.tobytes()
     if mode != 2:
         acc = A.astype(np.int64) @ W.astype(np.int64).T
