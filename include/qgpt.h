@@ -79,6 +79,11 @@ void gpt_free(GPT *m);
 KVCache gpt_kvcache_create(const GPT *m);
 // model.c:450-455
 void gpt_kvcache_free(KVCache *kv);
+// (no counterpart: the reference's step reads the host tensors every time)
+// The device copy of the weights is made when the cache is created and again
+// when gpt_decode_step is given a different model; weights changed in place
+// (the same buffers) are seen only after this call.  0 on success.
+int gpt_kvcache_refresh(KVCache *kv, const GPT *m);
 // model.c:457-520  One token at position kv->len; logits (1, vocab) in host memory.
 void gpt_decode_step(const GPT *m, KVCache *kv, int token, Tensor *logits);
 

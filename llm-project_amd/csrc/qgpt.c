@@ -369,6 +369,28 @@ void gpt_kvcache_free(KVCache *kv) {
   kv->len = 0;
 }
 
+// The cache's device copy of m's weights made again from the host model: for a
+// caller that changed weights in place (same buffers), which the step cannot
+// see (it copies only when it is given a different model).  Returns 0 on
+// success.  The cached keys and values are kept.
+int gpt_kvcache_refresh(KVCache *kv, const GPT *m) {
+  GDev *g = kv ? (GDev*)kv->dev : NULL;
+  if (!m || !g) {
+    fprintf(stderr, "Error: gpt_kvcache_refresh: the cache was not made by gpt_kvcache_create\n");
+    return 1;
+  }
+  if (m->vocab_size != g->vocab || m->d_model != g->dm || m->n_heads != g->nh || m->n_layers != g->L ||
+      m->d_ff != g->ff || m->max_seq_len != g->max_seq) {
+    fprintf(stderr, "Error: gpt_kvcache_refresh: the cache was made for a model of another shape\n");
+    return 1;
+  }
+  if (qhip_sync() || gdev_upload(g, m) || qhip_sync()) {
+    fprintf(stderr, "Error: gpt_kvcache_refresh: weight upload failed: %s\n", qhip_last_error());
+    return 1;
+  }
+  return 0;
+}
+
 void gpt_decode_step(const GPT *m, KVCache *kv, int token, Tensor *logits) {
   GDev *g = kv ? (GDev*)kv->dev : NULL;
   if (!m || !g || !logits || !logits->data) {

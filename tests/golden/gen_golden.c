@@ -16,7 +16,7 @@
 //                                  and print its digest
 //   gen_golden <outdir> sample     sample_token draws, and the `llama` command's
 //                                  sampled loop (main.c:658-669) on the tiny model
-//   gen_golden <outdir> gpt <name>  tiny | gpt2s: greedy streams of the GPT-2 KV
+//   gen_golden <outdir> gpt <name>  tiny | gpt2s | long: greedy streams of the GPT-2 KV
 //                                  decode (gpt_decode_step, model.c:457-520)
 //   gen_golden <outdir> gpthash <file>   load a GPTC file with gpt_load and print
 //                                  its digest
@@ -624,9 +624,12 @@ static void fx_cli_f32(FILE *js) {
 // LayerNorm betas N(0, 0.02); gammas 1 + N(0, 0.1).
 // ---------------------------------------------------------------------------
 typedef struct { const char *name; int32_t cfg[6]; int prompt, gen; } GCase;   // vocab, dm, heads, layers, ff, seq
-static const GCase GCASES[2] = {
+static const GCase GCASES[3] = {
   {"tiny", {512, 64, 4, 2, 256, 128}, 48, 48},
   {"gpt2s", {50257, 768, 12, 12, 3072, 1024}, 32, 32},
+  // GPT-2-small's width, heads and context with 2 layers and a short vocabulary,
+  // decoded to position 1000 of its 1024
+  {"long", {2048, 768, 12, 2, 3072, 1024}, 32, 968},
 };
 
 static int gpt_list(GPT *m, Tensor **t) {
@@ -846,7 +849,7 @@ int main(int argc, char **argv) {
     return 0;
   }
   if (!strcmp(argv[2], "gpt") && argc > 3) {
-    for (int i = 0; i < 2; i++) if (!strcmp(argv[3], GCASES[i].name)) { run_gpt(&GCASES[i]); return 0; }
+    for (int i = 0; i < 3; i++) if (!strcmp(argv[3], GCASES[i].name)) { run_gpt(&GCASES[i]); return 0; }
   }
   if (!strcmp(argv[2], "gpthash") && argc > 3) {
     GPT m;

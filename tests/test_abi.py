@@ -28,7 +28,7 @@ def test_header_declares_the_reference_api():
     for ref in ("q_llama_model_load", "q_llama_model_free", "q_llama_quantize_from", "q_llama_kv_create",
                 "llama_kv_free", "q_llama_decode_step", "qtensor_create", "qtensor_free", "qtensor_quantize",
                 "qmatmul", "quantize_int8_percol", "dequantize_int8_percol", "qacc_columns",
-                "gpt_load", "gpt_save", "gpt_free", "gpt_kvcache_create", "gpt_kvcache_free", "gpt_decode_step"):
+                "gpt_load", "gpt_save", "gpt_free", "gpt_kvcache_create", "gpt_kvcache_free", "gpt_kvcache_refresh", "gpt_decode_step"):
         assert ref in names
 
 

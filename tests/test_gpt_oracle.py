@@ -21,7 +21,7 @@ def bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("name", ["tiny", "gpt2s"])
+@pytest.mark.parametrize("name", ["tiny", "gpt2s", "long"])
 def test_gpt_oracle_matches_reference(name):
     meta = golden_json(f"gpt_{name}")
     m = O.GPTModel(meta["cfg"], seed=meta["seed"])

@@ -47,7 +47,7 @@ def _host_model(Q, om):
     return Q.host_gpt(om.cfg, om.tensors())
 
 
-@pytest.mark.parametrize("name", ["tiny", "gpt2s"])
+@pytest.mark.parametrize("name", ["tiny", "gpt2s", "long"])
 def test_gpt_decode_matches_reference(Q, name):
     meta = golden_json(f"gpt_{name}")
     om = O.GPTModel(meta["cfg"], seed=meta["seed"])
@@ -119,3 +119,35 @@ def test_gpt_cache_takes_another_model(Q):
         dec.close()
         a.close()
         b.close()
+
+
+def test_gpt_weights_changed_in_place_need_a_refresh(Q):
+    """The device copy of a cache's weights is made at creation (and when the
+    step is given another model): weights edited in place are not seen until
+    gpt_kvcache_refresh, as INTEGRATION.md documents.  The edit here is the
+    final LayerNorm gain, which leaves the cached keys and values alone, so after
+    the refresh every step equals the oracle's on the edited weights again."""
+    meta = golden_json("gpt_tiny")
+    om = O.GPTModel(meta["cfg"], seed=meta["seed"])          # the host GPT shares its arrays
+    old = O.GPTModel(meta["cfg"], seed=meta["seed"])         # the same weights, never edited
+    dec = Q.GPTDecoder(_host_model(Q, om))
+    try:
+        ids = meta["prompt"][:8]
+        for t in ids[:4]:
+            g = dec.step(t).copy()
+            assert np.array_equal(bits(g), bits(om.step(t))) and np.array_equal(bits(g), bits(old.step(t)))
+        gain = dict(om.tensors())["ln_f_gamma"]
+        gain *= np.float32(1.5)                               # in place: the host GPT sees the same memory
+        assert np.array_equal(dict(Q.gpt_tensors(dec.m))["ln_f_gamma"], gain)
+        g = dec.step(ids[4]).copy()
+        a, b = om.step(ids[4]).copy(), old.step(ids[4]).copy()
+        assert np.array_equal(bits(g), bits(b)) and not np.array_equal(bits(g), bits(a))   # stale copy
+        assert Q.lib().gpt_kvcache_refresh(C.byref(dec.kv), C.byref(dec.m)) == 0
+        for t in ids[5:]:
+            g = dec.step(t).copy()
+            assert np.array_equal(bits(g), bits(om.step(t)))
+            old.step(t)
+    finally:
+        dec.close()
+        om.close()
+        old.close()
