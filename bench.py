@@ -90,11 +90,17 @@ def decode_bytes(cfg, t):
     return w + scales + f32 + kv + dm
 
 
-def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
+def cpu_baseline(Q, gm, cfg, base, pos0, seconds, prefill_tokens=0, prefill_seconds=0.0):
     """The CPU oracle (a C11 restatement of the reference decode step, threaded
-    like the reference) on this host's cores: same weights, exported from the
-    device; the first pos0 cache rows filled with N(0,1); decode steps timed at
-    positions pos0.. until `seconds` of work."""
+    like the reference, matrix.c:110-117) on this host's cores: same weights,
+    exported from the device; cache rows N(0,1) up to pos0.
+
+    decode: steps timed at positions pos0.. until `seconds` of work.
+    prefill (when prefill_tokens > 0): the reference's prompt ingestion is one
+    decode step per token (main.c:662), so its rate is 1 / the mean step time
+    over positions 0 .. prefill_tokens-1; a bounded sample of steps at evenly
+    spaced positions of that range (each from a cache holding the rows before
+    it) until `prefill_seconds` of work."""
     import oracle_lib as O
     nthreads = len(os.sched_getaffinity(0))
     O.lib().or_set_threads(nthreads)
@@ -114,10 +120,11 @@ def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
     kvd = cfg[4] * cfg[5]
     per = cfg[7] * kvd
     rng = np.random.default_rng(7)
+    fill = max(pos0, prefill_tokens)
     for arr_ptr in (om.kv.k, om.kv.v):
         view = np.ctypeslib.as_array(arr_ptr, shape=(L * per,))
         for l in range(L):
-            view[l * per:l * per + pos0 * kvd] = rng.standard_normal(pos0 * kvd, dtype=np.float32)
+            view[l * per:l * per + fill * kvd] = rng.standard_normal(fill * kvd, dtype=np.float32)
     om.reset(pos0)
     om.step(1)                                   # warm-up
     times = []
@@ -128,138 +135,53 @@ def cpu_baseline(Q, gm, cfg, base, pos0, seconds):
         lg = om.step(tok)
         times.append(time.perf_counter() - t0)
         tok = int(np.argmax(lg))
+    pf = None
+    if prefill_tokens > 0:
+        ptimes, positions = [], []
+        t_start = time.perf_counter()
+        for k in range(64):
+            p = (k * 37 % 64) * prefill_tokens // 64          # evenly spaced positions, visited in a spread order
+            om.reset(p)
+            t0 = time.perf_counter()
+            om.step(tok)
+            ptimes.append(time.perf_counter() - t0)
+            positions.append(p)
+            if len(ptimes) >= 4 and time.perf_counter() - t_start >= prefill_seconds:
+                break
+        mean = statistics.mean(ptimes)
+        pf = {"tok_s": round(1.0 / mean, 4), "prompt_tokens": prefill_tokens,
+              "sample": f"{len(ptimes)} decode steps at positions {sorted(positions)[0]}..{sorted(positions)[-1]} "
+                        f"spread over the {prefill_tokens}-token prompt (the reference ingests a prompt one decode "
+                        f"step per token, main.c:662); mean step {mean * 1e3:.2f} ms"}
     om.close()
     med = statistics.median(times)
     cpu_model, libc = host_info()
-    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": nthreads, "kind": "port",
-            "cpu_model": cpu_model, "libc": libc,
-            "sample": f"{len(times)} decode steps at positions {pos0 + 1}..{pos0 + len(times)} of the same "
-                      f"model (weights copied from the GPU, earlier cache rows N(0,1)); median step "
-                      f"{med * 1e3:.1f} ms, oracle/liboracle with {nthreads} threads"}
+    out = {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": nthreads, "kind": "port",
+           "cpu_model": cpu_model, "libc": libc, "lscpu": lscpu_info(),
+           "sample": f"{len(times)} decode steps at positions {pos0 + 1}..{pos0 + len(times)} of the same "
+                     f"model (weights copied from the GPU, earlier cache rows N(0,1)); median step "
+                     f"{med * 1e3:.1f} ms, oracle/liboracle with {nthreads} threads"}
+    if pf:
+        out["prefill"] = pf
+    return out
 
 
-def f32_host_model(Q, cfg, base, tied, seed=1234):
-    """A reference LlamaModel (host f32) with N(0, 0.02) weights from numpy, norms 1,
-    biases 0, in the canonical tensor order (llama.c:198-219)."""
-    vocab, dm, L, H, KVH, hd, ff, _ = cfg
-    qd, kvd = H * hd, KVH * hd
-    rng = np.random.default_rng(seed)
-
-    def w(*shape):
-        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
-
-    one = np.ones(dm, np.float32)
-    wte = w(vocab, dm)
-    t = [("wte", wte)]
-    for _ in range(L):
-        t += [("attn_norm", one), ("Wq", w(dm, qd)), ("Wk", w(dm, kvd)), ("Wv", w(dm, kvd)),
-              ("b_q", np.zeros(qd, np.float32)), ("b_k", np.zeros(kvd, np.float32)), ("b_v", np.zeros(kvd, np.float32)),
-              ("Wo", w(qd, dm)), ("ffn_norm", one), ("Wgate", w(dm, ff)), ("Wup", w(dm, ff)), ("Wdown", w(ff, dm))]
-    t += [("final_norm", one), ("lm_head", np.ascontiguousarray(wte.T) if tied else w(dm, vocab))]
-    return Q.host_model(cfg, base, 1e-5, t)
-
-
-def f32_bytes(cfg, t):
-    """HBM bytes of one fp32 decode token at context t: every weight once (f32),
-    the KV rows read and the new row written."""
-    vocab, dm, L, H, KVH, hd, ff, _ = cfg
-    qd, kvd = H * hd, KVH * hd
-    w = L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab
-    return 4 * w + L * (2 * kvd * 4 * t + 2 * kvd * 4)
-
-
-def main_f32(args, Q, cfg, base, tied, P):
-    """The fp32 (LLMA) decode path: llama_decode_step per token (host logits, as in
-    the reference), after P prompt tokens fed the same way."""
-    W, K, NP = args.warmup, args.steps, args.profile_steps
-    if P + W + K + NP > cfg[7]:
-        sys.exit("bench.py: prompt + warmup + steps + profile exceeds max_seq")
-    t0 = time.perf_counter()
-    host = f32_host_model(Q, cfg, base, tied)
-    t_host = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    m = Q.FModel(host)                                   # uploads the weights
-    t_up = time.perf_counter() - t0
-    ids = list(np.random.default_rng(1234).integers(0, cfg[0], P + 1))
-    for t in ids[:P]:
-        lg = m.step(int(t))
-    tok = int(np.argmax(lg)) if P else int(ids[P])
-    for _ in range(W):
-        tok = int(np.argmax(m.step(tok)))
-    pos0 = m.pos
-    t0 = time.perf_counter()
-    for _ in range(K):
-        tok = int(np.argmax(m.step(tok)))
-    t_dec = time.perf_counter() - t0
-    prof = {}
-    if NP:
-        Q.profile(True)
-        for _ in range(NP):
-            tok = int(np.argmax(m.step(tok)))
-        prof = Q.profile_read()
-        Q.profile(False)
-    fwd = None
-    FR = args.forward_rows
-    if FR:
-        # llama_model_forward (llama.c:167-186): FR rows through the batched
-        # GEMMs and prefill attention, host logits (FR, vocab) as in the reference
-        fids = [int(t) for t in np.random.default_rng(7).integers(0, cfg[0], FR)]
-        m.forward(fids)                                  # first call: buffers, kernel loads
-        t0 = time.perf_counter()
-        m.forward(fids)
-        t_fwd = time.perf_counter() - t0
-        Q.profile(True)
-        m.forward(fids)
-        fprof = Q.profile_read()
-        Q.profile(False)
-        fwd = f32_forward_line(cfg, FR, t_fwd, fprof)
-    m.close()
-    vocab, dm, L, H, KVH, hd, ff, _ = cfg
-    qd, kvd = H * hd, KVH * hd
-    gb = {"gemv_qkv": (L, 4 * dm * (qd + 2 * kvd)), "gemv_o": (L, 4 * qd * dm), "gemv_gate_up": (L, 8 * dm * ff),
-          "gemv_down": (L, 4 * ff * dm), "gemv_head": (1, 4 * dm * vocab)}
-    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
-    gemv_bytes = sum(n * b for n, b in gb.values())
-    step_bytes = statistics.mean(f32_bytes(cfg, pos0 + 1 + i) for i in range(K))
-    achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9 if gemv_ms else None
-    line = {
-        "metric": f"fp32 LLMA decode tok/s, {args.config}-shape (1 GPU)",
-        "value": round(K / t_dec, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
-        "ms_per_step": round(1e3 * t_dec / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (numpy N(0,0.02) f32 weights; uniform-random prompt ids)",
-        "config": {"workload": f"{args.config}-shape fp32 LLaMA greedy decode (llama_decode_step, host logits) "
-                               f"after {P} prompt tokens", "cfg": cfg, "context_timed": [pos0 + 1, pos0 + K]},
-        "decode_hbm_roofline_frac": round(step_bytes / (t_dec / K) / (HBM_PEAK_GBS * 1e9), 4),
-        "decode_bytes_per_token": int(step_bytes),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_f32 (f32 GEMV, k-order chains, all call sites)",
-                     "achieved": round(achieved, 1) if achieved else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None},
-        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
-        "host_model_s": round(t_host, 2), "upload_s": round(t_up, 3),
-        "forward": fwd,
-    }
-    print(json.dumps(line), flush=True)
-
-
-def f32_forward_line(cfg, rows, t_s, prof):
-    """The batched fp32 forward's rate and its GEMMs against the VALU bound: each
-    multiply-add is a separate v_mul_f32 and v_add_f32 (the reference rounds every
-    product before its add), so the ceiling is the unpacked, unfused fp32 lane rate."""
-    vocab, dm, L, H, KVH, hd, ff, _ = cfg
-    qd, kvd = H * hd, KVH * hd
-    macs = rows * (L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab)
-    ms = {k: v[0] * v[1] for k, v in prof.items()}
-    gemm_ms = ms.get("pf_gemm", 0.0)
-    tf = 2 * macs / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None
-    return {"rows": rows, "tok_s": round(rows / t_s, 1), "ms": round(1e3 * t_s, 3),
-            "note": "llama_model_forward, host logits (rows, vocab) copied back inside the timed call",
-            "kernel_ms": {k: round(v, 3) for k, v in sorted(ms.items())},
-            "gemm": {"bound": "valu", "achieved": round(tf, 2) if tf else None,
-                     "peak": F32_VALU_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tf / F32_VALU_TFLOPS, 4) if tf else None,
-                     "peak_note": "unpacked fp32 v_mul + v_add, 256 CUs x 64 lanes x 2.4 GHz (the product "
-                                  "is rounded before its add, as in matrix.c:188, so no FMA or packed math); "
-                                  f"the published fp32 matrix peak is {F32_MFMA_TFLOPS} TFLOP/s"}}
+def lscpu_info():
+    """The host CPU as lscpu names it (model, BIOS model name, family/model/stepping,
+    sockets and cores), for the CPU baseline's context."""
+    import subprocess
+    keys = ("Vendor ID", "Model name", "BIOS Model name", "CPU family", "Model", "Stepping", "Socket(s)",
+            "Core(s) per socket", "Thread(s) per core", "NUMA node(s)", "CPU max MHz", "L3 cache")
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    info = {}
+    for line in out.splitlines():
+        k, _, v = line.partition(":")
+        if k.strip() in keys:
+            info[k.strip()] = v.strip()
+    return info or None
 
 
 def host_info():
@@ -286,24 +208,32 @@ def op_gemv(Q, reps=100):
     """BASELINE's op-level int8 GEMV: W int8 (K, M) per-channel from the
     generator's N(0, 0.02) (the parity fixtures' weights), x fp32 N(0, 1) rows,
     batch 1 and 8, inputs resident in HBM.  Per call: activation quantization +
-    product; the product kernel's own duration gives the roofline."""
+    product; the product kernel's own duration gives the roofline.  "cold":
+    every call behind a 512 MB read (weights in neither L2 nor the 256 MB
+    memory-side cache, as in a model's decode step); "warm": back-to-back calls
+    on the same weights (the smaller shapes then come from the memory-side
+    cache).  Kernel durations are per launch on a drained stream."""
     out = []
     for si, (M, K) in enumerate(GEMV_SHAPES):
         W = Q.lib().qtensor_synth(K, M, 1234, 1000 + si, 0.02)
         try:
             for B in (1, 8):
-                call, prod, quant = C.c_double(0), C.c_double(0), C.c_double(0)
-                if Q.lib().qllama_bench_qmatmul(C.byref(W), B, reps, C.byref(call), C.byref(prod), C.byref(quant)):
-                    raise RuntimeError("qllama_bench_qmatmul failed")
+                row = {"M": M, "K": K, "batch": B, "kernel": "k_gemv_dec" if B == 1 else "k_gemv_mfma"}
                 op_bytes = M * K + 4 * M + 4 * B * K + 4 * B * M          # algorithmic bytes: weights, scales, x, y
                 kern_bytes = M * K + 4 * M + B * K + 4 * B * M            # the product kernel reads int8 rows
-                gbs = kern_bytes / (prod.value * 1e-6) / 1e9
-                out.append({"M": M, "K": K, "batch": B, "kernel": "k_gemv_dec" if B == 1 else "k_gemv_mfma",
-                            "us_per_call": round(call.value, 3), "us_product": round(prod.value, 3),
-                            "us_quant": round(quant.value, 3),
-                            "call_gbs": round(op_bytes / (call.value * 1e-6) / 1e9, 1),
-                            "product_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                for temp in ("cold", "warm"):
+                    Q.bench_cold(temp == "cold")
+                    call, prod, quant = C.c_double(0), C.c_double(0), C.c_double(0)
+                    if Q.lib().qllama_bench_qmatmul(C.byref(W), B, reps, C.byref(call), C.byref(prod), C.byref(quant)):
+                        raise RuntimeError("qllama_bench_qmatmul failed")
+                    gbs = kern_bytes / (prod.value * 1e-6) / 1e9
+                    row[temp] = {"us_per_call": round(call.value, 3), "us_product": round(prod.value, 3),
+                                 "us_quant": round(quant.value, 3),
+                                 "call_gbs": round(op_bytes / (call.value * 1e-6) / 1e9, 1),
+                                 "product_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                out.append(row)
         finally:
+            Q.bench_cold(False)
             Q.lib().qtensor_free(C.byref(W))
     return out
 
@@ -311,7 +241,10 @@ def op_gemv(Q, reps=100):
 def op_gqa(Q, reps=50):
     """BASELINE's op-level decode attention: 32 query / 8 KV heads, head_dim 128,
     RoPE theta 500000 applied on the device to q and the new k row, fp32 cache of
-    N(0, 1) at contexts 1, 512, 2048, 8192; exact and fast modes."""
+    N(0, 1) at contexts 1, 512, 2048, 8192; exact and fast modes.  "cold": each
+    call behind a 512 MB read (the cache in neither L2 nor the memory-side
+    cache); "warm": back-to-back calls (caches up to 256 MB then come from the
+    memory-side cache).  Kernel durations are per launch on a drained stream."""
     H, KVH, hd = 32, 8, 128
     rng = np.random.default_rng(11)
     out = []
@@ -319,25 +252,33 @@ def op_gqa(Q, reps=50):
         q = rng.standard_normal(H * hd, dtype=np.float32)
         k = rng.standard_normal((T, KVH * hd), dtype=np.float32)
         v = rng.standard_normal((T, KVH * hd), dtype=np.float32)
+        nbytes = 2 * T * KVH * hd * 4
         for mode, name in ((Q.MODE_EXACT, "exact"), (Q.MODE_FAST, "fast")):
-            _, _, us = Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
-            # kernel time per call: every launch's own events (one warm-up call + reps)
-            Q.profile(True)
-            Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
-            prof = Q.profile_read()
-            Q.profile(False)
-            kern = {c: v_[0] * v_[1] * 1e3 / (reps + 1) for c, v_ in prof.items() if c.startswith("attn")}
-            kus = sum(kern.values())
-            nbytes = 2 * T * KVH * hd * 4
-            out.append({"T": T, "mode": name, "us_per_call": round(us, 3),
-                        "kernel_us": {c: round(x, 3) for c, x in sorted(kern.items())},
-                        "gbs": round(nbytes / (kus * 1e-6) / 1e9, 1) if kus else None,
-                        "frac": round(nbytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if kus else None})
+            row = {"T": T, "mode": name}
+            for temp in ("cold", "warm"):
+                Q.bench_cold(temp == "cold")
+                try:
+                    _, _, us = Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
+                    # kernel time per call: every launch's own events (one warm-up call + reps)
+                    Q.profile(Q.PROFILE_COLD if temp == "cold" else Q.PROFILE_SERIAL)
+                    Q.gqa_decode(q, k, v, H, KVH, hd, mode=mode, rope_base=500000.0, reps=reps)
+                    prof = Q.profile_read()
+                    Q.profile(False)
+                finally:
+                    Q.bench_cold(False)
+                kern = {c: v_[0] * 1e3 for c, v_ in prof.items() if c.startswith("attn")}
+                kus = sum(kern.values())
+                row[temp] = {"us_per_call": round(us, 3),
+                             "kernel_us": {c: round(x, 3) for c, x in sorted(kern.items())},
+                             "gbs": round(nbytes / (kus * 1e-6) / 1e9, 1) if kus else None,
+                             "frac": round(nbytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if kus else None}
+            out.append(row)
     return out
 
 
-def small_config(Q, name, steps=64):
-    """Decode (exact and fast modes) and prefill of a smaller BASELINE config."""
+def small_config(Q, name, steps=64, cpu_seconds=0.0):
+    """Decode (exact and fast modes) and prefill of a smaller BASELINE config,
+    and (cpu_seconds > 0) the CPU oracle's decode and prefill rates beside them."""
     cfg, base, tied, P = CONFIGS[name]
     m = Q.Model.synth(cfg, base, seed=1234, tied=tied)
     f = m.fork(Q.MODE_FAST)
@@ -367,6 +308,9 @@ def small_config(Q, name, steps=64):
             res[f"decode_{key}_tok_s"] = round(n / t, 1)
             res[f"decode_{key}_hbm_roofline_frac"] = round(b / (t / n) / (HBM_PEAK_GBS * 1e9), 4)
         res["decode_context"] = [P + 5, P + 4 + n]
+        if cpu_seconds > 0:
+            res["cpu_baseline"] = cpu_baseline(Q, m, cfg, base, P, cpu_seconds, prefill_tokens=P,
+                                               prefill_seconds=cpu_seconds / 2)
         return res
     finally:
         f.close()
@@ -590,15 +534,20 @@ def main():
     if args.extras and args.config == "8b":
         extras["op_gemv"] = op_gemv(Q)
         extras["op_gqa"] = op_gqa(Q)
-        extras["config_1b"] = small_config(Q, "1b")
-        extras["config_tiny"] = small_config(Q, "tiny")
+        cs = 0.0 if args.no_cpu_baseline else args.cpu_seconds / 3
+        extras["config_1b"] = small_config(Q, "1b", cpu_seconds=cs)
+        extras["config_tiny"] = small_config(Q, "tiny", cpu_seconds=cs)
         extras["gpt2_decode"] = gpt2_decode(Q)
     if args.calib_copy_mib:
         Q.lib().qllama_test_copy.argtypes = [C.c_size_t]
         if Q.lib().qllama_test_copy(args.calib_copy_mib << 20) != 0:
             raise RuntimeError("calibration copy failed")
     gb = gemv_bytes(cfg)
-    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
+    # the GEMV sites that run as kernels of their own (the QKV GEMV runs inside the
+    # attention-half launch on the shapes that launch serves): bytes and times of
+    # the same sites
+    gb = {k: v for k, v in gb.items() if k in prof}
+    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items())
     gemv_bytes_tok = sum(n * b for (n, b) in gb.values())
     launches_per_tok = sum(n for (n, _) in gb.values())
     achieved = gemv_bytes_tok / (gemv_ms * 1e-3) / 1e9 if gemv_ms > 0 else None
@@ -650,7 +599,8 @@ def main():
                 "load_gbs": [round(size / t / 1e9, 2) for t in times]}
     cpu = None
     if not args.no_cpu_baseline and rank == 0:
-        cpu = cpu_baseline(Q, gm, cfg, base, pos_first, args.cpu_seconds)
+        cpu = cpu_baseline(Q, gm, cfg, base, pos_first, args.cpu_seconds, prefill_tokens=P,
+                           prefill_seconds=args.cpu_seconds / 2)
     gm.close()
 
     line = {
@@ -684,7 +634,8 @@ def main():
         "model_build_s": round(t_build, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gemv (W8A8 int8 GEMV, all call sites)",
+            "kernel": "W8A8 int8 decode GEMV (k_gemv_ws / k_gemv_dec), every site launched on its own: "
+                      + ", ".join(sorted(gb)),
             "achieved": round(achieved, 1) if achieved else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

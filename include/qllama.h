@@ -263,9 +263,15 @@ int  qllama_device_count(void);
 // cols) matrix (tensor id tid), quantized per column (quant.c:10-27) on the device.
 QTensor qtensor_synth(int rows, int cols, uint64_t seed, uint64_t tid, double sigma);
 // qmatmul on device-resident data (M rows of N(0, 1) inputs): mean microseconds
-// per call (quantization + product, events around reps calls) and of the product
-// and quantization kernels alone (events on each launch).  Returns 0 on success.
+// per call (quantization + product, events around reps back-to-back calls) and
+// of the product and quantization kernels alone (events on each launch, each
+// launched on a drained stream).  Returns 0 on success.
 int  qllama_bench_qmatmul(const QTensor *W, int M, int reps, double *us_call, double *us_product, double *us_quant);
+// Cold op-level timing for qllama_bench_qmatmul and qllama_gqa_decode_ex while
+// on: each timed call is preceded by a 512 MB read (twice the memory-side
+// cache), the per-call time is that of the (read, call) sequence less that of
+// the reads alone, and the per-launch times are taken behind a read each.
+int  qllama_bench_cold(int on);
 // Device buffers for callers that bring their own (qmatmul_device_noalloc's A
 // and C): allocate, free (after the stream drains), and synchronous copies in
 // stream order.
@@ -282,7 +288,10 @@ void *qllama_stream(void);               // the hipStream_t every launch goes to
 // QLLAMA_NO_ATTN_LAYER=1 in the environment when the model was made).
 int  qllama_attn_layer_active(const QLlamaModel *m);
 // Average duration (ms) of each kernel class over the decode steps run while
-// profiling was on; returns the number of classes written.
+// profiling was on; returns the number of classes written.  enable: 0 off,
+// 1 on; 3 serialized (each timed launch waits for the stream to drain, so the
+// events of back-to-back launches do not overlap); 5 cold (serialized, behind
+// a 512 MB read each).
 int  qllama_profile(int enable);
 int  qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max);
 // The device tanhf (the one GPT-2's GELU uses) on the float bit patterns start,
@@ -301,7 +310,8 @@ int  qllama_gqa_decode(const float *q, const float *k, const float *v, int T, in
 // unrotated; the device rotates q and k (host-libm tables, rope.c:48-68),
 // appends row T-1 to the cache and attends; k_row (n_kv*hd, may be NULL)
 // receives the rotated row as cached.  reps > 0 times that many launches after
-// one warm-up (HIP events on the library stream); *us_per_call receives the mean.
+// one warm-up (HIP events on the library stream, cold under qllama_bench_cold);
+// *us_per_call receives the mean.
 int  qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, int n_heads, int n_kv, int hd,
                           float rope_base, int mode, int reps, float *o, float *k_row, double *us_per_call);
 // Causal prompt attention (llama.c:554-576 for rows p0 .. p0+R-1) on the device:

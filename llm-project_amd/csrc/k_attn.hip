@@ -1228,11 +1228,11 @@ extern "C" int qhip_attn_layer(const float *x, const float *gain, float eps, int
     g_ly_attr[kch == 4] = kLyLds;
   }
   if (kch == 4)
-    QH_LAUNCH(QK_ATTN, (k_attn_layer<128, 4>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
+    QH_LAUNCH(QK_ATTN_LAYER, (k_attn_layer<128, 4>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
               bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
               obm);
   else
-    QH_LAUNCH(QK_ATTN, (k_attn_layer<128, 2>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
+    QH_LAUNCH(QK_ATTN_LAYER, (k_attn_layer<128, 2>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
               bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
               obm);
   return 0;

@@ -398,6 +398,36 @@ __global__ __launch_bounds__(256) void k_copy_v4(const v4i *src, v4i *dst, size_
 }
 }  // namespace
 
+// Reads every 16-byte word of a buffer twice the size of the memory-side cache,
+// so that the next kernel finds neither its operands in L2 nor in that cache
+// (cold timing of the op-level benchmarks).
+__global__ __launch_bounds__(256) void k_flush_read(const v4i *src, size_t n16, int *sink) {
+  int s = 0;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+    const v4i v = __builtin_nontemporal_load(src + i);
+    s ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (s == 0x5eed5eed) sink[0] = s;                // keeps the loads
+}
+
+namespace {
+void *g_flush_buf = nullptr;
+constexpr size_t kFlushBytes = (size_t)512 << 20;
+}  // namespace
+
+extern "C" int qhip_flush_caches(void) {
+  if (!g_flush_buf) {
+    if (hipMalloc(&g_flush_buf, kFlushBytes + 256) != hipSuccess) {
+      g_flush_buf = nullptr;
+      return qh::fail_msg("flush: allocation failed");
+    }
+    if (hipMemsetAsync(g_flush_buf, 1, kFlushBytes + 256, qh::stream()) != hipSuccess) return qh::fail_msg("flush");
+  }
+  QH_LAUNCH(QK_FLUSH, k_flush_read, dim3(4096), dim3(256), 0, (const v4i *)g_flush_buf, kFlushBytes / 16,
+            (int *)((char *)g_flush_buf + kFlushBytes));
+  return 0;
+}
+
 extern "C" int qllama_test_copy(size_t bytes) {
   if (qhip_init()) return 1;
   if (bytes == 0 || bytes % 16) return qh::fail_msg("test_copy: size must be a positive multiple of 16");

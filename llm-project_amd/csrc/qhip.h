@@ -28,6 +28,7 @@ int         qhip_d2h_async(void *host_dst, const void *src, size_t n);
 int         qhip_d2d_async(void *dst, const void *src, size_t n);
 int         qhip_copy2d_d2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, size_t height);
 int         qhip_fill_zero(void *p, size_t n);           // kernel, capture-safe
+int         qhip_flush_caches(void);                     // reads 512 MB: the next kernel starts cold
 // Staged upload from any host memory (a mapped file, say) through two pinned
 // buffers of `chunk` bytes: qhip_upload returns once src may be reused, the copy
 // itself completes in stream order; qhip_upload_end waits for all of it.
@@ -47,7 +48,13 @@ void qhip_graph_destroy(void *exec);
 int  qhip_timer_start(void);
 int  qhip_timer_stop(double *ms);
 
-// per-kernel-class timing with HIP events on the library stream
+// per-kernel-class timing with HIP events on the library stream.  on: 0 off,
+// 1 on; | QHIP_PROF_SERIAL: each timed launch first waits for the stream to
+// drain (events of back-to-back launches otherwise overlap); | QHIP_PROF_COLD:
+// and reads 512 MB first, so the kernel finds its operands in neither L2 nor
+// the memory-side cache.
+#define QHIP_PROF_SERIAL 2
+#define QHIP_PROF_COLD 4
 int  qhip_profile_enable(int on);
 int  qhip_profile_read(char *names, int names_len, double *ms, long long *count, int max);
 int  qhip_profiling(void);

@@ -9,7 +9,7 @@
 enum {
   QK_EMBED = 0, QK_RMSNORM, QK_GEMV_QKV, QK_ROPE, QK_ATTN, QK_QUANT, QK_GEMV_O, QK_GEMV_GU,
   QK_SWIGLU, QK_GEMV_DOWN, QK_GEMV_HEAD, QK_ARGMAX, QK_OTHER, QK_ATTN_PV, QK_PF_GEMM, QK_PF_ATTN, QK_PF_OTHER,
-  QK_ATTN_FAST, QK_NUM_CLASSES
+  QK_ATTN_FAST, QK_ATTN_LAYER, QK_FLUSH, QK_NUM_CLASSES
 };
 
 namespace qh {

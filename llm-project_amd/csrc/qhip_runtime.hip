@@ -21,12 +21,13 @@ std::mutex g_init_mu;
 
 struct ProfRec { int cls; hipEvent_t a, b; };
 bool g_prof = false;
+int g_prof_mode = 0;     // QHIP_PROF_* bits of the last qhip_profile_enable
 std::vector<ProfRec> g_prof_recs;
 std::vector<hipEvent_t> g_event_pool;
 const char *g_class_names[QK_NUM_CLASSES] = {
     "embed", "rmsnorm_quant", "gemv_qkv", "rope_append", "attn_scores", "quant_rows",
     "gemv_o", "gemv_gate_up", "swiglu_quant", "gemv_down", "gemv_head", "argmax", "other", "attn_pv", "pf_gemm", "pf_attn", "pf_other",
-    "attn_fast"};
+    "attn_fast", "attn_layer", "flush"};
 
 hipEvent_t take_event() {
   if (!g_event_pool.empty()) { hipEvent_t e = g_event_pool.back(); g_event_pool.pop_back(); return e; }
@@ -58,7 +59,13 @@ int check_launch(const char *what) {
 }
 
 bool prof_events(int cls, hipEvent_t *start, hipEvent_t *stop) {
-  if (!g_prof || g_prof_suspended) return false;
+  if (!g_prof || g_prof_suspended || cls == QK_FLUSH) return false;
+  // A kernel's start stamp is taken when the packet processor picks up its
+  // packet, which for back-to-back launches is before the previous kernel has
+  // ended: serialized profiling drains the stream first, so the interval is the
+  // kernel's own execution; cold profiling also flushes the caches first.
+  if ((g_prof_mode & QHIP_PROF_COLD) && qhip_flush_caches()) return false;
+  if ((g_prof_mode & (QHIP_PROF_SERIAL | QHIP_PROF_COLD)) && hipStreamSynchronize(g_stream) != hipSuccess) return false;
   hipEvent_t a = take_event(), b = take_event();
   if (!a || !b) {
     if (a) g_event_pool.push_back(a);
@@ -277,6 +284,7 @@ int qhip_profile_enable(int on) {
   if (qhip_init()) return 1;
   if (!on && g_prof) qhip_sync();
   g_prof = on != 0;
+  g_prof_mode = on;
   return 0;
 }
 

@@ -1543,8 +1543,53 @@ int qllama_sync(void) { return qhip_sync(); }
 int qllama_attn_layer_active(const QLlamaModel *m) { return m && m->dev && ((const QDev*)m->dev)->ly_ok; }
 void *qllama_stream(void) { return qhip_init() ? NULL : qhip_stream(); }
 int qllama_profile(int enable) { profiling = enable ? 1 : 0; return qhip_profile_enable(enable); }
+
+// Cold op-level timing (qllama_bench_qmatmul, qllama_gqa_decode_ex): every timed
+// call is preceded by a 512 MB read, and the call's time is that of the
+// (flush, call) sequence less that of the flushes alone.
+static int bench_cold = 0;
+int qllama_bench_cold(int on) { bench_cold = on ? 1 : 0; return 0; }
+
+// Mean time (us) of `reps` calls of fn: back to back, or, when cold, each
+// behind a cache flush with the flushes' own time taken out.
+typedef int (*BenchCall)(void *ctx);
+static int bench_time(BenchCall fn, void *ctx, int reps, double *us) {
+  double ms = 0.0, ms_flush = 0.0;
+  int rc = qhip_timer_start();
+  for (int i = 0; i < reps && !rc; i++) rc = (bench_cold && qhip_flush_caches()) || fn(ctx);
+  if (!rc) rc = qhip_timer_stop(&ms);
+  if (!rc && bench_cold) {
+    rc = qhip_timer_start();
+    for (int i = 0; i < reps && !rc; i++) rc = qhip_flush_caches();
+    if (!rc) rc = qhip_timer_stop(&ms_flush);
+  }
+  if (!rc && us) *us = 1e3 * (ms - ms_flush) / reps;
+  return rc;
+}
 int qllama_profile_read(char *names, int names_len, double *ms, long long *count, int max) {
   return qhip_profile_read(names, names_len, ms, count, max);
+}
+
+typedef struct {
+  int mode, rope, n_heads, n_kv, hd, T;
+  float scale;
+  float *qkv, *k, *v;
+  int *pos;
+  float *cos_t, *sin_t;
+  void *scratch;
+  float *out, *obm;
+} GqaCall;
+
+static int gqa_call(void *ctx) {
+  const GqaCall *g = (const GqaCall*)ctx;
+  if (g->mode == QLLAMA_MODE_FAST)
+    return qhip_fattn(g->qkv, g->k, g->v, g->pos, g->n_heads, g->n_kv, g->hd, g->T, g->scale, g->cos_t, g->sin_t,
+                      g->rope, g->scratch, g->out, g->obm);
+  if (g->rope)
+    return qhip_attention_rope(g->qkv, g->k, g->v, g->pos, g->n_heads, g->n_kv, g->hd, g->T, g->scale, g->cos_t,
+                               g->sin_t, (float*)g->scratch, g->out, g->obm);
+  return qhip_attention(g->qkv, g->k, g->v, g->pos, g->n_heads, g->n_kv, g->hd, g->T, g->scale, (float*)g->scratch,
+                        g->out, g->obm);
 }
 
 // Op-level decode attention on device-resident data (BASELINE's GQA config):
@@ -1580,22 +1625,10 @@ int qllama_gqa_decode_ex(const float *q, const float *k, const float *v, int T, 
                         rope_upload(dcos, dsin, T, hd, rope_base);
   if (!rc) rc = qhip_h2d(tmp, k, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dk) || qhip_sync() ||
                 qhip_h2d(tmp, v, kvn * 4) || qhip_kv_relayout(tmp, T, n_kv, hd, dv);
-  const float scale = 1.0f / sqrtf((float)hd);                  // llama.c:532
-#define GQA_LAUNCH()                                                                                            \
-  (mode == QLLAMA_MODE_FAST                                                                                      \
-       ? qhip_fattn(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dcos, dsin, rope, dsc, dout, dobm)          \
-       : (rope ? qhip_attention_rope(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, dcos, dsin, (float*)dsc,     \
-                                     dout, dobm)                                                                \
-               : qhip_attention(dqkv, dk, dv, dpos, n_heads, n_kv, hd, T, scale, (float*)dsc, dout, dobm)))
-  if (!rc) rc = GQA_LAUNCH() || qhip_sync();
-  if (!rc && reps > 0) {
-    double ms = 0.0;
-    rc = qhip_timer_start();
-    for (int i = 0; i < reps && !rc; i++) rc = GQA_LAUNCH();
-    if (!rc) rc = qhip_timer_stop(&ms);
-    if (!rc && us_per_call) *us_per_call = 1e3 * ms / reps;
-  }
-#undef GQA_LAUNCH
+  GqaCall g = {mode, rope, n_heads, n_kv, hd, T, 1.0f / sqrtf((float)hd),      // llama.c:532
+               dqkv, dk, dv, dpos, dcos, dsin, dsc, dout, dobm};
+  if (!rc) rc = gqa_call(&g) || qhip_sync();
+  if (!rc && reps > 0) rc = bench_time(gqa_call, &g, reps, us_per_call);
   if (!rc) rc = qhip_d2h(o, dout, (size_t)qd * 4);
   if (!rc && k_row)          // row T-1 of every KV head, in the reference's (n_kv*hd) order
     for (int h = 0; h < n_kv && !rc; h++) rc = qhip_d2h(k_row + (size_t)h * hd, dk + ((size_t)h * T + pos) * hd, (size_t)hd * 4);
@@ -1684,6 +1717,21 @@ QTensor qtensor_synth(int rows, int cols, uint64_t seed, uint64_t tid, double si
   return t;
 }
 
+typedef struct {
+  const QTensor *W;
+  int M;
+  float *a, *c;
+  int8_t *qa;
+  float *as;
+} QmmCall;
+
+static int qmm_call(void *ctx) {
+  const QmmCall *q = (const QmmCall*)ctx;
+  const QTensor *W = q->W;
+  return qhip_quant_rows(q->a, q->M, W->rows, q->qa, W->kpad, q->as) ||
+         qhip_qmm_product(q->qa, q->as, q->M, (const int8_t*)W->q, W->scale, W->cols, W->kpad, q->c);
+}
+
 // Op-level timing of qmatmul on device-resident data: M rows of N(0, 1) inputs
 // (K = W->rows), reps calls after one warm-up.  *us_call: mean time of one call
 // (activation quantization + product, HIP events around the whole sequence);
@@ -1696,21 +1744,17 @@ int qllama_bench_qmatmul(const QTensor *W, int M, int reps, double *us_call, dou
   int8_t *qa = (int8_t*)qhip_malloc((size_t)M * kp);
   float *as = (float*)qhip_malloc((size_t)M * 4);
   int rc = !da || !dc || !qa || !as || qhip_synth_f32(4321, 77, (size_t)M * K, 1.0, da);
-#define QMM_CALL() (qhip_quant_rows(da, M, K, qa, kp, as) || \
-                    qhip_qmm_product(qa, as, M, (const int8_t*)W->q, W->scale, N, kp, dc))
-  if (!rc) rc = QMM_CALL() || qhip_sync();
-  double ms = 0.0;
-  if (!rc) rc = qhip_timer_start();
-  for (int i = 0; i < reps && !rc; i++) rc = QMM_CALL();
-  if (!rc) rc = qhip_timer_stop(&ms);
-  if (!rc && us_call) *us_call = 1e3 * ms / reps;
-  // the same calls with per-launch events: product (class "other"), quantization ("quant_rows")
+  QmmCall c = {W, M, da, dc, qa, as};
+  if (!rc) rc = qmm_call(&c) || qhip_sync();
+  if (!rc) rc = bench_time(qmm_call, &c, reps, us_call);
+  // the same calls with per-launch events, each launch on a drained stream (and
+  // behind a cache flush when cold): product (class "other"), quantization ("quant_rows")
   if (!rc && (us_product || us_quant)) {
     char names[1024];
     double cms[32];
     long long cnt[32];
-    rc = qhip_profile_enable(1);
-    for (int i = 0; i < reps && !rc; i++) rc = QMM_CALL();
+    rc = qhip_profile_enable(1 | (bench_cold ? QHIP_PROF_COLD : QHIP_PROF_SERIAL));
+    for (int i = 0; i < reps && !rc; i++) rc = qmm_call(&c);
     if (!rc) rc = qhip_sync();
     const int n = rc ? 0 : qhip_profile_read(names, sizeof names, cms, cnt, 32);
     qhip_profile_enable(0);
@@ -1720,7 +1764,6 @@ int qllama_bench_qmatmul(const QTensor *W, int M, int reps, double *us_call, dou
       if (us_quant && !strcmp(tok, "quant_rows")) *us_quant = 1e3 * cms[i];
     }
   }
-#undef QMM_CALL
   qhip_free(da); qhip_free(dc); qhip_free(qa); qhip_free(as);
   return rc;
 }

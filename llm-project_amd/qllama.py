@@ -133,6 +133,8 @@ def lib():
         L.gpt_load.argtypes = [C.c_char_p, P(GPT)]
         L.gpt_save.argtypes = [C.c_char_p, P(GPT)]
         L.gpt_free.argtypes = [P(GPT)]
+        L.gpt_kvcache_refresh.argtypes = [P(KVCache), P(GPT)]
+        L.gpt_kvcache_refresh.restype = C.c_int
         L.gpt_kvcache_create.argtypes = [P(GPT)]
         L.gpt_kvcache_create.restype = KVCache
         L.gpt_kvcache_free.argtypes = [P(KVCache)]
@@ -160,6 +162,7 @@ def lib():
         L.qllama_attn_layer_active.restype = C.c_int
         L.qllama_stream.restype = C.c_void_p
         L.qllama_profile.argtypes = [C.c_int]
+        L.qllama_bench_cold.argtypes = [C.c_int]
         L.qllama_profile_read.argtypes = [C.c_char_p, C.c_int, P(C.c_double), P(C.c_longlong), C.c_int]
         _lib = L
     return _lib
@@ -575,8 +578,18 @@ def pf_attention(q, k, v, n_heads, n_kv, hd, p0=0, mode=MODE_EXACT, reps=0):
     return o, (us.value if reps else None)
 
 
+PROFILE_SERIAL, PROFILE_COLD = 3, 5
+
+
 def profile(enable):
-    lib().qllama_profile(1 if enable else 0)
+    """enable: False/0 off, True/1 on, PROFILE_SERIAL (each timed launch on a
+    drained stream), PROFILE_COLD (serialized, behind a 512 MB read each)."""
+    lib().qllama_profile(int(enable))
+
+
+def bench_cold(on):
+    """Cold op-level timing of qllama_bench_qmatmul / gqa_decode(reps=...)."""
+    lib().qllama_bench_cold(1 if on else 0)
 
 
 def profile_read():
