@@ -486,7 +486,8 @@ template <bool DIVW>
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, const float *bmax, const float *vc,
                                                         const int *d_pos, int H, int KVH, int hd, int max_seq,
                                                         int nch, float *o, float *obm) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds_raw[];
+  float *lds = lds_raw + ((16u - ((unsigned)(uintptr_t)lds_raw & 15u)) & 15u) / 4u;   // 16-byte reads; an LDS pointer
   __shared__ float red[kPvThreads / 64];
   __shared__ qd::SeqScratch seq;
   __shared__ uint64_t tab[32];
@@ -535,7 +536,8 @@ constexpr int kLyThreads = 512;
 constexpr int kLyWaves = kLyThreads / 64;
 constexpr int kLyPW = 4;                    // phase Q: prologue waves (rmsnorm, quantization of x) ...
 constexpr int kLyRW = kLyWaves - kLyPW;     // ... and row waves
-constexpr int kLyRowsPerWave = 6;           // QKV rows of a row wave: (G + 2) * hd / (32 * 4) at most
+// QKV rows of a row wave: (G + 2) * hd / (32 * 4) at most, G <= 4
+constexpr int ly_rows_per_wave(int hd) { return 6 * hd / (32 * 4); }
 constexpr int kLyKRows = 128;               // K rows of a block in LDS: at most 32 * 128 positions
 constexpr unsigned kLySpin = 1u << 18;      // polls before a meeting gives up (~0.1 s; a meeting takes ~1 us)
 static_assert(kLyThreads == kPvThreads, "phase P is the PV block");
@@ -633,7 +635,11 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
                                                            int KVH, int max_seq, float scale, const float *cos_t,
                                                            const float *sin_t, float *scores, float *bmax,
                                                            float *qx, unsigned *sync, float *o, float *obm) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];   // the K rows, then the PV weights and tiles
+  // the K rows, then the PV weights and tiles: 16-byte reads, so the array
+  // starts at the first 16-byte boundary past the static variables (the
+  // launch requests 16 bytes more than it uses)
+  extern __shared__ __attribute__((aligned(16))) float lds_raw[];
+  float *lds = lds_raw + ((16u - ((unsigned)(uintptr_t)lds_raw & 15u)) & 15u) / 4u;   // still an LDS pointer
   __shared__ __attribute__((aligned(16))) float qs[4 * HD];
   __shared__ __attribute__((aligned(16))) float kcur[HD];
   __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
@@ -684,12 +690,14 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     if (lane == 0) __hip_atomic_fetch_add(&ly_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #if QLLAMA_TIMELINE
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");            // (stamped builds only) x has arrived
-    if (wave == 0) QTL_MARK(3, 6);
+    if (wave == 0) { QTL_MARK(3, 6); QTL_MARK(4, 0); QTL_CYC(4, 3); }
 #endif
     const float as = qd::rmsnorm_apply<NTP, CMQ>(x, dm, eps, y, gm, red, seq, gs);
+    if (wave == 0) { QTL_MARK(4, 1); QTL_CYC(4, 5); }
     const float inv = 1.0f / as;
 #pragma unroll
     for (int c = 0; c < CMQ; c += 4) *reinterpret_cast<uint32_t *>(qsh + tid * CMQ + c) = qd::quant_word(y, c, inv);
+    if (wave == 0) { QTL_MARK(4, 2); QTL_MARK(4, 4); }
     if (tid == 0) ly_as = as;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");        // this wave's bytes (and as) have landed
     if (lane == 0) __hip_atomic_fetch_add(&ly_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -698,10 +706,11 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     const int rw = wave - kLyPW;
     while (__hip_atomic_load(&ly_issued, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (unsigned)kLyPW) {
     }
-    v4i w[kLyRowsPerWave][KCH];
-    float wsc[kLyRowsPerWave], wb[kLyRowsPerWave];
+    constexpr int RPW = ly_rows_per_wave(HD);
+    v4i w[RPW][KCH];
+    float wsc[RPW], wb[RPW];
 #pragma unroll
-    for (int s = 0; s < kLyRowsPerWave; s++) {
+    for (int s = 0; s < RPW; s++) {
       const int l = min(rw + kLyRW * s, RB - 1);                // rows past RB repeat the last (not used)
       const int j = ly_row(kvh, r * RB + l, G, H, KVH, HD);
       ly_load_row<KCH>(w[s], W + (size_t)j * kpad, lane);
@@ -719,7 +728,7 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
 #pragma unroll
     for (int i = 0; i < KCH; i++) a[i] = *reinterpret_cast<const v4i *>(qsh + 16 * (lane + 64 * i));
 #pragma unroll
-    for (int s = 0; s < kLyRowsPerWave; s++) {
+    for (int s = 0; s < RPW; s++) {
       const int l = rw + kLyRW * s;
       const int acc = qd::wave_sum_i32(ly_dot_row<KCH>(w[s], a));
       if (rw == 0 && s == 0) QTL_MARK(3, 2);
@@ -1105,8 +1114,10 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
 
 size_t g_pv_attr_bytes[2] = {0, 0};   // dynamic LDS the PV kernels are currently allowed
 
+// (16 bytes more than the weights and tiles take: the array starts on the first
+// 16-byte boundary past the static variables)
 size_t pv_lds_bytes(int max_seq) {
-  return ((size_t)(max_seq + kTile - 1) / kTile * kTile + kPBuf * kChains * kTS) * 4;
+  return ((size_t)(max_seq + kTile - 1) / kTile * kTile + kPBuf * kChains * kTS) * 4 + 16;
 }
 
 }  // namespace
@@ -1165,9 +1176,10 @@ extern "C" int qhip_attention_rope(const float *qkv, float *kc, float *vc, const
 // ---- the attention half of a decode layer in one launch (k_attn_layer) ----
 namespace {
 int g_ly_probe = -1;          // -1: not probed yet; 1: 32 * 8 blocks land on XCD (block % 8)
-size_t g_ly_attr[2] = {0, 0};
+size_t g_ly_attr[4] = {0, 0, 0, 0};   // dynamic LDS allowed per instantiation (hd 64/128 x kpad 2048/4096)
 constexpr size_t kLyLds = 96 * 1024;   // dynamic LDS: the K rows (64 KB) or the PV weights and tiles; with
                                        // the static arrays more than half of a CU's LDS: one block per CU
+constexpr size_t kLyLdsLaunch = kLyLds + 16;   // room to start the array on a 16-byte boundary
 }  // namespace
 
 // Whether a launch of 32 * 8 blocks puts block b on XCD (s + b) % 8 for one
@@ -1192,12 +1204,12 @@ extern "C" int qhip_attn_layer_probe(void) {
 }
 
 // Shapes k_attn_layer serves: 8 KV heads (one per XCD), at most 4 query heads
-// per KV head, head_dim 128, kpad 2048 or 4096, max_seq <= 4096, and a device
+// per KV head, head_dim 128 or 64, kpad 2048 or 4096, max_seq <= 4096, and a device
 // with the 256 CUs its blocks need at once.
 extern "C" int qhip_attn_layer_ok(int n_heads, int n_kv, int hd, int kpad, int max_seq) {
-  if (n_kv != 8 || n_heads % n_kv || hd != 128 || (kpad != 2048 && kpad != 4096)) return 0;
+  if (n_kv != 8 || n_heads % n_kv || (hd != 128 && hd != 64) || (kpad != 2048 && kpad != 4096)) return 0;
   const int G = n_heads / n_kv;
-  if (G < 1 || G > 4 || (G + 2) * hd % kLyNB || (G + 2) * hd / kLyNB > kLyRW * kLyRowsPerWave) return 0;
+  if (G < 1 || G > 4 || (G + 2) * hd % kLyNB || (G + 2) * hd / kLyNB > kLyRW * ly_rows_per_wave(hd)) return 0;
   if (G * ((hd + kChains - 1) / kChains) > kLyNB || max_seq > kLyNB * kLyKRows) return 0;
   if (pv_lds_bytes(max_seq) > kLyLds || (size_t)kLyKRows * hd * 4 > kLyLds) return 0;
   return qh::num_cus() >= kLyNB * n_kv && qhip_attn_layer_probe() == 1;
@@ -1219,22 +1231,27 @@ extern "C" int qhip_attn_layer(const float *x, const float *gain, float eps, int
     return qh::fail_msg("attn_layer: unsupported shape");
   const int G = n_heads / n_kv;
   float *qx = scratch, *bmax = scratch + (size_t)n_kv * (G + 2) * hd;
-  const int kch = kpad / 1024;
-  const void *fn = kch == 4 ? reinterpret_cast<const void *>(k_attn_layer<128, 4>)
-                            : reinterpret_cast<const void *>(k_attn_layer<128, 2>);
-  if (g_ly_attr[kch == 4] < kLyLds) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLyLds);
+  const int kch = kpad / 1024, v = (hd == 128 ? 2 : 0) + (kch == 4 ? 1 : 0);
+  const void *fns[4] = {reinterpret_cast<const void *>(k_attn_layer<64, 2>),
+                        reinterpret_cast<const void *>(k_attn_layer<64, 4>),
+                        reinterpret_cast<const void *>(k_attn_layer<128, 2>),
+                        reinterpret_cast<const void *>(k_attn_layer<128, 4>)};
+  if (g_ly_attr[v] < kLyLdsLaunch) {
+    hipError_t e = hipFuncSetAttribute(fns[v], hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLyLdsLaunch);
     if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_attn_layer)", e);
-    g_ly_attr[kch == 4] = kLyLds;
+    g_ly_attr[v] = kLyLdsLaunch;
   }
-  if (kch == 4)
-    QH_LAUNCH(QK_ATTN_LAYER, (k_attn_layer<128, 4>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
-              bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
-              obm);
-  else
-    QH_LAUNCH(QK_ATTN_LAYER, (k_attn_layer<128, 2>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLds, x, gain, eps, dm, W, ws,
-              bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx, sync, o,
-              obm);
+#define LY_LAUNCH(HD_, KCH_)                                                                                      \
+  QH_LAUNCH(QK_ATTN_LAYER, (k_attn_layer<HD_, KCH_>), dim3(kLyNB * n_kv), dim3(kLyThreads), kLyLdsLaunch, x, gain, \
+            eps, dm, W, ws, bias, kpad, kc, vc, d_pos, n_heads, n_kv, max_seq, scale, cos_t, sin_t, scores, bmax, qx,  \
+            sync, o, obm)
+  switch (v) {
+    case 0: LY_LAUNCH(64, 2); break;
+    case 1: LY_LAUNCH(64, 4); break;
+    case 2: LY_LAUNCH(128, 2); break;
+    default: LY_LAUNCH(128, 4); break;
+  }
+#undef LY_LAUNCH
   return 0;
 }
 

@@ -152,7 +152,7 @@ def _big_prefill(Q, name, fused=True):
     m = _synth_layer_path(Q, meta, fused)
     try:
         log(f"{name}: attention half of each decode layer in one launch: {m.attn_layer_active()}")
-        if name == "8b":      # the shape the one-launch path serves
+        if name in ("8b", "1b"):      # shapes the one-launch path serves (head_dim 128 and 64)
             assert m.attn_layer_active() == fused
         log(f"{name}: batched prefill of {len(meta['prompt'])} tokens")
         lg = m.prefill(meta["prompt"]).copy()
@@ -172,8 +172,9 @@ def _big_prefill(Q, name, fused=True):
     assert bits_equal(final[:head.size], head)
 
 
-def test_e2e_1b_batched_prefill_matches_reference(Q):
-    _big_prefill(Q, "1b")
+@pytest.mark.parametrize("path", ["one_launch", "separate"])
+def test_e2e_1b_batched_prefill_matches_reference(Q, path):
+    _big_prefill(Q, "1b", fused=path == "one_launch")
 
 
 @pytest.mark.parametrize("path", ["one_launch", "separate"])
@@ -412,8 +413,7 @@ def _big_e2e(Q, name):
     try:
         assert m.hash() == int(meta["model_hash"], 16)
         log(f"{name}: attention half of each decode layer in one launch: {m.attn_layer_active()}")
-        if name == "8b":
-            assert m.attn_layer_active()
+        assert m.attn_layer_active()          # the 1B and 8B shapes take the one-launch path
         log(f"{name}: weights match; decoding {len(meta['argmax'])} steps")
         gen, exact = _run_steps(m, meta)
         final = m.logits[0].copy()
