@@ -554,7 +554,7 @@ def main():
     traffic = None
     if args.config == "8b" and os.path.exists(TRAFFIC_JSON):
         per = json.load(open(TRAFFIC_JSON))["bytes_per_dispatch"]
-        if all(k in per for k in gb):
+        if gb and all(k in per for k in gb):
             traffic = round(sum(n * per[k] for k, (n, _) in gb.items()) / launches_per_tok)
 
     # prefill GEMMs on MFMA: a second, profiled ingestion of the same prompt

@@ -879,20 +879,57 @@ __device__ __forceinline__ void pf_softmax_row(float *row, int T, qd::SeqScratch
   }
 }
 
-template <int NT>
-__global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int Tp) {
+// Rows r_lo .. r_hi-1 of every head (T = p0 + r + 1 <= NT * CM), the longest
+// first.  One instantiation per row length band: a block's registers and its
+// terms per thread follow its own rows, not the longest row of the pass.
+template <int NT, int CM>
+__global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int Tp, int r_hi) {
   __shared__ qd::SeqScratch seq;
   __shared__ float red[NT / 64];
   __shared__ uint64_t tab[32];
   qd::exp_table_to_lds(tab);
   __syncthreads();                                   // publishes the exp table
-  const int h = blockIdx.x, r = R - 1 - blockIdx.y;   // the longest rows are dispatched first
+  const int h = blockIdx.x, r = r_hi - 1 - blockIdx.y;
   const int T = p0 + r + 1;
   float *row = w + ((size_t)h * R + r) * Tp;
-  if (T <= NT * 4) pf_softmax_row<NT, 4>(row, T, seq, red, tab);
-  else if (T <= NT * 8) pf_softmax_row<NT, 8>(row, T, seq, red, tab);
-  else if (T <= NT * 16) pf_softmax_row<NT, 16>(row, T, seq, red, tab);
-  else pf_softmax_row<NT, 32>(row, T, seq, red, tab);
+  pf_softmax_row<NT, CM>(row, T, seq, red, tab);
+}
+
+// The bands: (threads, terms per thread); a row of T positions takes the first
+// band with NT * CM >= T.  One wave per row up to 2048 positions (more waves
+// per row measured slower: each adds its share of the sum's fixed steps), in
+// bands of 512 positions past 1024.
+struct PfBand { int nt, cm; };
+constexpr PfBand kPfBands[] = {{64, 4}, {64, 8}, {64, 16}, {64, 24}, {64, 32}, {128, 24}, {128, 32},
+                               {256, 32}, {512, 32}};
+constexpr int kPfBandCount = sizeof(kPfBands) / sizeof(kPfBands[0]);
+
+int pf_softmax_band(int band, float *w, int R, int p0, int Tp, int r_lo, int r_hi, int H) {
+  const dim3 grid(H, r_hi - r_lo), block(kPfBands[band].nt);
+#define PF_SM(NT_, CM_) QH_LAUNCH(QK_PF_ATTN, (k_pf_softmax<NT_, CM_>), grid, block, 0, w, R, p0, Tp, r_hi)
+  switch (band) {
+    case 0: PF_SM(64, 4); break;
+    case 1: PF_SM(64, 8); break;
+    case 2: PF_SM(64, 16); break;
+    case 3: PF_SM(64, 24); break;
+    case 4: PF_SM(64, 32); break;
+    case 5: PF_SM(128, 24); break;
+    case 6: PF_SM(128, 32); break;
+    case 7: PF_SM(256, 32); break;
+    default: PF_SM(512, 32); break;
+  }
+#undef PF_SM
+  return 0;
+}
+
+// Softmax of rows 0 .. R-1 (T = p0 + r + 1), band by band from the longest rows.
+int pf_softmax_rows(float *w, int R, int p0, int Tp, int H) {
+  for (int b = kPfBandCount - 1; b >= 0; b--) {
+    const int cap = kPfBands[b].nt * kPfBands[b].cm, lo_cap = b ? kPfBands[b - 1].nt * kPfBands[b - 1].cm : 0;
+    const int r_lo = max(0, lo_cap - p0), r_hi = min(R, cap - p0);       // lo_cap < T <= cap
+    if (r_hi > r_lo && pf_softmax_band(b, w, R, p0, Tp, r_lo, r_hi, H)) return 1;
+  }
+  return 0;
 }
 
 // Block (KV head, 8 query rows), one wave per query head of the group: lane l
@@ -1103,9 +1140,7 @@ int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0
   const dim3 sgrid(KVH, (R + rbs - 1) / rbs, (Tmax + kPsKeys - 1) / kPsKeys);
   if (small) QH_LAUNCH(QK_PF_ATTN, (k_pf_scores<HD, kPsRows / 2>), sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
   else QH_LAUNCH(QK_PF_ATTN, (k_pf_scores<HD, kPsRows>), sgrid, dim3(kPsKeys), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
-  if (Tmax <= 64 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<64>, dim3(H, R), dim3(64), 0, w, R, p0, Tp);
-  else if (Tmax <= 256 * 32) QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<256>, dim3(H, R), dim3(256), 0, w, R, p0, Tp);
-  else QH_LAUNCH(QK_PF_ATTN, k_pf_softmax<512>, dim3(H, R), dim3(512), 0, w, R, p0, Tp);
+  if (pf_softmax_rows(w, R, p0, Tp, H)) return 1;
   const dim3 pgrid(KVH, (R + rbp - 1) / rbp);
   if (small) QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, kPvRows / 2>), pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);
   else QH_LAUNCH(QK_PF_ATTN, (k_pf_pv<HD, kPvRows>), pgrid, dim3(64 * G), 0, w, vc, R, p0, H, KVH, max_seq, Tp, o);

@@ -699,13 +699,18 @@ static int enqueue_step(const QDev *d, const KVDev *kd) {
       rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_ffn[l], d->eps, d->qa, d->kp_dm, d->as);
       rc |= qhip_gemv_dec(2, 7, d->qa, d->as, d->wgu[l], d->sgu[l], d->dff, d->kp_dm, d->gu, NULL, d->hbm, NULL);
     }
-    // h is quantized by its own kernel: quantizing the d_ff values inside the
-    // down GEMV (qhip_gemv_resid_q: prologue waves beside row waves holding the
-    // 14336-byte rows) measured 0.4-3.6% slower end to end at the 8B shape in
-    // every wave layout tried; the prologue's 57 KB of h per block and the fewer
-    // rows in flight cost more than the kernel boundary it saves
-    rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, nbh, d->qa, d->kp_ff, d->as);
-    rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
+    // Rows of up to 8192 bytes (the 1B shape): h is quantized inside the down
+    // GEMV (qhip_gemv_resid_q), one kernel boundary fewer: 1B decode +5.4% end
+    // to end.  Longer rows (8B, 14336 bytes) keep the separate quantization:
+    // there the fused form measured 0.4-3.6% slower in every wave layout tried
+    // (the prologue's 57 KB of h per block and the fewer rows in flight cost
+    // more than the boundary it saves).
+    if (d->kp_ff <= 8192 && qhip_gemv_fused_ok(d->kp_ff)) {
+      rc |= qhip_gemv_resid_q(9, d->gu, d->dff, d->hbm, nbh, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x);
+    } else {
+      rc |= qhip_quant_blocks(d->gu, d->dff, d->hbm, nbh, d->qa, d->kp_ff, d->as);
+      rc |= qhip_gemv_dec(1, 9, d->qa, d->as, d->wd[l], d->sd[l], d->dm, d->kp_ff, d->x, NULL, NULL, NULL);
+    }
   }
   if (!rc) rc |= qhip_rmsnorm_quant(d->x, 1, d->dm, d->g_final, d->eps, d->qa, d->kp_dm, d->as);
   if (!rc) rc |= qhip_gemv_dec(3, 10, d->qa, d->as, d->head, d->head_s, d->vocab, d->kp_dm, d->logits, NULL,
