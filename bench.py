@@ -641,7 +641,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
             "traffic": traffic,
-            "bytes_per_launch": round(gemv_bytes_tok / launches_per_tok),
+            "bytes_per_launch": round(gemv_bytes_tok / launches_per_tok) if launches_per_tok else None,
             "avg_launch_us": round(1e3 * gemv_ms / launches_per_tok, 3) if gemv_ms else None,
         },
         "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,

@@ -881,9 +881,11 @@ __device__ __forceinline__ void pf_softmax_row(float *row, int T, qd::SeqScratch
 
 // Rows r_lo .. r_hi-1 of every head (T = p0 + r + 1 <= NT * CM), the longest
 // first.  One instantiation per row length band: a block's registers and its
-// terms per thread follow its own rows, not the longest row of the pass.
+// terms per thread follow its own rows, not the longest row of the pass.  The
+// one-wave bands of 24 and 32 terms are held to 4 and 3 waves per SIMD (128 and
+// 168 registers, no spills): the 32-term band ran 10 % faster so.
 template <int NT, int CM>
-__global__ __launch_bounds__(NT) void k_pf_softmax(float *w, int R, int p0, int Tp, int r_hi) {
+__global__ __launch_bounds__(NT, NT == 64 && CM == 32 ? 3 : NT == 64 && CM == 24 ? 4 : 1) void k_pf_softmax(float *w, int R, int p0, int Tp, int r_hi) {
   __shared__ qd::SeqScratch seq;
   __shared__ float red[NT / 64];
   __shared__ uint64_t tab[32];

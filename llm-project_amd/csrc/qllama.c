@@ -54,6 +54,8 @@ typedef struct {
   int *d_in;         // max_seq + 1 input tokens by position
   int *d_out;        // max_seq argmax ids by position
   int *h_stage;      // pinned staging, max_seq + 2 ints
+  float *h_logits;   // pinned staging of the logits (vocab floats): a copy from the device into
+                     // pinned memory runs at the link's rate, one into pageable memory does not
   uint64_t gen;      // process-wide generation: identifies this model to the graphs of its caches
   // prompt ingestion (allocated on first use): rows of activations
   int pf_rows;
@@ -139,6 +141,7 @@ static void qdev_free(QDev *d) {
   pf_free(d);
   qhip_free(d->blob);
   qhip_host_free(d->h_stage);
+  qhip_host_free(d->h_logits);
   free(d->wqkv); free(d->wo); free(d->wgu); free(d->wd);
   free(d->sqkv); free(d->bqkv); free(d->so); free(d->sgu); free(d->sd);
   free(d->g_attn); free(d->g_ffn);
@@ -242,7 +245,8 @@ static int model_alloc(QLlamaModel *m, const int32_t cfg[8], float rope_base, fl
 #undef TAKE
   d->blob = (uint8_t*)qhip_malloc(off);
   d->h_stage = (int*)qhip_host_alloc((size_t)(d->max_seq + 2) * sizeof(int));
-  if (!d->blob || !d->h_stage) {
+  d->h_logits = (float*)qhip_host_alloc((size_t)d->vocab * sizeof(float));
+  if (!d->blob || !d->h_stage || !d->h_logits) {
     fprintf(stderr, "Error: device allocation of %zu bytes failed: %s\n", off, qhip_last_error());
     free(o_wqkv); free(o_wo); free(o_wgu); free(o_wd); free(o_s);
     qdev_free(d);
@@ -798,9 +802,10 @@ void q_llama_decode_step(const QLlamaModel *m, LlamaKV *kv, int token, Tensor *l
   const QDev *d = (const QDev*)m->dev;
   KVDev *kd = (KVDev*)kv->dev;
   if (stage_inputs(d, kv->len, &token, 1) || run_steps(d, kd, 1) ||
-      qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4) || qhip_sync() ||
+      qhip_d2h_async(d->h_logits, d->logits, (size_t)d->vocab * 4) || qhip_sync() ||
       layer_check(d, "q_llama_decode_step"))
     die("q_llama_decode_step");
+  memcpy(logits->data, d->h_logits, (size_t)d->vocab * 4);
   kv->len += 1;
 }
 
@@ -904,8 +909,9 @@ int q_llama_prefill(const QLlamaModel *m, LlamaKV *kv, const int *ids, int n, Te
   } else {
     if (stage_inputs(d, kv->len, ids, n) || run_steps(d, kd, n)) return 1;
   }
-  if (logits && qhip_d2h_async(logits->data, d->logits, (size_t)d->vocab * 4)) return 1;
+  if (logits && qhip_d2h_async(d->h_logits, d->logits, (size_t)d->vocab * 4)) return 1;
   if (qhip_sync() || layer_check(d, "q_llama_prefill")) return 1;
+  if (logits) memcpy(logits->data, d->h_logits, (size_t)d->vocab * 4);
   kv->len += n;
   return 0;
 }
