@@ -307,7 +307,8 @@ __global__ __launch_bounds__(64 * (PW + RWV)) void k_gemv_ws(const int8_t *W, co
   __shared__ __attribute__((aligned(16))) int8_t qsh[KCH * 1024];
   __shared__ typename std::conditional<PRO == 2, qd::SeqScratch, int>::type seq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  [[maybe_unused]] constexpr int TK = MODE == MODE_RESID && KCH > 8 ? 5 : MODE;   // timeline id: the down projection apart
+  // timeline id: the down projection (rows of 8 KiB and more) apart from Wo
+  [[maybe_unused]] constexpr int TK = MODE == MODE_RESID && KCH >= 8 ? 5 : MODE;
   if (wave == 0) QTL_MARK(TK, 0);
   QTL_ID(TK);
   if (threadIdx.x == 0) { gctr = 0u; ready = 0u; done = 0u; issued = 0u; }

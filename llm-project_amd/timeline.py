@@ -46,7 +46,6 @@ LAYER = [
     (("gemv", 0), "gemv_qkv (k_gemv_ws, rmsnorm prologue)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
     (("attn", 3), "attn_layer Q phase (QKV rows of one KV head)",
      {6: "x arrived", 1: "prologue done", 2: "first row (weights in)", 3: "rows stored", 5: "at the meeting"}),
-    (("attn", 4), "attn_layer Q prologue (wave 0, from x arrival)", {1: "rmsnorm applied", 2: "quantized"}),
     (("attn", 0), "attn_scores (k_attn_scores; S phase of k_attn_layer)", {1: "K tile + q in LDS"}),
     (("attn", 1), "attn_pv (k_attn_pv; P phase of k_attn_layer)", {1: "block maxima", 2: "exact sum", 3: "weights in LDS", 5: "chains end"}),
     (("gemv", 1), "gemv_o (k_gemv_ws, quantizes o)", {1: "prologue done", 2: "row waves see x", 3: "first row done"}),
@@ -178,10 +177,15 @@ def main():
         for label, p in r.get("phases", {}).items():
             print(f"| {r['kernel']} | {label} | {p['median_from_block_start_us']:.2f} | "
                   f"{p['max_from_kernel_start_us']:.2f} |")
+    # the Q prologue of k_attn_layer, wave 0 (kernel id 4): x arrival (event 0),
+    # rmsnorm applied (1), quantized (2); shader cycles of rmsnorm_apply (3 -> 5)
     q = bufs["attn"][4]
-    okq = (q[:, 0] > 0) & (q[:, 5] > q[:, 3])
+    okq = (q[:, 0] > 0) & (q[:, 2] > q[:, 0]) & (q[:, 5] > q[:, 3])
     if okq.any():
-        print(f"\nQ prologue: rmsnorm_apply {float(np.median(q[okq, 5] - q[okq, 3])):.0f} shader cycles (median over blocks)")
+        print(f"\nQ prologue (wave 0, median over blocks): rmsnorm applied "
+              f"{float(np.median(q[okq, 1] - q[okq, 0])) * TICK_US:.2f} us after x arrived "
+              f"({float(np.median(q[okq, 5] - q[okq, 3])):.0f} shader cycles), quantized "
+              f"{float(np.median(q[okq, 2] - q[okq, 0])) * TICK_US:.2f} us after")
     if chain:
         print(f"\nPV chains: {chain['cycles_per_position_median']} shader cycles per position "
               f"({chain['ns_per_position_median']} ns at {chain['clock_ghz_median']} GHz; median over blocks, "
