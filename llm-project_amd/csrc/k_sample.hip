@@ -12,7 +12,8 @@
 //                 by a bitwise search for the 64th largest; one block selects
 //                 the 64 largest of those (the global top-k is among the blocks'
 //                 top-k) and one wave sorts them.
-//   otherwise     a radix sort of all (p, index) pairs by p descending.  Both
+//   otherwise     a stable radix sort of all (p, index) pairs by p descending
+//                 (k_rs_*: four passes of 8 bits over the bits of p).  Both
 //                 orders are p descending, then index ascending: the order the
 //                 reference's qsort (glibc's merge sort, stable) leaves them in.
 //   k_smp_pick    one wave: keep = top-k, then the top-p cut over the running
@@ -21,7 +22,6 @@
 //                 running sum reaches u.  Every running sum is the reference's
 //                 left-to-right float sum.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <climits>
 
@@ -310,24 +310,115 @@ __global__ __launch_bounds__(64) void k_smp_pick(const float *ps, const int *is,
 
 size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-size_t sort_temp_bytes(int V) {
-  size_t bytes = 0;
-  const hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(
-      nullptr, bytes, (const float *)nullptr, (float *)nullptr, (const int *)nullptr, (int *)nullptr, V, 0, 32,
-      qh::stream());
-  return e == hipSuccess ? bytes : 0;
+// ---- stable LSD radix sort of (p, index) by p descending ----
+// p >= 0, so the bits of p order like its values; a pass sorts by one byte of
+// them, digit = 255 - byte (ascending digits = descending p), keeping the order
+// of equal digits, so four passes from the low byte leave p descending with
+// equal p in their input (index) order.  A block owns a tile of kRsTile items
+// taken in kRsRounds rounds of 256 (item = tile start + 256 * round + thread),
+// which is their input order.
+constexpr int kRsNT = 256, kRsRounds = 16, kRsTile = kRsNT * kRsRounds;
+
+int rs_blocks(int V) { return (V + kRsTile - 1) / kRsTile; }
+
+__device__ __forceinline__ int rs_digit(float p, int shift) {
+  return 255 - (int)((__float_as_uint(p) >> shift) & 255u);
+}
+
+// counts[d * nbs + b]: items of tile b with digit d
+__global__ __launch_bounds__(kRsNT) void k_rs_hist(const float *keys, int V, int shift, int *counts, int nbs) {
+  __shared__ int h[256];
+  const int tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const int j0 = blockIdx.x * kRsTile + tid;
+  for (int r = 0; r < kRsRounds; r++) {
+    const int j = j0 + kRsNT * r;
+    if (j < V) atomicAdd(&h[rs_digit(keys[j], shift)], 1);
+  }
+  __syncthreads();
+  counts[tid * nbs + blockIdx.x] = h[tid];
+}
+
+// In place: counts[d * nbs + b] becomes the output position of the first item of
+// tile b with digit d (an exclusive scan in (digit, tile) order).  One block.
+__global__ __launch_bounds__(kRsNT) void k_rs_scan(int *counts, int nbs) {
+  __shared__ int tot[256];
+  const int d = threadIdx.x;
+  int t = 0;
+  for (int b = 0; b < nbs; b++) t += counts[d * nbs + b];
+  tot[d] = t;
+  __syncthreads();
+  int base = 0;                                   // exclusive prefix over the digits below d
+  for (int e = 0; e < d; e++) base += tot[e];
+  for (int b = 0; b < nbs; b++) {
+    const int c = counts[d * nbs + b];
+    counts[d * nbs + b] = base;
+    base += c;
+  }
+}
+
+// Each item to offs[digit, tile] + the number of earlier items of its tile with
+// the same digit: in a round, the lanes of a wave with the same digit are found
+// by ballots over the digit's bits, and the waves' counts per digit are added in
+// wave order.
+__global__ __launch_bounds__(kRsNT) void k_rs_scatter(const float *kin, const int *vin, float *kout, int *vout, int V,
+                                                      int shift, const int *offs, int nbs) {
+  constexpr int NW = kRsNT / 64;
+  __shared__ int base[256];
+  __shared__ int wc[NW][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  base[tid] = offs[tid * nbs + blockIdx.x];
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int j0 = blockIdx.x * kRsTile + tid;
+  for (int r = 0; r < kRsRounds; r++) {
+#pragma unroll
+    for (int w = 0; w < NW; w++) wc[w][tid] = 0;
+    __syncthreads();
+    const int j = j0 + kRsNT * r;
+    const bool ok = j < V;
+    const float key = ok ? kin[j] : 0.0f;
+    const int val = ok ? vin[j] : 0;
+    const int d = ok ? rs_digit(key, shift) : 256;    // 256: no item (9 bits tell it apart)
+    unsigned long long peers = __ballot(1);
+#pragma unroll
+    for (int bit = 0; bit < 9; bit++) {
+      const bool set = (d >> bit) & 1;
+      const unsigned long long m = __ballot(set);
+      peers &= set ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt);
+    if (ok && rank == 0) wc[wave][d] = __popcll(peers);
+    __syncthreads();
+    {                                             // thread tid = digit tid: offsets of the waves
+      int acc = base[tid];
+#pragma unroll
+      for (int w = 0; w < NW; w++) {
+        const int c = wc[w][tid];
+        wc[w][tid] = acc;
+        acc += c;
+      }
+      base[tid] = acc;
+    }
+    __syncthreads();
+    if (ok) {
+      const int pos = wc[wave][d] + rank;
+      kout[pos] = key;
+      vout[pos] = val;
+    }
+    __syncthreads();
+  }
 }
 
 int nblocks(int V) { return (V + kSlice - 1) / kSlice; }
 
 // Scratch layout: e, p, sorted p, indices, sorted indices (V each), block maxima,
-// the sum, top-k candidates, then the radix sort's temporary storage.
+// the sum, top-k candidates, then the radix sort's digit counts per tile.
 struct Layout {
   float *e, *p, *ps, *bm, *S;
-  int *idx, *is;
+  int *idx, *is, *counts;
   unsigned long long *cand;
-  void *temp;
-  size_t temp_bytes, total;
+  size_t total;
 };
 
 Layout layout(void *base, int V) {
@@ -343,9 +434,8 @@ Layout layout(void *base, int V) {
   L.bm = reinterpret_cast<float *>(b + o); o += al256(nb * 4);
   L.S = reinterpret_cast<float *>(b + o); o += 256;
   L.cand = reinterpret_cast<unsigned long long *>(b + o); o += al256(nb * kTopC * 8);
-  L.temp = b + o;
-  L.temp_bytes = al256(sort_temp_bytes(V));
-  L.total = o + L.temp_bytes;
+  L.counts = reinterpret_cast<int *>(b + o); o += al256((size_t)256 * rs_blocks(V) * 4);
+  L.total = o;
   return L;
 }
 
@@ -357,8 +447,8 @@ extern "C" size_t qhip_sample_scratch(int V) {
   return layout(nullptr, V).total;
 }
 
-// Whether qhip_sample takes the top-k path for these arguments: its kernels are
-// all this library's (no library sort), so the launches can be graph-captured.
+// Whether qhip_sample takes the top-k path (top_k <= 64) for these arguments
+// rather than the full radix sort.
 extern "C" int qhip_sample_topk_path(int V, int top_k) {
   return top_k >= 1 && top_k <= kTopC && V > 0 && (size_t)nblocks(V) * kTopC <= (size_t)kMergeCap;
 }
@@ -378,12 +468,21 @@ extern "C" int qhip_sample(const float *logits, int V, float temperature, int to
     QH_LAUNCH(QK_OTHER, k_smp_topk_block, dim3(nb), dim3(256), 0, L.e, V, L.S, L.cand);
     QH_LAUNCH(QK_OTHER, k_smp_topk_merge, dim3(1), dim3(kNT), 0, L.cand, nb * kTopC, L.ps, L.is);
   } else {
-    QH_LAUNCH(QK_OTHER, k_smp_div, dim3(nb), dim3(256), 0, L.e, V, L.S, L.p);
-    QH_LAUNCH(QK_OTHER, k_smp_iota, dim3((V + 255) / 256), dim3(256), 0, L.idx, V);
-    size_t tb = L.temp_bytes;
-    hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(L.temp, tb, L.p, L.ps, L.idx, L.is, V, 0, 32,
-                                                                qh::stream());
-    if (e != hipSuccess) return qh::fail("sample: radix sort", e);
+    // p and the indices start in (ps, is); four passes, ping-ponging through
+    // (p, idx), leave them sorted in (ps, is)
+    QH_LAUNCH(QK_OTHER, k_smp_div, dim3(nb), dim3(256), 0, L.e, V, L.S, L.ps);
+    QH_LAUNCH(QK_OTHER, k_smp_iota, dim3((V + 255) / 256), dim3(256), 0, L.is, V);
+    const int nbs = rs_blocks(V);
+    for (int pass = 0; pass < 4; pass++) {
+      const int shift = 8 * pass;
+      const float *ki = pass & 1 ? L.p : L.ps;
+      const int *vi = pass & 1 ? L.idx : L.is;
+      float *ko = pass & 1 ? L.ps : L.p;
+      int *vo = pass & 1 ? L.is : L.idx;
+      QH_LAUNCH(QK_OTHER, k_rs_hist, dim3(nbs), dim3(kRsNT), 0, ki, V, shift, L.counts, nbs);
+      QH_LAUNCH(QK_OTHER, k_rs_scan, dim3(1), dim3(kRsNT), 0, L.counts, nbs);
+      QH_LAUNCH(QK_OTHER, k_rs_scatter, dim3(nbs), dim3(kRsNT), 0, ki, vi, ko, vo, V, shift, L.counts, nbs);
+    }
   }
   QH_LAUNCH(QK_OTHER, k_smp_pick, dim3(1), dim3(64), 0, L.ps, L.is, V, top_k, top_p, rng, tok, d_in, d_state,
             d_out, max_seq);

@@ -217,7 +217,7 @@ int qhip_pf_attention_fast(const float *q, const float *kc, const float *vc, int
 // token to *tok; with d_state (decode state [pos, fill_end]) they also record it
 // as the output of position d_state[0]-1 and the input of position d_state[0].
 size_t qhip_sample_scratch(int V);
-int qhip_sample_topk_path(int V, int top_k);     // 1: no library sort, the launches may be captured
+int qhip_sample_topk_path(int V, int top_k);     // 1: the top-k path (top_k <= 64), 0: the full radix sort
 int qhip_sample(const float *logits, int V, float temperature, int top_k, float top_p, void *scratch,
                 size_t scratch_bytes, unsigned long long *rng, int *tok, int *d_in, const int *d_state, int *d_out,
                 int max_seq);

@@ -1371,11 +1371,11 @@ static int enqueue_sampled(const QDev *d, const KVDev *kd, float temperature, in
   return rc || enqueue_step(d, kd);
 }
 
-// n sampled tokens: one graph replay each when every launch of the step is this
-// library's own (qhip_sample_topk_path), else eager launches.
+// n sampled tokens: one graph replay each (every launch of the step, the
+// sampler's sort included, is this library's own), or eager launches while
+// profiling.
 static int run_sampled_steps(const QDev *d, KVDev *kd, int n, float temperature, int top_k, float top_p) {
-  const int capturable = temperature <= 0.0f || qhip_sample_topk_path(d->vocab, top_k);
-  if (profiling || !capturable || getenv("QLLAMA_NO_GRAPH")) {
+  if (profiling || getenv("QLLAMA_NO_GRAPH")) {
     for (int i = 0; i < n; i++) if (enqueue_sampled(d, kd, temperature, top_k, top_p)) return 1;
     return 0;
   }

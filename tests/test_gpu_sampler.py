@@ -97,6 +97,21 @@ def test_generate_in_pieces_equals_one_call(Q):
         r = Q.rng_create(5)
         b = m.generate(10, 1.1, 0, 0.9, r) + m.generate(1, 1.1, 0, 0.9, r) + m.generate(13, 1.1, 0, 0.9, r)
         assert a == b
+        # top-k 0 sorts the whole vocabulary (the library's radix sort, captured in
+        # the sampled step's graph): the oracle's draws
+        ref = O.Model(TINY, 10000.0, seed=1234)
+        try:
+            for t in prompt:
+                lg = ref.step(t)
+            st = O.rng_create(5)
+            c = []
+            for _ in range(24):
+                t, st = O.sample_token(lg, 1.1, 0, 0.9, st)
+                c.append(t)
+                lg = ref.step(t)
+            assert a == c
+        finally:
+            ref.close()
         # the same through the captured sampled step (top-k path), with a change of
         # parameters in between (a second capture) and back
         m.reset(0)
