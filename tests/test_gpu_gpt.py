@@ -124,7 +124,7 @@ def test_gpt_cache_takes_another_model(Q):
 def test_gpt_weights_changed_in_place_need_a_refresh(Q):
     """The device copy of a cache's weights is made at creation (and when the
     step is given another model): weights edited in place are not seen until
-    gpt_kvcache_refresh, as INTEGRATION.md documents.  The edit here is the
+    gpt_kvcache_refresh (the contract include/qgpt.h states).  The edit here is the
     final LayerNorm gain, which leaves the cached keys and values alone, so after
     the refresh every step equals the oracle's on the edited weights again."""
     meta = golden_json("gpt_tiny")
