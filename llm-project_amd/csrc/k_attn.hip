@@ -40,6 +40,7 @@ QTL_DEFINE(attn)
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int kScoreBlock = 128;        // positions per scores block (two waves per query head)
 constexpr int kTile = 128;                  // positions per PV tile
@@ -390,11 +391,20 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void *)sh, (short)0, max_seq * 4, 0x00020000);
   const int j0 = tid * CM;
   float e[CM];
+  if constexpr (CM % 4 == 0) {
 #pragma unroll
-  for (int c = 0; c < CM; c += 4) {       // positions past max_seq read as 0; past T they are masked below
-    const v4i q = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
-    e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
-    e[c + 2] = __int_as_float(q.z); e[c + 3] = __int_as_float(q.w);
+    for (int c = 0; c < CM; c += 4) {     // positions past max_seq read as 0; past T they are masked below
+      const v4i q = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
+      e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
+      e[c + 2] = __int_as_float(q.z); e[c + 3] = __int_as_float(q.w);
+    }
+  } else {                                // CM = 6: 8-byte pieces (the chunks are 8-byte aligned)
+    static_assert(CM % 2 == 0, "pairs of terms");
+#pragma unroll
+    for (int c = 0; c < CM; c += 2) {
+      const v2i q = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
+      e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
+    }
   }
   const int pid = tid - 64;
   PvV own;
@@ -425,14 +435,23 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
   });
   const float inv = 1.0f / sum;
   if (tid < 64) QTL_MARK(1, 2);
+  if constexpr (CM % 4 == 0) {
 #pragma unroll
-  for (int c = 0; c < CM; c += 4)
-    if (j0 + c < wcap) {
-      if (DIVW)   // model.c:501: (e_j / sum) * V
-        *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] / sum, e[c + 1] / sum, e[c + 2] / sum, e[c + 3] / sum);
-      else        // llama.c:568-571: e_j * (1 / sum)
-        *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
-    }
+    for (int c = 0; c < CM; c += 4)
+      if (j0 + c < wcap) {
+        if (DIVW)   // model.c:501: (e_j / sum) * V
+          *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] / sum, e[c + 1] / sum, e[c + 2] / sum, e[c + 3] / sum);
+        else        // llama.c:568-571: e_j * (1 / sum)
+          *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
+      }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CM; c += 2)
+      if (j0 + c < wcap) {
+        if (DIVW) *reinterpret_cast<float2 *>(W + j0 + c) = make_float2(e[c] / sum, e[c + 1] / sum);
+        else *reinterpret_cast<float2 *>(W + j0 + c) = make_float2(e[c] * inv, e[c + 1] * inv);
+      }
+  }
   qd::lds_sync();
   if (tid < 64) QTL_MARK(1, 3);
 
@@ -498,6 +517,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
   if (T <= kPvThreads * 4) pv_block<4, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+  else if (T <= kPvThreads * 6) pv_block<6, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
   else if (T <= kPvThreads * 8) pv_block<8, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
   else if (T <= kPvThreads * 16) pv_block<16, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
   else pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
@@ -805,6 +825,9 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     const float *vrow = xq + (G + 1) * HD;
     if (T <= kPvThreads * 4)
       pv_block<4, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
+                                     pslice, NS, nbm, vrow, &vpre);
+    else if (T <= kPvThreads * 6)     // 6 terms a thread keep all eight waves busy up to 3072 positions
+      pv_block<6, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
                                      pslice, NS, nbm, vrow, &vpre);
     else
       pv_block<8, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
