@@ -398,13 +398,16 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
       e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
       e[c + 2] = __int_as_float(q.z); e[c + 3] = __int_as_float(q.w);
     }
-  } else {                                // CM = 6: 8-byte pieces (the chunks are 8-byte aligned)
-    static_assert(CM % 2 == 0, "pairs of terms");
+  } else if constexpr (CM % 2 == 0) {    // 8-byte pieces (the chunks are 8-byte aligned)
 #pragma unroll
     for (int c = 0; c < CM; c += 2) {
       const v2i q = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
       e[c] = __int_as_float(q.x); e[c + 1] = __int_as_float(q.y);
     }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CM; c++)
+      e[c] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, (j0 + c) * 4, 0, XCH ? 16 : 0));
   }
   const int pid = tid - 64;
   PvV own;
@@ -444,13 +447,17 @@ __device__ __forceinline__ void pv_block(const float *scores, const float *bmax,
         else        // llama.c:568-571: e_j * (1 / sum)
           *reinterpret_cast<float4 *>(W + j0 + c) = make_float4(e[c] * inv, e[c + 1] * inv, e[c + 2] * inv, e[c + 3] * inv);
       }
-  } else {
+  } else if constexpr (CM % 2 == 0) {
 #pragma unroll
     for (int c = 0; c < CM; c += 2)
       if (j0 + c < wcap) {
         if (DIVW) *reinterpret_cast<float2 *>(W + j0 + c) = make_float2(e[c] / sum, e[c + 1] / sum);
         else *reinterpret_cast<float2 *>(W + j0 + c) = make_float2(e[c] * inv, e[c + 1] * inv);
       }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CM; c++)
+      if (j0 + c < wcap) W[j0 + c] = DIVW ? e[c] / sum : e[c] * inv;
   }
   qd::lds_sync();
   if (tid < 64) QTL_MARK(1, 3);
@@ -516,11 +523,16 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(const float *scores, con
   const int h = head_of_block(blockIdx.x, H, KVH);
   const int T = *d_pos + 1;
   const int kvh = h / (H / KVH);
-  if (T <= kPvThreads * 4) pv_block<4, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
-  else if (T <= kPvThreads * 6) pv_block<6, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
-  else if (T <= kPvThreads * 8) pv_block<8, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
-  else if (T <= kPvThreads * 16) pv_block<16, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
-  else pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
+  // the fewest terms a thread that cover T: the exact sum's per-wave work shrinks with them
+#define PV_BAND(CM_)                                                                                              \
+  if (T <= kPvThreads * CM_) {                                                                                     \
+    pv_block<CM_, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y,       \
+                        gridDim.y);                                                                                \
+    return;                                                                                                        \
+  }
+  PV_BAND(1) PV_BAND(2) PV_BAND(3) PV_BAND(4) PV_BAND(5) PV_BAND(6) PV_BAND(8) PV_BAND(16)
+#undef PV_BAND
+  pv_block<32, DIVW>(scores, bmax, vc, T, h, kvh, hd, max_seq, nch, o, obm, lds, red, seq, tab, blockIdx.y, gridDim.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -823,15 +835,18 @@ __global__ __launch_bounds__(kLyThreads) void k_attn_layer(const float *x, const
     QTL_ID(1);
     const int nbm = (T + PB - 1) / PB;                         // blocks that had positions
     const float *vrow = xq + (G + 1) * HD;
-    if (T <= kPvThreads * 4)
-      pv_block<4, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
-                                     pslice, NS, nbm, vrow, &vpre);
-    else if (T <= kPvThreads * 6)     // 6 terms a thread keep all eight waves busy up to 3072 positions
-      pv_block<6, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
-                                     pslice, NS, nbm, vrow, &vpre);
-    else
-      pv_block<8, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
-                                     pslice, NS, nbm, vrow, &vpre);
+    // the fewest terms a thread that cover T (T <= 4096 here): the exact sum's
+    // per-wave work shrinks with them
+#define LY_PV_BAND(CM_)                                                                                          \
+  if (T <= kPvThreads * CM_) {                                                                                    \
+    pv_block<CM_, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab, \
+                                     pslice, NS, nbm, vrow, &vpre);                                                \
+    return;                                                                                                       \
+  }
+    LY_PV_BAND(1) LY_PV_BAND(2) LY_PV_BAND(3) LY_PV_BAND(4) LY_PV_BAND(5) LY_PV_BAND(6)
+#undef LY_PV_BAND
+    pv_block<8, false, true, true>(scores, bmax, vc, T, ph, kvh, HD, max_seq, kLyNB, o, obm, lds, red, seq, tab,
+                                   pslice, NS, nbm, vrow, &vpre);
   }
 }
 

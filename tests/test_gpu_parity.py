@@ -403,6 +403,49 @@ def test_gqa_decode_matches_reference(Q, T):
     assert bits_equal(o, ref)
 
 
+@pytest.mark.parametrize("T", [300, 700, 1300, 1800, 2300, 2800, 3500, 6000])
+def test_gqa_decode_softmax_bands_match_oracle(Q, T):
+    """The decode attention at a context in each band of softmax terms a thread
+    (1, 2, 3, 4, 5, 6, 8, 16 of 512 threads): bit-identical to the C restatement
+    of llama.c:554-576."""
+    H, KVH, hd = 32, 8, 128
+    rng = np.random.default_rng(900 + T)
+    q = rng.standard_normal(H * hd, dtype=np.float32)
+    K = rng.standard_normal((T, KVH * hd), dtype=np.float32)
+    V = rng.standard_normal((T, KVH * hd), dtype=np.float32)
+    o = np.zeros(H * hd, np.float32)
+    assert Q.lib().qllama_gqa_decode(O.fptr(q), O.fptr(K), O.fptr(V), T, H, KVH, hd, O.fptr(o)) == 0
+    assert bits_equal(o, O.attn_decode(q, K, V, T - 1, H, KVH, hd))
+
+
+def test_long_context_decode_matches_oracle(Q):
+    """A 2990-token prompt through the batched prefill, then decode steps at
+    2990-3089 cached positions through the one-launch attention (its 6- and
+    8-terms-a-thread softmax bands): every logit vector equals the oracle's
+    decode step after the same tokens, bit for bit."""
+    cfg = [512, 2048, 1, 32, 8, 64, 512, 4096]
+    n, extra = 2990, 100
+    ids = O.prompt(n, 78, cfg[0])
+    ref = O.Model(cfg, 500000.0, seed=4321)
+    m = Q.Model.synth(cfg, 500000.0, seed=4321)
+    try:
+        assert m.hash() == ref.hash()
+        assert m.attn_layer_active()
+        log(f"oracle: {n} decode steps")
+        for t in ids:
+            ref.step(t)
+        lg = m.prefill(ids).copy()
+        assert bits_equal(lg, ref.logits)
+        t = int(np.argmax(lg))
+        for s in range(extra):
+            a = m.step(t).copy()
+            assert bits_equal(a, ref.step(t)), f"decode step at position {n + s}"
+            t = int(np.argmax(a))
+    finally:
+        m.close()
+        ref.close()
+
+
 # ---- 1B and 8B shaped models --------------------------------------------------
 def _big_e2e(Q, name):
     if not have_golden(f"e2e_{name}.json"):
