@@ -346,6 +346,11 @@ int  qllama_test_copy(size_t bytes);
 // residual inputs on entry) and the split count used.  For parity tests.
 int  qllama_test_gemm_split(int mode, const int8_t *A, const float *as, const int8_t *W, const float *ws, int M,
                             int N, int kpad, const float *bias, float *out_plain, float *out_split, int *splits);
+// Prompt attention (the batched prefill's, llama.c:554-576 over P rows) on the
+// VALU-only kernels (on = 1: every product a v_mul_f32) or on the default
+// outer-product kernels (on = 0: products from K = 1 fp32 MFMAs); both give the
+// same bits.  Holds for the rest of the process.  For parity tests.
+int  qllama_test_pf_valu(int on);
 
 #ifdef __cplusplus
 }

@@ -1171,9 +1171,235 @@ __global__ __launch_bounds__(kPsKeys) void k_pf_scores(const float *q, const flo
   }
 }
 
+// Prompt attention with the products on the matrix cores.  A K = 1 fp32 MFMA
+// with a zero accumulator, v_mfma_f32_32x32x1_2b_f32, forms two 32 x 32 outer
+// products of 64-lane operands (lanes 32b .. 32b+31 give block b's rows and
+// columns), each element a * b rounded once to nearest even: the bits of
+// v_mul_f32, denormal and special results included, except that an exact -0
+// product comes out +0 (+0 + -0 rounds to +0).  Sums that start at +0.0f never
+// hold -0, so s + (+0) and s + (-0) are the same s and the sign cannot show.
+// The reference's sums stay in order on the VALU: one v_add_f32 per product
+// instead of a v_mul_f32 and a v_add_f32.
+// Element r of lane l of the result: block b = r / 16, row i = 8 * (r % 16 / 4)
+// + 4 * (l / 32) + r % 4, column l % 32.
+// A block's 32 (query head, row) pairs: pair p is head g = p / rbq of the KV
+// head's group and row r0 + p % rbq, rbq = 32 / G (pairs past G * rbq idle).
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+__device__ __forceinline__ v32f mx_outer(float a, float b) {
+  const v32f z = {};
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, z, 0, 0, 0);
+}
+__device__ __forceinline__ int mx_pair(int r, int lane) { return 8 * ((r & 15) >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Pair p < 32 to (head, row): p / rbq as (p * mg) >> 16 with mg = ceil(2^16 /
+// rbq), exact for p < 32 and rbq <= 32 (the error p * (mg - 2^16 / rbq) / 2^16
+// stays below 1 / rbq).
+struct MxPairs {
+  int rbq, mg;
+  __device__ explicit MxPairs(int G) : rbq(32 / G), mg((65536 + 32 / G - 1) / (32 / G)) {}
+  __device__ int head(int p) const { return (p * mg) >> 16; }
+  __device__ int row(int p) const { return p - head(p) * rbq; }
+};
+
+// The two outer-product shapes, as a 64-lane wave sees them.  NP = 32:
+// v_mfma_f32_32x32x1_2b_f32, lanes 32b + i give block b's row i and column i,
+// result element r of lane l is block r / 16, row 8 * (r % 16 / 4) + 4 * (l /
+// 32) + r % 4, column l % 32.  NP = 16: v_mfma_f32_16x16x1_4b_f32, lanes 16b + i
+// give block b's row i and column i, element r of lane l is block r / 4, row
+// 4 * (l / 16) + r % 4, column l % 16.  Every lane group supplies the same NP
+// rows, so a tile is NP rows x 64 columns (column c from lane c).
+template <int NP> struct MxShape;
+template <> struct MxShape<32> {
+  typedef v32f tile;
+  __device__ static tile outer(float a, float b) { return mx_outer(a, b); }
+  __device__ static int row(int r, int l) { return mx_pair(r, l); }
+  __device__ static int col(int r, int l) { return 32 * (r >> 4) + (l & 31); }
+};
+typedef float v16f __attribute__((ext_vector_type(16)));
+template <> struct MxShape<16> {
+  typedef v16f tile;
+  __device__ static tile outer(float a, float b) {
+    const v16f z = {};
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, z, 0, 0, 0);
+  }
+  __device__ static int row(int r, int l) { return 4 * (l >> 4) + (r & 3); }
+  __device__ static int col(int r, int l) { return 16 * (r >> 2) + (l & 15); }
+};
+
+// Scores: block (KV head, rbq rows, i.e. 32 pairs, 8 * NP keys) of four waves;
+// wave v takes pairs NP * (v % (32 / NP)) .. +NP-1 and keys j0 + 64 * (v / (32 /
+// NP)) .. +63 (lane l supplies key j0 + l, lane l % NP the pair) and forms the
+// dots over d in order for its NP x 64 (pair, key) elements at once.  Each lane
+// reads its q and K rows a whole 128-byte line at a time (32 dims), so a line
+// is fetched once while it is in the L1.
+template <int HD, int NP>
+__global__ __launch_bounds__(256) void k_pf_scores_mx(const float *q, const float *kc, int R, int p0, int H,
+                                                      int KVH, int max_seq, float scale, float *w, int Tp) {
+  typedef MxShape<NP> S;
+  typedef typename S::tile tile;
+  constexpr int CH = HD % 32 == 0 ? 32 : 16, NQ = CH / 4;           // dims per step, float4 loads per row
+  static_assert(HD % CH == 0, "whole steps");
+  const int kvh = blockIdx.x, G = H / KVH;
+  const MxPairs P(G);
+  const int r0 = blockIdx.y * P.rbq, rend = min(R, r0 + P.rbq);
+  const int jvis = p0 + rend - 1;                                    // last key any row here sees
+  const int lane = threadIdx.x & 63, wv_ = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int pb = NP * (wv_ % (32 / NP));
+  const int jw = blockIdx.z * 8 * NP + 64 * (wv_ / (32 / NP));
+  if (jw > jvis) return;                                             // uniform for the wave
+  const int pa = pb + (lane & (NP - 1)), ga = min(P.head(pa), G - 1), ra = min(r0 + P.row(pa), R - 1);
+  const float4 *qr = reinterpret_cast<const float4 *>(q + ((size_t)ra * H + kvh * G + ga) * HD);
+  const float4 *kr = reinterpret_cast<const float4 *>(kc + ((size_t)kvh * max_seq + min(jw + lane, jvis)) * HD);
+  tile s = {};
+  auto add = [&](float a, float b) {
+    s += S::outer(a, b);
+    __builtin_amdgcn_sched_barrier(0);                               // one product tile live at a time
+  };
+#pragma unroll 1
+  for (int c = 0; c < HD / 4; c += NQ) {
+    float4 qa[NQ], kb[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+      qa[i] = qr[c + i];
+      kb[i] = kr[c + i];
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+      add(qa[i].x, kb[i].x);
+      add(qa[i].y, kb[i].y);
+      add(qa[i].z, kb[i].z);
+      add(qa[i].w, kb[i].w);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NP; r++) {
+    const int p = pb + S::row(r, lane), g = P.head(p), row = r0 + p - g * P.rbq, j = jw + S::col(r, lane);
+    if (g < G && row < R && j <= p0 + row) w[((size_t)(kvh * G + g) * R + row) * Tp + j] = s[r] * scale;
+  }
+}
+
+// PV: block (KV head, rbq rows, i.e. 32 pairs); wave v takes pairs NP * (v % (32
+// / NP)) .. +NP-1 and dims 64 * (v / (32 / NP)) .. +63 (lane l supplies dim
+// d0 + l, lane l % NP the pair); for every key t in order the products
+// w[pair][t] * V[t][d] of the wave's NP x 64 elements are added at once (NP
+// adds a lane per key: with NP = 16 the longest rows' waves, which bound the
+// kernel, carry half the adds of NP = 32).  Keys up to the block's first row's
+// last are seen by every pair: they go 8 a chunk, one chunk in flight while the
+// other is added.  Past them (at most rbq - 1 + 7 keys) a pair whose row ends
+// before t supplies a zero weight, so its products are +-0 and its sums do not
+// move; should such a key's V value not be finite (0 * inf is NaN), that key
+// masks the products element by element instead.
+template <int HD, int NP>
+__global__ __launch_bounds__(64 * (32 / NP) * ((HD + 63) / 64)) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_pv_mx(
+    const float *w, const float *vc, int R, int p0, int H, int KVH, int max_seq, int Tp, float *o) {
+  typedef MxShape<NP> S;
+  typedef typename S::tile tile;
+  constexpr int NE = NP;                                             // tile elements per lane
+  const int kvh = blockIdx.x, G = H / KVH;
+  const MxPairs P(G);
+  const int r0 = (gridDim.y - 1 - blockIdx.y) * P.rbq;              // longest blocks first
+  const int rend = min(R, r0 + P.rbq);
+  const int lane = threadIdx.x & 63, wv_ = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int pb = NP * (wv_ % (32 / NP)), d0 = 64 * (wv_ / (32 / NP));
+  const int kall = p0 + r0 + 1, kend = p0 + rend;                   // keys every row sees / any row sees
+  const int k8 = kall & ~7;
+  const int pa = pb + (lane & (NP - 1)), ga = min(P.head(pa), G - 1), prow = P.row(pa), ra = min(r0 + prow, R - 1);
+  const float *wr = w + ((size_t)(kvh * G + ga) * R + ra) * Tp;
+  const float *vr = vc + (size_t)kvh * max_seq * HD + min(d0 + lane, HD - 1);
+  tile s = {};
+  auto add = [&](float a, float b) {
+    s += S::outer(a, b);
+    __builtin_amdgcn_sched_barrier(0);                               // one product tile live at a time
+  };
+  if (k8 > 0) {
+    float4 xa0 = *reinterpret_cast<const float4 *>(wr), xa1 = *reinterpret_cast<const float4 *>(wr + 4);
+    float xb[8], yb[8];
+    float4 ya0, ya1;
+#pragma unroll
+    for (int u = 0; u < 8; u++) xb[u] = vr[u * HD];
+    for (int t = 0; t < k8; t += 16) {
+      const int ty = min(t + 8, k8 - 8);
+      ya0 = *reinterpret_cast<const float4 *>(wr + ty);
+      ya1 = *reinterpret_cast<const float4 *>(wr + ty + 4);
+#pragma unroll
+      for (int u = 0; u < 8; u++) yb[u] = vr[(size_t)(ty + u) * HD];
+      __builtin_amdgcn_sched_barrier(0);                             // the requests go out before the adds
+      add(xa0.x, xb[0]); add(xa0.y, xb[1]); add(xa0.z, xb[2]); add(xa0.w, xb[3]);
+      add(xa1.x, xb[4]); add(xa1.y, xb[5]); add(xa1.z, xb[6]); add(xa1.w, xb[7]);
+      if (t + 8 >= k8) break;
+      const int tx = min(t + 16, k8 - 8);
+      xa0 = *reinterpret_cast<const float4 *>(wr + tx);
+      xa1 = *reinterpret_cast<const float4 *>(wr + tx + 4);
+#pragma unroll
+      for (int u = 0; u < 8; u++) xb[u] = vr[(size_t)(tx + u) * HD];
+      __builtin_amdgcn_sched_barrier(0);
+      add(ya0.x, yb[0]); add(ya0.y, yb[1]); add(ya0.z, yb[2]); add(ya0.w, yb[3]);
+      add(ya1.x, yb[4]); add(ya1.y, yb[5]); add(ya1.z, yb[6]); add(ya1.w, yb[7]);
+    }
+  }
+  // the rest (past the first row's last key the keys are masked per pair), 8
+  // keys a batch: a pair whose row ends before a key supplies a zero weight, and
+  // past the last key the V value is zero too; a batch with a masked key whose
+  // V value is not finite goes key by key instead, each product masked
+#pragma unroll 1
+  for (int t0 = k8; t0 < kend; t0 += 8) {
+    float wv[8], vv[8];
+    bool bad = false;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int t = min(t0 + u, kend - 1), dt = t0 + u - (p0 + r0);
+      const bool seen = t0 + u < kend;
+      wv[u] = seen && dt <= prow ? wr[t] : 0.0f;
+      vv[u] = seen ? vr[(size_t)t * HD] : 0.0f;
+      bad |= seen && dt > 0 && !__builtin_isfinite(vv[u]);
+    }
+    if (!__any(bad)) {
+#pragma unroll
+      for (int u = 0; u < 8; u++) add(wv[u], vv[u]);
+    } else {
+#pragma unroll 1
+      for (int t = t0; t < min(t0 + 8, kend); t++) {
+        const int dt = t - (p0 + r0);
+        const tile pr = S::outer(wr[t], vr[(size_t)t * HD]);
+#pragma unroll
+        for (int r = 0; r < NE; r++) {
+          s[r] += dt <= 0 || P.row(pb + S::row(r, lane)) >= dt ? pr[r] : 0.0f;
+          __builtin_amdgcn_sched_barrier(0);                         // each row test next to its add
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NE; r++) {
+    const int p = pb + S::row(r, lane), g = P.head(p), row = r0 + p - g * P.rbq, d = d0 + S::col(r, lane);
+    if (g < G && row < R && d < HD) o[((size_t)row * H + kvh * G + g) * HD + d] = s[r];
+  }
+}
+
+// 1: prompt attention on the VALU-only kernels (k_pf_scores / k_pf_pv), the
+// products as v_mul_f32; 0: the outer-product kernels (the same bits).  Read from
+// QLLAMA_PF_VALU at the first call; qllama_test_pf_valu sets it.
+int g_pf_valu = -1;
+
+bool pf_use_valu() {
+  if (g_pf_valu < 0) g_pf_valu = getenv("QLLAMA_PF_VALU") != NULL;
+  return g_pf_valu != 0;
+}
+
 template <int HD>
 int pf_attention(const float *q, const float *kc, const float *vc, int R, int p0, int H, int KVH, int max_seq,
                  float scale, float *w, float *o) {
+  if (!pf_use_valu()) {
+    const int G = H / KVH, Tp = (max_seq + 7) & ~7, rbq = 32 / G;         // rows of a pair block
+    const int nrb = (R + rbq - 1) / rbq;
+    const dim3 sgrid(KVH, nrb, (p0 + R + 255) / 256);
+    QH_LAUNCH(QK_PF_ATTN, (k_pf_scores_mx<HD, 32>), sgrid, dim3(256), 0, q, kc, R, p0, H, KVH, max_seq, scale, w, Tp);
+    if (pf_softmax_rows(w, R, p0, Tp, H)) return 1;
+    QH_LAUNCH(QK_PF_ATTN, (k_pf_pv_mx<HD, 16>), dim3(KVH, nrb), dim3(128 * ((HD + 63) / 64)), 0, w, vc, R, p0, H,
+              KVH, max_seq, Tp, o);
+    return 0;
+  }
   const int G = H / KVH, Tp = (max_seq + 7) & ~7;          // rows of whole 32-byte words
   const int Tmax = p0 + R;
   // short prompts: half the rows per block, twice the waves (the per-row sums
@@ -1393,6 +1619,13 @@ extern "C" int qhip_pf_attention(const float *q, const float *kc, const float *v
     }
     if (rc) return rc;
   }
+  return 0;
+}
+
+// Test hook: 1 puts prompt attention on the VALU-only kernels, 0 on the
+// outer-product kernels, for the rest of the process (both give the same bits).
+extern "C" int qllama_test_pf_valu(int on) {
+  g_pf_valu = on ? 1 : 0;
   return 0;
 }
 

@@ -196,17 +196,21 @@ PF_SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("path", ["outer", "valu"])
 @pytest.mark.parametrize("shape", PF_SHAPES, ids=lambda s: f"H{s[3]}kv{s[4]}hd{s[5]}T{s[7]}")
-def test_batched_prefill_groupings_match_oracle(Q, shape):
+def test_batched_prefill_groupings_match_oracle(Q, shape, path):
     """The prompt in two batched pieces (the second starting at an unaligned
     position), then decode steps from the cache they left: every logit vector
-    equals the oracle's after the same tokens, bit for bit."""
+    equals the oracle's after the same tokens, bit for bit.  path: prompt
+    attention with its products from fp32 MFMA outer products (the default) or
+    from v_mul_f32 (the VALU-only kernels)."""
     cfg, n = list(shape[:8]), shape[8]
     ids = O.prompt(n, 77, cfg[0])
     cut = 37
-    log(f"prefill {cfg}: {n} prompt tokens in pieces of {cut} and {n - cut}")
+    log(f"prefill {cfg}: {n} prompt tokens in pieces of {cut} and {n - cut}, {path} attention")
     ref = O.Model(cfg, 10000.0, seed=4321)
     m = Q.Model.synth(cfg, 10000.0, seed=4321)
+    Q.lib().qllama_test_pf_valu(1 if path == "valu" else 0)
     try:
         assert m.hash() == ref.hash()
         ref_cut = None
@@ -223,6 +227,7 @@ def test_batched_prefill_groupings_match_oracle(Q, shape):
             assert bits_equal(a, ref.step(t))
             t = int(np.argmax(a))
     finally:
+        Q.lib().qllama_test_pf_valu(0)
         m.close()
         ref.close()
 
