@@ -30,6 +30,7 @@ namespace {
 enum { MODE_PLAIN = 0, MODE_RESID = 1, MODE_SWIGLU = 2, MODE_HEAD = 3 };
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(4))) float cfloat_t;   // loads through the scalar cache
 
 template <int KCH>
 __device__ __forceinline__ void load_row(v4i (&w)[KCH], const int8_t *row, int lane) {
@@ -744,6 +745,112 @@ __global__ __launch_bounds__(64 * kSkWaves) void k_gemv_mfma(const int8_t *qa, c
   }
 }
 
+// Skinny W8A8 product for 2..16 activation rows, persistent (the op-level
+// batch-8 GEMV at the vocabulary-sized shape; qmatmul with a few rows).  The M
+// activation rows sit in LDS (row stride kpad + 16: the 16 rows of an MFMA
+// fragment fall on different banks).  A task is (group of 16 output channels, K
+// split): S waves of a block share a group, each taking a contiguous 1/S of its
+// 64-byte K steps, and form one v_mfma_i32_16x16x64_i8 per step (fragment
+// layout as k_gemv_mfma's: activation rows as A, rows past M zero without a
+// read; 16 weight rows as B, lane l holding row l % 16, bytes 16 * (l / 16) ..
+// +15 of the step).  The block takes 16 / S groups a round; a wave walks its
+// steps of all its rounds with the weight fragments of the next FD steps in
+// flight (a ring of registers), so its loads do not wait for a round to end.
+// With S > 1 the S int32 partial tiles of a group are added in LDS after the
+// round (exact in any order); then out[m][n] = (as[m] * ws[n]) * (float)acc
+// (quant.c:81-82), the 16 channel scales through scalar loads.
+constexpr int kSkRing = 8;                                       // K steps in flight per wave
+constexpr int kSkBlockWaves = 16;
+
+template <int S>
+__global__ __launch_bounds__(64 * kSkBlockWaves) void k_gemv_skinny(const int8_t *qa, const float *as, int M,
+                                                                    const int8_t *W, const float *ws, int N,
+                                                                    int kpad, float *out, int ldo) {
+  extern __shared__ __attribute__((aligned(16))) int8_t xs[];    // M rows, stride kpad + 16
+  __shared__ v4i part[S > 1 ? kSkBlockWaves : 1][64];            // partial tiles of the splits
+  constexpr int GPB = kSkBlockWaves / S;                         // groups per block and round
+  constexpr int FD = kSkRing;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int gsub = wave / S, split = wave % S;
+  const int nk = kpad / 64, ng = (N + 15) / 16;
+  const int k0 = split * nk / S, kn = (split + 1) * nk / S - k0;  // this wave's steps of a group (>= 1)
+  const int nround = (ng + GPB - 1) / GPB;                       // block rounds over all groups
+  const int myrounds = (int)blockIdx.x < nround ? (nround - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+  const int nunit = myrounds * kn;
+  if (nunit == 0) return;                                        // the same for every wave of the block
+  const int fr = lane & 15, kq = lane >> 4;
+  const int xstride = kpad + 16;
+  const v4i z = {0, 0, 0, 0};
+  float asl[4];                                                  // the scales of this lane's result rows
+#pragma unroll
+  for (int e = 0; e < 4; e++) asl[e] = as[min(4 * kq + e, M - 1)];
+  // The wave's units in order: round r (the block's groups r * gridDim.x +
+  // blockIdx.x), step k0 + t of the group, t < kn.  The loads run FD units
+  // ahead of the MFMAs; (lr, lt) is the unit being requested.  A group's rows
+  // past N repeat row N - 1, and requests past the last unit repeat the last.
+  int lr = 0, lt = 0;
+  auto load_next = [&](v4i &b) {
+    const int r = min(lr, myrounds - 1), t = lr < myrounds ? lt : kn - 1;
+    const int g = min(((int)blockIdx.x + r * (int)gridDim.x) * GPB + gsub, ng - 1), n = min(16 * g + fr, N - 1);
+    b = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(W + (size_t)n * kpad + 64 * (k0 + t) + 16 * kq));
+    if (++lt == kn) { lt = 0; lr++; }
+  };
+  v4i rb[FD];
+#pragma unroll
+  for (int u = 0; u < FD; u++) load_next(rb[u]);
+  for (int c = threadIdx.x; c < M * (kpad / 16); c += 64 * kSkBlockWaves) {
+    const int m = c / (kpad / 16), k = c - m * (kpad / 16);
+    *reinterpret_cast<v4i *>(xs + (size_t)m * xstride + 16 * k) = reinterpret_cast<const v4i *>(qa + (size_t)m * kpad)[k];
+  }
+  __syncthreads();
+  const int8_t *xrow = xs + (size_t)fr * xstride + 16 * kq;
+  v4i acc = z;
+  int cr = 0, ct = 0;                                            // the unit being added
+  for (int q0 = 0; q0 < nunit; q0 += FD) {
+#pragma unroll
+    for (int u = 0; u < FD; u++) {
+      if (q0 + u >= nunit) break;                                // uniform for the block
+      const v4i a = fr < M ? *reinterpret_cast<const v4i *>(xrow + 64 * (k0 + ct)) : z;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, rb[u], acc, 0, 0, 0);
+      load_next(rb[u]);
+      if (++ct == kn) {                                          // the group's last step: add the splits, store
+        ct = 0;
+        const int g = ((int)blockIdx.x + cr * (int)gridDim.x) * GPB + gsub;
+        cr++;
+        if constexpr (S > 1) {
+          // an LDS-only meeting (a __syncthreads would also wait for the ring)
+          part[wave][lane] = acc;
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          if (split == 0) {
+#pragma unroll
+            for (int t = 1; t < S; t++) acc += part[wave + t][lane];
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();                          // the partials are read before they are rewritten
+        }
+        if (split == 0 && g < ng) {
+          // the group's 16 channel scales through scalar loads (their own counter:
+          // a vector load here would make the next step wait for the whole ring)
+          float wsn = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 16; j++) {
+            const float v = ((cfloat_t *)ws)[min(16 * g + j, N - 1)];
+            wsn = fr == j ? v : wsn;
+          }
+          const int n = 16 * g + fr;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int m = 4 * kq + e;
+            if (m < M && n < N) out[(size_t)m * ldo + n] = (asl[e] * wsn) * (float)acc[e];
+          }
+        }
+        acc = z;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws,
@@ -753,11 +860,57 @@ extern "C" int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M,
   return 0;
 }
 
+namespace {
+template <int S>
+int launch_skinny(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
+                  int kpad, float *out, int ldo) {
+  static size_t attr = 0;
+  const size_t lds = (size_t)M * (kpad + 16);
+  if (lds > 64 * 1024 && lds > attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_gemv_skinny<S>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return qh::fail("hipFuncSetAttribute(k_gemv_skinny)", e);
+    attr = lds;
+  }
+  const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256;
+  const int nround = ((N + 15) / 16 + kSkBlockWaves / S - 1) / (kSkBlockWaves / S);
+  // one block of 16 waves per CU: every block resident at once
+  QH_LAUNCH(cls, k_gemv_skinny<S>, dim3(min(nround, cus)), dim3(64 * kSkBlockWaves), lds, qa, as, M, W, ws, N, kpad,
+            out, ldo);
+  return 0;
+}
+}  // namespace
+
+// 2..16 activation rows within 128 KiB of LDS, kpad a multiple of 64, and at least 2 * 4096 groups of
+// 16 channels per 2 K splits (N >= 65536 at 256 CUs: the vocabulary-sized
+// products).  Narrower products need more K splits, whose meetings per group
+// made this kernel slower than k_gemv_mfma (measured at N = 4096 and 14336).
+extern "C" int qhip_gemv_skinny_ok(int M, int N, int kpad) {
+  const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256;
+  return M >= 2 && M <= 16 && kpad % 64 == 0 && kpad >= 128 && (size_t)M * (kpad + 16) <= 128 * 1024 &&
+         (long)((N + 15) / 16) * 2 >= 2L * cus * kSkBlockWaves;
+}
+
+// K is split over two waves where the 16-channel groups alone would leave waves
+// idle (about 2 * 4096 tasks fill 256 CUs x 16 waves); every wave of a block has
+// steps (kpad >= 128), as the block's meetings need.
+extern "C" int qhip_gemv_skinny(int cls, const int8_t *qa, const float *as, int M, const int8_t *W,
+                                const float *ws, int N, int kpad, float *out, int ldo) {
+  if (!qhip_gemv_skinny_ok(M, N, kpad)) return qh::fail_msg("gemv_skinny: needs 2..16 rows, kpad % 64 == 0, N >= 65536");
+  const int ng = (N + 15) / 16, nk = kpad / 64, cus = qh::num_cus() > 0 ? qh::num_cus() : 256;
+  const long want = 2L * cus * kSkBlockWaves;
+  const int S = ng >= want || nk < 2 ? 1 : 2;                      // qhip_gemv_skinny_ok: ng >= want / 2
+  if (S == 1) return launch_skinny<1>(cls, qa, as, M, W, ws, N, kpad, out, ldo);
+  return launch_skinny<2>(cls, qa, as, M, W, ws, N, kpad, out, ldo);
+}
+
 // The W8A8 product of qmatmul for M quantized rows: the decode GEMV for one row,
-// the skinny MFMA kernel up to 16 rows, the MFMA GEMM beyond.
+// for 2..16 rows the persistent skinny kernel on vocabulary-sized products and
+// the per-block skinny kernel otherwise, the MFMA GEMM beyond.
 extern "C" int qhip_qmm_product(const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
                                 int kpad, float *C) {
   if (M == 1) return qhip_gemv_dec(MODE_PLAIN, QK_OTHER, qa, as, W, ws, N, kpad, C, NULL, NULL, NULL);
+  if (qhip_gemv_skinny_ok(M, N, kpad)) return qhip_gemv_skinny(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
   if (M <= 16) return qhip_gemv_mfma(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
   return qhip_gemm_i8(0, QK_OTHER, qa, as, W, ws, M, N, kpad, C, N, NULL);
 }

@@ -176,6 +176,11 @@ int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *q
 
 // 1..16 activation rows against W [N][kpad] on MFMA (k_gemv.hip):
 // out[m * ldo + j] = (as[m] * ws[j]) * (float)acc[m][j]  (quant.c:81-82).
+// Persistent skinny W8A8 product for 2..16 rows (k_gemv_skinny);
+// qhip_gemv_skinny_ok says which (M, N, kpad) it serves.
+int qhip_gemv_skinny_ok(int M, int N, int kpad);
+int qhip_gemv_skinny(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
+                     int kpad, float *out, int ldo);
 int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
                    int kpad, float *out, int ldo);
 

@@ -315,10 +315,14 @@ def test_qmatmul_many_rows_matches_oracle(Q, M, K, N):
     assert bits_equal(Cg, ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(2, 64, 48), (5, 300, 200), (8, 4096, 4096), (16, 1000, 517), (11, 14336, 96)])
+@pytest.mark.parametrize("M,K,N", [(2, 64, 48), (5, 300, 200), (16, 1000, 517), (11, 14336, 96),
+                                   (8, 4096, 4096), (2, 2048, 33), (3, 4096, 1001), (4, 8192, 96), (6, 14336, 257),
+                                   (8, 512, 70001), (3, 256, 140000), (16, 128, 65536)])
 def test_qmatmul_few_rows_matches_oracle(Q, M, K, N):
-    """2..16 rows go through the skinny MFMA kernel (k_gemv_mfma): bit-identical
-    to quant.c:60-85, including K that is not a multiple of the 64-byte step."""
+    """2..16 rows: vocabulary-sized outputs (N >= 65536) through the persistent
+    skinny kernel (k_gemv_skinny: K split over 2 waves or not, N odd), the rest
+    through the per-block skinny kernel (k_gemv_mfma, including K that is not a
+    multiple of the 64-byte step): all bit-identical to quant.c:60-85."""
     rng = np.random.default_rng(M * 131 + K)
     A = rng.standard_normal((M, K)).astype(np.float32)
     A[M - 1] = 0.0                               # an all-zero row: scale 1
