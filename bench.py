@@ -387,6 +387,9 @@ def main():
                     help="f32 path: also time llama_model_forward over this many rows (0: skip)")
     ap.add_argument("--path", default="int8", choices=["int8", "f32"],
                     help="int8: the headline LLMQ decode (default); f32: the LLMA decode path")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="measure only the op-level GEMV and GQA configs (BASELINE configs 2-3) and print "
+                         "them as the one JSON line (no model is built)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -395,6 +398,12 @@ def main():
     rank = int(os.environ.get("RANK", "0"))
 
     Q = load_qllama()
+    if args.ops_only:
+        line = {"metric": "op-level int8 GEMV and GQA decode attention (HBM roofline fraction)", "n_gpus": 1,
+                "higher_is_better": True, "data": "synthetic", "op_gemv": op_gemv(Q), "op_gqa": op_gqa(Q)}
+        if rank == 0:
+            print(json.dumps(line), flush=True)
+        return
     cfg, base, tied, prefill = CONFIGS[args.config]
     P = args.prefill if args.prefill is not None else prefill
     if args.path == "f32":
