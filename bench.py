@@ -38,7 +38,7 @@ METRIC = "decode tok/s + % HBM roofline, 8B-shape int8 LLaMA (1 GPU); prefill to
 HBM_PEAK_GBS = 8000.0
 INT8_MFMA_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 F32_MFMA_TFLOPS = 157.3           # MI355X published fp32 peak
-F32_VALU_TFLOPS = 39.3            # 256 CUs x 64 lanes x 2.4 GHz, one unpacked fp32 op per lane
+F32_VALU_TFLOPS = 78.6            # 256 CUs x 128 lanes x 2.4 GHz: unpacked, unfused fp32 ops (the published 157.3 counts an FMA as 2)
 # HBM bytes per GEMV dispatch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs
 # (scaled by a plain copy of known size), written by llm-project_amd/profsum.py
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "k_gemv_dec_traffic_8b.json")
@@ -356,6 +356,131 @@ def gpt2_decode(Q, prompt=32, steps=32):
             "ms_per_step": round(1e3 * dt / steps, 3), "context": [prompt + 1, prompt + steps],
             "hbm_roofline_frac": round((wbytes + kv) / (dt / steps) / (HBM_PEAK_GBS * 1e9), 4),
             "note": "gpt_decode_step with host logits each step (as model.c's callers use it)"}
+
+
+def f32_host_model(Q, cfg, base, tied, seed=1234):
+    """A reference LlamaModel (host f32) with N(0, 0.02) weights from numpy, norms 1,
+    biases 0, in the canonical tensor order (llama.c:198-219)."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    rng = np.random.default_rng(seed)
+
+    def w(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+    one = np.ones(dm, np.float32)
+    wte = w(vocab, dm)
+    t = [("wte", wte)]
+    for _ in range(L):
+        t += [("attn_norm", one), ("Wq", w(dm, qd)), ("Wk", w(dm, kvd)), ("Wv", w(dm, kvd)),
+              ("b_q", np.zeros(qd, np.float32)), ("b_k", np.zeros(kvd, np.float32)), ("b_v", np.zeros(kvd, np.float32)),
+              ("Wo", w(qd, dm)), ("ffn_norm", one), ("Wgate", w(dm, ff)), ("Wup", w(dm, ff)), ("Wdown", w(ff, dm))]
+    t += [("final_norm", one), ("lm_head", np.ascontiguousarray(wte.T) if tied else w(dm, vocab))]
+    return Q.host_model(cfg, base, 1e-5, t)
+
+
+def f32_bytes(cfg, t):
+    """HBM bytes of one fp32 decode token at context t: every weight once (f32),
+    the KV rows read and the new row written."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    w = L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab
+    return 4 * w + L * (2 * kvd * 4 * t + 2 * kvd * 4)
+
+
+def main_f32(args, Q, cfg, base, tied, P):
+    """The fp32 (LLMA) decode path: llama_decode_step per token (host logits, as in
+    the reference), after P prompt tokens fed the same way."""
+    W, K, NP = args.warmup, args.steps, args.profile_steps
+    if P + W + K + NP > cfg[7]:
+        sys.exit("bench.py: prompt + warmup + steps + profile exceeds max_seq")
+    t0 = time.perf_counter()
+    host = f32_host_model(Q, cfg, base, tied)
+    t_host = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    m = Q.FModel(host)                                   # uploads the weights
+    t_up = time.perf_counter() - t0
+    ids = list(np.random.default_rng(1234).integers(0, cfg[0], P + 1))
+    for t in ids[:P]:
+        lg = m.step(int(t))
+    tok = int(np.argmax(lg)) if P else int(ids[P])
+    for _ in range(W):
+        tok = int(np.argmax(m.step(tok)))
+    pos0 = m.pos
+    t0 = time.perf_counter()
+    for _ in range(K):
+        tok = int(np.argmax(m.step(tok)))
+    t_dec = time.perf_counter() - t0
+    prof = {}
+    if NP:
+        Q.profile(True)
+        for _ in range(NP):
+            tok = int(np.argmax(m.step(tok)))
+        prof = Q.profile_read()
+        Q.profile(False)
+    fwd = None
+    FR = args.forward_rows
+    if FR:
+        # llama_model_forward (llama.c:167-186): FR rows through the batched
+        # GEMMs and prefill attention, host logits (FR, vocab) as in the reference
+        fids = [int(t) for t in np.random.default_rng(7).integers(0, cfg[0], FR)]
+        m.forward(fids)                                  # first call: buffers, kernel loads
+        t0 = time.perf_counter()
+        m.forward(fids)
+        t_fwd = time.perf_counter() - t0
+        Q.profile(True)
+        m.forward(fids)
+        fprof = Q.profile_read()
+        Q.profile(False)
+        fwd = f32_forward_line(cfg, FR, t_fwd, fprof)
+    m.close()
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    gb = {"gemv_qkv": (L, 4 * dm * (qd + 2 * kvd)), "gemv_o": (L, 4 * qd * dm), "gemv_gate_up": (L, 8 * dm * ff),
+          "gemv_down": (L, 4 * ff * dm), "gemv_head": (1, 4 * dm * vocab)}
+    gemv_ms = sum(prof[k][0] * n for k, (n, _) in gb.items() if k in prof)
+    gemv_bytes = sum(n * b for n, b in gb.values())
+    step_bytes = statistics.mean(f32_bytes(cfg, pos0 + 1 + i) for i in range(K))
+    achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9 if gemv_ms else None
+    line = {
+        "metric": f"fp32 LLMA decode tok/s, {args.config}-shape (1 GPU)",
+        "value": round(K / t_dec, 3), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(1e3 * t_dec / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (numpy N(0,0.02) f32 weights; uniform-random prompt ids)",
+        "config": {"workload": f"{args.config}-shape fp32 LLaMA greedy decode (llama_decode_step, host logits) "
+                               f"after {P} prompt tokens", "cfg": cfg, "context_timed": [pos0 + 1, pos0 + K]},
+        "decode_hbm_roofline_frac": round(step_bytes / (t_dec / K) / (HBM_PEAK_GBS * 1e9), 4),
+        "decode_bytes_per_token": int(step_bytes),
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_f32 (f32 GEMV, k-order chains, all call sites)",
+                     "achieved": round(achieved, 1) if achieved else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None},
+        "kernel_ms_per_token": {k: round(v[0] * v[1] / NP, 4) for k, v in sorted(prof.items())} if NP else None,
+        "host_model_s": round(t_host, 2), "upload_s": round(t_up, 3),
+        "forward": fwd,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def f32_forward_line(cfg, rows, t_s, prof):
+    """The batched fp32 forward's rate and its GEMMs against the VALU bound: each
+    multiply-add is a separate v_mul_f32 and v_add_f32 (the reference rounds every
+    product before its add), so the ceiling is the unpacked, unfused fp32 lane rate."""
+    vocab, dm, L, H, KVH, hd, ff, _ = cfg
+    qd, kvd = H * hd, KVH * hd
+    macs = rows * (L * (dm * (qd + 2 * kvd) + qd * dm + 2 * dm * ff + ff * dm) + dm * vocab)
+    ms = {k: v[0] * v[1] for k, v in prof.items()}
+    gemm_ms = ms.get("pf_gemm", 0.0)
+    tf = 2 * macs / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None
+    return {"rows": rows, "tok_s": round(rows / t_s, 1), "ms": round(1e3 * t_s, 3),
+            "note": "llama_model_forward, host logits (rows, vocab) copied back inside the timed call",
+            "kernel_ms": {k: round(v, 3) for k, v in sorted(ms.items())},
+            "gemm": {"bound": "valu", "achieved": round(tf, 2) if tf else None,
+                     "peak": F32_VALU_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / F32_VALU_TFLOPS, 4) if tf else None,
+                     "peak_note": "unpacked fp32 v_mul + v_add, 256 CUs x 128 lanes x 2.4 GHz (a wave64 op "
+                                  "every 2 cycles per SIMD; the product is rounded before its add, as in "
+                                  "matrix.c:188, so no FMA or packed math); the published fp32 peak, "
+                                  f"{F32_MFMA_TFLOPS} TFLOP/s, counts an FMA as two"}}
 
 
 def main():
