@@ -219,7 +219,8 @@ def op_gemv(Q, reps=100):
         try:
             for B in (1, 8):
                 row = {"M": M, "K": K, "batch": B,
-                       "kernel": "k_gemv_dec" if B == 1 else "k_gemv_skinny" if M >= 65536 else "k_gemv_mfma"}
+                       "kernel": "k_gemv_dec" if B == 1 else "k_gemv_rows" if K % 1024 == 0 and K <= 8192
+                       else "k_gemv_skinny" if M >= 65536 else "k_gemv_mfma"}
                 op_bytes = M * K + 4 * M + 4 * B * K + 4 * B * M          # algorithmic bytes: weights, scales, x, y
                 kern_bytes = M * K + 4 * M + B * K + 4 * B * M            # the product kernel reads int8 rows
                 for temp in ("cold", "warm"):

@@ -851,12 +851,195 @@ __global__ __launch_bounds__(64 * kSkBlockWaves) void k_gemv_skinny(const int8_t
   }
 }
 
+// Few-row W8A8 product with whole-row weight loads (qmatmul with 2..8 rows,
+// kpad a multiple of 1024 up to 8192: the batch-8 GEMV of the op-level
+// configuration at K = 4096).  A block has kpad / 1024 waves; wave w owns the K
+// bytes 1024 w .. +1023, lane l the 16 bytes 1024 w + 16 l .. +15, and keeps
+// those bytes of every activation row in registers.  The block walks groups of
+// 8 output channels (g = blockIdx.x, += gridDim.x); a wave requests the 8
+// channels' 1 KiB slices of a group (one coalesced 1 KiB wave load each, as in
+// k_gemv_dec) two groups ahead and forms 4 v_dot4_i32_i8 per row and channel.
+// The (channel, row) int32 sums of a lane are folded across the wave by a
+// transpose reduction: at each of the six lane bits a lane keeps half of its
+// values and adds its partner's copy of the same half, so after the folds lane e
+// holds the wave's whole sum for entry e (row e % MR, channel e / MR; the index
+// bits in fold order).  The waves' sums meet in LDS (exact in any order; an
+// LDS-only meeting, the ring stays in flight) and wave 0 stores out[m][n] =
+// (as[m] * ws[n]) * (float)acc (quant.c:81-82), the row and channel scales
+// through scalar loads.  (Scalars only: a private array read across the
+// group's lambdas was placed in LDS, a copy per thread, and cost 11 us a call.)
+constexpr int kRowsGroup = 8;                                    // output channels per group
+
+template <int CTRL>
+__device__ __forceinline__ int rows_dpp(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true); }
+
+// partner copy across fold level L: row_mirror (bit 3), row_half_mirror (bit 2),
+// quad_perm xor 2 (bit 1), xor 1 (bit 0), swizzle xor 16 (bit 4), bpermute xor 32 (bit 5)
+template <int L>
+__device__ __forceinline__ int rows_partner(int v) {
+  if constexpr (L == 0) return rows_dpp<0x140>(v);
+  else if constexpr (L == 1) return rows_dpp<0x141>(v);
+  else if constexpr (L == 2) return rows_dpp<0x4E>(v);
+  else if constexpr (L == 3) return rows_dpp<0xB1>(v);
+  else if constexpr (L == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+  else return __shfl_xor(v, 32, 64);
+}
+constexpr int kRowsLaneBit[6] = {3, 2, 1, 0, 4, 5};
+
+// one fold of NV values at level L: NV / 2 values remain (NV >= 2), or with one
+// value a plain add of the partner's
+template <int L, int NV>
+__device__ __forceinline__ void rows_fold(int (&v)[16], int lane) {
+  if constexpr (NV == 1) {
+    v[0] += rows_partner<L>(v[0]);
+  } else {
+    const bool hi = (lane >> kRowsLaneBit[L]) & 1;
+#pragma unroll
+    for (int j = 0; j < NV / 2; j++) {
+      const int keep = hi ? v[2 * j + 1] : v[2 * j], send = hi ? v[2 * j] : v[2 * j + 1];
+      v[j] = keep + rows_partner<L>(send);
+    }
+  }
+}
+
+template <int MR>
+__global__ __launch_bounds__(1024) void k_gemv_rows(const int8_t *qa, const float *as, int M, const int8_t *W,
+                                                    const float *ws, int N, int kpad, float *out, int ldo) {
+  __shared__ int part[8][64];
+  constexpr int G = kRowsGroup;
+  static_assert(MR == 2 || MR == 4 || MR == 8, "rows per pass");
+  constexpr int NF = MR == 2 ? 4 : MR == 4 ? 5 : 6;             // folds that halve (8 * MR entries)
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int nw = (int)(blockDim.x >> 6);
+  const int ng = (N + G - 1) / G;
+  const int ni = ((ng - 1 - (int)blockIdx.x) / (int)gridDim.x) + 1;  // groups of this block (grid <= ng)
+  const unsigned kb = 1024u * w + 16u * lane;                    // lane offset (uniform row + 32-bit offset)
+  const v4i z = {0, 0, 0, 0};
+  // The wave's units in order: channel c of group i (the block's groups i *
+  // gridDim.x + blockIdx.x), unit 8 i + c.  The loads run 2 groups ahead of the
+  // dots through a ring of registers; requests past the last unit repeat it.
+  const int nunit = G * ni;
+  int lu = 0;                                                    // the unit being requested
+  auto load_next = [&](v4i &b) {
+    const int u = min(lu, nunit - 1), g = (int)blockIdx.x + (u / G) * (int)gridDim.x;
+    const int8_t *row = W + (size_t)min(G * g + u % G, N - 1) * kpad;   // uniform
+    b = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(row + kb));
+    lu++;
+  };
+  v4i x[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) x[m] = m < M ? *reinterpret_cast<const v4i *>(qa + (size_t)m * kpad + kb) : z;
+  float asl[MR];                                                 // scalar loads: their own counter
+#pragma unroll
+  for (int m = 0; m < MR; m++) asl[m] = ((cfloat_t *)as)[min(m, M - 1)];
+  // this lane's entry after the folds: the index bits in fold order
+  int e = 0;
+#pragma unroll
+  for (int L = 0; L < NF; L++) e |= ((lane >> kRowsLaneBit[L]) & 1) << L;
+  bool writer = true;                                            // lanes past the folds hold copies
+#pragma unroll
+  for (int L = NF; L < 6; L++) writer = writer && !((lane >> kRowsLaneBit[L]) & 1);
+  const int em = e % MR, ec = e / MR;
+  float ase = asl[0];
+#pragma unroll
+  for (int m = 1; m < MR; m++) ase = em == m ? asl[m] : ase;
+
+  // the wave's sums of group i meet in LDS; wave 0 stores the group's outputs
+  auto finish = [&](int i, int vsum) {
+    part[w][lane] = vsum;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();                                // an LDS-only meeting (a __syncthreads
+    if (w == 0) {                                                // would also wait for the ring)
+      int t = 0;
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (u < nw) t += part[u][lane];                           // uniform
+      const int g = (int)blockIdx.x + i * (int)gridDim.x;
+      float wsn = 0.0f;                                          // the 8 channel scales: scalar loads
+#pragma unroll
+      for (int c = 0; c < G; c++) {
+        const float sv = ((cfloat_t *)ws)[min(G * g + c, N - 1)];
+        wsn = ec == c ? sv : wsn;
+      }
+      const int n = G * g + ec;
+      if (writer && em < M && n < N) out[(size_t)em * ldo + n] = (ase * wsn) * (float)t;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();                                // the sums are read before they are rewritten
+  };
+
+  constexpr int FD = 2 * G;
+  v4i rb[FD];
+#pragma unroll
+  for (int u = 0; u < FD; u++) load_next(rb[u]);
+  int v[16];
+  // unit q0 + u from ring slot u (then that slot requests the unit FD ahead)
+  auto unit = [&](int q0, int u, bool more) {
+    int a[16];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      int t = __builtin_amdgcn_sdot4(x[m].x, rb[u].x, 0, false);
+      t = __builtin_amdgcn_sdot4(x[m].y, rb[u].y, t, false);
+      t = __builtin_amdgcn_sdot4(x[m].z, rb[u].z, t, false);
+      a[m] = __builtin_amdgcn_sdot4(x[m].w, rb[u].w, t, false);
+    }
+    if (more) load_next(rb[u]);
+    // the channel's MR row sums folded over the first log2(MR) lane bits
+    if constexpr (MR >= 2) rows_fold<0, MR>(a, lane);
+    if constexpr (MR >= 4) rows_fold<1, MR / 2>(a, lane);
+    if constexpr (MR >= 8) rows_fold<2, MR / 4>(a, lane);
+    v[u % G] = a[0];
+    if (u % G == G - 1) {                                        // the group's last channel
+      constexpr int L0 = MR == 2 ? 1 : MR == 4 ? 2 : 3;          // next fold level
+      rows_fold<L0, 8>(v, lane);
+      rows_fold<L0 + 1, 4>(v, lane);
+      rows_fold<L0 + 2, 2>(v, lane);
+      if constexpr (L0 + 3 < 6) rows_fold<L0 + 3, 1>(v, lane);
+      if constexpr (L0 + 4 < 6) rows_fold<L0 + 4, 1>(v, lane);
+      if constexpr (L0 + 5 < 6) rows_fold<L0 + 5, 1>(v, lane);
+      finish((q0 + u) / G, v[0]);
+    }
+  };
+  // whole turns of the ring with no exit inside (so the wait before each unit
+  // is for that unit's load alone), then the one group that may remain (the
+  // unit count is a multiple of G)
+  int q0 = 0;
+  for (; q0 + FD <= nunit; q0 += FD) {
+#pragma unroll
+    for (int u = 0; u < FD; u++) unit(q0, u, true);
+  }
+  if (q0 < nunit) {
+#pragma unroll
+    for (int u = 0; u < G; u++) unit(q0, u, false);
+  }
+}
+
 }  // namespace
 
 extern "C" int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws,
                               int N, int kpad, float *out, int ldo) {
   if (M < 1 || M > 16 || kpad % 16 || N < 1) return qh::fail_msg("gemv_mfma: needs 1..16 rows and kpad % 16 == 0");
   QH_LAUNCH(cls, k_gemv_mfma, dim3((N + 15) / 16), dim3(64 * kSkWaves), 0, qa, as, M, W, ws, N, kpad, out, ldo);
+  return 0;
+}
+
+// 2..8 activation rows, kpad a multiple of 1024 up to 8192 (k_gemv_rows; at
+// kpad = 14336 its 14-wave blocks, one a CU, ran 5 % behind k_gemv_mfma: 20.0
+// against 19.0 us at N = 4096, so longer rows stay there).
+extern "C" int qhip_gemv_rows_ok(int M, int N, int kpad) {
+  return M >= 2 && M <= 8 && N >= 1 && kpad % 1024 == 0 && kpad >= 1024 && kpad <= 8192;
+}
+
+extern "C" int qhip_gemv_rows(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws,
+                              int N, int kpad, float *out, int ldo) {
+  if (!qhip_gemv_rows_ok(M, N, kpad)) return qh::fail_msg("gemv_rows: needs 2..8 rows and kpad = 1024 * (1..8)");
+  const int nw = kpad / 1024, ng = (N + kRowsGroup - 1) / kRowsGroup;
+  const int cus = qh::num_cus() > 0 ? qh::num_cus() : 256;
+  const int grid = min(ng, cus * max(1, 16 / nw));               // about 16 waves a CU, all resident
+  const dim3 block(64 * nw);
+  if (M <= 2) QH_LAUNCH(cls, k_gemv_rows<2>, dim3(grid), block, 0, qa, as, M, W, ws, N, kpad, out, ldo);
+  else if (M <= 4) QH_LAUNCH(cls, k_gemv_rows<4>, dim3(grid), block, 0, qa, as, M, W, ws, N, kpad, out, ldo);
+  else QH_LAUNCH(cls, k_gemv_rows<8>, dim3(grid), block, 0, qa, as, M, W, ws, N, kpad, out, ldo);
   return 0;
 }
 
@@ -904,12 +1087,16 @@ extern "C" int qhip_gemv_skinny(int cls, const int8_t *qa, const float *as, int 
   return launch_skinny<2>(cls, qa, as, M, W, ws, N, kpad, out, ldo);
 }
 
-// The W8A8 product of qmatmul for M quantized rows: the decode GEMV for one row,
-// for 2..16 rows the persistent skinny kernel on vocabulary-sized products and
-// the per-block skinny kernel otherwise, the MFMA GEMM beyond.
+// The W8A8 product of qmatmul for M quantized rows: the decode GEMV for one row;
+// for 2..8 rows with kpad = 1024 * (1..8) the whole-row kernel k_gemv_rows; for
+// the other few-row shapes the persistent skinny kernel on vocabulary-sized
+// products and the per-block skinny kernel otherwise; the MFMA GEMM beyond.
 extern "C" int qhip_qmm_product(const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
                                 int kpad, float *C) {
   if (M == 1) return qhip_gemv_dec(MODE_PLAIN, QK_OTHER, qa, as, W, ws, N, kpad, C, NULL, NULL, NULL);
+#ifndef QLLAMA_NO_GEMV_ROWS
+  if (qhip_gemv_rows_ok(M, N, kpad)) return qhip_gemv_rows(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
+#endif
   if (qhip_gemv_skinny_ok(M, N, kpad)) return qhip_gemv_skinny(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
   if (M <= 16) return qhip_gemv_mfma(QK_OTHER, qa, as, M, W, ws, N, kpad, C, N);
   return qhip_gemm_i8(0, QK_OTHER, qa, as, W, ws, M, N, kpad, C, N, NULL);

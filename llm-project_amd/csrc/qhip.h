@@ -179,6 +179,11 @@ int qhip_quant_blocks(const float *v, int n, const float *bm, int nbm, int8_t *q
 // Persistent skinny W8A8 product for 2..16 rows (k_gemv_skinny);
 // qhip_gemv_skinny_ok says which (M, N, kpad) it serves.
 int qhip_gemv_skinny_ok(int M, int N, int kpad);
+// k_gemv_rows: 2..8 rows, kpad = 1024 * (1..8), whole 1 KiB weight-row loads;
+// qhip_gemv_rows_ok says which (M, N, kpad) it serves.
+int qhip_gemv_rows_ok(int M, int N, int kpad);
+int qhip_gemv_rows(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
+                   int kpad, float *out, int ldo);
 int qhip_gemv_skinny(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
                      int kpad, float *out, int ldo);
 int qhip_gemv_mfma(int cls, const int8_t *qa, const float *as, int M, const int8_t *W, const float *ws, int N,
