@@ -1233,8 +1233,11 @@ template <> struct MxShape<16> {
 // dots over d in order for its NP x 64 (pair, key) elements at once.  Each lane
 // reads its q and K rows a whole 128-byte line at a time (32 dims), so a line
 // is fetched once while it is in the L1.
+// Held to 4 waves per SIMD (128 registers; 134 unbounded, i.e. 3 waves): the
+// issue rate of a SIMD's MFMAs and adds rises with its waves (365 against 378
+// us per layer at the 8B shape, 2048 rows).
 template <int HD, int NP>
-__global__ __launch_bounds__(256) void k_pf_scores_mx(const float *q, const float *kc, int R, int p0, int H,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_scores_mx(const float *q, const float *kc, int R, int p0, int H,
                                                       int KVH, int max_seq, float scale, float *w, int Tp) {
   typedef MxShape<NP> S;
   typedef typename S::tile tile;
