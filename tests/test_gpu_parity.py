@@ -318,7 +318,8 @@ def test_qmatmul_many_rows_matches_oracle(Q, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(2, 64, 48), (5, 300, 200), (16, 1000, 517), (11, 14336, 96),
                                    (8, 4096, 4096), (2, 2048, 33), (3, 4096, 1001), (4, 8192, 96), (6, 14336, 257),
                                    (8, 512, 70001), (3, 256, 140000), (16, 128, 65536),
-                                   (7, 1024, 5000), (2, 8192, 77), (5, 3072, 70001), (8, 14336, 4096)])
+                                   (7, 1024, 5000), (2, 8192, 77), (5, 3072, 70001), (8, 14336, 4096),
+                                   (8, 8192, 1000), (6, 2048, 333)])
 def test_qmatmul_few_rows_matches_oracle(Q, M, K, N):
     """2..16 rows.  2..8 rows with K a multiple of 1024 up to 8192 go through
     the whole-row kernel (k_gemv_rows: 1..8 waves a block, 2, 4 or 8 rows a
